@@ -1,0 +1,880 @@
+/*
+ * be42_oracle.c -- CPU restatement of 42-Berlin-Engine's decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see be42_oracle.h).  Compiled with
+ * -ffp-contract=off: every fused multiply-add of the reference is an explicit
+ * fmaf() below, every unfused one is a separate multiply and add.
+ */
+#include "be42_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ======================================================================== */
+/* numerics primitives                                                      */
+/* ======================================================================== */
+
+/* Schraudolph exponential, src/compute/ops_math_fast.h:48-64.  The reference
+ * expression 12102203.0f * x + 1065353216.0f is fused by gcc (GNU C, -mfma);
+ * the cast truncates toward zero. */
+float or_fast_expf(float x)
+{
+    if (x < -87.0f)
+        return 0.0f;
+    if (x > 87.0f)
+        x = 87.0f;
+    int32_t bits = (int32_t)fmaf(12102203.0f, x, 1065353216.0f);
+    float r;
+    memcpy(&r, &bits, sizeof r);
+    return r;
+}
+
+/* round-to-nearest-even on the upper half, no NaN case: tensor.c:67-76 */
+uint16_t or_f32_to_bf16(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, sizeof u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* tensor.c:78-85 */
+float or_bf16_to_f32(uint16_t b)
+{
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+
+/* Horizontal sum of 8 lanes, simd_hsum_ps (simd_kernels.h:57-68):
+ * lo[i] = v[i] + v[i+4]; hadd; hadd  ==  (lo0 + lo1) + (lo2 + lo3). */
+static float hsum8(const float v[8])
+{
+    float l0 = v[0] + v[4], l1 = v[1] + v[5], l2 = v[2] + v[6], l3 = v[3] + v[7];
+    return (l0 + l1) + (l2 + l3);
+}
+
+/* simd_dot_f32_f32, simd_kernels.h:162-191: 8 lanes, lane l accumulates
+ * indices i = l (mod 8) with FMA in ascending order, then hsum8.  The scalar
+ * tail loop (:185-189) is itself vectorized by gcc -O3: when 4 or more
+ * elements remain, 4 products are formed unfused and added in order, and the
+ * last (< 4) elements are fused.  head_dim 64/128 has no tail. */
+float or_dot_f32_f32(const float *a, const float *b, int n)
+{
+    float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 7 < n; i += 8)
+        for (int l = 0; l < 8; l++)
+            lane[l] = fmaf(a[i + l], b[i + l], lane[l]);
+    float sum = hsum8(lane);
+    if (n - i >= 4) {
+        for (int l = 0; l < 4; l++)
+            sum = sum + a[i + l] * b[i + l];
+        i += 4;
+    }
+    for (; i < n; i++)
+        sum = fmaf(a[i], b[i], sum);
+    return sum;
+}
+
+/* simd_dot_bf16_f32, simd_kernels.h:97-156, as compiled without AVX-512
+ * (the AVX2 loop, then 0.0f + hsum, then a fused scalar tail). */
+float or_dot_bf16_f32(const uint16_t *a, const float *b, int n)
+{
+    float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 7 < n; i += 8)
+        for (int l = 0; l < 8; l++)
+            lane[l] = fmaf(or_bf16_to_f32(a[i + l]), b[i + l], lane[l]);
+    float sum = 0.0f;
+    sum = sum + hsum8(lane);
+    for (; i < n; i++)
+        sum = fmaf(or_bf16_to_f32(a[i]), b[i], sum);
+    return sum;
+}
+
+/* ======================================================================== */
+/* quant codecs                                                             */
+/* ======================================================================== */
+
+/* ops_quant.c:229-270: absmax, scale = amax/127 and inv = 127/amax (both 1
+ * when amax == 0), code = clamp((int)roundf(x * inv), -127, 127). */
+float or_quant_f32_to_int8(int8_t *out, const float *in, int n)
+{
+    float amax = 0.0f;
+    for (int i = 0; i < n; i++)
+        if (fabsf(in[i]) > amax)
+            amax = fabsf(in[i]);
+    float scale = 1.0f, inv = 1.0f;
+    if (amax > 0.0f) {
+        scale = amax / 127.0f;
+        inv = 127.0f / amax;
+    }
+    for (int i = 0; i < n; i++) {
+        int v = (int)roundf(in[i] * inv);
+        if (v > 127) v = 127;
+        if (v < -127) v = -127;
+        out[i] = (int8_t)v;
+    }
+    return scale;
+}
+
+/* ops_quant.c:275-305 (and dequant_int8, ops_quant.h:104-107) */
+void or_dequant_int8(float *out, const int8_t *in, float scale, int n)
+{
+    for (int i = 0; i < n; i++)
+        out[i] = (float)in[i] * scale;
+}
+
+/* E4M3 decode, bias 7, no NaN: ops_quant.c:27-48, table built at :53-63. */
+void or_fp8_lut(float *lut)
+{
+    for (int c = 0; c < 256; c++) {
+        int e = (c >> 3) & 0xF, m = c & 7;
+        float v = (e == 0) ? ldexpf((float)m / 8.0f, -6)
+                           : ldexpf(1.0f + (float)m / 8.0f, e - 7);
+        lut[c] = (c & 0x80) ? -v : v;
+    }
+}
+
+/* E4M3 encode, ops_quant.c:68-98: clamp to 448, exponent from floorf(log2f),
+ * mantissa rounded half-up and clamped to 7 (no carry into the exponent). */
+uint8_t or_float_to_fp8(float v)
+{
+    if (v == 0.0f)
+        return 0;
+    int sign = v < 0.0f;
+    float a = fabsf(v);
+    if (a > 448.0f)
+        a = 448.0f;
+    int e = (int)floorf(log2f(a)) + 7;
+    if (e < 0) e = 0;
+    if (e > 15) e = 15;
+    float frac = (e == 0) ? a * 64.0f : a / ldexpf(1.0f, e - 7) - 1.0f;
+    int m = (int)fmaf(frac, 8.0f, 0.5f);
+    if (m > 7) m = 7;
+    return (uint8_t)((sign << 7) | (e << 3) | m);
+}
+
+/* ops_quant.c:103-136: scale = amax/224, inv = 1/scale, codes of x*inv. */
+void or_quant_f32_to_fp8(uint8_t *out, const float *in, int n, float *scale)
+{
+    float amax = 0.0f;
+    for (int i = 0; i < n; i++)
+        if (fabsf(in[i]) > amax)
+            amax = fabsf(in[i]);
+    float inv;
+    if (amax > 0.0f) {
+        *scale = amax / 224.0f;
+        inv = 1.0f / *scale;
+    } else {
+        *scale = 1.0f;
+        inv = 1.0f;
+    }
+    for (int i = 0; i < n; i++)
+        out[i] = or_float_to_fp8(in[i] * inv);
+}
+
+void or_quantize_rows_int8(int8_t *q, float *scales, const float *w, int rows, int k)
+{
+    for (int r = 0; r < rows; r++)
+        scales[r] = or_quant_f32_to_int8(q + (size_t)r * k, w + (size_t)r * k, k);
+}
+
+void or_quantize_rows_fp8(uint8_t *q, float *scales, const float *w, int rows, int k)
+{
+    for (int r = 0; r < rows; r++)
+        or_quant_f32_to_fp8(q + (size_t)r * k, w + (size_t)r * k, k, &scales[r]);
+}
+
+/* ======================================================================== */
+/* quantized linear layers                                                  */
+/* ======================================================================== */
+
+static void set_threads(int n_threads)
+{
+#ifdef _OPENMP
+    if (n_threads > 0)
+        omp_set_num_threads(n_threads);
+#else
+    (void)n_threads;
+#endif
+}
+
+/* One output row in the structure of matvec_bf16_f32_blocked
+ * (ops_matmul.c:57-153): four 8-lane FMA accumulators over j step 32, an
+ * 8-lane cleanup into the first, (s0+s1)+(s2+s3), hsum8, fused scalar tail.
+ * The weight element is dequantized first: (float)q * scale (ops_quant.h:104)
+ * or lut[q] * scale. */
+#define GEMV_ROW(DEQ)                                                            \
+    do {                                                                         \
+        float acc[4][8];                                                         \
+        memset(acc, 0, sizeof acc);                                              \
+        int j = 0;                                                               \
+        for (; j + 31 < k; j += 32)                                              \
+            for (int a = 0; a < 4; a++)                                          \
+                for (int l = 0; l < 8; l++) {                                    \
+                    int jj = j + 8 * a + l;                                      \
+                    acc[a][l] = fmaf(DEQ(row[jj]), xv[jj], acc[a][l]);           \
+                }                                                                \
+        for (; j + 7 < k; j += 8)                                                \
+            for (int l = 0; l < 8; l++)                                          \
+                acc[0][l] = fmaf(DEQ(row[j + l]), xv[j + l], acc[0][l]);         \
+        float s[8];                                                              \
+        for (int l = 0; l < 8; l++)                                              \
+            s[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);            \
+        float sum = hsum8(s);                                                    \
+        for (; j < k; j++)                                                       \
+            sum = fmaf(DEQ(row[j]), xv[j], sum);                                 \
+        yv[i] = sum;                                                             \
+    } while (0)
+
+void or_gemv_q8(float *y, const int8_t *w, const float *scales, const float *x,
+                int n, int k, int batch, int n_threads)
+{
+    set_threads(n_threads);
+    for (int b = 0; b < batch; b++) {
+        const float *xv = x + (size_t)b * k;
+        float *yv = y + (size_t)b * n;
+        #pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; i++) {
+            const int8_t *row = w + (size_t)i * k;
+            const float sc = scales[i];
+#define DEQ_I8(q) ((float)(q) * sc)
+            GEMV_ROW(DEQ_I8);
+#undef DEQ_I8
+        }
+    }
+}
+
+void or_gemv_fp8(float *y, const uint8_t *w, const float *scales, const float *x,
+                 int n, int k, int batch, int n_threads)
+{
+    float lut[256];
+    or_fp8_lut(lut);
+    set_threads(n_threads);
+    for (int b = 0; b < batch; b++) {
+        const float *xv = x + (size_t)b * k;
+        float *yv = y + (size_t)b * n;
+        #pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; i++) {
+            const uint8_t *row = w + (size_t)i * k;
+            const float sc = scales[i];
+#define DEQ_F8(q) (lut[(q)] * sc)
+            GEMV_ROW(DEQ_F8);
+#undef DEQ_F8
+        }
+    }
+}
+
+void or_gemv_bf16(float *y, const uint16_t *w, const float *x, int n, int k, int n_threads)
+{
+    set_threads(n_threads);
+    const float *xv = x;
+    float *yv = y;
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < n; i++) {
+        const uint16_t *row = w + (size_t)i * k;
+#define DEQ_BF(q) or_bf16_to_f32(q)
+        GEMV_ROW(DEQ_BF);
+#undef DEQ_BF
+    }
+}
+
+void or_gemm_i8_acc(int32_t *acc, const int8_t *xq, const int8_t *wq,
+                    int m, int n, int k, int n_threads)
+{
+    set_threads(n_threads);
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int r = 0; r < m; r++)
+        for (int i = 0; i < n; i++) {
+            const int8_t *a = xq + (size_t)r * k, *b = wq + (size_t)i * k;
+            int32_t s = 0;
+            for (int j = 0; j < k; j++)
+                s += (int32_t)a[j] * (int32_t)b[j];
+            acc[(size_t)r * n + i] = s;
+        }
+}
+
+void or_gemm_i8(float *y, const int8_t *xq, const float *sx, const int8_t *wq,
+                const float *sw, int m, int n, int k, int n_threads)
+{
+    set_threads(n_threads);
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int r = 0; r < m; r++)
+        for (int i = 0; i < n; i++) {
+            const int8_t *a = xq + (size_t)r * k, *b = wq + (size_t)i * k;
+            int32_t s = 0;
+            for (int j = 0; j < k; j++)
+                s += (int32_t)a[j] * (int32_t)b[j];
+            y[(size_t)r * n + i] = ((float)s * sx[r]) * sw[i];
+        }
+}
+
+void or_gemm_fp8(float *y, const uint8_t *xq, const float *sx, const uint8_t *wq,
+                 const float *sw, int m, int n, int k, int n_threads)
+{
+    float lut[256];
+    or_fp8_lut(lut);
+    set_threads(n_threads);
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int r = 0; r < m; r++)
+        for (int i = 0; i < n; i++) {
+            const uint8_t *a = xq + (size_t)r * k, *b = wq + (size_t)i * k;
+            float s = 0.0f;
+            for (int j = 0; j < k; j++)
+                s = fmaf(lut[a[j]], lut[b[j]], s);
+            y[(size_t)r * n + i] = (s * sx[r]) * sw[i];
+        }
+}
+
+/* ======================================================================== */
+/* LSH                                                                      */
+/* ======================================================================== */
+
+/* ops_lsh.c:22-34: LCG, 15-bit uniforms, Box-Muller with libm. */
+static float lcg_gaussian(unsigned int *s)
+{
+    *s = *s * 1103515245u + 12345u;
+    float u1 = (float)((*s >> 16) & 0x7FFF) / 32767.0f;
+    *s = *s * 1103515245u + 12345u;
+    float u2 = (float)((*s >> 16) & 0x7FFF) / 32767.0f;
+    if (u1 < 1e-6f)
+        u1 = 1e-6f;
+    return sqrtf(-2.0f * logf(u1)) * cosf(2.0f * 3.14159265f * u2);
+}
+
+/* ops_lsh.c:40-85: 16 Gaussian rows, each L2-normalised (the squared norm is
+ * accumulated with a fused multiply-add), then transposed to [dim][16]. */
+void or_lsh_init(float *hp, float *hpT, int dim, unsigned int seed)
+{
+    if (dim > 256)
+        dim = 256;
+    for (int h = 0; h < OR_LSH_BITS; h++) {
+        float nrm = 0.0f;
+        for (int d = 0; d < dim; d++) {
+            float g = lcg_gaussian(&seed);
+            hp[h * dim + d] = g;
+            nrm = fmaf(g, g, nrm);
+        }
+        nrm = sqrtf(nrm);
+        if (nrm > 1e-6f)
+            for (int d = 0; d < dim; d++)
+                hp[h * dim + d] /= nrm;
+    }
+    for (int d = 0; d < dim; d++)
+        for (int h = 0; h < OR_LSH_BITS; h++)
+            hpT[d * OR_LSH_BITS + h] = hp[h * dim + d];
+}
+
+/* ops_lsh.c:138-242: bit h is set when the FMA chain over d ascending,
+ * s_h = fma(v[d], hpT[d][h], s_h) from +0, ends strictly above zero. */
+uint16_t or_lsh_hash(const float *hpT, int dim, const float *v)
+{
+    if (dim > 256) dim = 256;
+    if (dim <= 0) return 0;
+    float s[OR_LSH_BITS];
+    for (int h = 0; h < OR_LSH_BITS; h++)
+        s[h] = 0.0f;
+    for (int d = 0; d < dim; d++)
+        for (int h = 0; h < OR_LSH_BITS; h++)
+            s[h] = fmaf(v[d], hpT[d * OR_LSH_BITS + h], s[h]);
+    uint16_t hash = 0;
+    for (int h = 0; h < OR_LSH_BITS; h++)
+        if (s[h] > 0.0f)
+            hash |= (uint16_t)(1u << h);
+    return hash;
+}
+
+int or_hamming(uint16_t a, uint16_t b)
+{
+    return __builtin_popcount((unsigned)(a ^ b));
+}
+
+int or_lsh_index_create(or_lsh_index *ix, int cap)
+{
+    memset(ix, 0, sizeof *ix);
+    ix->cap = cap;
+    ix->hash = calloc((size_t)cap, sizeof *ix->hash);
+    ix->start = calloc((size_t)cap, sizeof *ix->start);
+    ix->len = calloc((size_t)cap, sizeof *ix->len);
+    ix->next = calloc((size_t)cap, sizeof *ix->next);
+    ix->heads = malloc(sizeof(int) * OR_LSH_BUCKETS);
+    if (!ix->hash || !ix->start || !ix->len || !ix->next || !ix->heads) {
+        or_lsh_index_destroy(ix);
+        return -1;
+    }
+    or_lsh_index_reset(ix);
+    return 0;
+}
+
+void or_lsh_index_destroy(or_lsh_index *ix)
+{
+    free(ix->hash); free(ix->start); free(ix->len); free(ix->next); free(ix->heads);
+    memset(ix, 0, sizeof *ix);
+}
+
+/* ops_lsh.c:90-118 */
+void or_lsh_index_reset(or_lsh_index *ix)
+{
+    ix->n_blocks = 0;
+    for (int b = 0; b < OR_LSH_BUCKETS; b++)
+        ix->heads[b] = -1;
+}
+
+/* ops_lsh.c:256-272: append, then push on the bucket's chain (LIFO);
+ * silently dropped once the index is full. */
+void or_lsh_insert_block(or_lsh_index *ix, uint16_t h, int start, int len)
+{
+    if (ix->n_blocks >= ix->cap)
+        return;
+    int id = ix->n_blocks;
+    ix->hash[id] = h;
+    ix->start[id] = start;
+    ix->len[id] = len;
+    int bucket = h % OR_LSH_BUCKETS;
+    ix->next[id] = ix->heads[bucket];
+    ix->heads[bucket] = id;
+    ix->n_blocks++;
+}
+
+/* ops_lsh.c:361-418: probe 0 is the query hash, probe p>0 flips bit p-1;
+ * each probed bucket's chain is walked newest first, filtered by Hamming
+ * radius 4 and de-duplicated with a bitmap; stops at max_ids. */
+int or_lsh_find_candidates(const or_lsh_index *ix, uint16_t qh, int *ids, int max_ids)
+{
+    int words = (ix->cap + 63) / 64;
+    uint64_t *seen = calloc((size_t)(words ? words : 1), sizeof(uint64_t));
+    int n = 0;
+    for (int probe = 0; probe <= OR_LSH_BITS && n < max_ids; probe++) {
+        uint16_t ph = probe == 0 ? qh : (uint16_t)(qh ^ (1u << (probe - 1)));
+        int id = ix->heads[ph % OR_LSH_BUCKETS];
+        while (id != -1 && n < max_ids) {
+            if (or_hamming(qh, ix->hash[id]) <= OR_LSH_RADIUS) {
+                uint64_t bit = 1ull << (id % 64);
+                if (!(seen[id / 64] & bit)) {
+                    seen[id / 64] |= bit;
+                    ids[n++] = id;
+                }
+            }
+            id = ix->next[id];
+        }
+    }
+    free(seen);
+    return n;
+}
+
+void or_q_mean(float *qm, const float *q, int n_heads, int hd)
+{
+    for (int d = 0; d < hd; d++)
+        qm[d] = 0.0f;
+    for (int h = 0; h < n_heads; h++)
+        for (int d = 0; d < hd; d++)
+            qm[d] += q[h * hd + d];
+    for (int d = 0; d < hd; d++)
+        qm[d] /= (float)n_heads;
+}
+
+/* ======================================================================== */
+/* selection                                                                */
+/* ======================================================================== */
+
+/* ops_heap.h:33-100: min-heap on score; a full heap replaces its root only
+ * for a strictly larger score. */
+static void heap_down(float *hs, int *hi, int size, int i)
+{
+    for (;;) {
+        int sm = i, l = 2 * i + 1, r = 2 * i + 2;
+        if (l < size && hs[l] < hs[sm]) sm = l;
+        if (r < size && hs[r] < hs[sm]) sm = r;
+        if (sm == i) break;
+        float ts = hs[i]; hs[i] = hs[sm]; hs[sm] = ts;
+        int ti = hi[i]; hi[i] = hi[sm]; hi[sm] = ti;
+        i = sm;
+    }
+}
+
+static void heap_up(float *hs, int *hi, int i)
+{
+    while (i > 0) {
+        int p = (i - 1) / 2;
+        if (hs[p] <= hs[i]) break;
+        float ts = hs[i]; hs[i] = hs[p]; hs[p] = ts;
+        int ti = hi[i]; hi[i] = hi[p]; hi[p] = ti;
+        i = p;
+    }
+}
+
+void or_heap_push(float *hs, int *hi, int *size, int cap, float score, int index)
+{
+    if (*size < cap) {
+        hs[*size] = score;
+        hi[*size] = index;
+        heap_up(hs, hi, *size);
+        (*size)++;
+    } else if (score > hs[0]) {
+        hs[0] = score;
+        hi[0] = index;
+        heap_down(hs, hi, *size, 0);
+    }
+}
+
+/* paged.c:439-495: first and last entries are anchors; the heap keeps the
+ * best min(k-2, n-2, 62) of entries 1..n-2; output is the heap array order. */
+int or_select_top_k_blocks(int *selected, const or_block_score *s, int n_blocks, int k)
+{
+    if (n_blocks <= 0)
+        return 0;
+    int first = s[0].phys_idx, cnt = 0;
+    selected[cnt++] = first;
+    int last = s[n_blocks - 1].phys_idx;
+    if (last != first && n_blocks > 1)
+        selected[cnt++] = last;
+    if (n_blocks <= 2 || k <= 2)
+        return cnt;
+    int ak = k - 2;
+    if (ak > n_blocks - 2) ak = n_blocks - 2;
+    if (ak > OR_HEAP_MAX) ak = OR_HEAP_MAX;
+    float hs[OR_HEAP_MAX];
+    int hi[OR_HEAP_MAX], hsize = 0;
+    for (int i = 1; i < n_blocks - 1; i++)
+        or_heap_push(hs, hi, &hsize, ak, s[i].score, i);
+    for (int i = 0; i < hsize; i++)
+        selected[cnt++] = s[hi[i]].phys_idx;
+    return cnt;
+}
+
+/* ======================================================================== */
+/* paged KV cache                                                           */
+/* ======================================================================== */
+
+static size_t page_elems(const or_paged *p) { return (size_t)p->n_kv * OR_PAGE_TOKENS * p->hd; }
+
+int or_paged_init(or_paged *p, int n_layers, int n_kv, int hd, int max_logical, int kind)
+{
+    memset(p, 0, sizeof *p);
+    p->n_layers = n_layers; p->n_kv = n_kv; p->hd = hd;
+    p->max_logical = max_logical; p->kind = kind;
+    p->cap = n_layers * max_logical;
+    size_t pe = page_elems(p), cap = (size_t)p->cap;
+    if (kind == OR_KV_INT8) {
+        p->kq = calloc(cap * pe, 1);
+        p->vq = calloc(cap * pe, 1);
+        p->ks = calloc(cap * n_kv * OR_PAGE_TOKENS, sizeof(float));
+        p->vs = calloc(cap * n_kv * OR_PAGE_TOKENS, sizeof(float));
+    } else {
+        p->kb = calloc(cap * pe, sizeof(uint16_t));
+        p->vb = calloc(cap * pe, sizeof(uint16_t));
+    }
+    p->centroid = calloc(cap * hd, sizeof(float));
+    p->ntok = calloc(cap, sizeof(int));
+    p->start_pos = malloc(cap * sizeof(int));
+    p->registered = calloc(cap, sizeof(int));
+    p->page_table = malloc(cap * sizeof(int));
+    p->free_stack = malloc(cap * sizeof(int));
+    p->logical_len = calloc((size_t)n_layers, sizeof(int));
+    if (!p->centroid || !p->ntok || !p->start_pos || !p->registered || !p->page_table ||
+        !p->free_stack || !p->logical_len || (kind == OR_KV_INT8 ? (!p->kq || !p->vq || !p->ks || !p->vs)
+                                                                 : (!p->kb || !p->vb))) {
+        or_paged_free(p);
+        return -1;
+    }
+    for (int i = 0; i < p->cap; i++) {
+        p->start_pos[i] = -1;
+        p->page_table[i] = -1;
+        p->free_stack[i] = i;
+    }
+    p->free_top = p->cap - 1;
+    return 0;
+}
+
+void or_paged_free(or_paged *p)
+{
+    free(p->kq); free(p->vq); free(p->kb); free(p->vb); free(p->ks); free(p->vs);
+    free(p->centroid); free(p->ntok); free(p->start_pos); free(p->registered);
+    free(p->page_table); free(p->free_stack); free(p->logical_len);
+    memset(p, 0, sizeof *p);
+}
+
+/* paged.c:159-179: pop the free stack (first allocation is cap-1); the page
+ * keeps its old centroid and codes. */
+int or_paged_alloc(or_paged *p)
+{
+    if (p->free_top < 0)
+        return -1;
+    int phys = p->free_stack[p->free_top--];
+    p->ntok[phys] = 0;
+    p->start_pos[phys] = -1;
+    p->registered[phys] = 0;
+    return phys;
+}
+
+void or_paged_release(or_paged *p, int phys)
+{
+    if (phys < 0 || phys >= p->cap)
+        return;
+    p->free_stack[++p->free_top] = phys;
+}
+
+/* paged.c:350-393: per dimension, the head-0 keys of the page are dequantized
+ * and summed token by token, then multiplied by 1.0f/n. */
+void or_centroid_int8(float *c, const int8_t *kq, const float *ks, int ntok, int hd)
+{
+    if (ntok <= 0)
+        return;
+    for (int d = 0; d < hd; d++)
+        c[d] = 0.0f;
+    for (int t = 0; t < ntok; t++)
+        for (int d = 0; d < hd; d++)
+            c[d] = c[d] + (float)kq[t * hd + d] * ks[t];
+    float inv = 1.0f / (float)ntok;
+    for (int d = 0; d < hd; d++)
+        c[d] = c[d] * inv;
+}
+
+/* The same centroid on bf16 rows (storage extension, same summation order). */
+void or_centroid_bf16(float *c, const uint16_t *kb, int ntok, int hd)
+{
+    if (ntok <= 0)
+        return;
+    for (int d = 0; d < hd; d++)
+        c[d] = 0.0f;
+    for (int t = 0; t < ntok; t++)
+        for (int d = 0; d < hd; d++)
+            c[d] = c[d] + or_bf16_to_f32(kb[t * hd + d]);
+    float inv = 1.0f / (float)ntok;
+    for (int d = 0; d < hd; d++)
+        c[d] = c[d] * inv;
+}
+
+/* paged.c:195-272: page = pos/16, slot = pos%16; a new logical page takes
+ * the top of the free stack; every KV head's K and V row is quantized
+ * (INT8: quant_f32_to_int8; BF16: tensor.c:67-76); a page that becomes full
+ * gets its head-0 centroid. */
+int or_paged_append(or_paged *p, int layer, const float *k, const float *v, int pos)
+{
+    int blk = pos / OR_PAGE_TOKENS, off = pos % OR_PAGE_TOKENS;
+    int base = layer * p->max_logical;
+    if (blk >= p->logical_len[layer]) {
+        int phys = or_paged_alloc(p);
+        if (phys < 0)
+            return -1;
+        p->page_table[base + blk] = phys;
+        p->logical_len[layer] = blk + 1;
+        p->start_pos[phys] = blk * OR_PAGE_TOKENS;
+    }
+    int phys = p->page_table[base + blk];
+    int hd = p->hd;
+    for (int h = 0; h < p->n_kv; h++) {
+        size_t row = (size_t)phys * page_elems(p) + ((size_t)h * OR_PAGE_TOKENS + off) * hd;
+        size_t sidx = ((size_t)phys * p->n_kv + h) * OR_PAGE_TOKENS + off;
+        if (p->kind == OR_KV_INT8) {
+            p->ks[sidx] = or_quant_f32_to_int8(p->kq + row, k + h * hd, hd);
+            p->vs[sidx] = or_quant_f32_to_int8(p->vq + row, v + h * hd, hd);
+        } else {
+            for (int d = 0; d < hd; d++) {
+                p->kb[row + d] = or_f32_to_bf16(k[h * hd + d]);
+                p->vb[row + d] = or_f32_to_bf16(v[h * hd + d]);
+            }
+        }
+    }
+    p->ntok[phys] = off + 1;
+    if (p->ntok[phys] == OR_PAGE_TOKENS && !p->registered[phys]) {
+        size_t head0 = (size_t)phys * page_elems(p);
+        if (p->kind == OR_KV_INT8)
+            or_centroid_int8(p->centroid + (size_t)phys * hd, p->kq + head0,
+                             p->ks + (size_t)phys * p->n_kv * OR_PAGE_TOKENS, OR_PAGE_TOKENS, hd);
+        else
+            or_centroid_bf16(p->centroid + (size_t)phys * hd, p->kb + head0, OR_PAGE_TOKENS, hd);
+        p->registered[phys] = 1;
+    }
+    return phys;
+}
+
+/* paged.c:312-336 */
+void or_paged_reset(or_paged *p, int layer)
+{
+    int base = layer * p->max_logical;
+    for (int i = 0; i < p->logical_len[layer]; i++) {
+        int phys = p->page_table[base + i];
+        if (phys >= 0)
+            or_paged_release(p, phys);
+        p->page_table[base + i] = -1;
+    }
+    p->logical_len[layer] = 0;
+}
+
+/* paged.c:401-431 */
+void or_score_blocks(or_block_score *s, const float *q, const or_paged *p, int layer, int n_blocks)
+{
+    int base = layer * p->max_logical;
+    for (int i = 0; i < n_blocks; i++) {
+        int phys = p->page_table[base + i];
+        s[i].block_idx = i;
+        s[i].phys_idx = phys;
+        s[i].score = phys < 0 ? -1e9f : or_dot_f32_f32(q, p->centroid + (size_t)phys * p->hd, p->hd);
+    }
+}
+
+/* ======================================================================== */
+/* attention                                                                */
+/* ======================================================================== */
+
+/* One online-softmax step of the INT8 block kernel (ops_attention.c:330-346):
+ *   m' = max(m, s); a = fast_expf(m - m'); p = fast_expf(s - m');
+ *   l = l * a + p (fused); out = out * a; out = fma(p, v, out). */
+static void attend_page_int8(float *o, float *m, float *l, const float *qh, const int8_t *kq,
+                             const float *ks, const int8_t *vq, const float *vs, int ntok,
+                             int hd, float scale, float *kbuf, float *vbuf)
+{
+    for (int t = 0; t < ntok; t++) {
+        or_dequant_int8(kbuf + t * hd, kq + t * hd, ks[t], hd);
+        or_dequant_int8(vbuf + t * hd, vq + t * hd, vs[t], hd);
+    }
+    for (int t = 0; t < ntok; t++) {
+        float s = or_dot_f32_f32(qh, kbuf + t * hd, hd) * scale;
+        float prev = *m;
+        if (s > prev)
+            *m = s;
+        float a = or_fast_expf(prev - *m);
+        float pr = or_fast_expf(s - *m);
+        *l = fmaf(*l, a, pr);
+        for (int d = 0; d < hd; d++)
+            o[d] = o[d] * a;
+        for (int d = 0; d < hd; d++)
+            o[d] = fmaf(pr, vbuf[t * hd + d], o[d]);
+    }
+}
+
+/* One step of the BF16 token kernel (ops_attention.c:131-170): score from
+ * simd_dot_bf16_f32, out = out * a then fma(p, bf16(v), out)
+ * (simd_rescale_fma_bf16, simd_kernels.h:264-301). */
+static void attend_page_bf16(float *o, float *m, float *l, const float *qh, const uint16_t *kb,
+                             const uint16_t *vb, int ntok, int hd, float scale)
+{
+    for (int t = 0; t < ntok; t++) {
+        float s = or_dot_bf16_f32(kb + t * hd, qh, hd) * scale;
+        float prev = *m;
+        if (s > prev)
+            *m = s;
+        float a = or_fast_expf(prev - *m);
+        float pr = or_fast_expf(s - *m);
+        *l = fmaf(*l, a, pr);
+        for (int d = 0; d < hd; d++)
+            o[d] = fmaf(pr, or_bf16_to_f32(vb[t * hd + d]), o[d] * a);
+    }
+}
+
+static void attend_head(float *o, const float *qh, const or_paged *p, const int *pages,
+                        int n_pages, int kvh, float scale)
+{
+    int hd = p->hd;
+    float m = -INFINITY, l = 0.0f;
+    float *kbuf = malloc(sizeof(float) * OR_PAGE_TOKENS * hd);
+    float *vbuf = malloc(sizeof(float) * OR_PAGE_TOKENS * hd);
+    for (int d = 0; d < hd; d++)
+        o[d] = 0.0f;
+    for (int i = 0; i < n_pages; i++) {
+        int phys = pages[i];
+        if (phys < 0 || p->ntok[phys] <= 0)
+            continue;
+        size_t row = (size_t)phys * page_elems(p) + (size_t)kvh * OR_PAGE_TOKENS * hd;
+        if (p->kind == OR_KV_INT8) {
+            size_t sidx = ((size_t)phys * p->n_kv + kvh) * OR_PAGE_TOKENS;
+            attend_page_int8(o, &m, &l, qh, p->kq + row, p->ks + sidx, p->vq + row, p->vs + sidx,
+                             p->ntok[phys], hd, scale, kbuf, vbuf);
+        } else {
+            attend_page_bf16(o, &m, &l, qh, p->kb + row, p->vb + row, p->ntok[phys], hd, scale);
+        }
+    }
+    if (l > 0.0f) {
+        float inv = 1.0f / l;
+        for (int d = 0; d < hd; d++)
+            o[d] = o[d] * inv;
+    }
+    free(kbuf);
+    free(vbuf);
+}
+
+/* ops_attention.c:443-461: query head h reads KV head h / (n_heads / n_kv). */
+void or_paged_attention_pages(float *out, const float *q, const or_paged *p,
+                              const int *pages, int n_pages, int n_heads,
+                              float scale, int n_threads)
+{
+    set_threads(n_threads);
+    int group = n_heads / p->n_kv;
+    #pragma omp parallel for schedule(static)
+    for (int h = 0; h < n_heads; h++)
+        attend_head(out + (size_t)h * p->hd, q + (size_t)h * p->hd, p, pages, n_pages,
+                    h / group, scale);
+}
+
+void or_paged_attention_dense(float *out, const float *q, const or_paged *p, int layer,
+                              int n_heads, float scale, int n_threads)
+{
+    int n = p->logical_len[layer];
+    int *pages = malloc(sizeof(int) * (n > 0 ? n : 1));
+    for (int i = 0; i < n; i++)
+        pages[i] = p->page_table[layer * p->max_logical + i];
+    or_paged_attention_pages(out, q, p, pages, n, n_heads, scale, n_threads);
+    free(pages);
+}
+
+/* ======================================================================== */
+/* routing composition                                                      */
+/* ======================================================================== */
+
+int or_route_pages(int *selected, int *n_cand_out, int *cand_out,
+                   const or_paged *p, int layer, const float *q, int n_heads,
+                   const float *hpT, const or_lsh_index *ix, int cand_cap, int k)
+{
+    int n = p->logical_len[layer], base = layer * p->max_logical;
+    if (n_cand_out)
+        *n_cand_out = 0;
+    if (n <= 0)
+        return 0;
+    if (n <= k) {
+        for (int i = 0; i < n; i++)
+            selected[i] = p->page_table[base + i];
+        return n;
+    }
+    float *qm = malloc(sizeof(float) * p->hd);
+    or_q_mean(qm, q, n_heads, p->hd);
+    uint16_t qh = or_lsh_hash(hpT, p->hd, qm);
+    free(qm);
+    int *cand = malloc(sizeof(int) * (cand_cap > 0 ? cand_cap : 1));
+    int nc = or_lsh_find_candidates(ix, qh, cand, cand_cap);
+    if (n_cand_out)
+        *n_cand_out = nc;
+    if (cand_out)
+        memcpy(cand_out, cand, sizeof(int) * nc);
+    or_block_score *list = malloc(sizeof(or_block_score) * (nc + 2));
+    int m = 0;
+    list[m].block_idx = 0;
+    list[m].phys_idx = p->page_table[base];
+    m++;
+    for (int i = 0; i < nc; i++) {
+        int lg = cand[i];
+        if (lg == 0 || lg == n - 1 || lg >= n)
+            continue;
+        list[m].block_idx = lg;
+        list[m].phys_idx = p->page_table[base + lg];
+        m++;
+    }
+    list[m].block_idx = n - 1;
+    list[m].phys_idx = p->page_table[base + n - 1];
+    m++;
+    for (int i = 0; i < m; i++) {
+        int phys = list[i].phys_idx;
+        list[i].score = phys < 0 ? -1e9f : or_dot_f32_f32(q, p->centroid + (size_t)phys * p->hd, p->hd);
+    }
+    int ns = or_select_top_k_blocks(selected, list, m, k);
+    free(list);
+    free(cand);
+    return ns;
+}

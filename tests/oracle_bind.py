@@ -1,0 +1,342 @@
+"""ctypes bindings for the CPU checkers (test infrastructure only).
+
+* ``Oracle``  -- oracle/liboracle42.so, the C restatement of the reference path.
+* ``RefLib``  -- oracle/_ref/libref42.so, the reference's own sources compiled in
+  place (present only where oracle/Makefile could build it).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle42.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libref42.so")
+
+f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+PAGE = 16
+OR_KV_INT8, OR_KV_BF16 = 0, 1
+
+
+def _sig(lib, name, res, *args):
+    fn = getattr(lib, name)
+    fn.restype = res
+    fn.argtypes = list(args)
+    return fn
+
+
+class OrLshIndex(C.Structure):
+    _fields_ = [("cap", C.c_int), ("n_blocks", C.c_int), ("hash", C.POINTER(C.c_uint16)),
+                ("start", C.POINTER(C.c_int)), ("len", C.POINTER(C.c_int)),
+                ("next", C.POINTER(C.c_int)), ("heads", C.POINTER(C.c_int))]
+
+
+class OrPaged(C.Structure):
+    _fields_ = [("n_layers", C.c_int), ("n_kv", C.c_int), ("hd", C.c_int),
+                ("max_logical", C.c_int), ("cap", C.c_int), ("kind", C.c_int),
+                ("kq", C.POINTER(C.c_int8)), ("vq", C.POINTER(C.c_int8)),
+                ("kb", C.POINTER(C.c_uint16)), ("vb", C.POINTER(C.c_uint16)),
+                ("ks", C.POINTER(C.c_float)), ("vs", C.POINTER(C.c_float)),
+                ("centroid", C.POINTER(C.c_float)), ("ntok", C.POINTER(C.c_int)),
+                ("start_pos", C.POINTER(C.c_int)), ("registered", C.POINTER(C.c_int)),
+                ("page_table", C.POINTER(C.c_int)), ("free_stack", C.POINTER(C.c_int)),
+                ("free_top", C.c_int), ("logical_len", C.POINTER(C.c_int))]
+
+
+class Oracle:
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run __graft_entry__.build()")
+        L = self.lib = C.CDLL(path)
+        _sig(L, "or_fast_expf", C.c_float, C.c_float)
+        _sig(L, "or_f32_to_bf16", C.c_uint16, C.c_float)
+        _sig(L, "or_bf16_to_f32", C.c_float, C.c_uint16)
+        _sig(L, "or_dot_f32_f32", C.c_float, f32p, f32p, C.c_int)
+        _sig(L, "or_dot_bf16_f32", C.c_float, u16p, f32p, C.c_int)
+        _sig(L, "or_quant_f32_to_int8", C.c_float, i8p, f32p, C.c_int)
+        _sig(L, "or_fp8_lut", None, f32p)
+        _sig(L, "or_float_to_fp8", C.c_uint8, C.c_float)
+        _sig(L, "or_quant_f32_to_fp8", None, u8p, f32p, C.c_int, C.POINTER(C.c_float))
+        _sig(L, "or_quantize_rows_int8", None, i8p, f32p, f32p, C.c_int, C.c_int)
+        _sig(L, "or_quantize_rows_fp8", None, u8p, f32p, f32p, C.c_int, C.c_int)
+        _sig(L, "or_gemv_q8", None, f32p, i8p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int)
+        _sig(L, "or_gemv_fp8", None, f32p, u8p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int)
+        _sig(L, "or_gemv_bf16", None, f32p, u16p, f32p, C.c_int, C.c_int, C.c_int)
+        _sig(L, "or_gemm_i8_acc", None, i32p, i8p, i8p, C.c_int, C.c_int, C.c_int, C.c_int)
+        _sig(L, "or_gemm_i8", None, f32p, i8p, f32p, i8p, f32p, C.c_int, C.c_int, C.c_int, C.c_int)
+        _sig(L, "or_gemm_fp8", None, f32p, u8p, f32p, u8p, f32p, C.c_int, C.c_int, C.c_int, C.c_int)
+        _sig(L, "or_lsh_init", None, f32p, f32p, C.c_int, C.c_uint)
+        _sig(L, "or_lsh_hash", C.c_uint16, f32p, C.c_int, f32p)
+        _sig(L, "or_hamming", C.c_int, C.c_uint16, C.c_uint16)
+        _sig(L, "or_lsh_index_create", C.c_int, C.POINTER(OrLshIndex), C.c_int)
+        _sig(L, "or_lsh_index_destroy", None, C.POINTER(OrLshIndex))
+        _sig(L, "or_lsh_index_reset", None, C.POINTER(OrLshIndex))
+        _sig(L, "or_lsh_insert_block", None, C.POINTER(OrLshIndex), C.c_uint16, C.c_int, C.c_int)
+        _sig(L, "or_lsh_find_candidates", C.c_int, C.POINTER(OrLshIndex), C.c_uint16, i32p, C.c_int)
+        _sig(L, "or_heap_push", None, f32p, i32p, C.POINTER(C.c_int), C.c_int, C.c_float, C.c_int)
+        _sig(L, "or_paged_init", C.c_int, C.POINTER(OrPaged), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int)
+        _sig(L, "or_paged_free", None, C.POINTER(OrPaged))
+        _sig(L, "or_paged_append", C.c_int, C.POINTER(OrPaged), C.c_int, f32p, f32p, C.c_int)
+        _sig(L, "or_paged_reset", None, C.POINTER(OrPaged), C.c_int)
+        _sig(L, "or_centroid_int8", None, f32p, i8p, f32p, C.c_int, C.c_int)
+        _sig(L, "or_centroid_bf16", None, f32p, u16p, C.c_int, C.c_int)
+        _sig(L, "or_paged_attention_pages", None, f32p, f32p, C.POINTER(OrPaged), i32p, C.c_int,
+             C.c_int, C.c_float, C.c_int)
+        _sig(L, "or_paged_attention_dense", None, f32p, f32p, C.POINTER(OrPaged), C.c_int, C.c_int,
+             C.c_float, C.c_int)
+        _sig(L, "or_route_pages", C.c_int, i32p, C.POINTER(C.c_int), i32p, C.POINTER(OrPaged), C.c_int,
+             f32p, C.c_int, f32p, C.POINTER(OrLshIndex), C.c_int, C.c_int)
+        _sig(L, "or_q_mean", None, f32p, f32p, C.c_int, C.c_int)
+
+    # -- scalar helpers -----------------------------------------------------
+    def fast_expf(self, x):
+        return np.array([self.lib.or_fast_expf(float(v)) for v in np.ravel(x)], np.float32)
+
+    def f32_to_bf16(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        u = x.view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    def fp8_lut(self):
+        lut = np.zeros(256, np.float32)
+        self.lib.or_fp8_lut(lut)
+        return lut
+
+    def quant_int8(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        q = np.zeros(x.shape[-1], np.int8)
+        s = self.lib.or_quant_f32_to_int8(q, x, x.shape[-1])
+        return q, np.float32(s)
+
+    def quant_fp8(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        q = np.zeros(x.shape[-1], np.uint8)
+        s = C.c_float()
+        self.lib.or_quant_f32_to_fp8(q, x, x.shape[-1], C.byref(s))
+        return q, np.float32(s.value)
+
+    def quantize_rows(self, w, kind):
+        w = np.ascontiguousarray(w, np.float32)
+        n, k = w.shape
+        sc = np.zeros(n, np.float32)
+        if kind == "int8":
+            q = np.zeros((n, k), np.int8)
+            self.lib.or_quantize_rows_int8(q, sc, w, n, k)
+        else:
+            q = np.zeros((n, k), np.uint8)
+            self.lib.or_quantize_rows_fp8(q, sc, w, n, k)
+        return q, sc
+
+    def gemv(self, wq, sc, x, kind, threads=0):
+        n, k = wq.shape
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, k)
+        y = np.zeros((x.shape[0], n), np.float32)
+        fn = self.lib.or_gemv_q8 if kind == "int8" else self.lib.or_gemv_fp8
+        fn(y, np.ascontiguousarray(wq), np.ascontiguousarray(sc, np.float32), x, n, k, x.shape[0], threads)
+        return y
+
+    def gemm_i8_acc(self, xq, wq, threads=0):
+        m, k = xq.shape
+        n = wq.shape[0]
+        acc = np.zeros((m, n), np.int32)
+        self.lib.or_gemm_i8_acc(acc, np.ascontiguousarray(xq), np.ascontiguousarray(wq), m, n, k, threads)
+        return acc
+
+    def gemm(self, xq, sx, wq, sw, kind, threads=0):
+        m, k = xq.shape
+        n = wq.shape[0]
+        y = np.zeros((m, n), np.float32)
+        fn = self.lib.or_gemm_i8 if kind == "int8" else self.lib.or_gemm_fp8
+        fn(y, np.ascontiguousarray(xq), np.ascontiguousarray(sx, np.float32), np.ascontiguousarray(wq),
+           np.ascontiguousarray(sw, np.float32), m, n, k, threads)
+        return y
+
+    def lsh_init(self, dim, seed):
+        hp = np.zeros(16 * dim, np.float32)
+        hpT = np.zeros(dim * 16, np.float32)
+        self.lib.or_lsh_init(hp, hpT, dim, seed)
+        return hp.reshape(16, dim), hpT.reshape(dim, 16)
+
+    def lsh_hash(self, hpT, v):
+        return int(self.lib.or_lsh_hash(np.ascontiguousarray(hpT, np.float32).ravel(), hpT.shape[0],
+                                        np.ascontiguousarray(v, np.float32)))
+
+    def q_mean(self, q, n_heads, hd):
+        out = np.zeros(hd, np.float32)
+        self.lib.or_q_mean(out, np.ascontiguousarray(q, np.float32).ravel(), n_heads, hd)
+        return out
+
+
+class OracleIndex:
+    """The reference LSH index (heads + LIFO chains) restated in the oracle."""
+
+    def __init__(self, orc, cap):
+        self.o = orc
+        self.ix = OrLshIndex()
+        if orc.lib.or_lsh_index_create(C.byref(self.ix), cap) != 0:
+            raise MemoryError("or_lsh_index_create")
+
+    def insert(self, h, start, length):
+        self.o.lib.or_lsh_insert_block(C.byref(self.ix), h, start, length)
+
+    def candidates(self, qh, cap):
+        ids = np.zeros(max(cap, 1), np.int32)
+        n = self.o.lib.or_lsh_find_candidates(C.byref(self.ix), qh, ids, cap)
+        return ids[:n].copy()
+
+    def __del__(self):
+        try:
+            self.o.lib.or_lsh_index_destroy(C.byref(self.ix))
+        except Exception:
+            pass
+
+
+class OraclePaged:
+    """The reference paged KV block manager restated in the oracle."""
+
+    def __init__(self, orc, n_layers, n_kv, hd, max_logical, kind):
+        self.o = orc
+        self.p = OrPaged()
+        if orc.lib.or_paged_init(C.byref(self.p), n_layers, n_kv, hd, max_logical, kind) != 0:
+            raise MemoryError("or_paged_init")
+        self.n_kv, self.hd, self.kind = n_kv, hd, kind
+
+    def append(self, layer, k, v, pos):
+        return self.o.lib.or_paged_append(C.byref(self.p), layer, np.ascontiguousarray(k, np.float32),
+                                          np.ascontiguousarray(v, np.float32), pos)
+
+    def reset(self, layer):
+        self.o.lib.or_paged_reset(C.byref(self.p), layer)
+
+    def n_blocks(self, layer):
+        return self.p.logical_len[layer]
+
+    def phys(self, layer, logical):
+        return self.p.page_table[layer * self.p.max_logical + logical]
+
+    def ntok(self, phys):
+        return self.p.ntok[phys]
+
+    def page_arrays(self, phys):
+        """(K, V, k_scales, v_scales, centroid) of one physical page as numpy copies."""
+        pe = self.n_kv * PAGE * self.hd
+        cen = np.ctypeslib.as_array(self.p.centroid, shape=(self.p.cap * self.hd,))[phys * self.hd:(phys + 1) * self.hd].copy()
+        if self.kind == OR_KV_INT8:
+            kq = np.ctypeslib.as_array(self.p.kq, shape=(self.p.cap * pe,))[phys * pe:(phys + 1) * pe]
+            vq = np.ctypeslib.as_array(self.p.vq, shape=(self.p.cap * pe,))[phys * pe:(phys + 1) * pe]
+            ns = self.n_kv * PAGE
+            ks = np.ctypeslib.as_array(self.p.ks, shape=(self.p.cap * ns,))[phys * ns:(phys + 1) * ns]
+            vs = np.ctypeslib.as_array(self.p.vs, shape=(self.p.cap * ns,))[phys * ns:(phys + 1) * ns]
+            return kq.copy(), vq.copy(), ks.copy(), vs.copy(), cen
+        kb = np.ctypeslib.as_array(self.p.kb, shape=(self.p.cap * pe,))[phys * pe:(phys + 1) * pe]
+        vb = np.ctypeslib.as_array(self.p.vb, shape=(self.p.cap * pe,))[phys * pe:(phys + 1) * pe]
+        return kb.copy(), vb.copy(), None, None, cen
+
+    def attention_pages(self, q, pages, n_heads, scale, threads=0):
+        out = np.zeros(n_heads * self.hd, np.float32)
+        pages = np.ascontiguousarray(pages, np.int32)
+        self.o.lib.or_paged_attention_pages(out, np.ascontiguousarray(q, np.float32).ravel(), C.byref(self.p),
+                                            pages, len(pages), n_heads, scale, threads)
+        return out
+
+    def attention_dense(self, q, layer, n_heads, scale, threads=0):
+        out = np.zeros(n_heads * self.hd, np.float32)
+        self.o.lib.or_paged_attention_dense(out, np.ascontiguousarray(q, np.float32).ravel(), C.byref(self.p),
+                                            layer, n_heads, scale, threads)
+        return out
+
+    def route(self, layer, q, n_heads, hpT, index, cand_cap, k):
+        sel = np.zeros(max(k, self.n_blocks(layer)) + 2, np.int32)
+        cand = np.zeros(max(cand_cap, 1), np.int32)
+        nc = C.c_int()
+        ns = self.o.lib.or_route_pages(sel, C.byref(nc), cand, C.byref(self.p), layer,
+                                       np.ascontiguousarray(q, np.float32).ravel(), n_heads,
+                                       np.ascontiguousarray(hpT, np.float32).ravel(), C.byref(index.ix),
+                                       cand_cap, k)
+        return sel[:ns].copy(), cand[:nc.value].copy()
+
+    def __del__(self):
+        try:
+            self.o.lib.or_paged_free(C.byref(self.p))
+        except Exception:
+            pass
+
+
+class RefLib:
+    """The compiled reference (oracle/_ref/libref42.so) through ref_shim.c."""
+
+    def __init__(self, path=REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path)
+        _sig(L, "ref_fast_expf", C.c_float, C.c_float)
+        _sig(L, "ref_dot_f32_f32", C.c_float, f32p, f32p, C.c_int)
+        _sig(L, "ref_dot_bf16_f32", C.c_float, u16p, f32p, C.c_int)
+        _sig(L, "ref_f32_to_bf16", C.c_uint16, C.c_float)
+        _sig(L, "ref_heap_run", C.c_int, f32p, C.c_int, C.c_int, f32p, i32p)
+        _sig(L, "ref_fp8_lut", None, f32p)
+        _sig(L, "quant_f32_to_fp8", None, u8p, f32p, C.c_int, C.POINTER(C.c_float))
+        _sig(L, "quant_f32_to_int8", C.c_float, i8p, f32p, C.c_int)
+        _sig(L, "ref_lsh_ctx_new", C.c_void_p, C.c_int, C.c_uint)
+        _sig(L, "ref_lsh_ctx_free", None, C.c_void_p)
+        _sig(L, "ref_lsh_ctx_get", None, C.c_void_p, f32p, f32p)
+        _sig(L, "ref_lsh_hash", C.c_uint16, C.c_void_p, f32p)
+        _sig(L, "ref_lsh_index_new", C.c_void_p)
+        _sig(L, "ref_lsh_index_free", None, C.c_void_p)
+        _sig(L, "ref_lsh_insert", None, C.c_void_p, C.c_uint16, C.c_int, C.c_int)
+        _sig(L, "ref_lsh_candidates", C.c_int, C.c_void_p, C.c_uint16, i32p, C.c_int)
+        _sig(L, "ref_paged_new", C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int)
+        _sig(L, "ref_paged_free", None, C.c_void_p)
+        _sig(L, "ref_paged_append", None, C.c_void_p, C.c_int, f32p, f32p, C.c_int)
+        _sig(L, "ref_paged_reset", None, C.c_void_p, C.c_int)
+        _sig(L, "ref_paged_n_blocks", C.c_int, C.c_void_p, C.c_int)
+        _sig(L, "ref_paged_phys", C.c_int, C.c_void_p, C.c_int, C.c_int)
+        _sig(L, "ref_paged_page", C.c_int, C.c_void_p, C.c_int, i8p, i8p, f32p, f32p, f32p)
+        _sig(L, "ref_score_blocks", None, C.c_void_p, C.c_int, f32p, C.c_int, i32p, f32p)
+        _sig(L, "ref_select_top_k", C.c_int, i32p, i32p, f32p, C.c_int, C.c_int, i32p)
+        _sig(L, "ref_paged_attention", None, C.c_void_p, C.c_int, f32p, f32p, C.c_int, C.c_float)
+        _sig(L, "ref_paged_attention_sparse", None, C.c_void_p, f32p, f32p, i32p, C.c_int, C.c_int,
+             C.c_float)
+        _sig(L, "ref_flash_attention_head", None, f32p, f32p, u16p, u16p, C.c_int, C.c_int, C.c_float)
+        _sig(L, "ref_matmul", C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
+             C.c_void_p, C.c_int, C.c_int)
+        _sig(L, "lsh_hamming_distance", C.c_int, C.c_uint16, C.c_uint16)
+        # the reference's block_manager_init prints a banner on stdout; silence nothing,
+        # tests capture it.
+
+    def fp8_lut(self):
+        lut = np.zeros(256, np.float32)
+        self.lib.ref_fp8_lut(lut)
+        return lut
+
+    def quant_int8(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        q = np.zeros(x.shape[-1], np.int8)
+        s = self.lib.quant_f32_to_int8(q, x, x.shape[-1])
+        return q, np.float32(s)
+
+    def quant_fp8(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        q = np.zeros(x.shape[-1], np.uint8)
+        s = C.c_float()
+        self.lib.quant_f32_to_fp8(q, x, x.shape[-1], C.byref(s))
+        return q, np.float32(s.value)
+
+    def lsh_init(self, dim, seed):
+        ctx = self.lib.ref_lsh_ctx_new(dim, seed)
+        hp = np.zeros(16 * dim, np.float32)
+        hpT = np.zeros(dim * 16, np.float32)
+        self.lib.ref_lsh_ctx_get(ctx, hp, hpT)
+        return ctx, hp.reshape(16, dim), hpT.reshape(dim, 16)
+
+
+def ref_available():
+    return os.path.exists(REF_SO)
