@@ -1,0 +1,111 @@
+// be42_common.h -- shared definitions of the gfx950 decode hot-path library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "be42_hip.h"
+
+// --------------------------------------------------------------------------
+// error handling: every entry point returns BE42_OK or a negative code and
+// records a message readable through be42_last_error().
+// --------------------------------------------------------------------------
+namespace be42 {
+
+void set_error(const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what, const char *file, int line);
+
+// Grow-only device workspace, one per device, owned by the library.
+void *workspace(size_t bytes, hipStream_t s);
+
+// FP8 encoder exponent thresholds (see quant.hip): thr[i] is the smallest
+// float a in [2^(i+e0-1), 2^(i+e0)) for which glibc's floorf(log2f(a)) returns
+// i+e0.  Uploaded once per device by be42_init().
+constexpr int kFp8ThrE0 = -10;   // exponent of thr[0]
+constexpr int kFp8ThrN = 21;     // exponents -10 .. 10
+int fp8_thresholds_ready(int device);
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace be42
+
+#define BE42_HIP(call)                                                          \
+    do {                                                                        \
+        hipError_t be42_e_ = (call);                                            \
+        if (be42_e_ != hipSuccess)                                              \
+            return be42::hip_fail(be42_e_, #call, __FILE__, __LINE__);          \
+    } while (0)
+
+#define BE42_CHECK(cond, ...)                                                   \
+    do {                                                                        \
+        if (!(cond)) {                                                          \
+            be42::set_error(__VA_ARGS__);                                       \
+            return BE42_EINVAL;                                                 \
+        }                                                                       \
+    } while (0)
+
+#define BE42_LAUNCH_CHECK()                                                     \
+    do {                                                                        \
+        hipError_t be42_e_ = hipGetLastError();                                 \
+        if (be42_e_ != hipSuccess)                                              \
+            return be42::hip_fail(be42_e_, "kernel launch", __FILE__, __LINE__); \
+    } while (0)
+
+// --------------------------------------------------------------------------
+// device helpers
+// --------------------------------------------------------------------------
+namespace be42 {
+
+constexpr int kWave = 64;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Schraudolph exponential with the reference's clamps; the product and the
+// bias are fused exactly as gcc fuses the reference expression.
+__device__ __forceinline__ float fast_expf(float x)
+{
+    if (x < -87.0f)
+        return 0.0f;
+    if (x > 87.0f)
+        x = 87.0f;
+    return __int_as_float((int)__fmaf_rn(12102203.0f, x, 1065353216.0f));
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// round-to-nearest-even on the upper half, without a NaN case
+__device__ __forceinline__ uint16_t f32_to_bf16(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+}  // namespace be42

@@ -1,0 +1,530 @@
+// gemv.hip -- decode GEMV for per-row-scaled INT8 / FP8 E4M3 weights on gfx950.
+//
+// Replaces the n == 1 GEMV of op_matmul (src/compute/ops_matmul.c:366-417;
+// structure of matvec_bf16_f32_blocked :57-153) for quantized weights:
+//     y[b][i] = w_scale[i] * sum_j w[i][j] * x[b][j],   x fp32, batch <= 16.
+//
+// The weight stream goes straight from HBM into the matrix cores with no
+// per-element dequantisation: the fp32 activations are split once per call
+// into fixed-point digits of the MFMA input type, so that
+//     x[b][j] = s_b * sum_d digit_d[b][j] * R^-d   (R = 254 for INT8, 30 for FP8)
+// to ~2^-24 relative to max|x[b]|, and each digit plane is one MFMA operand.
+//   INT8: 3 int8 digits in [-127, 127], v_mfma_i32_16x16x64_i8, exact int32
+//         accumulators, recombined in fp64 in the epilogue.
+//   FP8:  5 integer digits in [-15, 15] stored as E4M3 codes (exact),
+//         v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales, fp32 accumulators.
+// The per-row scale is applied once per output, in the epilogue.
+//
+// A lane (r = lane % 16, g = lane / 16) loads 16 (INT8) or 32 (FP8)
+// contiguous bytes of weight row r per MFMA; the same k positions of digit
+// column r form the B operand.  Tiling and K-split are described at k_gemv.
+#include <cstdio>
+#include <cstdlib>
+#include <type_traits>
+
+#include "be42_common.h"
+
+namespace be42 {
+
+constexpr int kI8Digits = 3;
+constexpr int kI8Base = 254;
+constexpr int kF8Digits = 5;
+constexpr int kF8Base = 30;
+
+// integer in [-15, 15] -> exact E4M3 code
+__device__ __forceinline__ uint8_t small_int_to_e4m3(int n)
+{
+    const uint32_t s = n < 0 ? 0x80u : 0u;
+    int a = n < 0 ? -n : n;
+    if (a == 0)
+        return 0;
+    int e = 31 - __clz(a);               // floor(log2 a), 0..3
+    int m = (a << (3 - e)) & 7;          // 3 mantissa bits below the leading one
+    return (uint8_t)(s | ((uint32_t)(e + 7) << 3) | (uint32_t)m);
+}
+
+// Digit planes of the activations.  Grid (chunks of kPrepChunk k, batch):
+// every block recomputes the row absmax (x is small and L2-resident), then
+// writes the digits of its chunk, 4 consecutive k per thread as one dword per
+// plane.  Layout dig[d][b][0..Kp), zero beyond K.
+constexpr int kPrepChunk = 1024;
+
+// Per-thread partial absmax of x[0..K) (K % 4 == 0 on this path) with four
+// independent 16-byte loads in flight per iteration.
+__device__ __forceinline__ float absmax_vec(const float *x, int K)
+{
+    const float4 *x4 = (const float4 *)x;
+    const int n4 = K >> 2;
+    float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
+    int i = threadIdx.x;
+    for (; i + 3 * (int)blockDim.x < n4; i += 4 * blockDim.x) {
+        const float4 a = x4[i], b = x4[i + blockDim.x], c = x4[i + 2 * blockDim.x], d = x4[i + 3 * blockDim.x];
+        m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+        m2 = fmaxf(m2, fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))));
+        m3 = fmaxf(m3, fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w))));
+    }
+    for (; i < n4; i += blockDim.x) {
+        const float4 a = x4[i];
+        m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    }
+    return fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+}
+
+template <bool FP8>
+__global__ __launch_bounds__(256) void k_gemv_prep(const float *__restrict__ x, int K, int Kp, int B,
+                                                   uint8_t *__restrict__ dig, float *__restrict__ sx)
+{
+    __shared__ float red[4];
+    const int b = blockIdx.y;
+    const float *xr = x + (size_t)b * K;
+    const float m = wave_max(absmax_vec(xr, K));
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    constexpr int R0 = FP8 ? 15 : 127;
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr float BASE = FP8 ? (float)kF8Base : (float)kI8Base;
+    const float s = amax > 0.0f ? amax / (float)R0 : 1.0f;
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        sx[b] = s;
+    const int k0 = blockIdx.x * kPrepChunk + threadIdx.x * 4;
+    if (k0 >= Kp)
+        return;
+    uint32_t word[ND];
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+        word[d] = 0;
+    const float4 xv4 = k0 < K ? *(const float4 *)(xr + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float xe[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float v = xe[e] / s;
+#pragma unroll
+        for (int d = 0; d < ND; d++) {
+            float dv = rintf(v);
+            dv = fminf(fmaxf(dv, -(float)R0), (float)R0);
+            v = (v - dv) * BASE;
+            const uint32_t code = FP8 ? small_int_to_e4m3((int)dv) : (uint32_t)(uint8_t)(int8_t)(int)dv;
+            word[d] |= code << (8 * e);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+        *(uint32_t *)(dig + ((size_t)d * B + b) * Kp + k0) = word[d];
+}
+
+__constant__ double kF8Weight[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 27000, 1.0 / 810000};
+
+// Main GEMV kernel.
+// Operands of one MFMA: A = 16 weight rows x STEP k (row r = lane % 16, k
+// slice lane / 16), B = STEP k x 16 columns, where column c of column group nc
+// is digit plane d = (16*nc + c) % ND of batch row b = (16*nc + c) / ND.
+// A batch of <= 5 (INT8) or <= 3 (FP8) rows therefore needs one MFMA per
+// weight tile: NC = ceil(batch * ND / 16) MFMAs in general.
+//   INT8: STEP 64, 16 bytes per lane, v_mfma_i32_16x16x64_i8, exact int32.
+//   FP8:  STEP 128, 32 bytes per lane, unit-scale v_mfma_scale_f32_16x16x128_f8f6f4.
+// A block holds WAVES waves in WAVES/KS groups; a group owns one tile of
+// 16*RT rows and its KS waves split K into contiguous slices.  A wave loads a
+// burst of U MFMA steps (RT*U KiB of INT8 weights) with unconditional 16-byte
+// loads, then runs its MFMAs; latency is hidden by the other resident waves
+// (MFMA time per burst is a few percent of the memory latency).  Epilogue: raw accumulators go through LDS one row tile at
+// a time and the group's first wave sums slices and digit columns per output,
+// weighting digit d by 254^(2-d) in exact int64 (INT8) or 30^-d in fp64 (FP8).
+template <bool FP8, int RT, int U, int KS, int NC, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_gemv(
+    float *__restrict__ y, const uint8_t *__restrict__ W, const float *__restrict__ sw,
+    const uint8_t *__restrict__ dig, const float *__restrict__ sx, int N, int K, int Kp, int B)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr int STEP = FP8 ? 128 : 64;
+    constexpr int NV = FP8 ? 2 : 1;          // 16-byte loads per lane per operand
+    constexpr int GROUPS = WAVES / KS;
+    using Tot = typename std::conditional<FP8, double, long long>::type;
+    using Acc = typename std::conditional<FP8, v4f, v4i>::type;
+    using Raw = typename std::conditional<FP8, float, int>::type;
+    __shared__ Raw part[WAVES][16][NC * 16];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int group = wave / KS, slice = wave % KS;
+    const int r = lane & 15, g = lane >> 4;
+    const int row0 = (blockIdx.x * GROUPS + group) * 16 * RT;
+    const int nburst = Kp / (STEP * U);
+    const int b0 = (nburst * slice) / KS, b1 = (nburst * (slice + 1)) / KS;
+
+    Acc acc[RT][NC];
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+            acc[t][c] = Acc{0, 0, 0, 0};
+
+    // Every load is unconditional and in bounds, so the loop carries no
+    // branches and the next burst stays in flight across the MFMAs: rows past
+    // N read row N-1 and columns past the batch read plane 0 (neither is ever
+    // written out); k past K reads the row's last 16 bytes against digits that
+    // are zero there.
+    const uint8_t *wrow[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const int row = min(row0 + t * 16 + r, N - 1);
+        wrow[t] = W + (size_t)row * K;
+    }
+    const uint8_t *xcolp[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int col = 16 * c + r, bb = col / ND, d = col % ND;
+        xcolp[c] = dig + ((size_t)d * B + (bb < B ? bb : 0)) * Kp;
+    }
+    const int klast = K - 16;
+
+    v4i wv[RT][U][NV], xv[NC][U][NV];
+    auto load = [&](int bi, v4i (&wd)[RT][U][NV], v4i (&xd)[NC][U][NV]) {
+        const int kb = bi * STEP * U + g * 16 * NV;
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int v = 0; v < NV; v++)
+                    wd[t][u][v] = *(const v4i *)(wrow[t] + min(kb + u * STEP + 16 * v, klast));
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int v = 0; v < NV; v++)
+                    xd[c][u][v] = *(const v4i *)(xcolp[c] + kb + u * STEP + 16 * v);
+    };
+    auto compute = [&](const v4i (&wd)[RT][U][NV], const v4i (&xd)[NC][U][NV]) {
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    if constexpr (FP8) {
+                        const v8i a = {wd[t][u][0][0], wd[t][u][0][1], wd[t][u][0][2], wd[t][u][0][3],
+                                       wd[t][u][1][0], wd[t][u][1][1], wd[t][u][1][2], wd[t][u][1][3]};
+                        const v8i bb = {xd[c][u][0][0], xd[c][u][0][1], xd[c][u][0][2], xd[c][u][0][3],
+                                        xd[c][u][1][0], xd[c][u][1][1], xd[c][u][1][2], xd[c][u][1][3]};
+                        acc[t][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bb, acc[t][c], 0, 0, 0,
+                                                                                     127, 0, 127);
+                    } else {
+                        acc[t][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wd[t][u][0], xd[c][u][0], acc[t][c],
+                                                                          0, 0, 0);
+                    }
+                }
+    };
+    // Ping-pong over two register sets: the loads of burst i+1 are issued
+    // before the MFMAs of burst i (the scheduling barriers keep that order),
+    // so a wave always has one burst in flight while it computes.
+    for (int bi = b0; bi < b1; bi++) {
+        load(bi, wv, xv);
+        compute(wv, xv);
+    }
+
+    // C layout of a 16x16 MFMA: lane holds rows 4*(lane/16)+j of column lane%16.
+    // One row tile at a time through LDS: slices and digit columns are summed
+    // per output by the group's first wave.
+    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        if (t > 0)
+            __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                part[wave][4 * g + j][16 * c + r] = acc[t][c][j];
+        __syncthreads();
+        if (slice == 0) {
+            for (int o = lane; o < 16 * B; o += kWave) {
+                const int bb = o / 16, i = o % 16;
+                const int row = row0 + t * 16 + i;
+                if (row >= N)
+                    continue;
+                Tot tot = 0;
+#pragma unroll
+                for (int d = 0; d < ND; d++) {
+                    Tot dsum = 0;
+#pragma unroll
+                    for (int s = 0; s < KS; s++)
+                        dsum += (Tot)part[group * KS + s][i][bb * ND + d];
+                    // digit weights: INT8 254^(2-d) (exact in int64), FP8 30^-d
+                    if constexpr (FP8)
+                        tot = tot + dsum * kF8Weight[d];
+                    else
+                        tot = tot + dsum * (Tot)(d == 0 ? kI8Base * kI8Base : (d == 1 ? kI8Base : 1));
+                }
+                y[(size_t)bb * N + row] = (float)((double)tot * ((double)sx[bb] * sxw * (double)sw[row]));
+            }
+        }
+    }
+}
+
+// Generic path for shapes the MFMA path does not take (k % 16 != 0, unaligned
+// pointers, batch > 16): one block per output row, fp32 dot of the
+// dequantized row, reduction through LDS.
+template <bool FP8>
+__global__ __launch_bounds__(256) void k_gemv_generic(float *y, const uint8_t *W, const float *sw,
+                                                      const float *x, int N, int K, int B)
+{
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const uint8_t *wr = W + (size_t)row * K;
+    for (int b = 0; b < B; b++) {
+        const float *xb = x + (size_t)b * K;
+        float s = 0.0f;
+        for (int k = threadIdx.x; k < K; k += blockDim.x) {
+            float w;
+            if (FP8) {
+                const uint8_t c = wr[k];
+                const int e = (c >> 3) & 0xF, m = c & 7;
+                w = (e == 0) ? (float)m * (1.0f / 512.0f)
+                             : __uint_as_float((uint32_t)(e + 120) << 23) * (1.0f + (float)m * 0.125f);
+                w = (c & 0x80) ? -w : w;
+            } else {
+                w = (float)(int8_t)wr[k];
+            }
+            s = __fmaf_rn(w, xb[k], s);
+        }
+        s = wave_sum(s);
+        if ((threadIdx.x & 63) == 0)
+            red[threadIdx.x >> 6] = s;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            y[(size_t)b * N + row] = ((red[0] + red[1]) + (red[2] + red[3])) * sw[row];
+        __syncthreads();
+    }
+}
+
+// Activation digit planes: layout of the buffer filled by be42_gemv_prepare.
+// Kp is K rounded up to the largest burst any tile configuration uses.
+struct XDigits {
+    int nd, step, burst;
+};
+static XDigits xdig_layout(bool fp8)
+{
+    return fp8 ? XDigits{kF8Digits, 128, 128 * 8} : XDigits{kI8Digits, 64, 64 * 16};
+}
+static size_t xdig_kp(int k, bool fp8)
+{
+    const XDigits L = xdig_layout(fp8);
+    return ((size_t)(k + L.burst - 1) / L.burst) * L.burst;
+}
+// digits first, then 16 float scales on a 256-byte boundary
+static size_t xdig_bytes(int k, int batch, bool fp8)
+{
+    const size_t dig = (size_t)xdig_layout(fp8).nd * batch * xdig_kp(k, fp8);
+    return ((dig + 255) & ~(size_t)255) + 16 * sizeof(float);
+}
+
+static int prepare_launch(void *buf, const float *x, int k, int batch, bool fp8, hipStream_t s)
+{
+    const int Kp = (int)xdig_kp(k, fp8);
+    uint8_t *dig = (uint8_t *)buf;
+    const size_t dbytes = (size_t)xdig_layout(fp8).nd * batch * Kp;
+    float *sx = (float *)(dig + ((dbytes + 255) & ~(size_t)255));
+    const dim3 grid((Kp + kPrepChunk - 1) / kPrepChunk, batch);
+    if (fp8)
+        hipLaunchKernelGGL(k_gemv_prep<true>, grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+    else
+        hipLaunchKernelGGL(k_gemv_prep<false>, grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
+template <bool FP8, int RT, int U, int NC, int KS>
+static void launch_ks(float *y, const uint8_t *w, const float *sw, const uint8_t *dig, const float *sx, int n,
+                      int k, int Kp, int batch, hipStream_t s)
+{
+    constexpr int WAVES = KS > 4 ? KS : 4;
+    const int tiles = (n + 16 * RT - 1) / (16 * RT);
+    constexpr int GROUPS = WAVES / KS;
+    const int blocks = (tiles + GROUPS - 1) / GROUPS;
+    hipLaunchKernelGGL((k_gemv<FP8, RT, U, KS, NC, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, y, w, sw, dig,
+                       sx, n, k, Kp, batch);
+}
+
+// K-split factor: the fewest waves per row tile that still give >= target
+// waves, and no more slices than there are bursts.
+template <bool FP8, int RT, int U, int NC>
+static int launch_shape(float *y, const uint8_t *w, const float *sw, const uint8_t *dig, const float *sx,
+                        int n, int k, int Kp, int batch, hipStream_t s, int ks_force)
+{
+    const int tiles = (n + 16 * RT - 1) / (16 * RT);
+    const int nburst = Kp / ((FP8 ? 128 : 64) * U);
+    int ks = 1;
+    while (ks < 8 && tiles * ks < 4096 && ks * 2 <= nburst)
+        ks *= 2;
+    if (ks_force > 0) {
+        ks = ks_force;
+        while (ks > 1 && ks > nburst)
+            ks /= 2;
+    }
+    switch (ks) {
+    case 1: launch_ks<FP8, RT, U, NC, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s); break;
+    case 2: launch_ks<FP8, RT, U, NC, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s); break;
+    case 4: launch_ks<FP8, RT, U, NC, 4>(y, w, sw, dig, sx, n, k, Kp, batch, s); break;
+    default: launch_ks<FP8, RT, U, NC, 8>(y, w, sw, dig, sx, n, k, Kp, batch, s); break;
+    }
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
+// Tile override for tuning: BE42_GEMV_TILE="<variant>,<ks>".
+static int tile_override(int *ks)
+{
+    int variant = -1, ksv = 0;
+    const char *e = getenv("BE42_GEMV_TILE");
+    if (e && sscanf(e, "%d,%d", &variant, &ksv) < 1)
+        variant = -1;
+    *ks = ksv;
+    return variant;
+}
+
+// Tile choice.  NC = ceil(batch*ND/16) MFMA column groups.  Variant 0 (one
+// row tile, deep bursts) maximises the number of waves for small n; variant 1
+// (four row tiles) amortises the activation operand over more weight rows
+// and keeps VGPRs low for large n.
+template <bool FP8>
+static int prepared_launch(float *y, const uint8_t *w, const float *sw, const void *buf, int n, int k,
+                           int batch, hipStream_t s)
+{
+    const int Kp = (int)xdig_kp(k, FP8);
+    const uint8_t *dig = (const uint8_t *)buf;
+    const size_t dbytes = (size_t)xdig_layout(FP8).nd * batch * Kp;
+    const float *sx = (const float *)(dig + ((dbytes + 255) & ~(size_t)255));
+    const int nc = (batch * (FP8 ? kF8Digits : kI8Digits) + 15) / 16;
+    int ksf = 0;
+    int variant = tile_override(&ksf);
+    if (variant < 0) {
+        // measured on MI355X over the 4 shapes x batch {1,4,16} x both dtypes
+        if (n <= 8192) {
+            variant = 0;
+            ksf = nc == 1 ? 8 : 4;
+        } else if (n <= 32768) {
+            variant = 1;
+            ksf = FP8 ? (nc == 1 ? 8 : 4) : (nc == 1 ? 4 : 8);
+        } else {
+            variant = 1;
+            ksf = FP8 ? (nc == 1 ? 8 : 2) : (nc == 1 ? 4 : 2);
+        }
+    }
+    if constexpr (FP8) {
+        if (variant == 0) {
+            switch (nc) {
+            case 1: return launch_shape<true, 1, 8, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+            case 2: return launch_shape<true, 1, 4, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+            default: return launch_shape<true, 2, 1, 5>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+            }
+        }
+        switch (nc) {
+        case 1: return launch_shape<true, 4, 2, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        case 2: return launch_shape<true, 4, 2, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        case 3: return launch_shape<true, 4, 1, 3>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        case 4: return launch_shape<true, 4, 1, 4>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        default: return launch_shape<true, 4, 1, 5>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        }
+    } else {
+        if (variant == 0) {
+            switch (nc) {
+            case 1: return launch_shape<false, 1, 16, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+            case 2: return launch_shape<false, 1, 8, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+            default: return launch_shape<false, 2, 4, 3>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+            }
+        }
+        switch (nc) {
+        case 1: return launch_shape<false, 4, 4, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        case 2: return launch_shape<false, 4, 4, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        default: return launch_shape<false, 4, 4, 3>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        }
+    }
+}
+
+static bool fast_path(const void *w, int k, int batch)
+{
+    return batch <= 16 && (k % 16) == 0 && (((uintptr_t)w) & 15) == 0;
+}
+
+static bool x_aligned(const float *x) { return (((uintptr_t)x) & 15) == 0; }
+
+template <bool FP8>
+static int gemv_launch(float *y, const uint8_t *w, const float *sw, const float *x, int n, int k,
+                       int batch, void *stream)
+{
+    const char *name = FP8 ? "be42_gemv_fp8" : "be42_gemv_q8";
+    BE42_CHECK(y && w && sw && x, "%s: null pointer", name);
+    BE42_CHECK(n >= 0 && k > 0 && batch >= 0, "%s: bad shape n=%d k=%d batch=%d", name, n, k, batch);
+    if (n == 0 || batch == 0)
+        return BE42_OK;
+    hipStream_t s = as_stream(stream);
+    if (!fast_path(w, k, batch) || !x_aligned(x)) {
+        hipLaunchKernelGGL(k_gemv_generic<FP8>, dim3(n), dim3(256), 0, s, y, w, sw, x, n, k, batch);
+        BE42_LAUNCH_CHECK();
+        return BE42_OK;
+    }
+    void *buf = workspace(xdig_bytes(k, batch, FP8), s);
+    if (!buf)
+        return BE42_ENOMEM;
+    int rc = prepare_launch(buf, x, k, batch, FP8, s);
+    if (rc)
+        return rc;
+    return prepared_launch<FP8>(y, w, sw, buf, n, k, batch, s);
+}
+
+}  // namespace be42
+
+using namespace be42;
+
+extern "C" int be42_gemv_q8(float *y, const int8_t *w, const float *w_scale, const float *x, int n,
+                            int k, int batch, void *stream)
+{
+    return gemv_launch<false>(y, (const uint8_t *)w, w_scale, x, n, k, batch, stream);
+}
+
+extern "C" int be42_gemv_fp8(float *y, const uint8_t *w, const float *w_scale, const float *x, int n,
+                             int k, int batch, void *stream)
+{
+    return gemv_launch<true>(y, w, w_scale, x, n, k, batch, stream);
+}
+
+extern "C" size_t be42_gemv_xdig_bytes(int k, int batch, int fp8)
+{
+    if (k <= 0 || batch <= 0 || batch > 16)
+        return 0;
+    return xdig_bytes(k, batch, fp8 != 0);
+}
+
+extern "C" int be42_gemv_prepare(void *xdig, const float *x, int k, int batch, int fp8, void *stream)
+{
+    BE42_CHECK(xdig && x, "be42_gemv_prepare: null pointer");
+    BE42_CHECK(k > 0 && k % 16 == 0 && batch > 0 && batch <= 16 && x_aligned(x),
+               "be42_gemv_prepare: needs k %% 16 == 0, 1 <= batch <= 16 and 16-byte aligned x (k=%d batch=%d)",
+               k, batch);
+    return prepare_launch(xdig, x, k, batch, fp8 != 0, as_stream(stream));
+}
+
+extern "C" int be42_gemv_q8_prepared(float *y, const int8_t *w, const float *w_scale, const void *xdig,
+                                     int n, int k, int batch, void *stream)
+{
+    BE42_CHECK(y && w && w_scale && xdig, "be42_gemv_q8_prepared: null pointer");
+    BE42_CHECK(n >= 0 && fast_path(w, k, batch) && batch > 0,
+               "be42_gemv_q8_prepared: needs 16-byte aligned weights, k %% 16 == 0, 1 <= batch <= 16");
+    if (n == 0)
+        return BE42_OK;
+    return prepared_launch<false>(y, (const uint8_t *)w, w_scale, xdig, n, k, batch, as_stream(stream));
+}
+
+extern "C" int be42_gemv_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, const void *xdig,
+                                      int n, int k, int batch, void *stream)
+{
+    BE42_CHECK(y && w && w_scale && xdig, "be42_gemv_fp8_prepared: null pointer");
+    BE42_CHECK(n >= 0 && fast_path(w, k, batch) && batch > 0,
+               "be42_gemv_fp8_prepared: needs 16-byte aligned weights, k %% 16 == 0, 1 <= batch <= 16");
+    if (n == 0)
+        return BE42_OK;
+    return prepared_launch<true>(y, w, w_scale, xdig, n, k, batch, as_stream(stream));
+}

@@ -8,6 +8,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 sys.path.insert(0, HERE)
 sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "42-berlin-engine_amd"))
 
 
 def pytest_configure(config):
@@ -39,4 +40,13 @@ def be():
     lib = be42.load()
     if not lib.device_available():
         pytest.fail("no HIP device: GPU tests must run on an MI355X")
+    lib.init(0)
     return lib
+
+
+def rel_err(got, want):
+    """max |got - want| / max |want| (normwise relative error)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    den = np.abs(want).max()
+    return float(np.abs(got - want).max() / (den if den > 0 else 1.0))

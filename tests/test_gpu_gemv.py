@@ -1,0 +1,94 @@
+"""GPU decode GEMV (INT8 / FP8 per-row weights, fp32 activations) vs the oracle.
+
+Tolerance (north star): max-rel-err <= 1e-3 with fp32 accumulation, written
+here as max|y - y_ref| / max|y_ref|; the digit-split MFMA path is expected at
+~1e-6.  Element-wise relative error is also bounded where |y_ref| is not tiny.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _check(y, want):
+    err = rel_err(y, want)
+    assert err <= TOL, err
+    big = np.abs(want) > 1e-2 * np.abs(want).max()
+    el = np.abs(y[big] - want[big]) / np.abs(want[big])
+    assert el.max() <= 1e-2, el.max()
+    return err
+
+
+SHAPES = [(37, 4096, 1), (64, 1024, 4), (100, 4096, 16), (16, 16, 1), (300, 512, 3),
+          (1408, 512, 1), (512, 1408, 2), (129, 4096, 8)]
+GENERIC = [(33, 7, 1), (20, 1000, 2), (5, 4099, 1), (40, 256, 17)]
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("n,k,b", SHAPES + GENERIC)
+def test_gemv_small(be, orc, kind, n, k, b):
+    rng = np.random.default_rng(n * 1000 + k + b)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    wq, ws = orc.quantize_rows(w, kind)
+    want = orc.gemv(wq, ws, x, kind)
+    # quantize on the GPU too: identical codes, then the GPU GEMV
+    wt = torch.from_numpy(w).cuda()
+    q, s = be.quant_rows_int8(wt) if kind == "int8" else be.quant_rows_fp8(wt)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+    y = be.gemv(q, s, torch.from_numpy(x).cuda(), kind).cpu().numpy()
+    _check(y, want)
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("b", [1, 4, 16])
+def test_gemv_config_shapes(be, orc, kind, n, k, b):
+    """BASELINE config 2 shapes; codes drawn directly to keep host time short."""
+    rng = np.random.default_rng(n + k + b)
+    if kind == "int8":
+        wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    else:
+        wq = rng.integers(0, 256, (n, k), dtype=np.uint8)
+        wq[(wq & 0x7F) == 0x7F] = 0x7E       # the reference encoder never emits 0x7F
+    ws = rng.uniform(0.005, 0.02, n).astype(np.float32) / (1.0 if kind == "int8" else 200.0)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    want = orc.gemv(wq, ws, x, kind)
+    y = be.gemv(torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda(),
+                torch.from_numpy(x).cuda(), kind).cpu().numpy()
+    _check(y, want)
+
+
+def test_gemv_lm_head_int8(be, orc):
+    """The largest config-2 shape (128256 x 4096) at batch 1."""
+    rng = np.random.default_rng(7)
+    n, k = 128256, 4096
+    wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = rng.uniform(0.005, 0.02, n).astype(np.float32)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    want = orc.gemv(wq, ws, x, "int8")
+    y = be.gemv(torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda(),
+                torch.from_numpy(x).cuda(), "int8").cpu().numpy()
+    _check(y, want)
+
+
+def test_gemv_outliers_and_zero(be, orc):
+    """Activations with 8-sigma outliers, an all-zero batch row, ragged n."""
+    rng = np.random.default_rng(8)
+    n, k, b = 77, 2048, 3
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    x[0, rng.integers(0, k, 20)] = 8.0
+    x[1] = 0.0
+    for kind in ("int8", "fp8"):
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        wq, ws = orc.quantize_rows(w, kind)
+        want = orc.gemv(wq, ws, x, kind)
+        y = be.gemv(torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda(),
+                    torch.from_numpy(x).cuda(), kind).cpu().numpy()
+        assert np.all(y[1] == 0.0)
+        _check(y, want)
