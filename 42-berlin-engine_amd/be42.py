@@ -39,7 +39,31 @@ SIGNATURES = {
     "be42_gemv_prepare": (i32, [vp, vp, i32, i32, i32, vp]),
     "be42_gemv_q8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemv_fp8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "be42_kv_create": (i32, [vp, i32, i32, i32, i32, i32, vp]),
+    "be42_kv_destroy": (None, [vp]),
+    "be42_kv_set_projection": (i32, [vp, vp]),
+    "be42_kv_append": (i32, [vp, i32, vp, vp, i32, i32, vp]),
+    "be42_kv_reset": (i32, [vp, i32, vp]),
+    "be42_kv_layer_pages": (i32, [vp, i32, vp, i32]),
+    "be42_lsh_projection": (None, [vp, vp, i32, C.c_uint]),
+    "be42_lsh_hash": (i32, [vp, vp, i32, vp, i32, vp]),
+    "be42_lsh_candidates": (i32, [vp, vp, vp, i32, vp, i32, i32, vp]),
+    "be42_lsh_route": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp, vp]),
+    "be42_attn_workspace_bytes": (sz, [i32, i32, i32, i32, i32]),
+    "be42_paged_attention": (i32, [vp, vp, i32, i32, vp, vp, i32, i32, f32, vp, i32, vp, sz, vp]),
 }
+
+KV_INT8, KV_BF16 = 0, 1
+
+
+class KVPoolStruct(C.Structure):
+    """Layout of be42_kv_pool (include/be42_hip.h)."""
+    _fields_ = [("kind", C.c_int), ("n_layers", C.c_int), ("n_kv", C.c_int), ("head_dim", C.c_int),
+                ("max_logical", C.c_int), ("capacity", C.c_int),
+                ("k", C.c_void_p), ("v", C.c_void_p), ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
+                ("centroid", C.c_void_p), ("ntok", C.c_void_p), ("page_table", C.c_void_p),
+                ("n_logical", C.c_void_p), ("page_hash", C.c_void_p), ("n_indexed", C.c_void_p),
+                ("hpT", C.c_void_p)]
 
 
 class Be42Error(RuntimeError):
@@ -151,6 +175,108 @@ class Lib:
         name = "be42_gemv_q8_prepared" if kind == "int8" else "be42_gemv_fp8_prepared"
         self._call(name, self.p(out), self.p(w), self.p(sw), self.p(xdig), n, k, batch, self.stream(stream))
         return out
+
+
+    # -- LSH / paged KV / attention --------------------------------------------
+    def lsh_projection(self, dim, seed):
+        import numpy as np
+        hp = np.zeros(16 * dim, np.float32)
+        hpT = np.zeros(dim * 16, np.float32)
+        self.lib.be42_lsh_projection(hp.ctypes.data, hpT.ctypes.data, dim, seed)
+        return hp.reshape(16, dim), hpT.reshape(dim, 16)
+
+    def lsh_hash(self, vecs, hpT):
+        t = self.torch
+        n, dim = vecs.shape
+        out = t.empty(n, dtype=t.int16, device=vecs.device)
+        self._call("be42_lsh_hash", self.p(out), self.p(vecs), n, self.p(hpT), dim, self.stream())
+        return out
+
+    def lsh_candidates(self, hashes, qh, cap):
+        t = self.torch
+        n_q = qh.numel()
+        ids = t.full((n_q, cap), -1, dtype=t.int32, device=qh.device)
+        n = t.zeros(n_q, dtype=t.int32, device=qh.device)
+        self._call("be42_lsh_candidates", self.p(ids), self.p(n), self.p(hashes), hashes.numel(), self.p(qh),
+                   n_q, cap, self.stream())
+        return ids, n
+
+    def kv_pool(self, kind, n_layers, n_kv, head_dim, max_logical, hpT=None):
+        return KVPool(self, kind, n_layers, n_kv, head_dim, max_logical, hpT)
+
+    def route(self, pool, q, k_sel, cap, slots=None, sel_stride=None):
+        t = self.torch
+        B, H, hd = q.shape
+        sel_stride = sel_stride or max(k_sel, 64, pool.max_logical if k_sel >= pool.max_logical else 0)
+        sel = t.full((B, sel_stride), -1, dtype=t.int32, device=q.device)
+        nsel = t.zeros(B, dtype=t.int32, device=q.device)
+        cand = t.full((B, cap), -1, dtype=t.int32, device=q.device)
+        ncand = t.zeros(B, dtype=t.int32, device=q.device)
+        qh = t.zeros(B, dtype=t.int16, device=q.device)
+        self._call("be42_lsh_route", pool.handle, self.p(q), self.p(slots), B, H, k_sel, cap, self.p(sel),
+                   self.p(nsel), sel_stride, self.p(cand), self.p(ncand), self.p(qh), self.stream())
+        return sel, nsel, cand, ncand, qh
+
+    def paged_attention(self, pool, q, sel, nsel, max_sel, scale, n_split=1, out=None, workspace=None):
+        t = self.torch
+        B, H, hd = q.shape
+        out = out if out is not None else t.empty((B, H, hd), dtype=t.float32, device=q.device)
+        ws, wsb = (self.p(workspace), workspace.numel()) if workspace is not None else (None, 0)
+        self._call("be42_paged_attention", pool.handle, self.p(q), B, H, self.p(sel), self.p(nsel),
+                   sel.shape[1], max_sel, float(scale), self.p(out), n_split, ws, wsb, self.stream())
+        return out
+
+
+class KVPool:
+    """Owner of a be42_kv_pool (device page pool + host page allocator)."""
+
+    def __init__(self, lib, kind, n_layers, n_kv, head_dim, max_logical, hpT=None):
+        import numpy as np
+        self.lib = lib
+        lib.init()
+        h = C.c_void_p()
+        hp = None if hpT is None else np.ascontiguousarray(hpT, np.float32)
+        lib.check(lib.lib.be42_kv_create(C.byref(h), kind, n_layers, n_kv, head_dim, max_logical,
+                                         None if hp is None else hp.ctypes.data), "be42_kv_create")
+        self.handle = h
+        self.s = C.cast(h, C.POINTER(KVPoolStruct)).contents
+        self.kind, self.n_layers, self.n_kv, self.head_dim = kind, n_layers, n_kv, head_dim
+        self.max_logical = max_logical
+
+    def append(self, layer, k, v, pos0):
+        n = k.shape[0]
+        self.lib._call("be42_kv_append", self.handle, layer, self.lib.p(k), self.lib.p(v), pos0, n,
+                       self.lib.stream())
+
+    def reset(self, layer):
+        self.lib._call("be42_kv_reset", self.handle, layer, self.lib.stream())
+
+    def layer_pages(self, layer):
+        import numpy as np
+        out = np.zeros(self.max_logical, np.int32)
+        n = self.lib.lib.be42_kv_layer_pages(self.handle, layer, out.ctypes.data, self.max_logical)
+        return out[:n].copy()
+
+    def fetch(self, field, count, dtype):
+        """Copy `count` elements of a device array of the pool to the host."""
+        import numpy as np
+        arr = np.empty(count, dtype)
+        self.lib.torch.cuda.synchronize()
+        self.lib.check(self.lib.lib.be42_memcpy_d2h(arr.ctypes.data, getattr(self.s, field), arr.nbytes, None),
+                       "be42_memcpy_d2h")
+        return arr
+
+    def close(self):
+        if self.handle:
+            self.lib.torch.cuda.synchronize()
+            self.lib.lib.be42_kv_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 _LIB = None

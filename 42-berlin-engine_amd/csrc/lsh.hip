@@ -1,0 +1,482 @@
+// lsh.hip -- LSH-routed page selection on gfx950.
+//
+// lsh_init (projection)         src/compute/ops_lsh.c:22-85     (host, at init)
+// lsh_hash                      src/compute/ops_lsh.c:138-242
+// lsh_find_candidates           src/compute/ops_lsh.c:361-418
+// q_mean routing glue           src/inference/inference.c:291-302
+// score_blocks                  src/memory/paged.c:401-431 (simd_dot_f32_f32,
+//                               src/compute/simd_kernels.h:162-191)
+// select_top_k_blocks + heap    src/memory/paged.c:439-495, src/compute/ops_heap.h:33-100
+//
+// One workgroup (4 waves) routes one query:
+//  1. q_mean over the heads (sum in head order, then / n_heads) and its hash:
+//     16 lanes each run the FMA chain over d, the sign bits are packed with a
+//     ballot.
+//  2. Candidates.  The reference walks, for probes p = 0..16 (p = 0: the query
+//     hash, p > 0: bit p-1 flipped), the bucket's LIFO chain.  A bucket holds
+//     exactly the blocks whose hash equals the probed hash, newest first, and
+//     the Hamming filter (radius 4) never rejects them, so the candidate list
+//     is: for p ascending, the indexed pages with hash == qh ^ flip(p) in
+//     descending id order, truncated at `cap`.  The waves scan the page-hash
+//     array in descending id order (wave 0 the highest ids) and file each hit
+//     under its probe with a ballot; per-probe lists are concatenated.
+//  3. Middle entries = candidates other than the first and last page; each is
+//     scored q[head 0] . centroid with the reference's 8-lane reduction tree.
+//  4. Selection = [first page, last page] + the exact min-heap of the
+//     reference (capacity min(k-2, #middle, 62), strict replacement), run in
+//     wave 0 with heap slot i held by lane i; the heap array order is the
+//     output order, as in the reference.
+// With n_pages <= k every page is selected in logical order (the dense path
+// of inference.c:447-494).
+#include <cmath>
+
+#include "be42_common.h"
+
+namespace be42 {
+
+constexpr int kProbes = 17;
+constexpr int kMaxCand = 256;
+constexpr int kHeapMax = 62;
+
+struct RouteSmem {
+    int off_qm, off_q0, off_hp, off_list, off_cnt, off_cand, off_mid, off_sc, bytes;
+};
+
+__host__ __device__ inline RouteSmem route_smem(int hd, int cap)
+{
+    RouteSmem r;
+    int o = 0;
+    r.off_qm = o;   o += 256 * 4;
+    r.off_q0 = o;   o += 256 * 4;
+    r.off_hp = o;   o += hd * 16 * 4;
+    r.off_list = o; o += 4 * kProbes * cap * 4;
+    r.off_cnt = o;  o += 4 * kProbes * 4 + 4 * 4;
+    r.off_cand = o; o += cap * 4;
+    r.off_mid = o;  o += cap * 4;
+    r.off_sc = o;   o += cap * 4;
+    r.bytes = o;
+    return r;
+}
+
+__device__ __forceinline__ int rl(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+__device__ __forceinline__ float rlf(float v, int lane)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// simd_dot_f32_f32 (simd_kernels.h:162-191) of q0 and c with the reference's
+// reduction tree, computed by the 8 lanes of a group (sub = lane % 8): lane l
+// accumulates i = l (mod 8) with FMA in order; ((s0+s4)+(s1+s5)) +
+// ((s2+s6)+(s3+s7)); then the compiled scalar tail (4 unfused products added
+// in order when >= 4 remain, the rest fused).  Result valid in sub == 0.
+__device__ __forceinline__ float dot_ref8(const float *q0, const float *c, int hd, int sub)
+{
+    const int main = hd & ~7;
+    float s = 0.0f;
+    for (int i = sub; i < main; i += 8)
+        s = __fmaf_rn(q0[i], c[i], s);
+    const float s4 = __shfl_down(s, 4, 8);      // lanes 0..3 get s_{l+4}
+    const float t = s + s4;                       // t_l = s_l + s_{l+4}
+    const float t1 = __shfl_down(t, 1, 8);
+    const float u = t + t1;                       // lane 0: t0+t1, lane 2: t2+t3
+    const float u2 = __shfl_down(u, 2, 8);
+    float sum = u + u2;                           // lane 0: (t0+t1)+(t2+t3)
+    if (sub == 0) {
+        int i = main;
+        if (hd - i >= 4) {
+            for (int j = 0; j < 4; j++)
+                sum = sum + q0[i + j] * c[i + j];
+            i += 4;
+        }
+        for (; i < hd; i++)
+            sum = __fmaf_rn(q0[i], c[i], sum);
+    }
+    return sum;
+}
+
+__global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float *__restrict__ q,
+                                               const int *__restrict__ slots, int H, int k_sel, int cap,
+                                               int *__restrict__ sel, int *__restrict__ nsel, int sel_stride,
+                                               int *__restrict__ cand_out, int *__restrict__ ncand_out,
+                                               uint16_t *__restrict__ qhash_out)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int hd = P.head_dim;
+    const RouteSmem L = route_smem(hd, cap);
+    float *qm = (float *)(smem + L.off_qm);
+    float *q0 = (float *)(smem + L.off_q0);
+    float *hp = (float *)(smem + L.off_hp);
+    int *list = (int *)(smem + L.off_list);
+    int *cnt = (int *)(smem + L.off_cnt);
+    int *cand = (int *)(smem + L.off_cand);
+    int *mid = (int *)(smem + L.off_mid);
+    float *sc = (float *)(smem + L.off_sc);
+
+    const int b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int layer = slots ? slots[b] : b;
+    const int base = layer * P.max_logical;
+    const int n = P.n_logical[layer];
+    const float *qb = q + (size_t)b * H * hd;
+    int *selb = sel + (size_t)b * sel_stride;
+
+    if (n <= 0 || n <= k_sel) {
+        // dense: every page, logical order
+        for (int i = tid; i < n; i += blockDim.x)
+            selb[i] = P.page_table[base + i];
+        if (tid == 0) {
+            nsel[b] = n > 0 ? n : 0;
+            if (ncand_out)
+                ncand_out[b] = 0;
+        }
+        return;
+    }
+
+    // 1. q_mean (inference.c:291-295), q head 0, projection to LDS
+    for (int d = tid; d < hd; d += blockDim.x) {
+        float s = 0.0f;
+#pragma unroll 8
+        for (int h = 0; h < H; h++)
+            s = s + qb[h * hd + d];
+        qm[d] = s / (float)H;
+        q0[d] = qb[d];
+    }
+    for (int i = tid; i < hd * 16; i += blockDim.x)
+        hp[i] = P.hpT[i];
+    __syncthreads();
+    if (wave == 0) {
+        float s = 0.0f;
+        if (lane < 16)
+            for (int i = 0; i < hd; i++)
+                s = __fmaf_rn(qm[i], hp[i * 16 + lane], s);
+        const unsigned long long m = __ballot(lane < 16 && s > 0.0f);
+        if (lane == 0)
+            cnt[4 * kProbes] = (int)(m & 0xFFFFu);
+    }
+    __syncthreads();
+    const int qh = cnt[4 * kProbes];
+    if (tid == 0 && qhash_out)
+        qhash_out[b] = (uint16_t)qh;
+
+    // 2. candidate scan: wave w owns ids [lo, hi), scanned from hi-1 down
+    const int nidx = min(P.n_indexed[layer], P.max_logical);
+    {
+        const int part = (nidx + 3) / 4;
+        const int hi = max(nidx - wave * part, 0), lo = max(nidx - (wave + 1) * part, 0);
+        int cntv = 0;    // lane p < 17 holds the hit count of probe p
+        int *mylist = list + wave * kProbes * cap;
+        for (int top = hi - 1; top >= lo; top -= kWave) {
+            const int id = top - lane;
+            const bool valid = id >= lo;
+            int p = kProbes;
+            if (valid) {
+                const int dd = (int)P.page_hash[base + id] ^ qh;
+                p = dd == 0 ? 0 : (((dd & (dd - 1)) == 0) ? __ffs(dd) : kProbes);
+            }
+            unsigned long long hits = __ballot(p < kProbes);
+            while (hits) {
+                const int l0 = __ffsll((long long)hits) - 1;
+                const int pp = rl(p, l0);
+                const unsigned long long m = __ballot(p == pp);
+                const int basec = rl(cntv, pp);
+                if (p == pp) {
+                    const int rank = __popcll(m & ((1ull << lane) - 1ull));
+                    if (basec + rank < cap)
+                        mylist[pp * cap + basec + rank] = id;
+                }
+                if (lane == pp)
+                    cntv += __popcll(m);
+                hits &= ~m;
+            }
+        }
+        if (lane < kProbes)
+            cnt[wave * kProbes + lane] = cntv;
+    }
+    __syncthreads();
+
+    // 3. concatenate per probe (wave order = descending id), then keep the
+    //    middle entries (not the first or last page)
+    if (wave == 0) {
+        int total = 0;
+        for (int p = 0; p < kProbes && total < cap; p++)
+            for (int w = 0; w < 4 && total < cap; w++) {
+                const int c = min(cnt[w * kProbes + p], cap);
+                const int take = min(c, cap - total);
+                for (int i = lane; i < take; i += kWave)
+                    cand[total + i] = list[(w * kProbes + p) * cap + i];
+                total += take;
+            }
+        __builtin_amdgcn_s_waitcnt(0);
+        int nm = 0;
+        for (int i0 = 0; i0 < total; i0 += kWave) {
+            const int i = i0 + lane;
+            const int id = i < total ? cand[i] : -1;
+            const bool keep = i < total && id != 0 && id != n - 1 && id < n;
+            const unsigned long long m = __ballot(keep);
+            if (keep)
+                mid[nm + __popcll(m & ((1ull << lane) - 1ull))] = id;
+            nm += __popcll(m);
+        }
+        if (lane == 0) {
+            cnt[4 * kProbes + 1] = total;
+            cnt[4 * kProbes + 2] = nm;
+        }
+        if (cand_out)
+            for (int i = lane; i < total; i += kWave)
+                cand_out[(size_t)b * cap + i] = cand[i];
+        if (lane == 0 && ncand_out)
+            ncand_out[b] = total;
+    }
+    __syncthreads();
+    const int nm = cnt[4 * kProbes + 2];
+
+    // 4. scores of the middle entries (score_blocks semantics)
+    for (int e0 = 0; e0 < nm; e0 += 32) {
+        const int e = e0 + (tid >> 3), sub = tid & 7;
+        const int ee = e < nm ? e : nm - 1;
+        const int phys = P.page_table[base + mid[ee]];
+        const float s = dot_ref8(q0, P.centroid + (size_t)phys * hd, hd, sub);
+        if (sub == 0 && e < nm)
+            sc[e] = s;
+    }
+    __syncthreads();
+
+    // 5. selection: anchors, then the reference heap in wave 0
+    if (wave != 0)
+        return;
+    const int first = P.page_table[base], last = P.page_table[base + n - 1];
+    int ns = 0;
+    if (lane == 0)
+        selb[0] = first;
+    ns = 1;
+    if (last != first) {
+        if (lane == 0)
+            selb[1] = last;
+        ns = 2;
+    }
+    int ak = min(k_sel - 2, min(nm, kHeapMax));
+    if (k_sel <= 2 || nm == 0)
+        ak = 0;
+    float hs = 0.0f;
+    int hi = 0, size = 0;
+    for (int e = 0; e < nm && ak > 0; e++) {
+        const float s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sc[e])));
+        if (size < ak) {
+            int i = size++;
+            while (i > 0) {
+                const int par = (i - 1) >> 1;
+                const float sp = rlf(hs, par);
+                if (sp <= s)
+                    break;
+                const int ip = rl(hi, par);
+                if (lane == i) {
+                    hs = sp;
+                    hi = ip;
+                }
+                i = par;
+            }
+            if (lane == i) {
+                hs = s;
+                hi = e;
+            }
+        } else if (s > rlf(hs, 0)) {
+            int i = 0;
+            for (;;) {
+                const int l = 2 * i + 1, r = 2 * i + 2;
+                int sm = i;
+                float ssm = s;
+                if (l < size) {
+                    const float sl = rlf(hs, l);
+                    if (sl < ssm) {
+                        sm = l;
+                        ssm = sl;
+                    }
+                }
+                if (r < size) {
+                    const float sr = rlf(hs, r);
+                    if (sr < ssm) {
+                        sm = r;
+                        ssm = sr;
+                    }
+                }
+                if (sm == i)
+                    break;
+                const int ism = rl(hi, sm);
+                if (lane == i) {
+                    hs = ssm;
+                    hi = ism;
+                }
+                i = sm;
+            }
+            if (lane == i) {
+                hs = s;
+                hi = e;
+            }
+        }
+    }
+    if (lane < size)
+        selb[ns + lane] = P.page_table[base + mid[hi]];
+    if (lane == 0)
+        nsel[b] = ns + size;
+}
+
+// Hash of n vectors: each wave hashes 4 vectors, 16 lanes per vector, one
+// ballot packs the 4 sign masks.
+__global__ __launch_bounds__(256) void k_lsh_hash(uint16_t *__restrict__ out, const float *__restrict__ vecs,
+                                                  int n, const float *__restrict__ hpT, int dim)
+{
+    const int lane = threadIdx.x & 63, wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int vi = wave * 4 + (lane >> 4), h = lane & 15;
+    float s = 0.0f;
+    if (vi < n) {
+        const float *v = vecs + (size_t)vi * dim;
+        for (int d = 0; d < dim; d++)
+            s = __fmaf_rn(v[d], hpT[d * 16 + h], s);
+    }
+    const unsigned long long m = __ballot(vi < n && s > 0.0f);
+    if (h == 0 && vi < n)
+        out[vi] = (uint16_t)((m >> (lane & 48)) & 0xFFFFu);
+}
+
+// Candidate lookup over a flat array of index hashes (index id = position):
+// the chain-walk order restated as probe order, then descending id.  One
+// block per query, same ballot scan as the router.
+__global__ __launch_bounds__(256) void k_lsh_candidates(const uint16_t *__restrict__ hashes, int n_ids,
+                                                        const uint16_t *__restrict__ qh, int n_q, int cap,
+                                                        int *__restrict__ ids, int *__restrict__ n_out)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    int *list = (int *)smem;                          // [4][17][cap]
+    int *cnt = list + 4 * kProbes * cap;              // [4][17]
+    const int b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int q = qh[b];
+    const int part = (n_ids + 3) / 4;
+    const int hi = max(n_ids - wave * part, 0), lo = max(n_ids - (wave + 1) * part, 0);
+    int cntv = 0;
+    int *mylist = list + wave * kProbes * cap;
+    for (int top = hi - 1; top >= lo; top -= kWave) {
+        const int id = top - lane;
+        int p = kProbes;
+        if (id >= lo) {
+            const int dd = (int)hashes[id] ^ q;
+            p = dd == 0 ? 0 : (((dd & (dd - 1)) == 0) ? __ffs(dd) : kProbes);
+        }
+        unsigned long long hits = __ballot(p < kProbes);
+        while (hits) {
+            const int l0 = __ffsll((long long)hits) - 1;
+            const int pp = rl(p, l0);
+            const unsigned long long m = __ballot(p == pp);
+            const int basec = rl(cntv, pp);
+            if (p == pp) {
+                const int rank = __popcll(m & ((1ull << lane) - 1ull));
+                if (basec + rank < cap)
+                    mylist[pp * cap + basec + rank] = id;
+            }
+            if (lane == pp)
+                cntv += __popcll(m);
+            hits &= ~m;
+        }
+    }
+    if (lane < kProbes)
+        cnt[wave * kProbes + lane] = cntv;
+    __syncthreads();
+    if (wave != 0)
+        return;
+    int total = 0;
+    for (int p = 0; p < kProbes && total < cap; p++)
+        for (int w = 0; w < 4 && total < cap; w++) {
+            const int c = min(cnt[w * kProbes + p], cap);
+            const int take = min(c, cap - total);
+            for (int i = lane; i < take; i += kWave)
+                ids[(size_t)b * cap + total + i] = list[(w * kProbes + p) * cap + i];
+            total += take;
+        }
+    if (lane == 0)
+        n_out[b] = total;
+}
+
+}  // namespace be42
+
+using namespace be42;
+
+// lsh_init (ops_lsh.c:22-85): LCG uniforms, Box-Muller with libm, rows
+// L2-normalised (squared norm accumulated with fused multiply-add, as the
+// reference's compiled loop does), transposed.  Host code: it runs once at
+// model load and its libm-dependent output is uploaded.
+extern "C" void be42_lsh_projection(float *hp, float *hpT, int dim, unsigned int seed)
+{
+    if (dim > 256)
+        dim = 256;
+    for (int h = 0; h < 16; h++) {
+        float nrm = 0.0f;
+        for (int d = 0; d < dim; d++) {
+            seed = seed * 1103515245u + 12345u;
+            float u1 = (float)((seed >> 16) & 0x7FFF) / 32767.0f;
+            seed = seed * 1103515245u + 12345u;
+            const float u2 = (float)((seed >> 16) & 0x7FFF) / 32767.0f;
+            if (u1 < 1e-6f)
+                u1 = 1e-6f;
+            const float g = sqrtf(-2.0f * logf(u1)) * cosf(2.0f * 3.14159265f * u2);
+            hp[h * dim + d] = g;
+            nrm = fmaf(g, g, nrm);
+        }
+        nrm = sqrtf(nrm);
+        if (nrm > 1e-6f)
+            for (int d = 0; d < dim; d++)
+                hp[h * dim + d] /= nrm;
+    }
+    if (hpT)
+        for (int d = 0; d < dim; d++)
+            for (int h = 0; h < 16; h++)
+                hpT[d * 16 + h] = hp[h * dim + d];
+}
+
+extern "C" int be42_lsh_hash(uint16_t *out, const float *vecs, int n, const float *hpT, int dim, void *stream)
+{
+    BE42_CHECK(out && vecs && hpT, "be42_lsh_hash: null pointer");
+    BE42_CHECK(n >= 0 && dim > 0 && dim <= 256, "be42_lsh_hash: bad shape n=%d dim=%d", n, dim);
+    if (n == 0)
+        return BE42_OK;
+    const int waves = (n + 3) / 4;
+    const int blocks = (waves + 3) / 4;
+    hipLaunchKernelGGL(k_lsh_hash, dim3(blocks), dim3(256), 0, as_stream(stream), out, vecs, n, hpT, dim);
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
+extern "C" int be42_lsh_candidates(int *ids, int *n_out, const uint16_t *hashes, int n_ids, const uint16_t *qh,
+                                   int n_q, int cap, void *stream)
+{
+    BE42_CHECK(ids && n_out && hashes && qh, "be42_lsh_candidates: null pointer");
+    BE42_CHECK(n_ids >= 0 && n_q >= 0 && cap > 0 && cap <= kMaxCand, "be42_lsh_candidates: bad sizes (cap %d)",
+               cap);
+    if (n_q == 0)
+        return BE42_OK;
+    const size_t smem = (size_t)(4 * kProbes * cap + 4 * kProbes) * sizeof(int);
+    if (smem > 65536)
+        BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_candidates, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)smem));
+    hipLaunchKernelGGL(k_lsh_candidates, dim3(n_q), dim3(256), smem, as_stream(stream), hashes, n_ids, qh, n_q,
+                       cap, ids, n_out);
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
+extern "C" int be42_lsh_route(const be42_kv_pool *pool, const float *q, const int *slots, int n_queries,
+                              int n_heads, int k_sel, int cand_cap, int *sel, int *n_sel, int sel_stride,
+                              int *cand, int *n_cand, uint16_t *qhash, void *stream)
+{
+    BE42_CHECK(pool && q && sel && n_sel, "be42_lsh_route: null pointer");
+    BE42_CHECK(n_queries >= 0 && n_heads > 0 && k_sel > 0 && cand_cap > 0 && cand_cap <= kMaxCand,
+               "be42_lsh_route: bad sizes (heads %d, k %d, cap %d)", n_heads, k_sel, cand_cap);
+    BE42_CHECK(sel_stride >= k_sel && sel_stride >= kHeapMax + 2,
+               "be42_lsh_route: sel_stride %d must be >= max(k, 64)", sel_stride);
+    if (n_queries == 0)
+        return BE42_OK;
+    const RouteSmem L = route_smem(pool->head_dim, cand_cap);
+    if (L.bytes > 65536)
+        BE42_HIP(hipFuncSetAttribute((const void *)k_route, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes));
+    hipLaunchKernelGGL(k_route, dim3(n_queries), dim3(256), (size_t)L.bytes, as_stream(stream), *pool, q, slots,
+                       n_heads, k_sel, cand_cap, sel, n_sel, sel_stride, cand, n_cand, qhash);
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}

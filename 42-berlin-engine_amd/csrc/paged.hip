@@ -1,0 +1,390 @@
+// paged.hip -- paged KV cache in HBM: page pool, quantizing append, page
+// centroids and their LSH hashes.
+//
+// block_manager_init / block_alloc / block_free   src/memory/paged.c:29-187
+// paged_kv_append                                 src/memory/paged.c:195-272
+// paged_kv_reset                                  src/memory/paged.c:312-336
+// calc_block_centroid_int8                        src/memory/paged.c:350-393
+// quant_f32_to_int8                               src/compute/ops_quant.c:229-270
+// float_to_bf16                                   src/tensor/tensor.c:67-76
+// lsh_hash                                        src/compute/ops_lsh.c:138-242
+//
+// Layout in HBM (one allocation per array, pages indexed by physical id):
+//   k, v        [cap][n_kv][16][hd]   int8 codes or bf16
+//   k_scale...  [cap][n_kv][16]       fp32 (INT8 pages)
+//   centroid    [cap][hd]             fp32, head 0 of the page
+//   ntok        [cap]                 tokens written in the page
+//   page_table  [n_layers][max_logical] -> physical id
+//   page_hash   [n_layers][max_logical]   16-bit hash of logical page j's
+//               centroid; page j is the j-th page to fill, so the index id of
+//               lsh_insert_block (ops_lsh.c:256-272) is the logical page.
+// The page allocator (free stack, page table, logical lengths) is host
+// bookkeeping exactly as in the reference; the device copies of the page
+// table and per-layer counts are updated with each append.
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "be42_common.h"
+
+namespace be42 {
+
+constexpr int kPage = 16;
+
+// Bookkeeping of one append of up to kArgTok tokens, passed by value as a
+// kernel argument so that a decode step needs no host-to-device copy.
+constexpr int kArgTok = 64;
+constexpr int kArgPages = kArgTok / 16 + 2;
+struct AppendArgs {
+    int pos0, n_tok, layer_base;
+    int tok_phys[kArgTok];
+    int n_new, new_first;              // page-table entries to publish
+    int new_phys[kArgPages];
+    int n_logical;                     // value of n_logical[layer] after the append
+    int n_seal, n_indexed;             // pages to seal, n_indexed[layer] after
+    int seal_phys[kArgPages], seal_logical[kArgPages];
+    int layer;
+};
+
+struct PoolImpl {
+    be42_kv_pool pub;
+    std::vector<int> page_table;   // host shadow [n_layers * max_logical]
+    std::vector<int> free_stack;
+    int free_top = -1;
+    std::vector<int> logical_len;  // [n_layers]
+    std::vector<int> registered;   // [cap]
+    std::vector<int> n_indexed;    // [n_layers]
+};
+
+static PoolImpl *impl(be42_kv_pool *p) { return reinterpret_cast<PoolImpl *>(p); }
+
+// One wave per (token, kv head): quantize (INT8) or round (BF16) the K and V
+// rows of that head into the page slot.  INT8 follows quant_f32_to_int8:
+// exact absmax, IEEE scale = amax/127 and inv = 127/amax, roundf, clamp.
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_kv_append(void *__restrict__ kdst, void *__restrict__ vdst,
+                                                  float *__restrict__ kscale, float *__restrict__ vscale,
+                                                  int *__restrict__ ntok, int *__restrict__ page_table,
+                                                  int *__restrict__ n_logical, const AppendArgs a,
+                                                  const float *__restrict__ k, const float *__restrict__ v,
+                                                  int n_kv, int hd)
+{
+    const int tok = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int pos = a.pos0 + tok, off = pos % kPage;
+    const int phys = a.tok_phys[tok];
+    if (tok == 0 && h == 0) {
+        if (lane < a.n_new)
+            page_table[a.layer_base + a.new_first + lane] = a.new_phys[lane];
+        if (lane == 0)
+            n_logical[a.layer] = a.n_logical;
+    }
+    const size_t slot = ((size_t)phys * n_kv + h) * kPage + off;
+    const float *ks = k + (size_t)tok * n_kv * hd + (size_t)h * hd;
+    const float *vs = v + (size_t)tok * n_kv * hd + (size_t)h * hd;
+    if constexpr (BF16) {
+        uint16_t *kd = (uint16_t *)kdst + slot * hd, *vd = (uint16_t *)vdst + slot * hd;
+        for (int d = lane; d < hd; d += kWave) {
+            kd[d] = f32_to_bf16(ks[d]);
+            vd[d] = f32_to_bf16(vs[d]);
+        }
+    } else {
+        float km = 0.0f, vm = 0.0f;
+        for (int d = lane; d < hd; d += kWave) {
+            km = fmaxf(km, fabsf(ks[d]));
+            vm = fmaxf(vm, fabsf(vs[d]));
+        }
+        km = wave_max(km);
+        vm = wave_max(vm);
+        float ksc = 1.0f, kinv = 1.0f, vsc = 1.0f, vinv = 1.0f;
+        if (km > 0.0f) {
+            ksc = km / 127.0f;
+            kinv = 127.0f / km;
+        }
+        if (vm > 0.0f) {
+            vsc = vm / 127.0f;
+            vinv = 127.0f / vm;
+        }
+        int8_t *kd = (int8_t *)kdst + slot * hd, *vd = (int8_t *)vdst + slot * hd;
+        for (int d = lane; d < hd; d += kWave) {
+            const int kc = (int)roundf(ks[d] * kinv), vc = (int)roundf(vs[d] * vinv);
+            kd[d] = (int8_t)(kc > 127 ? 127 : (kc < -127 ? -127 : kc));
+            vd[d] = (int8_t)(vc > 127 ? 127 : (vc < -127 ? -127 : vc));
+        }
+        if (lane == 0) {
+            kscale[slot] = ksc;
+            vscale[slot] = vsc;
+        }
+    }
+    // the page's last token in this append publishes the count (blocks of
+    // one page run concurrently)
+    if (h == 0 && lane == 0 && (off == kPage - 1 || tok == a.n_tok - 1))
+        ntok[phys] = off + 1;
+}
+
+// One block per page that became full: centroid of the head-0 keys (per
+// dimension, tokens summed in order, then * (1.0f/16)), then its hash: 16
+// lanes each run the FMA chain over d ascending from +0 (bit h = sum > 0).
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_kv_seal(const void *__restrict__ kpool, const float *__restrict__ kscale,
+                                                 float *__restrict__ centroid, uint16_t *__restrict__ page_hash,
+                                                 int *__restrict__ n_indexed, const AppendArgs a,
+                                                 const float *__restrict__ hpT, int n_kv, int hd)
+{
+    __shared__ float c[256];
+    const int phys = a.seal_phys[blockIdx.x];
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        n_indexed[a.layer] = a.n_indexed;
+    const size_t head0 = (size_t)phys * n_kv * kPage;      // slot of (phys, head 0, token 0)
+    const int d = threadIdx.x;
+    if (d < hd) {
+        float acc = 0.0f;
+        for (int t = 0; t < kPage; t++) {
+            float val;
+            if constexpr (BF16)
+                val = bf16_to_f32(((const uint16_t *)kpool)[(head0 + t) * hd + d]);
+            else
+                val = (float)((const int8_t *)kpool)[(head0 + t) * hd + d] * kscale[head0 + t];
+            acc = acc + val;
+        }
+        acc = acc * (1.0f / (float)kPage);
+        c[d] = acc;
+        centroid[(size_t)phys * hd + d] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int h = threadIdx.x;
+        float s = 0.0f;
+        if (h < 16)
+            for (int i = 0; i < hd; i++)
+                s = __fmaf_rn(c[i], hpT[i * 16 + h], s);
+        const unsigned long long m = __ballot(h < 16 && s > 0.0f);
+        if (h == 0)
+            page_hash[a.layer_base + a.seal_logical[blockIdx.x]] = (uint16_t)(m & 0xFFFFu);
+    }
+}
+
+}  // namespace be42
+
+using namespace be42;
+
+extern "C" int be42_kv_create(be42_kv_pool **out, int kind, int n_layers, int n_kv, int head_dim,
+                              int max_logical, const float *hpT_host)
+{
+    BE42_CHECK(out, "be42_kv_create: null out");
+    *out = nullptr;
+    BE42_CHECK(kind == BE42_KV_INT8 || kind == BE42_KV_BF16, "be42_kv_create: bad kind %d", kind);
+    BE42_CHECK(n_layers > 0 && n_kv > 0 && max_logical > 0 && head_dim > 0 && head_dim <= 256 &&
+                   head_dim % 8 == 0,
+               "be42_kv_create: bad shape (layers %d, kv heads %d, head_dim %d, pages %d)", n_layers, n_kv,
+               head_dim, max_logical);
+    PoolImpl *p = new PoolImpl();
+    be42_kv_pool &P = p->pub;
+    memset(&P, 0, sizeof P);
+    P.kind = kind;
+    P.n_layers = n_layers;
+    P.n_kv = n_kv;
+    P.head_dim = head_dim;
+    P.max_logical = max_logical;
+    P.capacity = n_layers * max_logical;
+    const size_t cap = (size_t)P.capacity;
+    const size_t elem = kind == BE42_KV_INT8 ? 1 : 2;
+    const size_t kvbytes = cap * n_kv * kPage * head_dim * elem;
+    hipError_t e = hipSuccess;
+    auto alloc = [&](void **ptr, size_t bytes) {
+        if (e == hipSuccess)
+            e = hipMalloc(ptr, bytes ? bytes : 1);
+    };
+    alloc(&P.k, kvbytes);
+    alloc(&P.v, kvbytes);
+    if (kind == BE42_KV_INT8) {
+        alloc((void **)&P.k_scale, cap * n_kv * kPage * sizeof(float));
+        alloc((void **)&P.v_scale, cap * n_kv * kPage * sizeof(float));
+    }
+    alloc((void **)&P.centroid, cap * head_dim * sizeof(float));
+    alloc((void **)&P.ntok, cap * sizeof(int));
+    alloc((void **)&P.page_table, cap * sizeof(int));
+    alloc((void **)&P.n_logical, n_layers * sizeof(int));
+    alloc((void **)&P.page_hash, cap * sizeof(uint16_t));
+    alloc((void **)&P.n_indexed, n_layers * sizeof(int));
+    alloc((void **)&P.hpT, head_dim * 16 * sizeof(float));
+    if (e == hipSuccess) e = hipMemset(P.k, 0, kvbytes);
+    if (e == hipSuccess) e = hipMemset(P.v, 0, kvbytes);
+    if (e == hipSuccess) e = hipMemset(P.ntok, 0, cap * sizeof(int));
+    if (e == hipSuccess) e = hipMemset(P.centroid, 0, cap * head_dim * sizeof(float));
+    if (e == hipSuccess) e = hipMemset(P.page_table, 0xFF, cap * sizeof(int));
+    if (e == hipSuccess) e = hipMemset(P.n_logical, 0, n_layers * sizeof(int));
+    if (e == hipSuccess) e = hipMemset(P.n_indexed, 0, n_layers * sizeof(int));
+    if (e == hipSuccess) e = hipMemset(P.page_hash, 0, cap * sizeof(uint16_t));
+    if (e == hipSuccess && hpT_host)
+        e = hipMemcpy((void *)P.hpT, hpT_host, head_dim * 16 * sizeof(float), hipMemcpyHostToDevice);
+    else if (e == hipSuccess)
+        e = hipMemset((void *)P.hpT, 0, head_dim * 16 * sizeof(float));
+    if (e != hipSuccess) {
+        be42_kv_destroy(&P);
+        return hip_fail(e, "be42_kv_create", __FILE__, __LINE__);
+    }
+    p->page_table.assign(cap, -1);
+    p->free_stack.resize(cap);
+    for (size_t i = 0; i < cap; i++)
+        p->free_stack[i] = (int)i;
+    p->free_top = (int)cap - 1;
+    p->logical_len.assign(n_layers, 0);
+    p->registered.assign(cap, 0);
+    p->n_indexed.assign(n_layers, 0);
+    *out = &P;
+    return BE42_OK;
+}
+
+extern "C" void be42_kv_destroy(be42_kv_pool *pool)
+{
+    if (!pool)
+        return;
+    void *ptrs[] = {pool->k, pool->v, pool->k_scale, pool->v_scale, pool->centroid, pool->ntok,
+                    pool->page_table, pool->n_logical, pool->page_hash, pool->n_indexed, (void *)pool->hpT};
+    for (void *q : ptrs)
+        if (q)
+            (void)hipFree(q);
+    delete impl(pool);
+}
+
+extern "C" int be42_kv_set_projection(be42_kv_pool *pool, const float *hpT_host)
+{
+    BE42_CHECK(pool && hpT_host, "be42_kv_set_projection: null pointer");
+    BE42_HIP(hipMemcpy((void *)pool->hpT, hpT_host, pool->head_dim * 16 * sizeof(float), hipMemcpyHostToDevice));
+    return BE42_OK;
+}
+
+// Host page allocator, paged.c:159-179 (pop the free stack).
+static int pool_alloc(PoolImpl *p)
+{
+    if (p->free_top < 0)
+        return -1;
+    const int phys = p->free_stack[p->free_top--];
+    p->registered[phys] = 0;
+    return phys;
+}
+
+// One chunk of <= kArgTok tokens: host bookkeeping of paged.c:195-272, then
+// the quantizing store and, for pages that fill, centroid + hash.
+static int append_chunk(PoolImpl *p, int layer, const float *k, const float *v, int pos0, int n, hipStream_t s)
+{
+    be42_kv_pool &P = p->pub;
+    AppendArgs a;
+    memset(&a, 0, sizeof a);
+    a.pos0 = pos0;
+    a.n_tok = n;
+    a.layer = layer;
+    a.layer_base = layer * P.max_logical;
+    a.new_first = p->logical_len[layer];
+    const int last_blk = (pos0 + n - 1) / kPage;
+    for (int blk = pos0 / kPage; blk <= last_blk; blk++) {
+        if (blk >= p->logical_len[layer]) {
+            // pages are appended in order: a gap would leave unmapped pages
+            if (blk != p->logical_len[layer]) {
+                set_error("be42_kv_append: position %d skips page %d", blk * kPage, p->logical_len[layer]);
+                return BE42_EINVAL;
+            }
+            const int phys = pool_alloc(p);
+            if (phys < 0) {
+                set_error("be42_kv_append: page pool exhausted at pos %d", blk * kPage);
+                return BE42_ENOMEM;
+            }
+            p->page_table[a.layer_base + blk] = phys;
+            p->logical_len[layer] = blk + 1;
+            a.new_phys[a.n_new++] = phys;
+        }
+    }
+    a.n_logical = p->logical_len[layer];
+    for (int t = 0; t < n; t++) {
+        const int pos = pos0 + t, blk = pos / kPage;
+        const int phys = p->page_table[a.layer_base + blk];
+        a.tok_phys[t] = phys;
+        if (pos % kPage == kPage - 1 && !p->registered[phys]) {
+            p->registered[phys] = 1;
+            a.seal_phys[a.n_seal] = phys;
+            a.seal_logical[a.n_seal] = blk;
+            a.n_seal++;
+            if (blk + 1 > p->n_indexed[layer])
+                p->n_indexed[layer] = blk + 1;
+        }
+    }
+    a.n_indexed = p->n_indexed[layer];
+    const dim3 grid(n, P.n_kv);
+    if (P.kind == BE42_KV_BF16)
+        hipLaunchKernelGGL(k_kv_append<true>, grid, dim3(64), 0, s, P.k, P.v, P.k_scale, P.v_scale, P.ntok,
+                           P.page_table, P.n_logical, a, k, v, P.n_kv, P.head_dim);
+    else
+        hipLaunchKernelGGL(k_kv_append<false>, grid, dim3(64), 0, s, P.k, P.v, P.k_scale, P.v_scale, P.ntok,
+                           P.page_table, P.n_logical, a, k, v, P.n_kv, P.head_dim);
+    BE42_LAUNCH_CHECK();
+    if (a.n_seal) {
+        if (P.kind == BE42_KV_BF16)
+            hipLaunchKernelGGL(k_kv_seal<true>, dim3(a.n_seal), dim3(256), 0, s, P.k, P.k_scale, P.centroid,
+                               P.page_hash, P.n_indexed, a, P.hpT, P.n_kv, P.head_dim);
+        else
+            hipLaunchKernelGGL(k_kv_seal<false>, dim3(a.n_seal), dim3(256), 0, s, P.k, P.k_scale, P.centroid,
+                               P.page_hash, P.n_indexed, a, P.hpT, P.n_kv, P.head_dim);
+        BE42_LAUNCH_CHECK();
+    }
+    return BE42_OK;
+}
+
+extern "C" int be42_kv_append(be42_kv_pool *pool, int layer, const float *k, const float *v, int pos0,
+                              int n_tokens, void *stream)
+{
+    BE42_CHECK(pool && k && v, "be42_kv_append: null pointer");
+    PoolImpl *p = impl(pool);
+    be42_kv_pool &P = p->pub;
+    BE42_CHECK(layer >= 0 && layer < P.n_layers, "be42_kv_append: layer %d out of range", layer);
+    BE42_CHECK(pos0 >= 0 && n_tokens >= 0, "be42_kv_append: bad positions");
+    if (n_tokens == 0)
+        return BE42_OK;
+    BE42_CHECK((pos0 + n_tokens - 1) / kPage < P.max_logical, "be42_kv_append: position %d beyond %d pages",
+               pos0 + n_tokens - 1, P.max_logical);
+    hipStream_t s = as_stream(stream);
+    const size_t row = (size_t)P.n_kv * P.head_dim;
+    for (int t = 0; t < n_tokens; t += kArgTok) {
+        const int n = n_tokens - t < kArgTok ? n_tokens - t : kArgTok;
+        const int rc = append_chunk(p, layer, k + t * row, v + t * row, pos0 + t, n, s);
+        if (rc)
+            return rc;
+    }
+    return BE42_OK;
+}
+
+extern "C" int be42_kv_reset(be42_kv_pool *pool, int layer, void *stream)
+{
+    BE42_CHECK(pool, "be42_kv_reset: null pool");
+    PoolImpl *p = impl(pool);
+    be42_kv_pool &P = p->pub;
+    BE42_CHECK(layer >= 0 && layer < P.n_layers, "be42_kv_reset: layer %d out of range", layer);
+    const int base = layer * P.max_logical;
+    // paged.c:312-336: return pages to the free stack, unmap
+    for (int i = 0; i < p->logical_len[layer]; i++) {
+        const int phys = p->page_table[base + i];
+        if (phys >= 0)
+            p->free_stack[++p->free_top] = phys;
+        p->page_table[base + i] = -1;
+    }
+    const int n = p->logical_len[layer];
+    p->logical_len[layer] = 0;
+    p->n_indexed[layer] = 0;
+    hipStream_t s = as_stream(stream);
+    if (n > 0)
+        BE42_HIP(hipMemsetAsync(P.page_table + base, 0xFF, n * sizeof(int), s));
+    BE42_HIP(hipMemsetAsync(P.n_logical + layer, 0, sizeof(int), s));
+    BE42_HIP(hipMemsetAsync(P.n_indexed + layer, 0, sizeof(int), s));
+    return BE42_OK;
+}
+
+extern "C" int be42_kv_layer_pages(const be42_kv_pool *pool, int layer, int *phys_out, int max_out)
+{
+    BE42_CHECK(pool, "be42_kv_layer_pages: null pool");
+    const PoolImpl *p = reinterpret_cast<const PoolImpl *>(pool);
+    BE42_CHECK(layer >= 0 && layer < pool->n_layers, "be42_kv_layer_pages: layer out of range");
+    const int n = p->logical_len[layer];
+    if (phys_out)
+        for (int i = 0; i < n && i < max_out; i++)
+            phys_out[i] = p->page_table[layer * pool->max_logical + i];
+    return n;
+}

@@ -74,6 +74,86 @@ int be42_gemv_q8_prepared(float *y, const int8_t *w, const float *w_scale, const
 int be42_gemv_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, const void *xdig,
                            int n, int k, int batch, void *stream);
 
+/* ---- paged KV cache in HBM ------------------------------------------------------
+ * Mirrors t_block_manager / t_paged_kv_cache (src/memory/paged.h:53-99): pages
+ * of 16 tokens, [n_kv][16][head_dim] per page, INT8 codes with a per-(token,
+ * head) scale (quant_f32_to_int8) or bf16 (float_to_bf16, tensor.c:67-76).
+ * Page allocation is the reference's LIFO free stack (paged.c:159-187), kept
+ * on the host.  A page that fills gets its head-0 centroid
+ * (calc_block_centroid_int8, paged.c:350-393) and the 16-bit lsh_hash of that
+ * centroid (ops_lsh.c:138-242) under the projection `hpT` [head_dim][16];
+ * logical page j is LSH index id j.  "Layers" are independent page tables,
+ * usable as (sequence, layer) slots. */
+#define BE42_KV_INT8 0
+#define BE42_KV_BF16 1
+
+typedef struct be42_kv_pool {
+    int       kind;            /* BE42_KV_INT8 or BE42_KV_BF16 */
+    int       n_layers, n_kv, head_dim, max_logical, capacity;
+    void     *k, *v;           /* [capacity][n_kv][16][head_dim] int8 or bf16 */
+    float    *k_scale, *v_scale; /* [capacity][n_kv][16], INT8 pages only */
+    float    *centroid;        /* [capacity][head_dim] */
+    int      *ntok;            /* [capacity] tokens written per page */
+    int      *page_table;      /* [n_layers][max_logical] -> physical page, -1 unmapped */
+    int      *n_logical;       /* [n_layers] pages in use */
+    uint16_t *page_hash;       /* [n_layers][max_logical] hash of logical page j */
+    int      *n_indexed;       /* [n_layers] pages sealed (hashed) */
+    const float *hpT;          /* [head_dim][16] LSH projection */
+} be42_kv_pool;
+
+/* block_manager_init (paged.c:29-131) for n_layers page tables of
+ * max_logical pages each; hpT_host (may be NULL) is uploaded. */
+int  be42_kv_create(be42_kv_pool **pool, int kind, int n_layers, int n_kv, int head_dim,
+                    int max_logical, const float *hpT_host);
+void be42_kv_destroy(be42_kv_pool *pool);
+int  be42_kv_set_projection(be42_kv_pool *pool, const float *hpT_host);
+/* paged_kv_append (paged.c:195-272) for n_tokens consecutive positions
+ * pos0.. of one layer; k, v are device [n_tokens][n_kv*head_dim] fp32.
+ * Returns BE42_ENOMEM when the pool is exhausted (the reference exits). */
+int  be42_kv_append(be42_kv_pool *pool, int layer, const float *k, const float *v, int pos0,
+                    int n_tokens, void *stream);
+/* paged_kv_reset (paged.c:312-336) */
+int  be42_kv_reset(be42_kv_pool *pool, int layer, void *stream);
+/* host copy of a layer's page table; returns the number of logical pages */
+int  be42_kv_layer_pages(const be42_kv_pool *pool, int layer, int *phys_out, int max_out);
+
+/* ---- LSH routing ------------------------------------------------------------------ */
+/* lsh_init (src/compute/ops_lsh.c:22-85) on the host: hp [16][dim] and its
+ * transpose hpT [dim][16] (hpT may be NULL). */
+void be42_lsh_projection(float *hp, float *hpT, int dim, unsigned int seed);
+/* lsh_hash (ops_lsh.c:138-242) of n device vectors [n][dim] -> out[n] */
+int  be42_lsh_hash(uint16_t *out, const float *vecs, int n, const float *hpT, int dim, void *stream);
+/* lsh_find_candidates (ops_lsh.c:361-418) for n_q query hashes over an index
+ * whose block id i has hash hashes[i] (ids inserted in order, i < n_ids):
+ * ids[q*cap + 0..n_out[q]) in the reference's probe-then-chain order. */
+int  be42_lsh_candidates(int *ids, int *n_out, const uint16_t *hashes, int n_ids, const uint16_t *qh,
+                         int n_q, int cap, void *stream);
+/* Page selection for n_queries queries q [n_queries][n_heads][head_dim]
+ * (fp32), query b reading page table slots[b] (slots NULL: b):
+ *   pages <= k_sel: every page in logical order (inference.c:447-494, dense);
+ *   else q_mean -> lsh_hash -> lsh_find_candidates(cap) over the page hashes
+ *   -> score_blocks(q head 0) -> select_top_k_blocks(k_sel), in the
+ *   reference's output order (anchors, then the min-heap array).
+ * sel[b*sel_stride ..] receives physical page ids, n_sel[b] their count
+ * (sel_stride >= max(k_sel, 64)); cand/n_cand (optional) the candidate logical
+ * ids [b*cand_cap ..]; qhash (optional) the query hash. */
+int  be42_lsh_route(const be42_kv_pool *pool, const float *q, const int *slots, int n_queries,
+                    int n_heads, int k_sel, int cand_cap, int *sel, int *n_sel, int sel_stride,
+                    int *cand, int *n_cand, uint16_t *qhash, void *stream);
+
+/* ---- attention over selected pages --------------------------------------------------
+ * op_paged_attention_sparse (src/compute/ops_attention.c:443-461) for
+ * n_queries queries: query head h reads KV head h / (n_heads / n_kv) of the
+ * pages sel[b*sel_stride + 0..n_sel[b]) in that order, with the reference's
+ * online softmax (fast_expf) evaluated in closed form.  out [n_queries]
+ * [n_heads][head_dim] fp32.  max_sel bounds n_sel[b]; n_split splits the
+ * pages of a query over workgroups.  workspace may be NULL (library-owned,
+ * grow-only) or a device buffer of be42_attn_workspace_bytes() bytes. */
+size_t be42_attn_workspace_bytes(int n_queries, int n_heads, int head_dim, int max_sel, int n_split);
+int  be42_paged_attention(const be42_kv_pool *pool, const float *q, int n_queries, int n_heads,
+                          const int *sel, const int *n_sel, int sel_stride, int max_sel, float scale,
+                          float *out, int n_split, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

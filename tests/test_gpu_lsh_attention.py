@@ -1,0 +1,241 @@
+"""GPU LSH routing, paged KV cache and sparse attention vs the oracle.
+
+Bit-exact: projection, hashes, candidate ids and order, page tables, INT8
+codes and scales, bf16 rows, centroids, page hashes, selected pages and their
+order.  Floating point: attention outputs within max-rel-err 1e-3 (fp32
+accumulate) as max|out - ref| / max|ref|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden, rel_err
+from oracle_bind import OR_KV_BF16, OR_KV_INT8, PAGE, OracleIndex, OraclePaged
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+def test_projection_host_matches_reference(be):
+    g = golden("lsh")
+    for dim, seed in ((128, 42), (64, 42), (128, 7)):
+        hp, hpT = be.lsh_projection(dim, seed)
+        np.testing.assert_array_equal(bits(hp), bits(g[f"hp_{dim}_{seed}"]))
+        np.testing.assert_array_equal(bits(hpT), bits(g[f"hpT_{dim}_{seed}"]))
+
+
+def test_lsh_hash_gpu(be, orc):
+    g = golden("lsh")
+    rng = np.random.default_rng(200)
+    for dim, seed in ((128, 42), (64, 42), (128, 7)):
+        hpT = g[f"hpT_{dim}_{seed}"]
+        vs = np.concatenate([g[f"vec_{dim}_{seed}"], rng.standard_normal((333, dim)).astype(np.float32)])
+        out = be.lsh_hash(torch.from_numpy(vs).cuda(), torch.from_numpy(hpT).cuda()).cpu().numpy().view(np.uint16)
+        want = np.array([orc.lsh_hash(hpT, v) for v in vs], np.uint16)
+        np.testing.assert_array_equal(out, want)
+        np.testing.assert_array_equal(out[:len(g[f"hash_{dim}_{seed}"])], g[f"hash_{dim}_{seed}"])
+
+
+def _closed_form_candidates(hashes, qh, cap):
+    ids = []
+    for p in range(17):
+        ph = qh if p == 0 else qh ^ (1 << (p - 1))
+        ids += [i for i in range(len(hashes) - 1, -1, -1) if hashes[i] == ph]
+    return np.array(ids[:cap], np.int32)
+
+
+def test_lsh_candidates_gpu(be):
+    g = golden("lsh_candidates")
+    hashes = g["hashes"][:4096]         # the reference index keeps the first 4096 blocks
+    qs = g["queries"]
+    ht = torch.from_numpy(hashes.view(np.int16).copy()).cuda()
+    qt = torch.from_numpy(qs.view(np.int16).copy()).cuda()
+    for cap in (1, 64):
+        ids, n = be.lsh_candidates(ht, qt, cap)
+        ids, n = ids.cpu().numpy(), n.cpu().numpy()
+        lens, flat = g[f"cand_{cap}_len"], g[f"cand_{cap}_ids"]
+        off = 0
+        for i in range(len(qs)):
+            np.testing.assert_array_equal(ids[i, :n[i]], flat[off:off + lens[i]])
+            off += lens[i]
+    ids, n = be.lsh_candidates(ht, qt, 256)
+    ids, n = ids.cpu().numpy(), n.cpu().numpy()
+    for i, q in enumerate(qs):
+        np.testing.assert_array_equal(ids[i, :n[i]], _closed_form_candidates(hashes, int(q), 256))
+
+
+def _build(be, orc, kind, n_layers, n_kv, hd, max_pages, lens, rng, hpT, planted=None, chunks=(1, 7, 64, 100)):
+    """The same appends on the GPU pool and the oracle; returns both plus the
+    per-layer oracle LSH indexes (page hashes inserted as pages fill)."""
+    gp = be.kv_pool(be42_kind(kind), n_layers, n_kv, hd, max_pages, hpT)
+    op = OraclePaged(orc, n_layers, n_kv, hd, max_pages, kind)
+    idx = [OracleIndex(orc, max_pages) for _ in range(n_layers)]
+    for layer, T in enumerate(lens):
+        K = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+        V = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+        if planted is not None:
+            for pg, vec in planted(layer, T):
+                K[pg * PAGE:(pg + 1) * PAGE, :hd] = vec + 0.05 * rng.standard_normal((PAGE, hd))
+        pos = 0
+        ci = 0
+        while pos < T:
+            n = min(chunks[ci % len(chunks)], T - pos)
+            ci += 1
+            gp.append(layer, torch.from_numpy(K[pos:pos + n]).cuda(), torch.from_numpy(V[pos:pos + n]).cuda(), pos)
+            for t in range(pos, pos + n):
+                op.append(layer, K[t], V[t], t)
+                if t % PAGE == PAGE - 1:
+                    c = op.page_arrays(op.phys(layer, t // PAGE))[4]
+                    idx[layer].insert(orc.lsh_hash(hpT, c), t - PAGE + 1, PAGE)
+            pos += n
+    torch.cuda.synchronize()
+    return gp, op, idx
+
+
+def be42_kind(kind):
+    return 0 if kind == OR_KV_INT8 else 1
+
+
+@pytest.mark.parametrize("kind", [OR_KV_INT8, OR_KV_BF16])
+def test_kv_append_matches_oracle(be, orc, kind):
+    rng = np.random.default_rng(300 + kind)
+    n_layers, n_kv, hd, max_pages = 3, 2, 64, 12
+    _, hpT = orc.lsh_init(hd, 42)
+    gp, op, _ = _build(be, orc, kind, n_layers, n_kv, hd, max_pages, (150, 37, 16), rng, hpT)
+    cap = n_layers * max_pages
+    pe = n_kv * PAGE * hd
+    if kind == OR_KV_INT8:
+        gk = gp.fetch("k", cap * pe, np.int8).reshape(cap, pe)
+        gv = gp.fetch("v", cap * pe, np.int8).reshape(cap, pe)
+        gks = gp.fetch("k_scale", cap * n_kv * PAGE, np.float32).reshape(cap, n_kv * PAGE)
+        gvs = gp.fetch("v_scale", cap * n_kv * PAGE, np.float32).reshape(cap, n_kv * PAGE)
+    else:
+        gk = gp.fetch("k", cap * pe, np.uint16).reshape(cap, pe)
+        gv = gp.fetch("v", cap * pe, np.uint16).reshape(cap, pe)
+    gc = gp.fetch("centroid", cap * hd, np.float32).reshape(cap, hd)
+    gnt = gp.fetch("ntok", cap, np.int32)
+    gh = gp.fetch("page_hash", cap, np.uint16).reshape(n_layers, max_pages)
+    gnl = gp.fetch("n_logical", n_layers, np.int32)
+    gni = gp.fetch("n_indexed", n_layers, np.int32)
+    gpt = gp.fetch("page_table", cap, np.int32).reshape(n_layers, max_pages)
+    for layer in range(n_layers):
+        nb = op.n_blocks(layer)
+        assert gnl[layer] == nb
+        phys = [op.phys(layer, i) for i in range(nb)]
+        np.testing.assert_array_equal(gp.layer_pages(layer), phys)
+        np.testing.assert_array_equal(gpt[layer, :nb], phys)
+        for i, p in enumerate(phys):
+            kq, vq, ks, vs, cen = op.page_arrays(p)
+            nt = op.ntok(p)
+            assert gnt[p] == nt
+            rows = (np.arange(n_kv * PAGE) % PAGE) < nt
+            np.testing.assert_array_equal(gk[p].reshape(n_kv * PAGE, hd)[rows], kq.reshape(n_kv * PAGE, hd)[rows])
+            np.testing.assert_array_equal(gv[p].reshape(n_kv * PAGE, hd)[rows], vq.reshape(n_kv * PAGE, hd)[rows])
+            if kind == OR_KV_INT8:
+                np.testing.assert_array_equal(bits(gks[p])[rows], bits(ks)[rows])
+                np.testing.assert_array_equal(bits(gvs[p])[rows], bits(vs)[rows])
+            if nt == PAGE:
+                np.testing.assert_array_equal(bits(gc[p]), bits(cen))
+                assert gh[layer, i] == orc.lsh_hash(hpT, cen)
+        assert gni[layer] == sum(1 for p in phys if op.ntok(p) == PAGE)
+    # reset returns pages LIFO; re-appending reuses them in the reference order
+    gp.reset(0)
+    op.reset(0)
+    K = rng.standard_normal((40, n_kv * hd)).astype(np.float32)
+    gp.append(0, torch.from_numpy(K).cuda(), torch.from_numpy(K).cuda(), 0)
+    for t in range(40):
+        op.append(0, K[t], K[t], t)
+    np.testing.assert_array_equal(gp.layer_pages(0), [op.phys(0, i) for i in range(op.n_blocks(0))])
+    gp.close()
+
+
+def _planter(orc, hpT, hd, n_heads, q_by_layer, frac, rng):
+    def plant(layer, T):
+        npg = T // PAGE
+        qm = orc.q_mean(q_by_layer[layer], n_heads, hd)
+        u = qm / np.linalg.norm(qm)
+        k = max(1, int(round(frac * npg)))
+        pages = rng.choice(np.arange(1, max(2, npg - 1)), size=min(k, max(1, npg - 2)), replace=False)
+        return [(int(p), (6.0 * u).astype(np.float32)) for p in pages]
+    return plant
+
+
+@pytest.mark.parametrize("kind", [OR_KV_INT8, OR_KV_BF16])
+@pytest.mark.parametrize("cap,k_sel", [(64, 64), (16, 8), (256, 64)])
+def test_route_matches_oracle(be, orc, kind, cap, k_sel):
+    rng = np.random.default_rng(400 + cap + kind)
+    n_layers, n_kv, hd, H = 4, 4, 64, 8
+    lens = (70 * PAGE + 5, 130 * PAGE, 40 * PAGE + 3, 5 * PAGE)
+    max_pages = 140
+    _, hpT = orc.lsh_init(hd, 42)
+    q = rng.standard_normal((n_layers, H, hd)).astype(np.float32)
+    gp, op, idx = _build(be, orc, kind, n_layers, n_kv, hd, max_pages, lens, rng, hpT,
+                         planted=_planter(orc, hpT, hd, H, q, 0.1, rng), chunks=(64, 3, 17))
+    sel, nsel, cand, ncand, qh = be.route(gp, torch.from_numpy(q).cuda(), k_sel, cap)
+    sel, nsel, cand, ncand, qh = (x.cpu().numpy() for x in (sel, nsel, cand, ncand, qh))
+    for layer in range(n_layers):
+        want_sel, want_cand = op.route(layer, q[layer], H, hpT, idx[layer], cap, k_sel)
+        np.testing.assert_array_equal(sel[layer, :nsel[layer]], want_sel)
+        if op.n_blocks(layer) > k_sel:
+            assert qh.view(np.uint16)[layer] == orc.lsh_hash(hpT, orc.q_mean(q[layer], H, hd))
+            np.testing.assert_array_equal(cand[layer, :ncand[layer]], want_cand)
+    gp.close()
+
+
+@pytest.mark.parametrize("kind", [OR_KV_INT8, OR_KV_BF16])
+@pytest.mark.parametrize("n_split", [1, 3, 8])
+def test_attention_matches_oracle(be, orc, kind, n_split):
+    rng = np.random.default_rng(500 + kind + n_split)
+    n_layers, n_kv, hd, H = 3, 2, 128, 8
+    lens = (33 * PAGE + 7, 3 * PAGE, 1)
+    _, hpT = orc.lsh_init(hd, 42)
+    gp, op, _ = _build(be, orc, kind, n_layers, n_kv, hd, 40, lens, rng, hpT, chunks=(64,))
+    q = rng.standard_normal((n_layers, H, hd)).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    # dense (all pages, logical order), and an arbitrary sparse order incl. a partial page
+    sels = []
+    for layer in range(n_layers):
+        sels.append([op.phys(layer, i) for i in range(op.n_blocks(layer))])
+    p0 = sels[0]
+    sels2 = [[p0[0], p0[-1]] + [p0[i] for i in (17, 3, 30, 9, 22)], [sels[1][2], sels[1][0]], sels[2]]
+    for sl in (sels, sels2):
+        max_sel = max(len(x) for x in sl)
+        st = max(max_sel, 64)
+        sel = np.full((n_layers, st), -1, np.int32)
+        nsel = np.array([len(x) for x in sl], np.int32)
+        for i, x in enumerate(sl):
+            sel[i, :len(x)] = x
+        out = be.paged_attention(gp, torch.from_numpy(q).cuda(), torch.from_numpy(sel).cuda(),
+                                 torch.from_numpy(nsel).cuda(), max_sel, scale, n_split=n_split).cpu().numpy()
+        for layer in range(n_layers):
+            want = op.attention_pages(q[layer], sl[layer], H, scale)
+            err = rel_err(out[layer].ravel(), want)
+            assert err <= TOL, (layer, err)
+            assert err <= 2e-5, (layer, err)      # the closed form keeps every fast_expf argument
+    gp.close()
+
+
+def test_lsh_attention_pipeline_c4_shape(be, orc):
+    """Config-4 shape at 8k context: 32 query heads, 8 KV heads, head_dim 128,
+    bf16 pages, 5% planted pages, top-K 64 pages, candidate cap 64."""
+    rng = np.random.default_rng(600)
+    n_kv, hd, H, T = 8, 128, 32, 8192
+    _, hpT = orc.lsh_init(hd, 42)
+    q = rng.standard_normal((1, H, hd)).astype(np.float32)
+    gp, op, idx = _build(be, orc, OR_KV_BF16, 1, n_kv, hd, T // PAGE + 1, (T,), rng, hpT,
+                         planted=_planter(orc, hpT, hd, H, q, 0.05, rng), chunks=(64,))
+    sel, nsel, cand, ncand, qh = be.route(gp, torch.from_numpy(q).cuda(), 64, 64)
+    want_sel, want_cand = op.route(0, q[0], H, hpT, idx[0], 64, 64)
+    s = sel.cpu().numpy()[0, :nsel.item()]
+    np.testing.assert_array_equal(s, want_sel)
+    np.testing.assert_array_equal(cand.cpu().numpy()[0, :ncand.item()], want_cand)
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    out = be.paged_attention(gp, torch.from_numpy(q).cuda(), sel, nsel, 64, scale, n_split=4).cpu().numpy()
+    want = op.attention_pages(q[0], want_sel, H, scale)
+    assert rel_err(out.ravel(), want) <= TOL
+    gp.close()
