@@ -257,6 +257,246 @@ static void launch_scores_apply(const be42_kv_pool &P, const float *q, const int
                        t_stride, part, n_split);
 }
 
+
+// ---------------------------------------------------------------------------
+// Fused attention for up to 64 selected pages: one block of 8 waves per
+// (query, KV head) serves the G query heads of the group.
+//  A. scores: a row (token) of K is read by RL = HD/8 lanes (16 bytes bf16 or
+//     8 bytes INT8 each), RPW = 64/RL rows per wave per step, 8 steps in
+//     flight; each lane forms the G partial dots of its 8 elements, the RL
+//     lanes of a row reduce them; s = dot * scale goes to LDS.
+//  B. weights: wave g scans head g's scores, lane = selected page (LDS padded
+//     to 17 floats per page against bank conflicts), the closed-form online
+//     softmax of the file header, l = sum w.
+//  C. V: the same row mapping accumulates o[g][8 dims] for all G heads, summed
+//     over the row groups of a wave and then over the waves through LDS;
+//     out = o * (1 / l).
+// Every K and V row of the selected pages is read once per KV head.
+constexpr int kFusedMaxPages = 64;
+constexpr int kFusedWaves = 8;
+
+template <bool BF16, int HD, int G>
+__global__ __launch_bounds__(kFusedWaves * 64) void k_attn_fused(const be42_kv_pool P, const float *__restrict__ q,
+                                                                 const int *__restrict__ sel,
+                                                                 const int *__restrict__ nsel, int sel_stride,
+                                                                 int H, float scale, float *__restrict__ out)
+{
+    constexpr int RL = HD / 8;                 // lanes per row
+    constexpr int RPW = kWave / RL;            // rows per wave per step
+    constexpr int UNR = 8;                     // steps in flight
+    __shared__ float qs[G][HD];
+    __shared__ float sc[G][kFusedMaxPages * 17];
+    __shared__ float red[kFusedWaves][G][HD];
+    __shared__ float lsh[G];
+    __shared__ int pphys[kFusedMaxPages], pnt[kFusedMaxPages];
+
+    const int b = blockIdx.x, kvh = blockIdx.y;
+    const int n_kv = P.n_kv;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int ns = min(nsel[b], kFusedMaxPages);
+    const int *selb = sel + (size_t)b * sel_stride;
+    for (int i = tid; i < G * HD; i += blockDim.x)
+        qs[i / HD][i % HD] = q[((size_t)b * H + kvh * G + i / HD) * HD + i % HD];
+    for (int i = tid; i < ns; i += blockDim.x) {
+        const int ph = selb[i];
+        pphys[i] = ph;
+        pnt[i] = P.ntok[ph];
+    }
+    __syncthreads();
+
+    const int rsub = lane / RL, rl = lane % RL;   // row within the step, lane within the row
+    const int T = ns * kPg;
+    const int rows_per_iter = kFusedWaves * RPW;
+
+    // A. scores
+    float qv[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            qv[g][j] = qs[g][rl * 8 + j];
+    for (int r0 = wave * RPW; r0 < T; r0 += rows_per_iter * UNR) {
+        float kv[UNR][8];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int r = r0 + u * rows_per_iter + rsub;
+            const int rr = r < T ? r : T - 1;
+            const int pg = rr / kPg, t = rr % kPg;
+            const size_t slot = ((size_t)pphys[pg] * n_kv + kvh) * kPg + t;
+            load_row_f32(kv[u], P.k, slot * HD + rl * 8, 8, BF16, BF16 ? 1.0f : P.k_scale[slot]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int r = r0 + u * rows_per_iter + rsub;
+            float acc[G];
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    a = __fmaf_rn(qv[g][j], kv[u][j], a);
+#pragma unroll
+                for (int x = 1; x < RL; x <<= 1)
+                    a += __shfl_xor(a, x, RL);
+                acc[g] = a;
+            }
+            if (rl == 0 && r < T) {
+                const int pg = r / kPg, t = r % kPg;
+#pragma unroll
+                for (int g = 0; g < G; g++)
+                    sc[g][pg * 17 + t] = acc[g] * scale;
+            }
+        }
+    }
+    __syncthreads();
+
+    // B. weights, wave g <-> head g, lane <-> page
+    for (int g = wave; g < G; g += kFusedWaves) {
+        float *s = sc[g];
+        const int nt = lane < ns ? pnt[lane] : 0;
+        float lm = -INFINITY;
+        for (int t = 0; t < nt; t++)
+            lm = fmaxf(lm, s[lane * 17 + t]);
+        float inc = lm;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const float v = __shfl_up(inc, o, kWave);
+            if (lane >= o)
+                inc = fmaxf(inc, v);
+        }
+        float m = __shfl_up(inc, 1, kWave);
+        if (lane == 0)
+            m = -INFINITY;
+        float av[kPg], lprod = 1.0f;
+#pragma unroll
+        for (int t = 0; t < kPg; t++) {
+            av[t] = 1.0f;
+            if (t < nt) {
+                const float st = s[lane * 17 + t];
+                const float mprev = m;
+                m = fmaxf(m, st);
+                const float at = mprev == -INFINITY ? 1.0f : fast_expf(mprev - m);
+                s[lane * 17 + t] = fast_expf(st - m);
+                av[t] = at;
+                lprod *= at;
+            }
+        }
+        float suf = lprod;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const float v = __shfl_down(suf, o, kWave);
+            if (lane + o < kWave)
+                suf *= v;
+        }
+        float pr = __shfl_down(suf, 1, kWave);
+        if (lane == kWave - 1)
+            pr = 1.0f;
+        float ls = 0.0f;
+#pragma unroll
+        for (int t = kPg - 1; t >= 0; t--) {
+            if (t < nt) {
+                const float w = s[lane * 17 + t] * pr;
+                s[lane * 17 + t] = w;
+                ls += w;
+                pr *= av[t];
+            }
+        }
+        ls = wave_sum(ls);
+        if (lane == 0)
+            lsh[g] = ls;
+    }
+    __syncthreads();
+
+    // C. o = sum_t w_t v_t
+    float o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            o[g][j] = 0.0f;
+    for (int r0 = wave * RPW; r0 < T; r0 += rows_per_iter * UNR) {
+        float vv[UNR][8];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int r = r0 + u * rows_per_iter + rsub;
+            const int rr = r < T ? r : T - 1;
+            const int pg = rr / kPg, t = rr % kPg;
+            const size_t slot = ((size_t)pphys[pg] * n_kv + kvh) * kPg + t;
+            load_row_f32(vv[u], P.v, slot * HD + rl * 8, 8, BF16, BF16 ? 1.0f : P.v_scale[slot]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int r = r0 + u * rows_per_iter + rsub;
+            if (r < T) {
+                const int pg = r / kPg, t = r % kPg;
+                if (t < pnt[pg]) {
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        const float w = sc[g][pg * 17 + t];
+#pragma unroll
+                        for (int j = 0; j < 8; j++)
+                            o[g][j] = __fmaf_rn(w, vv[u][j], o[g][j]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float v = o[g][j];
+#pragma unroll
+            for (int x = RL; x < kWave; x <<= 1)
+                v += __shfl_xor(v, x, kWave);
+            o[g][j] = v;
+        }
+    if (rsub == 0)
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                red[wave][g][rl * 8 + j] = o[g][j];
+    __syncthreads();
+    for (int i = tid; i < G * HD; i += blockDim.x) {
+        const int g = i / HD, d = i % HD;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kFusedWaves; w++)
+            v += red[w][g][d];
+        const float l = lsh[g];
+        out[((size_t)b * H + kvh * G + g) * HD + d] = l > 0.0f ? v * (1.0f / l) : v;
+    }
+}
+
+template <bool BF16, int HD>
+static bool launch_fused_hd(const be42_kv_pool &P, const float *q, const int *sel, const int *nsel, int sel_stride,
+                            int B, int H, float scale, float *out, hipStream_t s)
+{
+    const int G = H / P.n_kv;
+    const dim3 grid(B, P.n_kv), blk(kFusedWaves * 64);
+    switch (G) {
+    case 1: hipLaunchKernelGGL((k_attn_fused<BF16, HD, 1>), grid, blk, 0, s, P, q, sel, nsel, sel_stride, H, scale, out); return true;
+    case 2: hipLaunchKernelGGL((k_attn_fused<BF16, HD, 2>), grid, blk, 0, s, P, q, sel, nsel, sel_stride, H, scale, out); return true;
+    case 3: hipLaunchKernelGGL((k_attn_fused<BF16, HD, 3>), grid, blk, 0, s, P, q, sel, nsel, sel_stride, H, scale, out); return true;
+    case 4: hipLaunchKernelGGL((k_attn_fused<BF16, HD, 4>), grid, blk, 0, s, P, q, sel, nsel, sel_stride, H, scale, out); return true;
+    default: return false;
+    }
+}
+
+static bool launch_fused(const be42_kv_pool &P, const float *q, const int *sel, const int *nsel, int sel_stride, int B,
+                         int H, float scale, float *out, hipStream_t s)
+{
+    const bool bf16 = P.kind == BE42_KV_BF16;
+    if (P.head_dim == 128)
+        return bf16 ? launch_fused_hd<true, 128>(P, q, sel, nsel, sel_stride, B, H, scale, out, s)
+                    : launch_fused_hd<false, 128>(P, q, sel, nsel, sel_stride, B, H, scale, out, s);
+    if (P.head_dim == 64)
+        return bf16 ? launch_fused_hd<true, 64>(P, q, sel, nsel, sel_stride, B, H, scale, out, s)
+                    : launch_fused_hd<false, 64>(P, q, sel, nsel, sel_stride, B, H, scale, out, s);
+    return false;
+}
+
 }  // namespace be42
 
 using namespace be42;
@@ -284,6 +524,13 @@ extern "C" int be42_paged_attention(const be42_kv_pool *pool, const float *q, in
     BE42_CHECK(max_sel > 0 && max_sel <= sel_stride, "be42_paged_attention: bad max_sel %d", max_sel);
     if (n_queries <= 0)
         return BE42_OK;
+    hipStream_t s0 = as_stream(stream);
+    // up to 64 pages per query and no split requested: one fused kernel
+    if (max_sel <= kFusedMaxPages && n_split <= 1 &&
+        launch_fused(P, q, sel, n_sel, sel_stride, n_queries, n_heads, scale, out, s0)) {
+        BE42_LAUNCH_CHECK();
+        return BE42_OK;
+    }
     if (n_split < 1)
         n_split = 1;
     if (n_split > max_sel)

@@ -38,11 +38,16 @@ constexpr int kProbes = 17;
 constexpr int kMaxCand = 256;
 constexpr int kHeapMax = 62;
 
+constexpr int kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
+
 struct RouteSmem {
-    int off_qm, off_q0, off_hp, off_list, off_cnt, off_cand, off_mid, off_sc, bytes;
+    int off_qm, off_q0, off_hp, off_list, off_cnt, off_offs, off_cand, off_mid, off_sc, off_pt, off_ph, stage, bytes;
 };
 
-__host__ __device__ inline RouteSmem route_smem(int hd, int cap)
+// LDS layout of the router.  When they fit in the workgroup's LDS, the
+// layer's page table and page hashes are staged there (stage = max_logical),
+// else read from HBM (stage = 0).
+__host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical)
 {
     RouteSmem r;
     int o = 0;
@@ -51,9 +56,13 @@ __host__ __device__ inline RouteSmem route_smem(int hd, int cap)
     r.off_hp = o;   o += hd * 16 * 4;
     r.off_list = o; o += 4 * kProbes * cap * 4;
     r.off_cnt = o;  o += 4 * kProbes * 4 + 4 * 4;
+    r.off_offs = o; o += 4 * kProbes * 4 + 4 * 4;
     r.off_cand = o; o += cap * 4;
     r.off_mid = o;  o += cap * 4;
     r.off_sc = o;   o += cap * 4;
+    r.stage = o + max_logical * 6 + 16 <= kLdsBytes ? max_logical : 0;
+    r.off_pt = o;   o += r.stage * 4;
+    r.off_ph = o;   o += (r.stage * 2 + 15) & ~15;
     r.bytes = o;
     return r;
 }
@@ -65,23 +74,33 @@ __device__ __forceinline__ float rlf(float v, int lane)
 }
 
 // simd_dot_f32_f32 (simd_kernels.h:162-191) of q0 and c with the reference's
-// reduction tree, computed by the 8 lanes of a group (sub = lane % 8): lane l
-// accumulates i = l (mod 8) with FMA in order; ((s0+s4)+(s1+s5)) +
-// ((s2+s6)+(s3+s7)); then the compiled scalar tail (4 unfused products added
-// in order when >= 4 remain, the rest fused).  Result valid in sub == 0.
-__device__ __forceinline__ float dot_ref8(const float *q0, const float *c, int hd, int sub)
+// reduction tree, computed by a lane pair (half = lane % 2): the eight
+// accumulator chains i = k (mod 8) run with FMA in order, chains 0-3 in half 0
+// and 4-7 in half 1 (one 16-byte load per lane per 8 elements); then
+// t_k = s_k + s_{k+4}, ((t0+t1)+(t2+t3)), and the compiled scalar tail (4
+// unfused products added in order when >= 4 remain, the rest fused).  hd is a
+// multiple of 8, so the tail is empty for every pool; it is kept for parity
+// with the reference routine.  The result is valid in half 0.
+__device__ __forceinline__ float dot_ref8x2(const float *q0, const float *c, int hd, int half)
 {
     const int main = hd & ~7;
-    float s = 0.0f;
-    for (int i = sub; i < main; i += 8)
-        s = __fmaf_rn(q0[i], c[i], s);
-    const float s4 = __shfl_down(s, 4, 8);      // lanes 0..3 get s_{l+4}
-    const float t = s + s4;                       // t_l = s_l + s_{l+4}
-    const float t1 = __shfl_down(t, 1, 8);
-    const float u = t + t1;                       // lane 0: t0+t1, lane 2: t2+t3
-    const float u2 = __shfl_down(u, 2, 8);
-    float sum = u + u2;                           // lane 0: (t0+t1)+(t2+t3)
-    if (sub == 0) {
+    const float4 *c4 = (const float4 *)c;
+    const float4 *q4 = (const float4 *)q0;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < main / 8; j++) {
+        const float4 cv = c4[2 * j + half], qv = q4[2 * j + half];
+        s0 = __fmaf_rn(qv.x, cv.x, s0);
+        s1 = __fmaf_rn(qv.y, cv.y, s1);
+        s2 = __fmaf_rn(qv.z, cv.z, s2);
+        s3 = __fmaf_rn(qv.w, cv.w, s3);
+    }
+    const float t0 = s0 + __shfl_down(s0, 1, 2);
+    const float t1 = s1 + __shfl_down(s1, 1, 2);
+    const float t2 = s2 + __shfl_down(s2, 1, 2);
+    const float t3 = s3 + __shfl_down(s3, 1, 2);
+    float sum = (t0 + t1) + (t2 + t3);
+    if (half == 0) {
         int i = main;
         if (hd - i >= 4) {
             for (int j = 0; j < 4; j++)
@@ -94,6 +113,14 @@ __device__ __forceinline__ float dot_ref8(const float *q0, const float *c, int h
     return sum;
 }
 
+// 1-based heap position l1 lies on the path from the root to n1.
+__device__ __forceinline__ bool heap_on_path(int n1, int l1)
+{
+    const int sh = __clz(l1) - __clz(n1);
+    return sh >= 0 && (n1 >> sh) == l1;
+}
+
+template <bool STAGE>
 __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float *__restrict__ q,
                                                const int *__restrict__ slots, int H, int k_sel, int cap,
                                                int *__restrict__ sel, int *__restrict__ nsel, int sel_stride,
@@ -102,15 +129,18 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
 {
     extern __shared__ __align__(16) unsigned char smem[];
     const int hd = P.head_dim;
-    const RouteSmem L = route_smem(hd, cap);
+    const RouteSmem L = route_smem(hd, cap, P.max_logical);
     float *qm = (float *)(smem + L.off_qm);
     float *q0 = (float *)(smem + L.off_q0);
     float *hp = (float *)(smem + L.off_hp);
     int *list = (int *)(smem + L.off_list);
     int *cnt = (int *)(smem + L.off_cnt);
+    int *offs = (int *)(smem + L.off_offs);
     int *cand = (int *)(smem + L.off_cand);
     int *mid = (int *)(smem + L.off_mid);
     float *sc = (float *)(smem + L.off_sc);
+    int *pt_s = (int *)(smem + L.off_pt);
+    uint16_t *ph_s = (uint16_t *)(smem + L.off_ph);
 
     const int b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int layer = slots ? slots[b] : b;
@@ -130,24 +160,46 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
         }
         return;
     }
+    const int nidx = min(P.n_indexed[layer], P.max_logical);
 
-    // 1. q_mean (inference.c:291-295), q head 0, projection to LDS
+    // 0. loads that do not depend on the query hash are issued together:
+    //    page table and page hashes (staged), projection, q
+    if (STAGE) {
+        for (int i = tid; i < n; i += blockDim.x)
+            pt_s[i] = P.page_table[base + i];
+        for (int i = tid; i < nidx; i += blockDim.x)
+            ph_s[i] = P.page_hash[base + i];
+    }
+    const int *pt = STAGE ? pt_s : P.page_table + base;
+    const uint16_t *ph = STAGE ? ph_s : P.page_hash + base;
+    for (int i = tid; i < hd * 16; i += blockDim.x)
+        hp[i] = P.hpT[i];
+
+    // 1. q_mean (inference.c:291-295): sum in head order, then / n_heads;
+    //    32 heads' loads are issued before the sum consumes them
     for (int d = tid; d < hd; d += blockDim.x) {
         float s = 0.0f;
-#pragma unroll 8
-        for (int h = 0; h < H; h++)
-            s = s + qb[h * hd + d];
+        for (int h0 = 0; h0 < H; h0 += 32) {
+            float v[32];
+#pragma unroll
+            for (int j = 0; j < 32; j++)
+                v[j] = h0 + j < H ? qb[(h0 + j) * hd + d] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 32; j++)
+                if (h0 + j < H)
+                    s = s + v[j];
+        }
         qm[d] = s / (float)H;
         q0[d] = qb[d];
     }
-    for (int i = tid; i < hd * 16; i += blockDim.x)
-        hp[i] = P.hpT[i];
     __syncthreads();
     if (wave == 0) {
         float s = 0.0f;
-        if (lane < 16)
+        if (lane < 16) {
+#pragma unroll 16
             for (int i = 0; i < hd; i++)
                 s = __fmaf_rn(qm[i], hp[i * 16 + lane], s);
+        }
         const unsigned long long m = __ballot(lane < 16 && s > 0.0f);
         if (lane == 0)
             cnt[4 * kProbes] = (int)(m & 0xFFFFu);
@@ -158,7 +210,6 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
         qhash_out[b] = (uint16_t)qh;
 
     // 2. candidate scan: wave w owns ids [lo, hi), scanned from hi-1 down
-    const int nidx = min(P.n_indexed[layer], P.max_logical);
     {
         const int part = (nidx + 3) / 4;
         const int hi = max(nidx - wave * part, 0), lo = max(nidx - (wave + 1) * part, 0);
@@ -169,7 +220,7 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
             const bool valid = id >= lo;
             int p = kProbes;
             if (valid) {
-                const int dd = (int)P.page_hash[base + id] ^ qh;
+                const int dd = (int)ph[id] ^ qh;
                 p = dd == 0 ? 0 : (((dd & (dd - 1)) == 0) ? __ffs(dd) : kProbes);
             }
             unsigned long long hits = __ballot(p < kProbes);
@@ -193,19 +244,46 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     }
     __syncthreads();
 
-    // 3. concatenate per probe (wave order = descending id), then keep the
-    //    middle entries (not the first or last page)
+    // 3. concatenation: list j = 4 * probe + wave (probe order, then
+    //    descending id) starts at offs[j]; lane l of wave 0 owns lists 2l, 2l+1
     if (wave == 0) {
-        int total = 0;
-        for (int p = 0; p < kProbes && total < cap; p++)
-            for (int w = 0; w < 4 && total < cap; w++) {
-                const int c = min(cnt[w * kProbes + p], cap);
-                const int take = min(c, cap - total);
-                for (int i = lane; i < take; i += kWave)
-                    cand[total + i] = list[(w * kProbes + p) * cap + i];
-                total += take;
-            }
-        __builtin_amdgcn_s_waitcnt(0);
+        int c0 = 0, c1 = 0;
+        if (lane < 2 * kProbes) {
+            const int j0 = 2 * lane, j1 = j0 + 1;
+            c0 = min(cnt[(j0 & 3) * kProbes + (j0 >> 2)], cap);
+            c1 = min(cnt[(j1 & 3) * kProbes + (j1 >> 2)], cap);
+        }
+        int inc = c0 + c1;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int v = __shfl_up(inc, o, kWave);
+            if (lane >= o)
+                inc += v;
+        }
+        if (lane < 2 * kProbes) {
+            offs[2 * lane] = inc - c0 - c1;
+            offs[2 * lane + 1] = inc - c1;
+        }
+        if (lane == kWave - 1)
+            cnt[4 * kProbes + 1] = min(inc, cap);
+    }
+    __syncthreads();
+    for (int j = wave; j < 4 * kProbes; j += 4) {
+        const int off = offs[j];
+        const int *src = list + ((j & 3) * kProbes + (j >> 2)) * cap;
+        const int take = min(min(cnt[(j & 3) * kProbes + (j >> 2)], cap), cap - off);
+        for (int i = lane; i < take; i += kWave)
+            cand[off + i] = src[i];
+    }
+    __syncthreads();
+    const int total = cnt[4 * kProbes + 1];
+    if (cand_out)
+        for (int i = tid; i < total; i += blockDim.x)
+            cand_out[(size_t)b * cap + i] = cand[i];
+    if (tid == 0 && ncand_out)
+        ncand_out[b] = total;
+    // middle entries: candidates other than the first and last page
+    if (wave == 0) {
         int nm = 0;
         for (int i0 = 0; i0 < total; i0 += kWave) {
             const int i = i0 + lane;
@@ -216,34 +294,32 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
                 mid[nm + __popcll(m & ((1ull << lane) - 1ull))] = id;
             nm += __popcll(m);
         }
-        if (lane == 0) {
-            cnt[4 * kProbes + 1] = total;
+        if (lane == 0)
             cnt[4 * kProbes + 2] = nm;
-        }
-        if (cand_out)
-            for (int i = lane; i < total; i += kWave)
-                cand_out[(size_t)b * cap + i] = cand[i];
-        if (lane == 0 && ncand_out)
-            ncand_out[b] = total;
     }
     __syncthreads();
     const int nm = cnt[4 * kProbes + 2];
 
-    // 4. scores of the middle entries (score_blocks semantics)
-    for (int e0 = 0; e0 < nm; e0 += 32) {
-        const int e = e0 + (tid >> 3), sub = tid & 7;
+    // 4. scores of the middle entries (score_blocks semantics), a lane pair each
+    for (int e0 = 0; e0 < nm; e0 += 128) {
+        const int e = e0 + (tid >> 1), half = tid & 1;
         const int ee = e < nm ? e : nm - 1;
-        const int phys = P.page_table[base + mid[ee]];
-        const float s = dot_ref8(q0, P.centroid + (size_t)phys * hd, hd, sub);
-        if (sub == 0 && e < nm)
+        const int phys = pt[mid[ee]];
+        const float s = dot_ref8x2(q0, P.centroid + (size_t)phys * hd, hd, half);
+        if (half == 0 && e < nm)
             sc[e] = s;
     }
     __syncthreads();
 
-    // 5. selection: anchors, then the reference heap in wave 0
+    // 5. selection: anchors, then the reference min-heap (capacity
+    //    min(k-2, #middle, 62), strict replacement) in wave 0, heap slot i in
+    //    lane i.  Values along any root-to-leaf path are non-decreasing, so a
+    //    sift-up or sift-down moves exactly the path entries on one side of s
+    //    by one level: each push is one parallel step over the path's lanes.
+    //    (Scores are finite: q and the centroids are finite.)
     if (wave != 0)
         return;
-    const int first = P.page_table[base], last = P.page_table[base + n - 1];
+    const int first = pt[0], last = pt[n - 1];
     int ns = 0;
     if (lane == 0)
         selb[0] = first;
@@ -258,63 +334,55 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
         ak = 0;
     float hs = 0.0f;
     int hi = 0, size = 0;
-    for (int e = 0; e < nm && ak > 0; e++) {
-        const float s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sc[e])));
-        if (size < ak) {
-            int i = size++;
-            while (i > 0) {
-                const int par = (i - 1) >> 1;
-                const float sp = rlf(hs, par);
-                if (sp <= s)
-                    break;
-                const int ip = rl(hi, par);
-                if (lane == i) {
-                    hs = sp;
-                    hi = ip;
-                }
-                i = par;
-            }
-            if (lane == i) {
-                hs = s;
-                hi = e;
-            }
-        } else if (s > rlf(hs, 0)) {
-            int i = 0;
-            for (;;) {
-                const int l = 2 * i + 1, r = 2 * i + 2;
-                int sm = i;
-                float ssm = s;
-                if (l < size) {
-                    const float sl = rlf(hs, l);
-                    if (sl < ssm) {
-                        sm = l;
-                        ssm = sl;
+    const int par = lane > 0 ? (lane - 1) >> 1 : 0;
+    const int cl = (2 * lane + 1) & 63, cr = (2 * lane + 2) & 63;
+    for (int e0 = 0; e0 < nm && ak > 0; e0 += kWave) {
+        const float sv = e0 + lane < nm ? sc[e0 + lane] : 0.0f;
+        const int ecnt = min(kWave, nm - e0);
+        for (int u = 0; u < ecnt; u++) {
+            const int e = e0 + u;
+            const float s = rlf(sv, u);
+            if (size < ak) {
+                // sift-up from slot `size`: path entries > s move down one level
+                const float pv = __shfl(hs, par, kWave);
+                const int pi = __shfl(hi, par, kWave);
+                if (heap_on_path(size + 1, lane + 1)) {
+                    if (lane > 0 && pv > s) {
+                        hs = pv;
+                        hi = pi;
+                    } else if (lane == size || hs > s) {
+                        hs = s;
+                        hi = e;
                     }
                 }
-                if (r < size) {
-                    const float sr = rlf(hs, r);
-                    if (sr < ssm) {
-                        sm = r;
-                        ssm = sr;
+                size++;
+            } else if (s > rlf(hs, 0)) {
+                // sift-down from the root along the min-child path (left on
+                // ties): path entries < s move up one level
+                const float hl = __shfl(hs, cl, kWave), hr = __shfl(hs, cr, kWave);
+                const int il = __shfl(hi, cl, kWave), ir = __shfl(hi, cr, kWave);
+                const bool hasl = 2 * lane + 1 < size;
+                const bool right = 2 * lane + 2 < size && hr < hl;
+                const unsigned long long mh = __ballot(hasl), mr = __ballot(right);
+                int end = 0;
+                while ((mh >> end) & 1ull)
+                    end = 2 * end + 1 + (int)((mr >> end) & 1ull);
+                if (heap_on_path(end + 1, lane + 1)) {
+                    const float cv = right ? hr : hl;
+                    const int ci = right ? ir : il;
+                    if (hasl && cv < s) {
+                        hs = cv;
+                        hi = ci;
+                    } else if (lane == 0 || hs < s) {
+                        hs = s;
+                        hi = e;
                     }
                 }
-                if (sm == i)
-                    break;
-                const int ism = rl(hi, sm);
-                if (lane == i) {
-                    hs = ssm;
-                    hi = ism;
-                }
-                i = sm;
-            }
-            if (lane == i) {
-                hs = s;
-                hi = e;
             }
         }
     }
     if (lane < size)
-        selb[ns + lane] = P.page_table[base + mid[hi]];
+        selb[ns + lane] = pt[mid[hi]];
     if (lane == 0)
         nsel[b] = ns + size;
 }
@@ -472,11 +540,16 @@ extern "C" int be42_lsh_route(const be42_kv_pool *pool, const float *q, const in
                "be42_lsh_route: sel_stride %d must be >= max(k, 64)", sel_stride);
     if (n_queries == 0)
         return BE42_OK;
-    const RouteSmem L = route_smem(pool->head_dim, cand_cap);
+    const RouteSmem L = route_smem(pool->head_dim, cand_cap, pool->max_logical);
+    const void *fn = L.stage ? (const void *)k_route<true> : (const void *)k_route<false>;
     if (L.bytes > 65536)
-        BE42_HIP(hipFuncSetAttribute((const void *)k_route, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes));
-    hipLaunchKernelGGL(k_route, dim3(n_queries), dim3(256), (size_t)L.bytes, as_stream(stream), *pool, q, slots,
-                       n_heads, k_sel, cand_cap, sel, n_sel, sel_stride, cand, n_cand, qhash);
+        BE42_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes));
+    if (L.stage)
+        hipLaunchKernelGGL(k_route<true>, dim3(n_queries), dim3(256), (size_t)L.bytes, as_stream(stream), *pool, q,
+                           slots, n_heads, k_sel, cand_cap, sel, n_sel, sel_stride, cand, n_cand, qhash);
+    else
+        hipLaunchKernelGGL(k_route<false>, dim3(n_queries), dim3(256), (size_t)L.bytes, as_stream(stream), *pool, q,
+                           slots, n_heads, k_sel, cand_cap, sel, n_sel, sel_stride, cand, n_cand, qhash);
     BE42_LAUNCH_CHECK();
     return BE42_OK;
 }

@@ -67,12 +67,169 @@ def cpu_baseline(seconds=10.0):
                       f"median of {len(times)} runs over {seconds:.0f} s"}
 
 
+# ---- LSH sparse attention ------------------------
+LSH = dict(heads=32, kv_heads=8, head_dim=128, page=16, ctx=32768, k_sel=64, cap=64, planted=0.05)
+LSH_BATCHES = [1, 16, 64, 128]
+
+
+def lsh_bytes(n_sel, n_cand, cfg=LSH):
+    """Algorithmic bytes of one query step, all heads: selected pages' bf16
+    K+V, candidate centroids, projection, q, out, bucket/chain metadata."""
+    page_kv = cfg["page"] * cfg["kv_heads"] * cfg["head_dim"] * 2 * 2
+    hd = cfg["head_dim"]
+    return (n_sel * page_kv + n_cand * hd * 4 + hd * 16 * 4 + cfg["heads"] * hd * 4 * 2
+            + 4 * (17 + n_cand))
+
+
+def plant_keys(K, q, rng, cfg=LSH):
+    """5% of the pages (never the first or last) get keys 6*unit(q_mean) +
+    N(0, 0.05^2) on every KV head."""
+    import numpy as np
+    hd, P = cfg["head_dim"], cfg["page"]
+    npg = K.shape[0] // P
+    qm = q.reshape(cfg["heads"], hd).astype(np.float64).mean(0)
+    u = (6.0 * qm / np.linalg.norm(qm)).astype(np.float32)
+    pages = rng.choice(np.arange(1, npg - 1), size=int(round(cfg["planted"] * npg)), replace=False)
+    for pg in pages:
+        for h in range(cfg["kv_heads"]):
+            K[pg * P:(pg + 1) * P, h * hd:(h + 1) * hd] = u + 0.05 * rng.standard_normal((P, hd)).astype(np.float32)
+    return pages
+
+
+def plant_keys_gpu(K, q, gen, cfg=LSH):
+    """plant_keys on the device: K is a (T, kv_heads * head_dim) cuda tensor."""
+    import numpy as np
+    import torch
+    hd, P, KVH = cfg["head_dim"], cfg["page"], cfg["kv_heads"]
+    T = K.shape[0]
+    npg = T // P
+    qm = q.reshape(cfg["heads"], hd).astype(np.float64).mean(0)
+    u = torch.from_numpy((6.0 * qm / np.linalg.norm(qm)).astype(np.float32)).to(K.device)
+    n = int(round(cfg["planted"] * npg))
+    pages = torch.randperm(npg - 2, generator=gen, device=K.device)[:n] + 1
+    rows = (pages[:, None] * P + torch.arange(P, device=K.device)).reshape(-1)
+    noise = torch.randn(rows.numel(), KVH, hd, generator=gen, device=K.device) * 0.05
+    K.view(T, KVH, hd)[rows] = u + noise
+
+
+def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
+    """Route + sparse attention over the first B sequences of one pool, for
+    each B in `batches`; every sequence is a 32k-token bf16 context."""
+    import numpy as np
+    import torch
+    cfg = LSH
+    H, KVH, hd, T = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["ctx"]
+    BM = max(batches)
+    _, hpT = lib.lsh_projection(hd, 42)
+    pool = lib.kv_pool(1, BM, KVH, hd, T // cfg["page"] + 1, hpT)
+    rng = np.random.default_rng(4)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    q = rng.standard_normal((BM, H, hd)).astype(np.float32)
+    for b in range(BM):
+        K = torch.randn(T, KVH * hd, generator=gen, device="cuda")
+        plant_keys_gpu(K, q[b], gen)
+        V = torch.randn(T, KVH * hd, generator=gen, device="cuda")
+        pool.append(b, K, V, 0)
+        del K, V
+    torch.cuda.synchronize()
+    qall = torch.from_numpy(q).cuda()
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    sel_stride = 64
+    n_split = 1        # <= 64 pages: the single fused kernel
+    rows = []
+    for B in batches:
+        qd = qall[:B].contiguous()
+        sel = torch.empty((B, sel_stride), dtype=torch.int32, device="cuda")
+        nsel = torch.empty(B, dtype=torch.int32, device="cuda")
+        cand = torch.empty((B, cfg["cap"]), dtype=torch.int32, device="cuda")
+        ncand = torch.empty(B, dtype=torch.int32, device="cuda")
+        out = torch.empty((B, H, hd), device="cuda")
+        ws = torch.empty(max(1, lib.lib.be42_attn_workspace_bytes(B, H, hd, cfg["k_sel"], n_split)),
+                         dtype=torch.uint8, device="cuda")
+
+        def step(ev=None):
+            if ev is not None:
+                ev[0].record()
+            lib._call("be42_lsh_route", pool.handle, lib.p(qd), None, B, H, cfg["k_sel"], cfg["cap"], lib.p(sel),
+                      lib.p(nsel), sel_stride, lib.p(cand), lib.p(ncand), None, lib.stream())
+            if ev is not None:
+                ev[1].record()
+            lib.paged_attention(pool, qd, sel, nsel, cfg["k_sel"], scale, n_split=n_split, out=out, workspace=ws)
+            if ev is not None:
+                ev[2].record()
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        for i in range(steps):
+            step(evs[i])
+        torch.cuda.synchronize()
+        route_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+        attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+        tot_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / steps
+        ns = nsel.cpu().numpy()
+        nc = ncand.cpu().numpy()
+        nbytes = sum(lsh_bytes(int(a), int(c)) for a, c in zip(ns, nc))
+        kv_bytes = sum(int(a) * cfg["page"] * KVH * hd * 2 * 2 for a in ns)
+        rows.append({"batch": B, "us_per_token": round(tot_ms * 1e3 / B, 3), "step_us": round(tot_ms * 1e3, 2),
+                     "route_us": round(route_ms * 1e3, 2), "attention_us": round(attn_ms * 1e3, 2),
+                     "n_sel_mean": float(ns.mean()), "n_cand_mean": float(nc.mean()),
+                     "bytes_per_step": nbytes, "GBps": round(nbytes / (tot_ms * 1e-3) / 1e9, 1),
+                     "frac_of_hbm_peak": round(nbytes / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "attention_GBps": round(kv_bytes / (attn_ms * 1e-3) / 1e9, 1)})
+    pool.close()
+    head = max(rows, key=lambda r: r["batch"])
+    return {"workload": f"configs[3]: B sequences x {T}-token bf16 paged KV (page 16), {H} heads / {KVH} KV heads, "
+                        f"head_dim {hd}, top-K {cfg['k_sel']} pages, candidate cap {cfg['cap']}, 5% planted pages; "
+                        f"one step = route + sparse attention of one decode token per sequence",
+            "us_per_token": head["us_per_token"], "batch": head["batch"],
+            "frac_of_hbm_peak": head["frac_of_hbm_peak"], "by_batch": rows}
+
+
+def lsh_cpu_baseline(seconds=10.0):
+    """The oracle (port of the reference route + paged sparse attention, bf16
+    pages) on one 32k-token sequence of the configs[3] workload."""
+    import numpy as np
+    from oracle_bind import OR_KV_BF16, Oracle, OracleIndex, OraclePaged
+    cfg = LSH
+    orc = Oracle()
+    cores = min(16, host_cores())
+    H, KVH, hd, T, P = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["ctx"], cfg["page"]
+    rng = np.random.default_rng(5)
+    _, hpT = orc.lsh_init(hd, 42)
+    q = rng.standard_normal((H, hd)).astype(np.float32)
+    K = rng.standard_normal((T, KVH * hd)).astype(np.float32)
+    V = rng.standard_normal((T, KVH * hd)).astype(np.float32)
+    plant_keys(K, q, rng)
+    pk = OraclePaged(orc, 1, KVH, hd, T // P + 1, OR_KV_BF16)
+    ix = OracleIndex(orc, T // P + 1)
+    for t in range(T):
+        pk.append(0, K[t], V[t], t)
+        if t % P == P - 1:
+            ix.insert(orc.lsh_hash(hpT, pk.page_arrays(pk.phys(0, t // P))[4]), t - P + 1, P)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end and len(times) < 2000:
+        t0 = time.perf_counter()
+        sel, _ = pk.route(0, q, H, hpT, ix, cfg["cap"], cfg["k_sel"])
+        pk.attention_pages(q, sel, H, scale, threads=cores)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"value": round(med * 1e6, 1), "unit": "us/token", "cores": cores, "kind": "port",
+            "sample": f"oracle or_route_pages + or_paged_attention_pages (bf16 pages), one {T}-token sequence, "
+                      f"OpenMP {cores} threads over heads, median of {len(times)} runs"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-lsh", action="store_true", help="skip the LSH attention leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -178,8 +335,15 @@ def main():
         "gemv_sweep": sweep,
         "wall_s": round(wall, 2),
     }
+    if not args.no_lsh:
+        # free the GEMV pools first
+        configs.clear()
+        torch.cuda.empty_cache()
+        out["lsh_attention"] = lsh_bench(lib, max(args.steps, 10), max(args.warmup, 2))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
+        if not args.no_lsh:
+            out["lsh_attention"]["cpu_baseline"] = lsh_cpu_baseline()
     print(json.dumps(out), flush=True)
 
 

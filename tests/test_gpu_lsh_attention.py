@@ -69,14 +69,15 @@ def test_lsh_candidates_gpu(be):
         np.testing.assert_array_equal(ids[i, :n[i]], _closed_form_candidates(hashes, int(q), 256))
 
 
-def _build(be, orc, kind, n_layers, n_kv, hd, max_pages, lens, rng, hpT, planted=None, chunks=(1, 7, 64, 100)):
+def _build(be, orc, kind, n_layers, n_kv, hd, max_pages, lens, rng, hpT, planted=None, chunks=(1, 7, 64, 100),
+           kgen=None):
     """The same appends on the GPU pool and the oracle; returns both plus the
     per-layer oracle LSH indexes (page hashes inserted as pages fill)."""
     gp = be.kv_pool(be42_kind(kind), n_layers, n_kv, hd, max_pages, hpT)
     op = OraclePaged(orc, n_layers, n_kv, hd, max_pages, kind)
     idx = [OracleIndex(orc, max_pages) for _ in range(n_layers)]
     for layer, T in enumerate(lens):
-        K = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+        K = rng.standard_normal((T, n_kv * hd)).astype(np.float32) if kgen is None else kgen(layer, T)
         V = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
         if planted is not None:
             for pg, vec in planted(layer, T):
@@ -166,12 +167,13 @@ def _planter(orc, hpT, hd, n_heads, q_by_layer, frac, rng):
 
 
 @pytest.mark.parametrize("kind", [OR_KV_INT8, OR_KV_BF16])
-@pytest.mark.parametrize("cap,k_sel", [(64, 64), (16, 8), (256, 64)])
-def test_route_matches_oracle(be, orc, kind, cap, k_sel):
+@pytest.mark.parametrize("cap,k_sel,max_pages", [(64, 64, 140), (16, 8, 140), (256, 64, 140), (256, 40, 20000)])
+def test_route_matches_oracle(be, orc, kind, cap, k_sel, max_pages):
+    """With 20000 pages per layer the page table and hashes (6 bytes a page)
+    do not fit in LDS next to the candidate lists and are read from HBM."""
     rng = np.random.default_rng(400 + cap + kind)
     n_layers, n_kv, hd, H = 4, 4, 64, 8
     lens = (70 * PAGE + 5, 130 * PAGE, 40 * PAGE + 3, 5 * PAGE)
-    max_pages = 140
     _, hpT = orc.lsh_init(hd, 42)
     q = rng.standard_normal((n_layers, H, hd)).astype(np.float32)
     gp, op, idx = _build(be, orc, kind, n_layers, n_kv, hd, max_pages, lens, rng, hpT,
@@ -184,6 +186,31 @@ def test_route_matches_oracle(be, orc, kind, cap, k_sel):
         if op.n_blocks(layer) > k_sel:
             assert qh.view(np.uint16)[layer] == orc.lsh_hash(hpT, orc.q_mean(q[layer], H, hd))
             np.testing.assert_array_equal(cand[layer, :ncand[layer]], want_cand)
+    gp.close()
+
+
+@pytest.mark.parametrize("k_sel,cap", [(64, 256), (8, 64)])
+def test_route_tied_scores(be, orc, k_sel, cap):
+    """Pages built from three repeated patterns: equal hashes, equal centroids,
+    equal scores -- the heap's strict comparisons decide the order."""
+    rng = np.random.default_rng(450 + k_sel)
+    n_kv, hd, H = 2, 64, 4
+    pats = rng.standard_normal((3, PAGE, n_kv * hd)).astype(np.float32)
+
+    def kgen(layer, T):
+        K = np.empty((T, n_kv * hd), np.float32)
+        for pg in range((T + PAGE - 1) // PAGE):
+            rows = K[pg * PAGE:(pg + 1) * PAGE]
+            rows[:] = pats[(pg * 7) % 3][:len(rows)]
+        return K
+    _, hpT = orc.lsh_init(hd, 42)
+    q = np.repeat(pats[0, :, :hd].mean(axis=0)[None, None], H, axis=1).astype(np.float32)   # ~ pattern 0's centroid
+    gp, op, idx = _build(be, orc, OR_KV_BF16, 1, n_kv, hd, 300, (290 * PAGE,), rng, hpT, chunks=(64,), kgen=kgen)
+    sel, nsel, cand, ncand, qh = be.route(gp, torch.from_numpy(q).cuda(), k_sel, cap)
+    want_sel, want_cand = op.route(0, q[0], H, hpT, idx[0], cap, k_sel)
+    np.testing.assert_array_equal(cand.cpu().numpy()[0, :ncand.item()], want_cand)
+    np.testing.assert_array_equal(sel.cpu().numpy()[0, :nsel.item()], want_sel)
+    assert len(want_cand) > k_sel
     gp.close()
 
 
@@ -220,6 +247,32 @@ def test_attention_matches_oracle(be, orc, kind, n_split):
     gp.close()
 
 
+@pytest.mark.parametrize("kind", [OR_KV_INT8, OR_KV_BF16])
+@pytest.mark.parametrize("n_kv,H,hd", [(8, 8, 64), (8, 24, 128), (2, 6, 64), (1, 2, 128)])
+def test_attention_fused_group_shapes(be, orc, kind, n_kv, H, hd):
+    """Single-kernel path (n_split 1, <= 64 pages) for every GQA group size it
+    instantiates and both head dims: the tiny model (8/8, hd 64), the 3B
+    model (24/8, hd 128)."""
+    rng = np.random.default_rng(700 + kind + H + hd)
+    lens = (64 * PAGE, 20 * PAGE + 5, 9)
+    _, hpT = orc.lsh_init(hd, 42)
+    gp, op, _ = _build(be, orc, kind, 3, n_kv, hd, 70, lens, rng, hpT, chunks=(64,))
+    q = rng.standard_normal((3, H, hd)).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    sl = [[op.phys(layer, i) for i in range(op.n_blocks(layer))] for layer in range(3)]
+    sl[1] = sl[1][::-1]
+    sel = np.full((3, 64), -1, np.int32)
+    nsel = np.array([len(x) for x in sl], np.int32)
+    for i, x in enumerate(sl):
+        sel[i, :len(x)] = x
+    out = be.paged_attention(gp, torch.from_numpy(q).cuda(), torch.from_numpy(sel).cuda(),
+                             torch.from_numpy(nsel).cuda(), 64, scale, n_split=1).cpu().numpy()
+    for layer in range(3):
+        want = op.attention_pages(q[layer], sl[layer], H, scale)
+        assert rel_err(out[layer].ravel(), want) <= 2e-5, layer
+    gp.close()
+
+
 def test_lsh_attention_pipeline_c4_shape(be, orc):
     """Config-4 shape at 8k context: 32 query heads, 8 KV heads, head_dim 128,
     bf16 pages, 5% planted pages, top-K 64 pages, candidate cap 64."""
@@ -235,7 +288,7 @@ def test_lsh_attention_pipeline_c4_shape(be, orc):
     np.testing.assert_array_equal(s, want_sel)
     np.testing.assert_array_equal(cand.cpu().numpy()[0, :ncand.item()], want_cand)
     scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
-    out = be.paged_attention(gp, torch.from_numpy(q).cuda(), sel, nsel, 64, scale, n_split=4).cpu().numpy()
+    out = be.paged_attention(gp, torch.from_numpy(q).cuda(), sel, nsel, 64, scale, n_split=1).cpu().numpy()
     want = op.attention_pages(q[0], want_sel, H, scale)
     assert rel_err(out.ravel(), want) <= TOL
     gp.close()
