@@ -39,6 +39,8 @@ SIGNATURES = {
     "be42_gemv_prepare": (i32, [vp, vp, i32, i32, i32, vp]),
     "be42_gemv_q8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemv_fp8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "be42_gemm_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+    "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_kv_create": (i32, [vp, i32, i32, i32, i32, i32, vp]),
     "be42_kv_destroy": (None, [vp]),
     "be42_kv_set_projection": (i32, [vp, vp]),
@@ -176,6 +178,17 @@ class Lib:
         self._call(name, self.p(out), self.p(w), self.p(sw), self.p(xdig), n, k, batch, self.stream(stream))
         return out
 
+
+    # -- prefill GEMM -----------------------------------------------------------
+    def gemm(self, xq, sx, wq, sw, kind, out=None, stream=None):
+        """Y [M][N] = per-token-quantized xq [M][K] x per-row-quantized wq [N][K]."""
+        t = self.torch
+        m, k = xq.shape
+        n = wq.shape[0]
+        y = out if out is not None else t.empty((m, n), dtype=t.float32, device=xq.device)
+        name = "be42_gemm_i8" if kind == "int8" else "be42_gemm_fp8"
+        self._call(name, self.p(y), self.p(xq), self.p(sx), self.p(wq), self.p(sw), m, n, k, self.stream(stream))
+        return y
 
     # -- LSH / paged KV / attention --------------------------------------------
     def lsh_projection(self, dim, seed):

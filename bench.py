@@ -188,6 +188,53 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
             "frac_of_hbm_peak": head["frac_of_hbm_peak"], "by_batch": rows}
 
 
+# ---- prefill GEMM ---------------------------------
+GEMM_M = [512, 2048, 8192]
+MFMA_PEAK_TOPS = {"int8": 5000.0, "fp8": 5000.0}     # dense, MI355X datasheet
+
+
+def gemm_bench(lib, steps, warmup):
+    """M tokens in {512, 2048, 8192} x the GEMV (N, K) shapes,
+    INT8 x INT8 (per-token activations, per-row weights, int32 accumulate)
+    and FP8 x FP8 (fp32 accumulate); inputs N(0,1) with 1% outliers at +-8."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    rows = []
+    for kind in KINDS:
+        qf = lib.quant_rows_int8 if kind == "int8" else lib.quant_rows_fp8
+        for (n, k) in SHAPES:
+            wq, sw = qf(torch.randn(n, k, generator=g, device="cuda") * 0.02)
+            for m in GEMM_M:
+                x = torch.randn(m, k, generator=g, device="cuda")
+                mask = torch.rand(m, k, generator=g, device="cuda") < 0.01
+                x[mask] = torch.where(torch.rand(int(mask.sum()), generator=g, device="cuda") < 0.5, -8.0, 8.0)
+                xq, sx = qf(x)
+                del x, mask
+                y = torch.empty(m, n, device="cuda")
+                for _ in range(warmup):
+                    lib.gemm(xq, sx, wq, sw, kind, out=y)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(steps):
+                    lib.gemm(xq, sx, wq, sw, kind, out=y)
+                e1.record()
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1) / steps
+                tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+                rows.append({"kind": kind, "m": m, "n": n, "k": k, "us": round(ms * 1e3, 1),
+                             "TOPS": round(tops, 1), "frac_of_mfma_peak": round(tops / MFMA_PEAK_TOPS[kind], 4)})
+                del xq, sx, y
+            del wq, sw
+            torch.cuda.empty_cache()
+    tot_ops = sum(2.0 * r["m"] * r["n"] * r["k"] for r in rows)
+    tot_s = sum(r["us"] for r in rows) * 1e-6
+    best = max(rows, key=lambda r: r["TOPS"])
+    return {"workload": "configs[2]: M in {512,2048,8192} x (N,K) in {4096x4096, 14336x4096, 4096x14336, "
+                        "128256x4096}, INT8xINT8 and FP8xFP8 per-token x per-row scaled",
+            "TOPS_aggregate": round(tot_ops / tot_s / 1e12, 1), "best": best, "by_shape": rows}
+
+
 def lsh_cpu_baseline(seconds=10.0):
     """The oracle (port of the reference route + paged sparse attention, bf16
     pages) on one 32k-token sequence of the configs[3] workload."""
@@ -230,6 +277,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-lsh", action="store_true", help="skip the LSH attention leg")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -335,6 +383,10 @@ def main():
         "gemv_sweep": sweep,
         "wall_s": round(wall, 2),
     }
+    if not args.no_gemm:
+        configs.clear()
+        torch.cuda.empty_cache()
+        out["prefill_gemm"] = gemm_bench(lib, 5, 1)
     if not args.no_lsh:
         # free the GEMV pools first
         configs.clear()

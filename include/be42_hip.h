@@ -74,6 +74,22 @@ int be42_gemv_q8_prepared(float *y, const int8_t *w, const float *w_scale, const
 int be42_gemv_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, const void *xdig,
                            int n, int k, int batch, void *stream);
 
+/* ---- prefill GEMM ---------------------------------------------------------------
+ * Y[m][n] for m < M tokens, n < N features, both operands K-contiguous
+ * ([M][K] activations, [N][K] weights), fp32 output [M][N].  Replaces the
+ * n > 1 tiled-GEMM branch of op_matmul (src/compute/ops_matmul.c:366-477,
+ * gemm_bf16_f32_tiled :231) for quantized operands.
+ *   INT8: xq/sx from per-token quant_f32_to_int8 (be42_quant_rows_int8),
+ *         Y = ((float)sum_k xq*wq * sx[m]) * sw[n]; the int32 sum is exact, so
+ *         Y is bit-identical to any exact evaluation (k < 133144).
+ *   FP8:  xq/sx from per-token E4M3 (be42_quant_rows_fp8),
+ *         Y = (sum_k e4m3(xq)*e4m3(wq) * sx[m]) * sw[n], fp32 accumulation.
+ * k % 16 == 0, operands 16-byte aligned. */
+int be42_gemm_i8(float *y, const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
+                 int m, int n, int k, void *stream);
+int be42_gemm_fp8(float *y, const uint8_t *xq, const float *sx, const uint8_t *wq, const float *sw,
+                  int m, int n, int k, void *stream);
+
 /* ---- paged KV cache in HBM ------------------------------------------------------
  * Mirrors t_block_manager / t_paged_kv_cache (src/memory/paged.h:53-99): pages
  * of 16 tokens, [n_kv][16][head_dim] per page, INT8 codes with a per-(token,
