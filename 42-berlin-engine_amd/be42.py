@@ -47,6 +47,9 @@ SIGNATURES = {
     "be42_kv_append": (i32, [vp, i32, vp, vp, i32, i32, vp]),
     "be42_kv_reset": (i32, [vp, i32, vp]),
     "be42_kv_layer_pages": (i32, [vp, i32, vp, i32]),
+    "be42_kv_page_alloc": (i32, [vp]),
+    "be42_kv_page_free": (i32, [vp, i32]),
+    "be42_kv_export": (i32, [vp, vp, vp, vp, vp]),
     "be42_lsh_projection": (None, [vp, vp, i32, C.c_uint]),
     "be42_lsh_hash": (i32, [vp, vp, i32, vp, i32, vp]),
     "be42_lsh_candidates": (i32, [vp, vp, vp, i32, vp, i32, i32, vp]),

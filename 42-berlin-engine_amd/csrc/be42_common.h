@@ -108,4 +108,53 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f)
     return (uint16_t)(u >> 16);
 }
 
+// simd_dot_f32_f32 (simd_kernels.h:162-191) of q0 and c with the reference's
+// reduction tree, computed by a lane pair (half = lane % 2): the eight
+// accumulator chains i = k (mod 8) run with FMA in order, chains 0-3 in half 0
+// and 4-7 in half 1 (one 16-byte load per lane per 8 elements); then
+// t_k = s_k + s_{k+4}, ((t0+t1)+(t2+t3)), and the compiled scalar tail (4
+// unfused products added in order when >= 4 remain, the rest fused).  hd is a
+// multiple of 8, so the tail is empty for every pool; it is kept for parity
+// with the reference routine.  The result is valid in half 0.
+__device__ __forceinline__ float dot_ref8x2(const float *q0, const float *c, int hd, int half)
+{
+    const int main = hd & ~7;
+    const float4 *c4 = (const float4 *)c;
+    const float4 *q4 = (const float4 *)q0;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < main / 8; j++) {
+        const float4 cv = c4[2 * j + half], qv = q4[2 * j + half];
+        s0 = __fmaf_rn(qv.x, cv.x, s0);
+        s1 = __fmaf_rn(qv.y, cv.y, s1);
+        s2 = __fmaf_rn(qv.z, cv.z, s2);
+        s3 = __fmaf_rn(qv.w, cv.w, s3);
+    }
+    const float t0 = s0 + __shfl_down(s0, 1, 2);
+    const float t1 = s1 + __shfl_down(s1, 1, 2);
+    const float t2 = s2 + __shfl_down(s2, 1, 2);
+    const float t3 = s3 + __shfl_down(s3, 1, 2);
+    float sum = (t0 + t1) + (t2 + t3);
+    if (half == 0) {
+        int i = main;
+        if (hd - i >= 4) {
+            for (int j = 0; j < 4; j++)
+                sum = sum + q0[i + j] * c[i + j];
+            i += 4;
+        }
+        for (; i < hd; i++)
+            sum = __fmaf_rn(q0[i], c[i], sum);
+    }
+    return sum;
+}
+
+// g_fp8_lut entry (ops_quant.c:27-48): E4M3, bias 7, no NaN (0x7F -> 480)
+__device__ __forceinline__ float fp8_to_f32(uint8_t c)
+{
+    const int e = (c >> 3) & 0xF, m = c & 7;
+    float v = (e == 0) ? (float)m * (1.0f / 512.0f)
+                       : __uint_as_float((uint32_t)(e + 120) << 23) * (1.0f + (float)m * 0.125f);
+    return (c & 0x80) ? -v : v;
+}
+
 }  // namespace be42

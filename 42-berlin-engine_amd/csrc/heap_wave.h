@@ -1,0 +1,87 @@
+// heap_wave.h -- the reference's bounded min-heap (src/compute/ops_heap.h:33-100,
+// heap_push with strict root replacement) run by one wave, heap slot i in lane i.
+//
+// A binary min-heap is non-decreasing along every root-to-leaf path, so a
+// sift-up (or a sift-down) moves exactly the path entries on one side of the
+// new score by one level.  Each push is therefore one parallel step over the
+// lanes of the path:
+//   sift-up from slot `size`: path lanes whose parent holds a score > s take
+//     the parent's entry; the shallowest path lane with score > s (or slot
+//     `size`) takes s;
+//   sift-down from the root along the min-child path (the smaller child, the
+//     left one on ties, as heap_sift_down picks it): path lanes whose chosen
+//     child holds a score < s take the child's entry; the deepest such
+//     position (or the root) takes s.
+// The array order after every push equals the reference's.  Scores must not
+// be NaN.
+#pragma once
+
+#include "be42_common.h"
+
+namespace be42 {
+
+constexpr int kHeapMax = 62;
+
+// 1-based heap position l1 lies on the path from the root to n1.
+__device__ __forceinline__ bool heap_on_path(int n1, int l1)
+{
+    const int sh = __clz(l1) - __clz(n1);
+    return sh >= 0 && (n1 >> sh) == l1;
+}
+
+struct WaveHeap {
+    float hs = 0.0f;   // score of slot `lane`
+    int hi = 0;        // payload (index) of slot `lane`
+    int size = 0;      // uniform
+    int cap;           // uniform, <= kHeapMax
+    int lane, par, cl, cr;
+
+    __device__ explicit WaveHeap(int capacity) : cap(capacity)
+    {
+        lane = threadIdx.x & 63;
+        par = lane > 0 ? (lane - 1) >> 1 : 0;
+        cl = (2 * lane + 1) & 63;
+        cr = (2 * lane + 2) & 63;
+    }
+
+    // heap_push(heap, &size, cap, s, e) with s, e uniform across the wave
+    __device__ __forceinline__ void push(float s, int e)
+    {
+        if (size < cap) {
+            const float pv = __shfl(hs, par, 64);
+            const int pi = __shfl(hi, par, 64);
+            if (heap_on_path(size + 1, lane + 1)) {
+                if (lane > 0 && pv > s) {
+                    hs = pv;
+                    hi = pi;
+                } else if (lane == size || hs > s) {
+                    hs = s;
+                    hi = e;
+                }
+            }
+            size++;
+        } else if (s > __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), 0))) {
+            const float hl = __shfl(hs, cl, 64), hr = __shfl(hs, cr, 64);
+            const int il = __shfl(hi, cl, 64), ir = __shfl(hi, cr, 64);
+            const bool hasl = 2 * lane + 1 < size;
+            const bool right = 2 * lane + 2 < size && hr < hl;
+            const unsigned long long mh = __ballot(hasl), mr = __ballot(right);
+            int end = 0;
+            while ((mh >> end) & 1ull)
+                end = 2 * end + 1 + (int)((mr >> end) & 1ull);
+            if (heap_on_path(end + 1, lane + 1)) {
+                const float cv = right ? hr : hl;
+                const int ci = right ? ir : il;
+                if (hasl && cv < s) {
+                    hs = cv;
+                    hi = ci;
+                } else if (lane == 0 || hs < s) {
+                    hs = s;
+                    hi = e;
+                }
+            }
+        }
+    }
+};
+
+}  // namespace be42

@@ -31,12 +31,13 @@
 #include <cmath>
 
 #include "be42_common.h"
+#include "heap_wave.h"
 
 namespace be42 {
 
 constexpr int kProbes = 17;
-constexpr int kMaxCand = 256;
-constexpr int kHeapMax = 62;
+constexpr int kMaxCand = 256;       // router candidate cap
+constexpr int kMaxCandList = 512;   // be42_lsh_candidates cap
 
 constexpr int kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
 
@@ -71,53 +72,6 @@ __device__ __forceinline__ int rl(int v, int lane) { return __builtin_amdgcn_rea
 __device__ __forceinline__ float rlf(float v, int lane)
 {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
-// simd_dot_f32_f32 (simd_kernels.h:162-191) of q0 and c with the reference's
-// reduction tree, computed by a lane pair (half = lane % 2): the eight
-// accumulator chains i = k (mod 8) run with FMA in order, chains 0-3 in half 0
-// and 4-7 in half 1 (one 16-byte load per lane per 8 elements); then
-// t_k = s_k + s_{k+4}, ((t0+t1)+(t2+t3)), and the compiled scalar tail (4
-// unfused products added in order when >= 4 remain, the rest fused).  hd is a
-// multiple of 8, so the tail is empty for every pool; it is kept for parity
-// with the reference routine.  The result is valid in half 0.
-__device__ __forceinline__ float dot_ref8x2(const float *q0, const float *c, int hd, int half)
-{
-    const int main = hd & ~7;
-    const float4 *c4 = (const float4 *)c;
-    const float4 *q4 = (const float4 *)q0;
-    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-#pragma unroll 8
-    for (int j = 0; j < main / 8; j++) {
-        const float4 cv = c4[2 * j + half], qv = q4[2 * j + half];
-        s0 = __fmaf_rn(qv.x, cv.x, s0);
-        s1 = __fmaf_rn(qv.y, cv.y, s1);
-        s2 = __fmaf_rn(qv.z, cv.z, s2);
-        s3 = __fmaf_rn(qv.w, cv.w, s3);
-    }
-    const float t0 = s0 + __shfl_down(s0, 1, 2);
-    const float t1 = s1 + __shfl_down(s1, 1, 2);
-    const float t2 = s2 + __shfl_down(s2, 1, 2);
-    const float t3 = s3 + __shfl_down(s3, 1, 2);
-    float sum = (t0 + t1) + (t2 + t3);
-    if (half == 0) {
-        int i = main;
-        if (hd - i >= 4) {
-            for (int j = 0; j < 4; j++)
-                sum = sum + q0[i + j] * c[i + j];
-            i += 4;
-        }
-        for (; i < hd; i++)
-            sum = __fmaf_rn(q0[i], c[i], sum);
-    }
-    return sum;
-}
-
-// 1-based heap position l1 lies on the path from the root to n1.
-__device__ __forceinline__ bool heap_on_path(int n1, int l1)
-{
-    const int sh = __clz(l1) - __clz(n1);
-    return sh >= 0 && (n1 >> sh) == l1;
 }
 
 template <bool STAGE>
@@ -312,11 +266,7 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     __syncthreads();
 
     // 5. selection: anchors, then the reference min-heap (capacity
-    //    min(k-2, #middle, 62), strict replacement) in wave 0, heap slot i in
-    //    lane i.  Values along any root-to-leaf path are non-decreasing, so a
-    //    sift-up or sift-down moves exactly the path entries on one side of s
-    //    by one level: each push is one parallel step over the path's lanes.
-    //    (Scores are finite: q and the centroids are finite.)
+    //    min(k-2, #middle, 62), strict replacement) run by wave 0
     if (wave != 0)
         return;
     const int first = pt[0], last = pt[n - 1];
@@ -332,55 +282,14 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     int ak = min(k_sel - 2, min(nm, kHeapMax));
     if (k_sel <= 2 || nm == 0)
         ak = 0;
-    float hs = 0.0f;
-    int hi = 0, size = 0;
-    const int par = lane > 0 ? (lane - 1) >> 1 : 0;
-    const int cl = (2 * lane + 1) & 63, cr = (2 * lane + 2) & 63;
+    WaveHeap heap(ak);
     for (int e0 = 0; e0 < nm && ak > 0; e0 += kWave) {
         const float sv = e0 + lane < nm ? sc[e0 + lane] : 0.0f;
         const int ecnt = min(kWave, nm - e0);
-        for (int u = 0; u < ecnt; u++) {
-            const int e = e0 + u;
-            const float s = rlf(sv, u);
-            if (size < ak) {
-                // sift-up from slot `size`: path entries > s move down one level
-                const float pv = __shfl(hs, par, kWave);
-                const int pi = __shfl(hi, par, kWave);
-                if (heap_on_path(size + 1, lane + 1)) {
-                    if (lane > 0 && pv > s) {
-                        hs = pv;
-                        hi = pi;
-                    } else if (lane == size || hs > s) {
-                        hs = s;
-                        hi = e;
-                    }
-                }
-                size++;
-            } else if (s > rlf(hs, 0)) {
-                // sift-down from the root along the min-child path (left on
-                // ties): path entries < s move up one level
-                const float hl = __shfl(hs, cl, kWave), hr = __shfl(hs, cr, kWave);
-                const int il = __shfl(hi, cl, kWave), ir = __shfl(hi, cr, kWave);
-                const bool hasl = 2 * lane + 1 < size;
-                const bool right = 2 * lane + 2 < size && hr < hl;
-                const unsigned long long mh = __ballot(hasl), mr = __ballot(right);
-                int end = 0;
-                while ((mh >> end) & 1ull)
-                    end = 2 * end + 1 + (int)((mr >> end) & 1ull);
-                if (heap_on_path(end + 1, lane + 1)) {
-                    const float cv = right ? hr : hl;
-                    const int ci = right ? ir : il;
-                    if (hasl && cv < s) {
-                        hs = cv;
-                        hi = ci;
-                    } else if (lane == 0 || hs < s) {
-                        hs = s;
-                        hi = e;
-                    }
-                }
-            }
-        }
+        for (int u = 0; u < ecnt; u++)
+            heap.push(rlf(sv, u), e0 + u);
     }
+    const int size = heap.size, hi = heap.hi;
     if (lane < size)
         selb[ns + lane] = pt[mid[hi]];
     if (lane == 0)
@@ -515,7 +424,7 @@ extern "C" int be42_lsh_candidates(int *ids, int *n_out, const uint16_t *hashes,
                                    int n_q, int cap, void *stream)
 {
     BE42_CHECK(ids && n_out && hashes && qh, "be42_lsh_candidates: null pointer");
-    BE42_CHECK(n_ids >= 0 && n_q >= 0 && cap > 0 && cap <= kMaxCand, "be42_lsh_candidates: bad sizes (cap %d)",
+    BE42_CHECK(n_ids >= 0 && n_q >= 0 && cap > 0 && cap <= kMaxCandList, "be42_lsh_candidates: bad sizes (cap %d)",
                cap);
     if (n_q == 0)
         return BE42_OK;

@@ -388,3 +388,39 @@ extern "C" int be42_kv_layer_pages(const be42_kv_pool *pool, int layer, int *phy
             phys_out[i] = p->page_table[layer * pool->max_logical + i];
     return n;
 }
+
+// block_alloc / block_free (paged.c:159-187) on the pool's own free stack.
+extern "C" int be42_kv_page_alloc(be42_kv_pool *pool)
+{
+    BE42_CHECK(pool, "be42_kv_page_alloc: null pool");
+    const int phys = pool_alloc(impl(pool));
+    if (phys < 0)
+        set_error("be42_kv_page_alloc: page pool exhausted");
+    return phys;
+}
+
+extern "C" int be42_kv_page_free(be42_kv_pool *pool, int phys)
+{
+    BE42_CHECK(pool, "be42_kv_page_free: null pool");
+    PoolImpl *p = impl(pool);
+    if (phys < 0 || phys >= pool->capacity)
+        return BE42_OK;    // ignored, as block_free does
+    p->free_stack[++p->free_top] = phys;
+    return BE42_OK;
+}
+
+extern "C" int be42_kv_export(const be42_kv_pool *pool, int *page_table, int *free_stack, int *free_top,
+                              int *logical_len)
+{
+    BE42_CHECK(pool, "be42_kv_export: null pool");
+    const PoolImpl *p = reinterpret_cast<const PoolImpl *>(pool);
+    if (page_table)
+        memcpy(page_table, p->page_table.data(), p->page_table.size() * sizeof(int));
+    if (free_stack)
+        memcpy(free_stack, p->free_stack.data(), p->free_stack.size() * sizeof(int));
+    if (free_top)
+        *free_top = p->free_top;
+    if (logical_len)
+        memcpy(logical_len, p->logical_len.data(), p->logical_len.size() * sizeof(int));
+    return BE42_OK;
+}

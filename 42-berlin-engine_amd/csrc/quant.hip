@@ -42,13 +42,6 @@ __device__ __forceinline__ uint8_t f32_to_fp8(float v)
     return (uint8_t)(sign | ((uint32_t)e << 3) | (uint32_t)m);
 }
 
-__device__ __forceinline__ float fp8_to_f32(uint8_t c)
-{
-    const int e = (c >> 3) & 0xF, m = c & 7;
-    float v = (e == 0) ? (float)m * (1.0f / 512.0f)
-                       : __uint_as_float((uint32_t)(e + 120) << 23) * (1.0f + (float)m * 0.125f);
-    return (c & 0x80) ? -v : v;
-}
 
 // block-wide absmax of one row (256 threads)
 __device__ __forceinline__ float row_absmax(const float *x, int cols, float *red)

@@ -133,6 +133,16 @@ int  be42_kv_reset(be42_kv_pool *pool, int layer, void *stream);
 /* host copy of a layer's page table; returns the number of logical pages */
 int  be42_kv_layer_pages(const be42_kv_pool *pool, int layer, int *phys_out, int max_out);
 
+/* Host bookkeeping of the pool: block_alloc / block_free (paged.c:159-187) on
+ * the pool's free stack (page_free ignores ids outside [0, capacity), as
+ * block_free does), and a copy of the host page table
+ * [n_layers * max_logical], free stack [capacity], its top and the logical
+ * lengths [n_layers] (any output may be NULL). */
+int  be42_kv_page_alloc(be42_kv_pool *pool);
+int  be42_kv_page_free(be42_kv_pool *pool, int phys);
+int  be42_kv_export(const be42_kv_pool *pool, int *page_table, int *free_stack, int *free_top,
+                    int *logical_len);
+
 /* ---- LSH routing ------------------------------------------------------------------ */
 /* lsh_init (src/compute/ops_lsh.c:22-85) on the host: hp [16][dim] and its
  * transpose hpT [dim][16] (hpT may be NULL). */

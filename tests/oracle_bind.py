@@ -33,6 +33,9 @@ def _sig(lib, name, res, *args):
     return fn
 
 
+BLOCK_SCORE = np.dtype([("block_idx", np.int32), ("phys_idx", np.int32), ("score", np.float32)])
+
+
 class OrLshIndex(C.Structure):
     _fields_ = [("cap", C.c_int), ("n_blocks", C.c_int), ("hash", C.POINTER(C.c_uint16)),
                 ("start", C.POINTER(C.c_int)), ("len", C.POINTER(C.c_int)),
@@ -95,8 +98,26 @@ class Oracle:
         _sig(L, "or_route_pages", C.c_int, i32p, C.POINTER(C.c_int), i32p, C.POINTER(OrPaged), C.c_int,
              f32p, C.c_int, f32p, C.POINTER(OrLshIndex), C.c_int, C.c_int)
         _sig(L, "or_q_mean", None, f32p, f32p, C.c_int, C.c_int)
+        _sig(L, "or_paged_alloc", C.c_int, C.POINTER(OrPaged))
+        _sig(L, "or_paged_release", None, C.POINTER(OrPaged), C.c_int)
+        _sig(L, "or_score_blocks", None, C.c_void_p, f32p, C.POINTER(OrPaged), C.c_int, C.c_int)
+        _sig(L, "or_select_top_k_blocks", C.c_int, i32p, C.c_void_p, C.c_int, C.c_int)
 
     # -- scalar helpers -----------------------------------------------------
+    def gemv_bf16(self, wb, x, threads=0):
+        n, k = wb.shape
+        y = np.zeros(n, np.float32)
+        self.lib.or_gemv_bf16(y, np.ascontiguousarray(wb, np.uint16), np.ascontiguousarray(x, np.float32).ravel(),
+                              n, k, threads)
+        return y
+
+    def select_top_k(self, scores, k):
+        """select_top_k_blocks over a BLOCK_SCORE structured array."""
+        scores = np.ascontiguousarray(scores, BLOCK_SCORE)
+        sel = np.zeros(max(k, 2) + 2, np.int32)
+        n = self.lib.or_select_top_k_blocks(sel, scores.ctypes.data, len(scores), k)
+        return sel[:n].copy()
+
     def fast_expf(self, x):
         return np.array([self.lib.or_fast_expf(float(v)) for v in np.ravel(x)], np.float32)
 
@@ -218,6 +239,21 @@ class OraclePaged:
 
     def n_blocks(self, layer):
         return self.p.logical_len[layer]
+
+    def alloc(self):
+        return self.o.lib.or_paged_alloc(C.byref(self.p))
+
+    def free(self, phys):
+        self.o.lib.or_paged_release(C.byref(self.p), phys)
+
+    def free_top(self):
+        return self.p.free_top
+
+    def score_blocks(self, layer, q, n_blocks):
+        out = np.zeros(n_blocks, BLOCK_SCORE)
+        self.o.lib.or_score_blocks(out.ctypes.data, np.ascontiguousarray(q, np.float32).ravel(), C.byref(self.p),
+                                   layer, n_blocks)
+        return out
 
     def phys(self, layer, logical):
         return self.p.page_table[layer * self.p.max_logical + logical]

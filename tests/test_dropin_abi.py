@@ -1,0 +1,48 @@
+"""The drop-in ABI (include/be42_engine.h) without a GPU: struct layouts are
+the reference's (paged.h, ops_lsh.h, tensor.h) field for field, the ctypes
+mirror used by the GPU tests agrees with the C compiler, and the library
+exports every declared function and the g_fp8_lut table."""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+import dropin_bind as D
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PROBE = os.path.join(ROOT, "tests", "layout_probe.c")
+REF_SRC = "/root/reference/src"
+
+
+def _probe(tmp_path, extra):
+    exe = tmp_path / ("probe_ref" if "-DUSE_REF" in extra else "probe")
+    subprocess.run(["gcc", "-O0", "-o", str(exe), PROBE] + extra, check=True, capture_output=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    return dict(line.rsplit(" ", 1) for line in out.splitlines() if not line.startswith("DTYPE")), out
+
+
+def test_layouts_match_ctypes_mirror(tmp_path):
+    lay, _ = _probe(tmp_path, ["-I", os.path.join(ROOT, "include")])
+    mirror = {"t_lsh_ctx": D.LshCtx, "t_block_acc": D.BlockAcc, "t_lsh_index": D.LshIndex, "t_kv_block": D.KvBlock,
+              "t_block_manager": D.BlockManager, "t_paged_kv_cache": D.PagedKv, "t_block_score": D.BlockScore,
+              "t_tensor": D.Tensor}
+    for key, val in lay.items():
+        if "." in key:
+            t, f = key.split(".")
+            assert getattr(mirror[t], f).offset == int(val), key
+        else:
+            assert ctypes.sizeof(mirror[key]) == int(val), key
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_SRC), reason="reference sources not present")
+def test_layouts_match_reference_headers(tmp_path):
+    _, mine = _probe(tmp_path, ["-I", os.path.join(ROOT, "include")])
+    _, ref = _probe(tmp_path, ["-DUSE_REF", "-I", REF_SRC])
+    assert mine == ref
+
+
+def test_library_exports_lut_table():
+    lib = ctypes.CDLL(os.path.join(ROOT, "42-berlin-engine_amd", "lib42be_hip.so"))
+    assert ctypes.c_float.in_dll(lib, "g_fp8_lut") is not None
+    D.bind(lib)
