@@ -41,12 +41,18 @@ SIGNATURES = {
     "be42_gemv_fp8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+    "be42_decoder_create": (i32, [vp, vp, vp, vp]),
+    "be42_decoder_destroy": (None, [vp]),
+    "be42_decoder_pool": (vp, [vp]),
+    "be42_decoder_step": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "be42_decoder_next_tokens": (i32, [vp, vp]),
     "be42_kv_create": (i32, [vp, i32, i32, i32, i32, i32, vp]),
     "be42_kv_destroy": (None, [vp]),
     "be42_kv_set_projection": (i32, [vp, vp]),
     "be42_kv_append": (i32, [vp, i32, vp, vp, i32, i32, vp]),
     "be42_kv_reset": (i32, [vp, i32, vp]),
     "be42_kv_layer_pages": (i32, [vp, i32, vp, i32]),
+    "be42_kv_append_step": (i32, [vp, vp, vp, i32, vp, vp, vp]),
     "be42_kv_page_alloc": (i32, [vp]),
     "be42_kv_page_free": (i32, [vp, i32]),
     "be42_kv_export": (i32, [vp, vp, vp, vp, vp]),
@@ -59,6 +65,22 @@ SIGNATURES = {
 }
 
 KV_INT8, KV_BF16 = 0, 1
+
+
+class DecoderConfig(C.Structure):
+    """Layout of be42_decoder_config (include/be42_hip.h)."""
+    _fields_ = [(n, C.c_int) for n in ("n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "hidden_dim", "vocab",
+                                       "max_seq", "max_batch", "wkind", "kv_kind", "sparse_k", "cand_cap",
+                                       "rope_len")] + [("rope_theta", C.c_float), ("norm_eps", C.c_float)]
+
+
+class DecoderLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "sq", "sk", "sv", "so", "s1",
+                                          "s2", "s3", "attn_norm", "ffn_norm")]
+
+
+class DecoderWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("emb", "emb_s", "final_norm", "out", "out_s", "layers")]
 
 
 class KVPoolStruct(C.Structure):
@@ -246,14 +268,18 @@ class Lib:
 class KVPool:
     """Owner of a be42_kv_pool (device page pool + host page allocator)."""
 
-    def __init__(self, lib, kind, n_layers, n_kv, head_dim, max_logical, hpT=None):
+    def __init__(self, lib, kind, n_layers, n_kv, head_dim, max_logical, hpT=None, handle=None):
         import numpy as np
         self.lib = lib
         lib.init()
-        h = C.c_void_p()
-        hp = None if hpT is None else np.ascontiguousarray(hpT, np.float32)
-        lib.check(lib.lib.be42_kv_create(C.byref(h), kind, n_layers, n_kv, head_dim, max_logical,
-                                         None if hp is None else hp.ctypes.data), "be42_kv_create")
+        self.owned = handle is None
+        if handle is None:
+            h = C.c_void_p()
+            hp = None if hpT is None else np.ascontiguousarray(hpT, np.float32)
+            lib.check(lib.lib.be42_kv_create(C.byref(h), kind, n_layers, n_kv, head_dim, max_logical,
+                                             None if hp is None else hp.ctypes.data), "be42_kv_create")
+        else:
+            h = handle
         self.handle = h
         self.s = C.cast(h, C.POINTER(KVPoolStruct)).contents
         self.kind, self.n_layers, self.n_kv, self.head_dim = kind, n_layers, n_kv, head_dim
@@ -283,10 +309,10 @@ class KVPool:
         return arr
 
     def close(self):
-        if self.handle:
+        if self.handle and self.owned:
             self.lib.torch.cuda.synchronize()
             self.lib.lib.be42_kv_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:
@@ -297,6 +323,53 @@ class KVPool:
 
 _LIB = None
 
+
+
+class Decoder:
+    """A decode-step engine over device weights (dict of torch tensors, see
+    be42_decoder_weights): cfg is a dict of be42_decoder_config fields."""
+
+    def __init__(self, lib, cfg, w, hpT):
+        import numpy as np
+        self.lib = lib
+        self.cfg = cfg
+        self.w = w                      # keeps the device tensors alive
+        self.c = DecoderConfig(**cfg)
+        self.layers = (DecoderLayer * cfg["n_layers"])()
+        for i, L in enumerate(w["layers"]):
+            for k in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "sq", "sk", "sv", "so", "s1", "s2", "s3",
+                      "attn_norm", "ffn_norm"):
+                setattr(self.layers[i], k, L[k].data_ptr())
+        self.weights = DecoderWeights(w["emb"].data_ptr(), w["emb_s"].data_ptr(), w["final_norm"].data_ptr(),
+                                      w["out"].data_ptr(), w["out_s"].data_ptr(), C.cast(self.layers, C.c_void_p))
+        self.handle = C.c_void_p()
+        hpT = np.ascontiguousarray(hpT, np.float32)
+        lib._call("be42_decoder_create", C.byref(self.handle), C.byref(self.c), C.byref(self.weights),
+                  hpT.ctypes.data)
+        self.pool = KVPool(lib, cfg["kv_kind"], cfg["n_layers"] * cfg["max_batch"], cfg["n_kv_heads"],
+                           cfg["head_dim"], (cfg["max_seq"] + 15) // 16,
+                           handle=C.c_void_p(lib.lib.be42_decoder_pool(self.handle)))
+
+    def step(self, tokens, pos, logits=None, sync=True):
+        import numpy as np
+        t = np.ascontiguousarray(tokens, np.int32)
+        nxt = np.zeros(len(t), np.int32)
+        self.lib._call("be42_decoder_step", self.handle, t.ctypes.data, len(t), int(pos),
+                       nxt.ctypes.data if sync else None, self.lib.p(logits), self.lib.stream())
+        return nxt
+
+    def close(self):
+        if self.handle:
+            self.lib.torch.cuda.synchronize()
+            self.pool.close()
+            self.lib.lib.be42_decoder_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 def load():
     """The process-wide library handle (raises if the .so is not built)."""

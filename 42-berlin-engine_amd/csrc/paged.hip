@@ -58,29 +58,16 @@ struct PoolImpl {
 
 static PoolImpl *impl(be42_kv_pool *p) { return reinterpret_cast<PoolImpl *>(p); }
 
-// One wave per (token, kv head): quantize (INT8) or round (BF16) the K and V
-// rows of that head into the page slot.  INT8 follows quant_f32_to_int8:
-// exact absmax, IEEE scale = amax/127 and inv = 127/amax, roundf, clamp.
+// Quantize (INT8) or round (BF16) one K row and one V row of a kv head into
+// page slot `slot` (= (phys * n_kv + head) * 16 + offset), one wave.  INT8
+// follows quant_f32_to_int8: exact absmax, IEEE scale = amax/127 and
+// inv = 127/amax, roundf, clamp.
 template <bool BF16>
-__global__ __launch_bounds__(64) void k_kv_append(void *__restrict__ kdst, void *__restrict__ vdst,
-                                                  float *__restrict__ kscale, float *__restrict__ vscale,
-                                                  int *__restrict__ ntok, int *__restrict__ page_table,
-                                                  int *__restrict__ n_logical, const AppendArgs a,
-                                                  const float *__restrict__ k, const float *__restrict__ v,
-                                                  int n_kv, int hd)
+__device__ __forceinline__ void store_kv_row(void *__restrict__ kdst, void *__restrict__ vdst,
+                                             float *__restrict__ kscale, float *__restrict__ vscale, size_t slot,
+                                             const float *__restrict__ ks, const float *__restrict__ vs, int hd,
+                                             int lane)
 {
-    const int tok = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-    const int pos = a.pos0 + tok, off = pos % kPage;
-    const int phys = a.tok_phys[tok];
-    if (tok == 0 && h == 0) {
-        if (lane < a.n_new)
-            page_table[a.layer_base + a.new_first + lane] = a.new_phys[lane];
-        if (lane == 0)
-            n_logical[a.layer] = a.n_logical;
-    }
-    const size_t slot = ((size_t)phys * n_kv + h) * kPage + off;
-    const float *ks = k + (size_t)tok * n_kv * hd + (size_t)h * hd;
-    const float *vs = v + (size_t)tok * n_kv * hd + (size_t)h * hd;
     if constexpr (BF16) {
         uint16_t *kd = (uint16_t *)kdst + slot * hd, *vd = (uint16_t *)vdst + slot * hd;
         for (int d = lane; d < hd; d += kWave) {
@@ -115,25 +102,75 @@ __global__ __launch_bounds__(64) void k_kv_append(void *__restrict__ kdst, void 
             vscale[slot] = vsc;
         }
     }
+}
+
+// One wave per (token, kv head) of a run of consecutive positions of one
+// layer.
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_kv_append(void *__restrict__ kdst, void *__restrict__ vdst,
+                                                  float *__restrict__ kscale, float *__restrict__ vscale,
+                                                  int *__restrict__ ntok, int *__restrict__ page_table,
+                                                  int *__restrict__ n_logical, const AppendArgs a,
+                                                  const float *__restrict__ k, const float *__restrict__ v,
+                                                  int n_kv, int hd)
+{
+    const int tok = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int pos = a.pos0 + tok, off = pos % kPage;
+    const int phys = a.tok_phys[tok];
+    if (tok == 0 && h == 0) {
+        if (lane < a.n_new)
+            page_table[a.layer_base + a.new_first + lane] = a.new_phys[lane];
+        if (lane == 0)
+            n_logical[a.layer] = a.n_logical;
+    }
+    const size_t slot = ((size_t)phys * n_kv + h) * kPage + off;
+    store_kv_row<BF16>(kdst, vdst, kscale, vscale, slot, k + (size_t)tok * n_kv * hd + (size_t)h * hd,
+                       v + (size_t)tok * n_kv * hd + (size_t)h * hd, hd, lane);
     // the page's last token in this append publishes the count (blocks of
     // one page run concurrently)
     if (h == 0 && lane == 0 && (off == kPage - 1 || tok == a.n_tok - 1))
         ntok[phys] = off + 1;
 }
 
+// One token for each of n layer slots (a decode step of a batch): the same
+// store, with per-token slot, position and page bookkeeping.
+struct AppendStepArgs {
+    int n, max_logical;
+    int pos[kArgTok], phys[kArgTok], slot[kArgTok], publish[kArgTok];
+    int n_seal;
+    int seal_phys[kArgTok], seal_slot[kArgTok], seal_logical[kArgTok], seal_nidx[kArgTok];
+};
+
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_kv_append_step(void *__restrict__ kdst, void *__restrict__ vdst,
+                                                       float *__restrict__ kscale, float *__restrict__ vscale,
+                                                       int *__restrict__ ntok, int *__restrict__ page_table,
+                                                       int *__restrict__ n_logical, const AppendStepArgs a,
+                                                       const float *__restrict__ k, const float *__restrict__ v,
+                                                       int n_kv, int hd)
+{
+    const int tok = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int pos = a.pos[tok], off = pos % kPage, blk = pos / kPage, phys = a.phys[tok];
+    if (h == 0 && lane == 0) {
+        if (a.publish[tok]) {
+            page_table[(size_t)a.slot[tok] * a.max_logical + blk] = phys;
+            n_logical[a.slot[tok]] = blk + 1;
+        }
+        ntok[phys] = off + 1;
+    }
+    const size_t slot = ((size_t)phys * n_kv + h) * kPage + off;
+    store_kv_row<BF16>(kdst, vdst, kscale, vscale, slot, k + (size_t)tok * n_kv * hd + (size_t)h * hd,
+                       v + (size_t)tok * n_kv * hd + (size_t)h * hd, hd, lane);
+}
+
 // One block per page that became full: centroid of the head-0 keys (per
 // dimension, tokens summed in order, then * (1.0f/16)), then its hash: 16
 // lanes each run the FMA chain over d ascending from +0 (bit h = sum > 0).
 template <bool BF16>
-__global__ __launch_bounds__(256) void k_kv_seal(const void *__restrict__ kpool, const float *__restrict__ kscale,
-                                                 float *__restrict__ centroid, uint16_t *__restrict__ page_hash,
-                                                 int *__restrict__ n_indexed, const AppendArgs a,
-                                                 const float *__restrict__ hpT, int n_kv, int hd)
+__device__ __forceinline__ void seal_page(const void *__restrict__ kpool, const float *__restrict__ kscale,
+                                          float *__restrict__ centroid, uint16_t *__restrict__ hash_out, int phys,
+                                          const float *__restrict__ hpT, int n_kv, int hd, float *c)
 {
-    __shared__ float c[256];
-    const int phys = a.seal_phys[blockIdx.x];
-    if (blockIdx.x == 0 && threadIdx.x == 0)
-        n_indexed[a.layer] = a.n_indexed;
     const size_t head0 = (size_t)phys * n_kv * kPage;      // slot of (phys, head 0, token 0)
     const int d = threadIdx.x;
     if (d < hd) {
@@ -159,8 +196,35 @@ __global__ __launch_bounds__(256) void k_kv_seal(const void *__restrict__ kpool,
                 s = __fmaf_rn(c[i], hpT[i * 16 + h], s);
         const unsigned long long m = __ballot(h < 16 && s > 0.0f);
         if (h == 0)
-            page_hash[a.layer_base + a.seal_logical[blockIdx.x]] = (uint16_t)(m & 0xFFFFu);
+            *hash_out = (uint16_t)(m & 0xFFFFu);
     }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_kv_seal(const void *__restrict__ kpool, const float *__restrict__ kscale,
+                                                 float *__restrict__ centroid, uint16_t *__restrict__ page_hash,
+                                                 int *__restrict__ n_indexed, const AppendArgs a,
+                                                 const float *__restrict__ hpT, int n_kv, int hd)
+{
+    __shared__ float c[256];
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        n_indexed[a.layer] = a.n_indexed;
+    seal_page<BF16>(kpool, kscale, centroid, page_hash + a.layer_base + a.seal_logical[blockIdx.x],
+                    a.seal_phys[blockIdx.x], hpT, n_kv, hd, c);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_kv_seal_step(const void *__restrict__ kpool, const float *__restrict__ kscale,
+                                                      float *__restrict__ centroid, uint16_t *__restrict__ page_hash,
+                                                      int *__restrict__ n_indexed, const AppendStepArgs a,
+                                                      const float *__restrict__ hpT, int n_kv, int hd)
+{
+    __shared__ float c[256];
+    const int i = blockIdx.x, slot = a.seal_slot[i];
+    if (threadIdx.x == 0)
+        n_indexed[slot] = a.seal_nidx[i];
+    seal_page<BF16>(kpool, kscale, centroid, page_hash + (size_t)slot * a.max_logical + a.seal_logical[i],
+                    a.seal_phys[i], hpT, n_kv, hd, c);
 }
 
 }  // namespace be42
@@ -422,5 +486,76 @@ extern "C" int be42_kv_export(const be42_kv_pool *pool, int *page_table, int *fr
         *free_top = p->free_top;
     if (logical_len)
         memcpy(logical_len, p->logical_len.data(), p->logical_len.size() * sizeof(int));
+    return BE42_OK;
+}
+
+// One decode token for each of n layer slots (paged.c:195-272 per slot).
+extern "C" int be42_kv_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, const float *k,
+                                   const float *v, void *stream)
+{
+    BE42_CHECK(pool && slots && pos && k && v, "be42_kv_append_step: null pointer");
+    BE42_CHECK(n >= 0 && n <= kArgTok, "be42_kv_append_step: %d slots (at most %d)", n, kArgTok);
+    if (n == 0)
+        return BE42_OK;
+    PoolImpl *p = impl(pool);
+    be42_kv_pool &P = p->pub;
+    AppendStepArgs a;
+    memset(&a, 0, sizeof a);
+    a.n = n;
+    a.max_logical = P.max_logical;
+    for (int t = 0; t < n; t++) {
+        const int s = slots[t], ps = pos[t];
+        BE42_CHECK(s >= 0 && s < P.n_layers, "be42_kv_append_step: slot %d out of range", s);
+        BE42_CHECK(ps >= 0 && ps / kPage < P.max_logical, "be42_kv_append_step: position %d out of range", ps);
+        for (int u = 0; u < t; u++)
+            BE42_CHECK(slots[u] != s, "be42_kv_append_step: slot %d given twice", s);
+        const int blk = ps / kPage, base = s * P.max_logical;
+        if (blk >= p->logical_len[s]) {
+            if (blk != p->logical_len[s]) {
+                set_error("be42_kv_append_step: position %d skips page %d", ps, p->logical_len[s]);
+                return BE42_EINVAL;
+            }
+            const int phys = pool_alloc(p);
+            if (phys < 0) {
+                set_error("be42_kv_append_step: page pool exhausted at pos %d", ps);
+                return BE42_ENOMEM;
+            }
+            p->page_table[base + blk] = phys;
+            p->logical_len[s] = blk + 1;
+            a.publish[t] = 1;
+        }
+        const int phys = p->page_table[base + blk];
+        a.pos[t] = ps;
+        a.phys[t] = phys;
+        a.slot[t] = s;
+        if (ps % kPage == kPage - 1 && !p->registered[phys]) {
+            p->registered[phys] = 1;
+            if (blk + 1 > p->n_indexed[s])
+                p->n_indexed[s] = blk + 1;
+            a.seal_phys[a.n_seal] = phys;
+            a.seal_slot[a.n_seal] = s;
+            a.seal_logical[a.n_seal] = blk;
+            a.seal_nidx[a.n_seal] = p->n_indexed[s];
+            a.n_seal++;
+        }
+    }
+    hipStream_t st = as_stream(stream);
+    const dim3 grid(n, P.n_kv);
+    if (P.kind == BE42_KV_BF16)
+        hipLaunchKernelGGL(k_kv_append_step<true>, grid, dim3(64), 0, st, P.k, P.v, P.k_scale, P.v_scale, P.ntok,
+                           P.page_table, P.n_logical, a, k, v, P.n_kv, P.head_dim);
+    else
+        hipLaunchKernelGGL(k_kv_append_step<false>, grid, dim3(64), 0, st, P.k, P.v, P.k_scale, P.v_scale, P.ntok,
+                           P.page_table, P.n_logical, a, k, v, P.n_kv, P.head_dim);
+    BE42_LAUNCH_CHECK();
+    if (a.n_seal) {
+        if (P.kind == BE42_KV_BF16)
+            hipLaunchKernelGGL(k_kv_seal_step<true>, dim3(a.n_seal), dim3(256), 0, st, P.k, P.k_scale, P.centroid,
+                               P.page_hash, P.n_indexed, a, P.hpT, P.n_kv, P.head_dim);
+        else
+            hipLaunchKernelGGL(k_kv_seal_step<false>, dim3(a.n_seal), dim3(256), 0, st, P.k, P.k_scale,
+                               P.centroid, P.page_hash, P.n_indexed, a, P.hpT, P.n_kv, P.head_dim);
+        BE42_LAUNCH_CHECK();
+    }
     return BE42_OK;
 }

@@ -138,6 +138,10 @@ int  be42_kv_layer_pages(const be42_kv_pool *pool, int layer, int *phys_out, int
  * block_free does), and a copy of the host page table
  * [n_layers * max_logical], free stack [capacity], its top and the logical
  * lengths [n_layers] (any output may be NULL). */
+/* One token for each of n (<= 64) distinct layer slots, K and V device rows
+ * [n][n_kv * head_dim]: the per-step append of a decode batch in one launch. */
+int  be42_kv_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, const float *k,
+                         const float *v, void *stream);
 int  be42_kv_page_alloc(be42_kv_pool *pool);
 int  be42_kv_page_free(be42_kv_pool *pool, int phys);
 int  be42_kv_export(const be42_kv_pool *pool, int *page_table, int *free_stack, int *free_top,
@@ -179,6 +183,56 @@ size_t be42_attn_workspace_bytes(int n_queries, int n_heads, int head_dim, int m
 int  be42_paged_attention(const be42_kv_pool *pool, const float *q, int n_queries, int n_heads,
                           const int *sel, const int *n_sel, int sel_stride, int max_sel, float scale,
                           float *out, int n_split, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- decode step ------------------------------------------------------------------
+ * transformer_forward (src/inference/inference.c:60-696) on the paged path for a
+ * batch of independent sequences at one position: embedding (row-scaled codes),
+ * then per layer RMSNorm (ops_norm.c:126) -> q/k/v GEMV -> RoPE
+ * (ops_rope.c:192) -> paged append -> attention (dense over all pages while a
+ * layer has <= sparse_k pages, inference.c:447-494; else the LSH route and sparse
+ * attention) -> o GEMV -> residual -> RMSNorm -> gate/up GEMV -> SiLU*up
+ * (ops_activation.c:48) -> down GEMV -> residual; final RMSNorm, lm_head GEMV and
+ * argmax (sampler.c:42).  Weights are device arrays owned by the caller: codes
+ * [rows][cols] (INT8 or E4M3) with per-row fp32 scales, bf16 norm weights.  The
+ * KV pool has n_layers * max_batch slots: slot = layer * max_batch + b. */
+typedef struct be42_decoder_config {
+    int n_layers, dim, n_heads, n_kv_heads, head_dim, hidden_dim, vocab, max_seq, max_batch;
+    int wkind;      /* 0: INT8 codes, 1: FP8 E4M3 codes */
+    int kv_kind;    /* BE42_KV_INT8 / BE42_KV_BF16 */
+    int sparse_k;   /* pages attended per token once a layer has more */
+    int cand_cap;   /* LSH candidate cap of the router (<= 256) */
+    int rope_len;   /* RoPE table positions (0: max_seq); later positions are not rotated */
+    float rope_theta, norm_eps;
+} be42_decoder_config;
+
+typedef struct be42_decoder_layer {
+    const void *wq, *wk, *wv, *wo, *w1, *w2, *w3;   /* [out][in] codes */
+    const float *sq, *sk, *sv, *so, *s1, *s2, *s3; /* [out] scales */
+    const uint16_t *attn_norm, *ffn_norm;          /* [dim] bf16 */
+} be42_decoder_layer;
+
+typedef struct be42_decoder_weights {
+    const void *emb;             /* [vocab][dim] codes */
+    const float *emb_s;          /* [vocab] */
+    const uint16_t *final_norm;  /* [dim] bf16 */
+    const void *out;             /* [vocab][dim] codes */
+    const float *out_s;          /* [vocab] */
+    const be42_decoder_layer *layers;  /* [n_layers], copied at create */
+} be42_decoder_weights;
+
+typedef struct be42_decoder be42_decoder;
+
+int  be42_decoder_create(be42_decoder **out, const be42_decoder_config *cfg, const be42_decoder_weights *w,
+                         const float *hpT_host);
+void be42_decoder_destroy(be42_decoder *d);
+be42_kv_pool *be42_decoder_pool(be42_decoder *d);
+/* One token for each of `batch` sequences at position pos: tokens and
+ * next_tokens are host arrays (next_tokens may be NULL: the argmax stays on
+ * the device, be42_decoder_next_tokens); logits_out (device, [batch][vocab])
+ * may be NULL. */
+int  be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
+                       float *logits_out, void *stream);
+int  be42_decoder_next_tokens(be42_decoder *d, const int **dev_ptr);
 
 #ifdef __cplusplus
 }

@@ -878,3 +878,267 @@ int or_route_pages(int *selected, int *n_cand_out, int *cand_out,
     free(cand);
     return ns;
 }
+
+/* ======================================================================== */
+/* decode-step adjacents and the decoder loop                               */
+/* ======================================================================== */
+
+/* op_rmsnorm, ops_norm.c:27-124: sum of squares in 8 FMA lanes (lane l over
+ * i = l (mod 8)), hsum tree, fused scalar remainder; ss / dim;
+ * inv = 1 / sqrtf(ss + eps); out = (x * inv) * bf16(w). */
+void or_rmsnorm(float *out, const float *x, const uint16_t *w, int dim, float eps)
+{
+    float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int j = 0;
+    for (; j + 7 < dim; j += 8)
+        for (int l = 0; l < 8; l++)
+            lane[l] = fmaf(x[j + l], x[j + l], lane[l]);
+    float ss = hsum8(lane);
+    for (; j < dim; j++)
+        ss = fmaf(x[j], x[j], ss);
+    ss = ss / (float)dim;
+    const float inv = 1.0f / sqrtf(ss + eps);
+    for (int i = 0; i < dim; i++)
+        out[i] = (x[i] * inv) * or_bf16_to_f32(w[i]);
+}
+
+/* rope_cache_init, ops_rope.c:30-95 (libm): inv_freq[i] = 1 / powf(theta,
+ * (2i) / hd); angle = (float)p * inv_freq[i]; tables [pos][hd/2]. */
+void or_rope_table(float *cos_t, float *sin_t, int hd, int n_pos, float theta)
+{
+    int half = hd / 2;
+    float *inv = malloc(sizeof(float) * (size_t)half);
+    for (int i = 0; i < half; i++)
+        inv[i] = 1.0f / powf(theta, (float)(i * 2) / (float)hd);
+    for (int p = 0; p < n_pos; p++)
+        for (int i = 0; i < half; i++) {
+            float a = (float)p * inv[i];
+            cos_t[(size_t)p * half + i] = cosf(a);
+            sin_t[(size_t)p * half + i] = sinf(a);
+        }
+    free(inv);
+}
+
+/* rope_apply_multihead_cached, ops_rope.c:192-228, as the compiled loop
+ * evaluates it: x0' = fma(x0, c, -(x1 * s)), x1' = fma(x0, s, x1 * c);
+ * positions at or past the table are left unrotated. */
+void or_rope_apply(float *data, int n_heads, int hd, int pos, int n_pos, const float *cos_t, const float *sin_t)
+{
+    if (pos >= n_pos)
+        return;
+    int half = hd / 2;
+    const float *cr = cos_t + (size_t)pos * half, *sr = sin_t + (size_t)pos * half;
+    for (int h = 0; h < n_heads; h++) {
+        float *x = data + (size_t)h * hd;
+        for (int i = 0; i < half; i++) {
+            float c = cr[i], s = sr[i], x0 = x[i], x1 = x[i + half];
+            x[i] = fmaf(x0, c, -(x1 * s));
+            x[i + half] = fmaf(x0, s, x1 * c);
+        }
+    }
+}
+
+/* fast_expf_avx2, ops_math_fast.h:105-126: clamp to [-87, 87], fused
+ * 12102203 * x + 1065353216, convert with round-to-nearest-even. */
+static float fast_expf_vec(float x)
+{
+    x = x > -87.0f ? x : -87.0f;
+    x = x < 87.0f ? x : 87.0f;
+    float f = fmaf(x, 12102203.0f, 1065353216.0f);
+    int32_t i = (int32_t)lrintf(f);
+    float r;
+    memcpy(&r, &i, sizeof r);
+    return r;
+}
+
+/* op_silu_mul_fused_f32, ops_activation.c:48-105: in blocks of 8,
+ * sig = 1 / (1 + fast_expf_avx2(0 - g)); out = (g * sig) * u; the scalar
+ * remainder uses the truncating fast_expf. */
+void or_silu_mul(float *dst, const float *gate, const float *up, int n)
+{
+    int i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) {
+            float g = gate[i + l];
+            float sig = 1.0f / (1.0f + fast_expf_vec(0.0f - g));
+            dst[i + l] = (g * sig) * up[i + l];
+        }
+    for (; i < n; i++) {
+        float g = gate[i];
+        float sig = 1.0f / (1.0f + or_fast_expf(-g));
+        dst[i] = g * sig * up[i];
+    }
+}
+
+/* argmax_simd_f32, sampler.c:42-117: 8 lanes keep the first strict maximum
+ * of i = l (mod 8); lanes are reduced in order with strict >, then the
+ * scalar tail with strict >. */
+int or_argmax(const float *x, int n)
+{
+    if (n < 8) {
+        int b = 0;
+        for (int i = 1; i < n; i++)
+            if (x[i] > x[b])
+                b = i;
+        return b;
+    }
+    float mv[8];
+    int mi[8];
+    for (int l = 0; l < 8; l++) {
+        mv[l] = x[l];
+        mi[l] = l;
+    }
+    int i = 8;
+    for (; i + 7 < n; i += 8)
+        for (int l = 0; l < 8; l++)
+            if (x[i + l] > mv[l]) {
+                mv[l] = x[i + l];
+                mi[l] = i + l;
+            }
+    float bv = mv[0];
+    int bi = mi[0];
+    for (int l = 1; l < 8; l++)
+        if (mv[l] > bv) {
+            bv = mv[l];
+            bi = mi[l];
+        }
+    for (; i < n; i++)
+        if (x[i] > bv) {
+            bv = x[i];
+            bi = i;
+        }
+    return bi;
+}
+
+static void gemv_kind(float *y, int wkind, const void *w, const float *s, const float *x, int n, int k, int th)
+{
+    if (wkind == 0)
+        or_gemv_q8(y, (const int8_t *)w, s, x, n, k, 1, th);
+    else
+        or_gemv_fp8(y, (const uint8_t *)w, s, x, n, k, 1, th);
+}
+
+int or_decoder_init(or_decoder *d, const or_decoder_cfg *c, const or_model_w *w, const float *hpT)
+{
+    memset(d, 0, sizeof *d);
+    d->c = *c;
+    d->w = *w;
+    int max_pages = (c->max_seq + OR_PAGE_TOKENS - 1) / OR_PAGE_TOKENS;
+    if (or_paged_init(&d->kv, c->n_layers, c->n_kv, c->hd, max_pages, c->kv_kind))
+        return -1;
+    d->ix = calloc((size_t)c->n_layers, sizeof(or_lsh_index));
+    for (int l = 0; l < c->n_layers; l++)
+        if (or_lsh_index_create(&d->ix[l], max_pages))
+            return -1;
+    d->hpT = malloc(sizeof(float) * (size_t)c->hd * 16);
+    memcpy(d->hpT, hpT, sizeof(float) * (size_t)c->hd * 16);
+    size_t half = (size_t)c->hd / 2;
+    d->cos_t = malloc(sizeof(float) * (size_t)c->max_seq * half);
+    d->sin_t = malloc(sizeof(float) * (size_t)c->max_seq * half);
+    or_rope_table(d->cos_t, d->sin_t, c->hd, c->max_seq, c->theta);
+    int qd = c->n_heads * c->hd, kd = c->n_kv * c->hd;
+    d->x = calloc((size_t)c->dim, sizeof(float));
+    d->xb = calloc((size_t)(c->dim > qd ? c->dim : qd), sizeof(float));
+    d->q = calloc((size_t)qd, sizeof(float));
+    d->k = calloc((size_t)kd, sizeof(float));
+    d->v = calloc((size_t)kd, sizeof(float));
+    d->att = calloc((size_t)qd, sizeof(float));
+    d->hb = calloc((size_t)c->hidden, sizeof(float));
+    d->hb2 = calloc((size_t)c->hidden, sizeof(float));
+    return 0;
+}
+
+void or_decoder_free(or_decoder *d)
+{
+    or_paged_free(&d->kv);
+    for (int l = 0; l < d->c.n_layers && d->ix; l++)
+        or_lsh_index_destroy(&d->ix[l]);
+    free(d->ix);
+    free(d->hpT);
+    free(d->cos_t);
+    free(d->sin_t);
+    free(d->x);
+    free(d->xb);
+    free(d->q);
+    free(d->k);
+    free(d->v);
+    free(d->att);
+    free(d->hb);
+    free(d->hb2);
+    memset(d, 0, sizeof *d);
+}
+
+/* paged_kv_append plus the page index: a page that fills is hashed (its
+ * centroid under the projection) and inserted as logical page id. */
+int or_decoder_kv_append(or_decoder *d, int layer, const float *k, const float *v, int pos)
+{
+    int phys = or_paged_append(&d->kv, layer, k, v, pos);
+    if (phys < 0)
+        return -1;
+    if (pos % OR_PAGE_TOKENS == OR_PAGE_TOKENS - 1) {
+        uint16_t h = or_lsh_hash(d->hpT, d->c.hd, d->kv.centroid + (size_t)phys * d->c.hd);
+        or_lsh_insert_block(&d->ix[layer], h, pos - OR_PAGE_TOKENS + 1, OR_PAGE_TOKENS);
+    }
+    return 0;
+}
+
+/* transformer_forward, inference.c:60-696, on the paged path: embedding
+ * (row-scaled codes, dequantized), per layer RMSNorm -> q/k/v GEMV -> RoPE ->
+ * paged append -> attention (dense when n_pages <= sparse_k, else the LSH
+ * route + sparse attention) -> o GEMV -> residual -> RMSNorm -> gate/up GEMV
+ * -> SiLU*up -> down GEMV -> residual; final RMSNorm -> lm_head GEMV.  The
+ * zero-initialised adapter and bias stages are numerically no-ops. */
+int or_decoder_step(or_decoder *d, int token, int pos, float *logits, int th)
+{
+    const or_decoder_cfg *c = &d->c;
+    const int dim = c->dim, hd = c->hd, qd = c->n_heads * hd, kd = c->n_kv * hd;
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (c->wkind == 0) {
+        const int8_t *e = (const int8_t *)d->w.emb + (size_t)token * dim;
+        for (int i = 0; i < dim; i++)
+            d->x[i] = (float)e[i] * d->w.emb_s[token];
+    } else {
+        float lut[256];
+        or_fp8_lut(lut);
+        const uint8_t *e = (const uint8_t *)d->w.emb + (size_t)token * dim;
+        for (int i = 0; i < dim; i++)
+            d->x[i] = lut[e[i]] * d->w.emb_s[token];
+    }
+    int *sel = malloc(sizeof(int) * (size_t)(d->kv.max_logical + 2));
+    for (int l = 0; l < c->n_layers; l++) {
+        const or_layer_w *L = &d->w.layers[l];
+        or_rmsnorm(d->xb, d->x, L->attn_norm, dim, c->eps);
+        gemv_kind(d->q, c->wkind, L->wq, L->sq, d->xb, qd, dim, th);
+        gemv_kind(d->k, c->wkind, L->wk, L->sk, d->xb, kd, dim, th);
+        gemv_kind(d->v, c->wkind, L->wv, L->sv, d->xb, kd, dim, th);
+        or_rope_apply(d->q, c->n_heads, hd, pos, c->max_seq, d->cos_t, d->sin_t);
+        or_rope_apply(d->k, c->n_kv, hd, pos, c->max_seq, d->cos_t, d->sin_t);
+        if (or_decoder_kv_append(d, l, d->k, d->v, pos)) {
+            free(sel);
+            return -1;
+        }
+        int nb = d->kv.logical_len[l];
+        if (nb <= c->sparse_k) {
+            or_paged_attention_dense(d->att, d->q, &d->kv, l, c->n_heads, scale, th);
+        } else {
+            int nc = 0;
+            int ns = or_route_pages(sel, &nc, NULL, &d->kv, l, d->q, c->n_heads, d->hpT, &d->ix[l], c->cand_cap,
+                                    c->sparse_k);
+            or_paged_attention_pages(d->att, d->q, &d->kv, sel, ns, c->n_heads, scale, th);
+        }
+        gemv_kind(d->xb, c->wkind, L->wo, L->so, d->att, dim, qd, th);
+        for (int i = 0; i < dim; i++)
+            d->x[i] = d->x[i] + d->xb[i];
+        or_rmsnorm(d->xb, d->x, L->ffn_norm, dim, c->eps);
+        gemv_kind(d->hb, c->wkind, L->w1, L->s1, d->xb, c->hidden, dim, th);
+        gemv_kind(d->hb2, c->wkind, L->w3, L->s3, d->xb, c->hidden, dim, th);
+        or_silu_mul(d->hb, d->hb, d->hb2, c->hidden);
+        gemv_kind(d->xb, c->wkind, L->w2, L->s2, d->hb, dim, c->hidden, th);
+        for (int i = 0; i < dim; i++)
+            d->x[i] = d->x[i] + d->xb[i];
+    }
+    free(sel);
+    or_rmsnorm(d->x, d->x, d->w.final_norm, dim, c->eps);
+    gemv_kind(logits, c->wkind, d->w.out, d->w.out_s, d->x, c->vocab, dim, th);
+    return or_argmax(logits, c->vocab);
+}

@@ -155,6 +155,53 @@ int or_route_pages(int *selected, int *n_cand_out, int *cand_out,
                    const float *hpT, const or_lsh_index *ix, int cand_cap, int k);
 void or_q_mean(float *qm, const float *q, int n_heads, int hd);
 
+/* ---- decode-step adjacents (E rows) and the decoder loop ----------------- */
+void or_rmsnorm(float *out, const float *x, const uint16_t *w, int dim, float eps);      /* ops_norm.c:27-138 */
+void or_rope_table(float *cos_t, float *sin_t, int hd, int n_pos, float theta);          /* ops_rope.c:30-95 */
+void or_rope_apply(float *data, int n_heads, int hd, int pos, int n_pos,
+                   const float *cos_t, const float *sin_t);                              /* ops_rope.c:192-228 */
+void or_silu_mul(float *dst, const float *gate, const float *up, int n);                 /* ops_activation.c:48-105 */
+int  or_argmax(const float *x, int n);                                                   /* sampler.c:42-117 */
+
+typedef struct or_decoder_cfg {
+    int n_layers, dim, n_heads, n_kv, hd, hidden, vocab, max_seq;
+    int wkind;      /* 0: INT8 codes, 1: FP8 E4M3 codes; per-row fp32 scales */
+    int kv_kind;    /* OR_KV_INT8 / OR_KV_BF16 */
+    int sparse_k;   /* pages; dense attention while n_pages <= sparse_k */
+    int cand_cap;
+    float theta, eps;
+} or_decoder_cfg;
+
+typedef struct or_layer_w {
+    const void *wq, *wk, *wv, *wo, *w1, *w2, *w3;
+    const float *sq, *sk, *sv, *so, *s1, *s2, *s3;
+    const uint16_t *attn_norm, *ffn_norm;
+} or_layer_w;
+
+typedef struct or_model_w {
+    const void *emb;           /* [vocab][dim] codes */
+    const float *emb_s;        /* [vocab] */
+    const uint16_t *final_norm;
+    const void *out;           /* [vocab][dim] codes */
+    const float *out_s;
+    const or_layer_w *layers;  /* [n_layers] */
+} or_model_w;
+
+typedef struct or_decoder {
+    or_decoder_cfg c;
+    or_model_w w;
+    or_paged kv;
+    or_lsh_index *ix;
+    float *hpT, *cos_t, *sin_t;
+    float *x, *xb, *q, *k, *v, *att, *hb, *hb2;
+} or_decoder;
+
+int  or_decoder_init(or_decoder *d, const or_decoder_cfg *c, const or_model_w *w, const float *hpT);
+void or_decoder_free(or_decoder *d);
+int  or_decoder_kv_append(or_decoder *d, int layer, const float *k, const float *v, int pos);
+/* transformer_forward (inference.c:60-696), paged path; returns the argmax */
+int  or_decoder_step(or_decoder *d, int token, int pos, float *logits, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,6 +14,9 @@
 #include "compute/ops.h"
 #include "memory/paged.h"
 #include "tensor/tensor.h"
+#include "compute/ops_rope.h"
+#include "compute/ops_activation.h"
+#include "compute/sampler.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -188,4 +191,50 @@ int ref_matmul(void *out, int out_dtype, const void *a, int a_dtype, int m, int 
     tb.dtype = b_dtype;
     to.dtype = out_dtype;
     return op_matmul(&to, &ta, &tb);
+}
+
+/* decode-step adjacents */
+void ref_rmsnorm(float *out, const float *x, const uint16_t *w, int dim, float eps)
+{
+    int sx[2] = {dim, 1}, sw[1] = {dim};
+    t_tensor tx = tensor_view((void *)x, sx, 2), to = tensor_view(out, sx, 2);
+    t_tensor tw = tensor_view((void *)w, sw, 1);
+    tx.dtype = DTYPE_F32;
+    to.dtype = DTYPE_F32;
+    tw.dtype = DTYPE_BF16;
+    op_rmsnorm(&to, &tx, &tw, eps);
+}
+
+int ref_rope_table(float *cos_t, float *sin_t, int hd, int n_pos, float theta)
+{
+    t_rope_cache *c = rope_cache_init(hd, n_pos, theta);
+    if (!c)
+        return -1;
+    memcpy(cos_t, c->cos_table, sizeof(float) * (size_t)n_pos * (hd / 2));
+    memcpy(sin_t, c->sin_table, sizeof(float) * (size_t)n_pos * (hd / 2));
+    rope_cache_free(c);
+    return 0;
+}
+
+void ref_rope_apply(float *data, int n_heads, int hd, int pos, int n_pos, float *cos_t, float *sin_t)
+{
+    t_rope_cache c;
+    c.cos_table = cos_t;
+    c.sin_table = sin_t;
+    c.head_dim = hd;
+    c.max_seq_len = n_pos;
+    rope_apply_multihead_cached(data, n_heads, pos, &c);
+}
+
+void ref_silu_mul(float *dst, const float *gate, const float *up, int n)
+{
+    op_silu_mul_fused_f32(dst, gate, up, (size_t)n);
+}
+
+int ref_argmax(float *x, int n)
+{
+    int s[1] = {n};
+    t_tensor t = tensor_view(x, s, 1);
+    t.dtype = DTYPE_F32;
+    return sample_argmax(&t);
 }

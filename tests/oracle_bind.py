@@ -54,6 +54,71 @@ class OrPaged(C.Structure):
                 ("free_top", C.c_int), ("logical_len", C.POINTER(C.c_int))]
 
 
+class OrDecoderCfg(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layers", "dim", "n_heads", "n_kv", "hd", "hidden", "vocab", "max_seq",
+                                       "wkind", "kv_kind", "sparse_k", "cand_cap")] + \
+               [("theta", C.c_float), ("eps", C.c_float)]
+
+
+class OrLayerW(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "sq", "sk", "sv", "so", "s1",
+                                          "s2", "s3", "attn_norm", "ffn_norm")]
+
+
+class OrModelW(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("emb", "emb_s", "final_norm", "out", "out_s", "layers")]
+
+
+DECODER_CFG_KEYS = ("n_layers", "dim", "n_heads", "n_kv", "hd", "hidden", "vocab", "max_seq", "wkind", "kv_kind",
+                    "sparse_k", "cand_cap", "theta", "eps")
+LAYER_KEYS = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
+
+
+class OracleDecoder:
+    """The oracle's transformer_forward on the paged path over numpy weights
+    (dict: emb, emb_s, final_norm, out, out_s, layers=[{wq.., sq.., attn_norm,
+    ffn_norm}]); the arrays are kept alive by this object."""
+
+    def __init__(self, orc, cfg, w, hpT):
+        self.o = orc
+        self.cfg = OrDecoderCfg(*[cfg[k] for k in DECODER_CFG_KEYS])
+        self.keep = []
+
+        def ptr(a):
+            a = np.ascontiguousarray(a)
+            self.keep.append(a)
+            return a.ctypes.data
+        self.layers = (OrLayerW * cfg["n_layers"])()
+        for i, L in enumerate(w["layers"]):
+            for k in LAYER_KEYS:
+                setattr(self.layers[i], k, ptr(L[k]))
+                setattr(self.layers[i], "s" + k[1:], ptr(L["s" + k[1:]]))
+            self.layers[i].attn_norm = ptr(L["attn_norm"])
+            self.layers[i].ffn_norm = ptr(L["ffn_norm"])
+        self.mw = OrModelW(ptr(w["emb"]), ptr(w["emb_s"]), ptr(w["final_norm"]), ptr(w["out"]), ptr(w["out_s"]),
+                           C.cast(self.layers, C.c_void_p))
+        self.buf = C.create_string_buffer(4096)
+        hpT = np.ascontiguousarray(hpT, np.float32)
+        if orc.lib.or_decoder_init(self.buf, C.byref(self.cfg), C.byref(self.mw), hpT.ravel()) != 0:
+            raise MemoryError("or_decoder_init")
+        self.vocab = cfg["vocab"]
+
+    def kv_append(self, layer, k, v, pos):
+        return self.o.lib.or_decoder_kv_append(self.buf, layer, np.ascontiguousarray(k, np.float32),
+                                               np.ascontiguousarray(v, np.float32), pos)
+
+    def step(self, token, pos, threads=0):
+        logits = np.zeros(self.vocab, np.float32)
+        nxt = self.o.lib.or_decoder_step(self.buf, int(token), int(pos), logits, threads)
+        return nxt, logits
+
+    def __del__(self):
+        try:
+            self.o.lib.or_decoder_free(self.buf)
+        except Exception:
+            pass
+
+
 class Oracle:
     def __init__(self, path=ORACLE_SO):
         if not os.path.exists(path):
@@ -98,12 +163,46 @@ class Oracle:
         _sig(L, "or_route_pages", C.c_int, i32p, C.POINTER(C.c_int), i32p, C.POINTER(OrPaged), C.c_int,
              f32p, C.c_int, f32p, C.POINTER(OrLshIndex), C.c_int, C.c_int)
         _sig(L, "or_q_mean", None, f32p, f32p, C.c_int, C.c_int)
+        _sig(L, "or_rmsnorm", None, f32p, f32p, u16p, C.c_int, C.c_float)
+        _sig(L, "or_rope_table", None, f32p, f32p, C.c_int, C.c_int, C.c_float)
+        _sig(L, "or_rope_apply", None, f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p, f32p)
+        _sig(L, "or_silu_mul", None, f32p, f32p, f32p, C.c_int)
+        _sig(L, "or_argmax", C.c_int, f32p, C.c_int)
+        _sig(L, "or_decoder_init", C.c_int, C.c_void_p, C.POINTER(OrDecoderCfg), C.POINTER(OrModelW), f32p)
+        _sig(L, "or_decoder_free", None, C.c_void_p)
+        _sig(L, "or_decoder_kv_append", C.c_int, C.c_void_p, C.c_int, f32p, f32p, C.c_int)
+        _sig(L, "or_decoder_step", C.c_int, C.c_void_p, C.c_int, C.c_int, f32p, C.c_int)
         _sig(L, "or_paged_alloc", C.c_int, C.POINTER(OrPaged))
         _sig(L, "or_paged_release", None, C.POINTER(OrPaged), C.c_int)
         _sig(L, "or_score_blocks", None, C.c_void_p, f32p, C.POINTER(OrPaged), C.c_int, C.c_int)
         _sig(L, "or_select_top_k_blocks", C.c_int, i32p, C.c_void_p, C.c_int, C.c_int)
 
     # -- scalar helpers -----------------------------------------------------
+    def rmsnorm(self, x, w, eps=1e-5):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        self.lib.or_rmsnorm(out, x, np.ascontiguousarray(w, np.uint16), len(x), eps)
+        return out
+
+    def rope_table(self, hd, n_pos, theta):
+        c = np.zeros(n_pos * (hd // 2), np.float32)
+        s = np.zeros_like(c)
+        self.lib.or_rope_table(c, s, hd, n_pos, theta)
+        return c, s
+
+    def rope_apply(self, data, n_heads, hd, pos, cos_t, sin_t):
+        d = np.ascontiguousarray(data, np.float32).copy()
+        self.lib.or_rope_apply(d, n_heads, hd, pos, len(cos_t) // (hd // 2), cos_t, sin_t)
+        return d
+
+    def silu_mul(self, g, u):
+        out = np.zeros(len(g), np.float32)
+        self.lib.or_silu_mul(out, np.ascontiguousarray(g, np.float32), np.ascontiguousarray(u, np.float32), len(g))
+        return out
+
+    def argmax(self, x):
+        return self.lib.or_argmax(np.ascontiguousarray(x, np.float32), len(x))
+
     def gemv_bf16(self, wb, x, threads=0):
         n, k = wb.shape
         y = np.zeros(n, np.float32)
@@ -345,6 +444,11 @@ class RefLib:
         _sig(L, "ref_matmul", C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
              C.c_void_p, C.c_int, C.c_int)
         _sig(L, "lsh_hamming_distance", C.c_int, C.c_uint16, C.c_uint16)
+        _sig(L, "ref_rmsnorm", None, f32p, f32p, u16p, C.c_int, C.c_float)
+        _sig(L, "ref_rope_table", C.c_int, f32p, f32p, C.c_int, C.c_int, C.c_float)
+        _sig(L, "ref_rope_apply", None, f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p, f32p)
+        _sig(L, "ref_silu_mul", None, f32p, f32p, f32p, C.c_int)
+        _sig(L, "ref_argmax", C.c_int, f32p, C.c_int)
         # the reference's block_manager_init prints a banner on stdout; silence nothing,
         # tests capture it.
 
