@@ -46,6 +46,7 @@ SIGNATURES = {
     "be42_decoder_pool": (vp, [vp]),
     "be42_decoder_step": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "be42_decoder_next_tokens": (i32, [vp, vp]),
+    "be42_decoder_capture": (i32, [vp, vp, vp]),
     "be42_kv_create": (i32, [vp, i32, i32, i32, i32, i32, vp]),
     "be42_kv_destroy": (None, [vp]),
     "be42_kv_set_projection": (i32, [vp, vp]),
@@ -350,13 +351,22 @@ class Decoder:
                            cfg["head_dim"], (cfg["max_seq"] + 15) // 16,
                            handle=C.c_void_p(lib.lib.be42_decoder_pool(self.handle)))
 
-    def step(self, tokens, pos, logits=None, sync=True):
+    def step(self, tokens, pos, logits=None, sync=True, batch=None):
+        """tokens: host ints, or None to feed back the previous argmax (then
+        give batch); sync=False leaves the argmax on the device."""
         import numpy as np
-        t = np.ascontiguousarray(tokens, np.int32)
-        nxt = np.zeros(len(t), np.int32)
-        self.lib._call("be42_decoder_step", self.handle, t.ctypes.data, len(t), int(pos),
+        if tokens is None:
+            t, n = None, batch
+        else:
+            t = np.ascontiguousarray(tokens, np.int32)
+            n = len(t)
+        nxt = np.zeros(n, np.int32)
+        self.lib._call("be42_decoder_step", self.handle, None if t is None else t.ctypes.data, n, int(pos),
                        nxt.ctypes.data if sync else None, self.lib.p(logits), self.lib.stream())
         return nxt
+
+    def capture(self, q=None, nsel=None):
+        self.lib._call("be42_decoder_capture", self.handle, self.lib.p(q), self.lib.p(nsel))
 
     def close(self):
         if self.handle:

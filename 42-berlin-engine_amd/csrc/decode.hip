@@ -32,14 +32,17 @@ struct TokArgs {
     int tok[kMaxBatch];
 };
 
+// tokens from the kernel argument, or (dev_tok != NULL) from the device
+// argmax of the previous step
 template <bool FP8>
 __global__ __launch_bounds__(256) void k_embed(float *__restrict__ x, const uint8_t *__restrict__ emb,
-                                               const float *__restrict__ emb_s, const TokArgs t, int dim)
+                                               const float *__restrict__ emb_s, const TokArgs t,
+                                               const int *__restrict__ dev_tok, int dim)
 {
     const int b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= dim)
         return;
-    const int tok = t.tok[b];
+    const int tok = dev_tok ? dev_tok[b] : t.tok[b];
     const uint8_t c = emb[(size_t)tok * dim + i];
     const float v = FP8 ? fp8_to_f32(c) : (float)(int8_t)c;
     x[(size_t)b * dim + i] = v * emb_s[tok];
@@ -213,6 +216,8 @@ struct be42_decoder {
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     int *cand = nullptr, *ncand = nullptr;
+    float *capture_q = nullptr;   // optional [n_layers][max_batch][n_heads * head_dim]
+    int *capture_nsel = nullptr;  // optional [n_layers][max_batch] pages attended
 };
 
 static int dec_fail(be42_decoder *d, int rc)
@@ -336,7 +341,7 @@ static int gemv(be42_decoder *d, float *y, const void *w, const float *s, int n,
 extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
                                  float *logits_out, void *stream)
 {
-    BE42_CHECK(d && tokens, "be42_decoder_step: null pointer");
+    BE42_CHECK(d, "be42_decoder_step: null decoder");
     const be42_decoder_config &c = d->c;
     BE42_CHECK(batch > 0 && batch <= c.max_batch, "be42_decoder_step: batch %d (max %d)", batch, c.max_batch);
     BE42_CHECK(pos >= 0 && pos < c.max_seq, "be42_decoder_step: position %d (max %d)", pos, c.max_seq);
@@ -344,17 +349,20 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
     const int B = batch, dim = c.dim, hd = c.head_dim, H = c.n_heads, KV = c.n_kv_heads;
     const int qd = H * hd, kd = KV * hd, fp8 = c.wkind;
     TokArgs ta;
-    for (int b = 0; b < B; b++) {
+    memset(&ta, 0, sizeof ta);
+    for (int b = 0; tokens && b < B; b++) {
         BE42_CHECK(tokens[b] >= 0 && tokens[b] < c.vocab, "be42_decoder_step: token %d out of range", tokens[b]);
         ta.tok[b] = tokens[b];
     }
+    // the device argmax of the previous step is always in [0, vocab)
+    const int *dev_tok = tokens ? nullptr : d->next;
     const dim3 eg((dim + 255) / 256, B);
     if (fp8)
         hipLaunchKernelGGL(k_embed<true>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, ta,
-                           dim);
+                           dev_tok, dim);
     else
         hipLaunchKernelGGL(k_embed<false>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, ta,
-                           dim);
+                           dev_tok, dim);
     BE42_LAUNCH_CHECK();
     const size_t norm_lds = (size_t)dim * 4;
     const float scale = 1.0f / sqrtf((float)hd);
@@ -377,6 +385,9 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
                                d->cos_t, d->sin_t, pos, H, KV, hd);
             BE42_LAUNCH_CHECK();
         }
+        if (d->capture_q)
+            BE42_HIP(hipMemcpyAsync(d->capture_q + (size_t)l * c.max_batch * qd, d->q, (size_t)B * qd * 4,
+                                    hipMemcpyDeviceToDevice, st));
         for (int b = 0; b < B; b++)
             slot_ids[b] = l * c.max_batch + b;
         DEC_TRY(be42_kv_append_step(d->pool, slot_ids, positions, B, d->k, d->v, st));
@@ -393,6 +404,11 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
                                    d->cand, d->ncand, nullptr, st));
             DEC_TRY(be42_paged_attention(d->pool, d->q, B, H, d->sel, d->nsel, stride, c.sparse_k, scale, d->att,
                                          c.sparse_k <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
+        }
+        if (d->capture_nsel) {
+            const int *src = pages <= c.sparse_k ? d->pool->n_logical + (size_t)l * c.max_batch : d->nsel;
+            BE42_HIP(hipMemcpyAsync(d->capture_nsel + (size_t)l * c.max_batch, src, (size_t)B * 4,
+                                    hipMemcpyDeviceToDevice, st));
         }
         DEC_TRY(be42_gemv_prepare(d->xdig, d->att, qd, B, fp8, st));
         DEC_TRY(gemv(d, d->xb, L.wo, L.so, dim, qd, B, st));
@@ -431,5 +447,16 @@ extern "C" int be42_decoder_next_tokens(be42_decoder *d, const int **dev_ptr)
 {
     BE42_CHECK(d && dev_ptr, "be42_decoder_next_tokens: null pointer");
     *dev_ptr = d->next;
+    return BE42_OK;
+}
+
+// Inspection: copy each layer's rotated queries ([n_layers][max_batch]
+// [n_heads * head_dim]) and attended page counts ([n_layers][max_batch]) of
+// every step into device buffers; NULL stops either.
+extern "C" int be42_decoder_capture(be42_decoder *d, float *q_dst, int *nsel_dst)
+{
+    BE42_CHECK(d, "be42_decoder_capture: null decoder");
+    d->capture_q = q_dst;
+    d->capture_nsel = nsel_dst;
     return BE42_OK;
 }

@@ -235,6 +235,212 @@ def gemm_bench(lib, steps, warmup):
             "TOPS_aggregate": round(tot_ops / tot_s / 1e12, 1), "best": best, "by_shape": rows}
 
 
+# ---- decode step -----------------------
+TINY = dict(n_layers=4, dim=512, n_heads=8, n_kv_heads=8, head_dim=64, hidden_dim=1408, vocab=4096)
+B3 = dict(n_layers=28, dim=3072, n_heads=24, n_kv_heads=8, head_dim=128, hidden_dim=8192, vocab=128256)
+B3_CTX = 32768
+
+
+def decoder_weights(lib, arch, kind, gen):
+    """Random-init weights on the device: INT8 codes U{-127..127} with row
+    scales U[0.005, 0.02], or N(0, 0.02) weights quantized to FP8
+    E4M3 per row; RMSNorm weights 1.0 (bf16)."""
+    import torch
+    dev = "cuda"
+
+    def mat(r, c):
+        if kind == "int8":
+            q = torch.randint(-127, 128, (r, c), dtype=torch.int8, device=dev, generator=gen)
+            return q, torch.rand(r, device=dev, generator=gen) * 0.015 + 0.005
+        w = torch.randn(r, c, device=dev, generator=gen) * 0.02
+        q, sc = lib.quant_rows_fp8(w)
+        del w
+        return q, sc
+    d, H, KV, hd, F, V = (arch[k] for k in ("dim", "n_heads", "n_kv_heads", "head_dim", "hidden_dim", "vocab"))
+    one = torch.full((d,), 0x3F80, dtype=torch.int16, device=dev)
+    layers = []
+    for _ in range(arch["n_layers"]):
+        L = {}
+        for name, (r, c) in {"wq": (H * hd, d), "wk": (KV * hd, d), "wv": (KV * hd, d), "wo": (d, H * hd),
+                             "w1": (F, d), "w3": (F, d), "w2": (d, F)}.items():
+            L[name], L["s" + name[1:]] = mat(r, c)
+        L["attn_norm"], L["ffn_norm"] = one, one
+        layers.append(L)
+    emb, emb_s = mat(V, d)
+    out, out_s = mat(V, d)
+    return dict(emb=emb, emb_s=emb_s, final_norm=one, out=out, out_s=out_s, layers=layers)
+
+
+def weight_bytes(arch):
+    """Weight bytes one decode step streams: every layer's 7 matrices and the
+    lm_head (1 B per code + 4 B per row scale), plus one embedding row."""
+    d, H, KV, hd, F, V = (arch[k] for k in ("dim", "n_heads", "n_kv_heads", "head_dim", "hidden_dim", "vocab"))
+    rows_cols = [(H * hd, d), (KV * hd, d), (KV * hd, d), (d, H * hd), (F, d), (F, d), (d, F)]
+    per_layer = sum(r * c + 4 * r for r, c in rows_cols)
+    return arch["n_layers"] * per_layer + V * d + 4 * V + d
+
+
+def decoder_cfg(arch, max_seq, max_batch, wkind, kv_kind, sparse_k=64, cand_cap=64):
+    c = dict(arch)
+    c.update(max_seq=max_seq, max_batch=max_batch, wkind=wkind, kv_kind=kv_kind, sparse_k=sparse_k,
+             cand_cap=cand_cap, rope_len=0, rope_theta=1e4, norm_eps=1e-5)
+    return c
+
+
+def decode_tiny_bench(lib, n_gen=64, reps=3):
+    """128-token prompt, then 64 greedy tokens, each step fed the
+    previous step's device argmax (no host round trip); tokens/s over the 64."""
+    import numpy as np
+    import torch
+    import be42
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(31)
+    w = decoder_weights(lib, TINY, "int8", gen)
+    _, hpT = lib.lsh_projection(TINY["head_dim"], 42)
+    dec = be42.Decoder(lib, decoder_cfg(TINY, 256, 1, 0, be42.KV_INT8), w, hpT)
+    prompt = np.random.default_rng(3).integers(0, TINY["vocab"], 128)
+    best = None
+    for _ in range(reps):
+        for pos in range(128):
+            dec.step([int(prompt[pos])], pos, sync=False)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for pos in range(128, 128 + n_gen):
+            dec.step(None, pos, sync=False, batch=1)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        best = ms if best is None else min(best, ms)
+    dec.close()
+    wb = weight_bytes(TINY)
+    return {"workload": "configs[0]: tiny Llama (4 layers, d 512, 8/8 heads, FFN 1408, vocab 4096), INT8 row-scaled "
+                        "weights, 128-token prompt, 64 greedy tokens, dense paged INT8 attention, batch 1",
+            "tokens_per_s": round(n_gen / (best * 1e-3), 1), "ms_per_token": round(best / n_gen, 4),
+            "weight_bytes_per_token": wb, "weight_GBps": round(wb * n_gen / (best * 1e-3) / 1e9, 1)}
+
+
+def decode_3b_bench(lib, batches=(1, 8), steps=10):
+    """3B-class model, FP8 weights, LSH sparse attention (top-K 64
+    pages, candidate cap 64) over a 32k-token bf16 paged KV prefix per
+    sequence.  The prefix is N(0,1) K/V with the configs[3] planting: layer by
+    layer, a probe step at position 32768 captures the layer's queries and the
+    layer's prefix is rebuilt with 5% of its pages planted along their mean.
+    A timed step is one full decode step at position 32768 (re-running the
+    position overwrites its K/V), so every step routes to the planted pages."""
+    import numpy as np
+    import torch
+    import be42
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(41)
+    A = B3
+    BM = max(batches)
+    L, H, KVH, hd = A["n_layers"], A["n_heads"], A["n_kv_heads"], A["head_dim"]
+    w = decoder_weights(lib, A, "fp8", gen)
+    _, hpT = lib.lsh_projection(hd, 42)
+    cfg = decoder_cfg(A, B3_CTX + 64, BM, 1, be42.KV_BF16)
+    dec = be42.Decoder(lib, cfg, w, hpT)
+    T = B3_CTX
+    tok0 = np.random.default_rng(5).integers(0, A["vocab"], BM)
+    lsh_cfg = dict(LSH, heads=H, kv_heads=KVH, head_dim=hd)
+
+    def build(slot, q=None):
+        dec.pool.reset(slot)
+        for t0 in range(0, T, 8192):
+            n = min(8192, T - t0)
+            K = torch.randn(n, KVH * hd, generator=gen, device="cuda")
+            V = torch.randn(n, KVH * hd, generator=gen, device="cuda")
+            if q is not None:
+                plant_keys_gpu(K, q, gen, lsh_cfg)
+            dec.pool.append(slot, K, V, t0)
+            del K, V
+    for l in range(L):
+        for b in range(BM):
+            build(l * BM + b)
+    torch.cuda.synchronize()
+    cq = torch.zeros((L, BM, H * hd), device="cuda")
+    cn = torch.zeros((L, BM), dtype=torch.int32, device="cuda")
+    dec.capture(cq, cn)
+    for l in range(L):
+        dec.step(tok0, T, sync=True)
+        qs = cq[l].cpu().numpy()
+        for b in range(BM):
+            build(l * BM + b, qs[b])
+    torch.cuda.synchronize()
+    rows = []
+    for B in batches:
+        toks = tok0[:B]
+        for _ in range(2):
+            dec.step(toks, T, sync=False)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            dec.step(toks, T, sync=False)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        nsel = cn[:, :B].cpu().numpy()
+        kv_bytes = int(nsel.sum()) * 16 * KVH * hd * 2 * 2
+        wb = weight_bytes(A)
+        rows.append({"batch": B, "tokens_per_s": round(B / (ms * 1e-3), 1), "ms_per_step": round(ms, 3),
+                     "pages_attended_mean": round(float(nsel.mean()), 2),
+                     "step_bytes": wb + kv_bytes, "GBps": round((wb + kv_bytes) / (ms * 1e-3) / 1e9, 1),
+                     "frac_of_hbm_peak": round((wb + kv_bytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    dec.capture(None, None)
+    dec.close()
+    return {"workload": "configs[4]: 3B-class Llama (28 layers, d 3072, 24/8 heads, hd 128, FFN 8192, vocab "
+                        "128256), FP8 E4M3 per-row weights, 32k-token bf16 paged KV prefix per sequence with "
+                        "configs[3] planting, LSH sparse attention top-K 64 pages / candidate cap 64",
+            "by_batch": rows}
+
+
+def decode_cpu_baseline(seconds=10.0):
+    """The oracle's transformer_forward (OpenMP GEMVs, paged INT8 attention)
+    on configs[0]: tokens/s of greedy steps after a 128-token prompt."""
+    import numpy as np
+    from oracle_bind import OR_KV_INT8, Oracle, OracleDecoder
+    orc = Oracle()
+    cores = min(16, host_cores())
+    rng = np.random.default_rng(31)
+    A = TINY
+    d, H, KV, hd, F, V = (A[k] for k in ("dim", "n_heads", "n_kv_heads", "head_dim", "hidden_dim", "vocab"))
+
+    def q(r, c):
+        return rng.integers(-127, 128, (r, c), dtype=np.int8), rng.uniform(0.005, 0.02, r).astype(np.float32)
+    one = np.full(d, 0x3F80, np.uint16)
+    layers = []
+    for _ in range(A["n_layers"]):
+        Lw = {}
+        for name, (r, c) in {"wq": (H * hd, d), "wk": (KV * hd, d), "wv": (KV * hd, d), "wo": (d, H * hd),
+                             "w1": (F, d), "w3": (F, d), "w2": (d, F)}.items():
+            Lw[name], Lw["s" + name[1:]] = q(r, c)
+        Lw["attn_norm"], Lw["ffn_norm"] = one, one
+        layers.append(Lw)
+    emb, emb_s = q(V, d)
+    out, out_s = q(V, d)
+    w = dict(emb=emb, emb_s=emb_s, final_norm=one, out=out, out_s=out_s, layers=layers)
+    cfg = dict(n_layers=A["n_layers"], dim=d, n_heads=H, n_kv=KV, hd=hd, hidden=F, vocab=V, max_seq=4096, wkind=0,
+               kv_kind=OR_KV_INT8, sparse_k=64, cand_cap=64, theta=1e4, eps=1e-5)
+    _, hpT = orc.lsh_init(hd, 42)
+    dec = OracleDecoder(orc, cfg, w, hpT)
+    prompt = rng.integers(0, V, 128)
+    for pos in range(128):
+        nxt, _ = dec.step(prompt[pos], pos, threads=cores)
+    times = []
+    pos = 128
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end and pos < 1024:
+        t0 = time.perf_counter()
+        nxt, _ = dec.step(nxt, pos, threads=cores)
+        times.append(time.perf_counter() - t0)
+        pos += 1
+    med = sorted(times)[len(times) // 2]
+    return {"value": round(1.0 / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"oracle or_decoder_step on configs[0] after a 128-token prompt, greedy, batch 1, OpenMP "
+                      f"{cores} threads, median of {len(times)} steps"}
+
+
 def lsh_cpu_baseline(seconds=10.0):
     """The oracle (port of the reference route + paged sparse attention, bf16
     pages) on one 32k-token sequence of the configs[3] workload."""
@@ -270,6 +476,47 @@ def lsh_cpu_baseline(seconds=10.0):
                       f"OpenMP {cores} threads over heads, median of {len(times)} runs"}
 
 
+PMC_CONFIG = ("fp8", 128256, 4096, 16)
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_fp8_128256x4096_b16_pmc.txt")
+
+
+def pmc_probe():
+    """For rocprofv3 --pmc runs: 10 launches of the FP8 128256x4096 batch-16
+    GEMV, then 10 copies of 1 GiB (torch copy kernel) as the byte-count
+    reference of the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    import be42
+    lib = be42.load()
+    lib.init(0)
+    kind, n, k, b = PMC_CONFIG
+    w = torch.randn(n, k, device="cuda") * 0.02
+    q, sc = lib.quant_rows_fp8(w)
+    del w
+    x = torch.randn(b, k, device="cuda")
+    xdig = lib.gemv_prepare(x, kind)
+    y = torch.empty(b, n, device="cuda")
+    for _ in range(10):
+        lib.gemv_prepared(q, sc, xdig, b, kind, y)
+    src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc probe done", flush=True)
+
+
+def measured_traffic(dc):
+    """HBM bytes per launch of the dominant GEMV from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy
+    kernel's reading of a known byte count), when it covers this workload."""
+    if (dc["kind"], dc["n"], dc["k"], dc["b"]) != PMC_CONFIG or not os.path.exists(PMC_SUMMARY):
+        return None
+    for line in open(PMC_SUMMARY):
+        if line.startswith("traffic_bytes_per_launch"):
+            return int(line.split("=")[1].split()[0])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -278,7 +525,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-lsh", action="store_true", help="skip the LSH attention leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode-step leg")
+    ap.add_argument("--no-3b", action="store_true", help="skip the 3B-model decode (its setup takes ~1 minute)")
+    ap.add_argument("--pmc-probe", action="store_true", help="only run the kernels profiled for HBM traffic")
     args = ap.parse_args()
+    if args.pmc_probe:
+        pmc_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               f"(the multi-GPU design is described in DESIGN.md)", file=sys.stderr)
@@ -358,7 +611,7 @@ def main():
 
     dm, dc, dnb = dominant
     achieved = dnb / (dm * 1e-3) / 1e9
-    kname = "be42::k_gemv<%s, RT=%d>" % ("fp8" if dc["kind"] == "fp8" else "int8", 1 if dc["b"] <= 4 else 2)
+    kname = "be42::k_gemv (%s)" % dc["kind"]
     out = {
         "metric": "decode tokens/s; quant GEMV HBM GB/s (% of peak); LSH attn µs/token @32k",
         "value": round(value, 1),
@@ -378,11 +631,18 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kname,
                      "workload": f"{dc['kind']} {dc['n']}x{dc['k']} batch {dc['b']}",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dc),
                      "bytes_per_launch": dnb},
         "gemv_sweep": sweep,
         "wall_s": round(wall, 2),
     }
+    if not args.no_decode:
+        configs.clear()
+        torch.cuda.empty_cache()
+        out["decode"] = {"tiny": decode_tiny_bench(lib)}
+        if not args.no_3b:
+            out["decode"]["3b"] = decode_3b_bench(lib)
+        torch.cuda.empty_cache()
     if not args.no_gemm:
         configs.clear()
         torch.cuda.empty_cache()
@@ -396,6 +656,8 @@ def main():
         out["cpu_baseline"] = cpu_baseline()
         if not args.no_lsh:
             out["lsh_attention"]["cpu_baseline"] = lsh_cpu_baseline()
+        if not args.no_decode:
+            out["decode"]["tiny"]["cpu_baseline"] = decode_cpu_baseline()
     print(json.dumps(out), flush=True)
 
 

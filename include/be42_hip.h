@@ -227,12 +227,19 @@ int  be42_decoder_create(be42_decoder **out, const be42_decoder_config *cfg, con
 void be42_decoder_destroy(be42_decoder *d);
 be42_kv_pool *be42_decoder_pool(be42_decoder *d);
 /* One token for each of `batch` sequences at position pos: tokens and
- * next_tokens are host arrays (next_tokens may be NULL: the argmax stays on
- * the device, be42_decoder_next_tokens); logits_out (device, [batch][vocab])
- * may be NULL. */
+ * next_tokens are host arrays.  tokens == NULL feeds back the previous step's
+ * device argmax (greedy decoding with no host round trip); next_tokens may be
+ * NULL (the argmax stays on the device, be42_decoder_next_tokens);
+ * logits_out (device, [batch][vocab]) may be NULL.  Re-running a position
+ * overwrites that position's K/V. */
 int  be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
                        float *logits_out, void *stream);
 int  be42_decoder_next_tokens(be42_decoder *d, const int **dev_ptr);
+/* Inspection: each step copies every layer's rotated queries into q_dst
+ * ([n_layers][max_batch][n_heads * head_dim], device) and the number of pages
+ * each layer attended into nsel_dst ([n_layers][max_batch], device); NULL
+ * stops either. */
+int  be42_decoder_capture(be42_decoder *d, float *q_dst, int *nsel_dst);
 
 #ifdef __cplusplus
 }
