@@ -27,6 +27,8 @@
 //                   l = sum w_t;
 //   k_attn_apply    partial o = sum_t w_t v_t over the split's pages;
 //   k_attn_combine  out = (sum over splits) * (1 / l).
+#include <type_traits>
+
 #include "be42_common.h"
 
 namespace be42 {
@@ -259,12 +261,13 @@ static void launch_scores_apply(const be42_kv_pool &P, const float *q, const int
 
 
 // ---------------------------------------------------------------------------
-// Fused attention for up to 64 selected pages: one block of 8 waves per
-// (query, KV head) serves the G query heads of the group.
+// Fused attention for up to 64 selected pages: one workgroup of WAVES waves
+// per (query, KV head) serves the G query heads of the group.
 //  A. scores: a row (token) of K is read by RL = HD/8 lanes (16 bytes bf16 or
-//     8 bytes INT8 each), RPW = 64/RL rows per wave per step, 8 steps in
-//     flight; each lane forms the G partial dots of its 8 elements, the RL
-//     lanes of a row reduce them; s = dot * scale goes to LDS.
+//     8 bytes INT8 each), RPW = 64/RL rows per wave per step, UNR steps in
+//     flight as raw registers (16 waves x 8 steps = the 512 rows of 32 pages
+//     per pass); each lane forms the G partial dots of its 8 elements, the
+//     RL lanes of a row reduce them; s = dot * scale goes to LDS.
 //  B. weights: wave g scans head g's scores, lane = selected page (LDS padded
 //     to 17 floats per page against bank conflicts), the closed-form online
 //     softmax of the file header, l = sum w.
@@ -273,20 +276,70 @@ static void launch_scores_apply(const be42_kv_pool &P, const float *q, const int
 //     out = o * (1 / l).
 // Every K and V row of the selected pages is read once per KV head.
 constexpr int kFusedMaxPages = 64;
-constexpr int kFusedWaves = 8;
 
-template <bool BF16, int HD, int G>
-__global__ __launch_bounds__(kFusedWaves * 64) void k_attn_fused(const be42_kv_pool P, const float *__restrict__ q,
-                                                                 const int *__restrict__ sel,
-                                                                 const int *__restrict__ nsel, int sel_stride,
-                                                                 int H, float scale, float *__restrict__ out)
+template <bool BF16>
+struct RawRow {
+    using T = typename std::conditional<BF16, uint4, uint2>::type;
+};
+
+template <bool BF16>
+__device__ __forceinline__ void raw_to_f32(float *dst, const typename RawRow<BF16>::T &u, float scale)
+{
+    if constexpr (BF16) {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            dst[2 * j] = __uint_as_float(w[j] << 16);
+            dst[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+        }
+    } else {
+        const uint32_t w[2] = {u.x, u.y};
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                dst[4 * j + e] = (float)(int8_t)((w[j] >> (8 * e)) & 0xFF) * scale;
+    }
+}
+
+// Sum over aligned groups of RL (4, 8 or 16) lanes with DPP lane moves:
+// quad swaps (xor 1, xor 2), then the half-row and row mirrors, which pair
+// the remaining quads / halves.  Every lane of a group ends with the sum.
+template <int RL>
+__device__ __forceinline__ float group_sum(float a)
+{
+    auto mv = [](float v, int ctrl) -> float {
+        const int i = __float_as_int(v);
+        int r;
+        switch (ctrl) {
+        case 0: r = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false); break;   // quad_perm [1,0,3,2]
+        case 1: r = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false); break;   // quad_perm [2,3,0,1]
+        case 2: r = __builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+        default: r = __builtin_amdgcn_update_dpp(0, i, 0x140, 0xF, 0xF, false); break; // row_mirror
+        }
+        return __int_as_float(r);
+    };
+    a = a + mv(a, 0);
+    a = a + mv(a, 1);
+    if constexpr (RL >= 8)
+        a = a + mv(a, 2);
+    if constexpr (RL >= 16)
+        a = a + mv(a, 3);
+    return a;
+}
+
+template <bool BF16, int HD, int G, int WAVES, int UNR>
+__global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P, const float *__restrict__ q,
+                                                           const int *__restrict__ sel,
+                                                           const int *__restrict__ nsel, int sel_stride, int H,
+                                                           float scale, float *__restrict__ out)
 {
     constexpr int RL = HD / 8;                 // lanes per row
     constexpr int RPW = kWave / RL;            // rows per wave per step
-    constexpr int UNR = 8;                     // steps in flight
+    using Raw = typename RawRow<BF16>::T;
     __shared__ float qs[G][HD];
     __shared__ float sc[G][kFusedMaxPages * 17];
-    __shared__ float red[kFusedWaves][G][HD];
+    __shared__ float red[WAVES][G][HD];
     __shared__ float lsh[G];
     __shared__ int pphys[kFusedMaxPages], pnt[kFusedMaxPages];
 
@@ -306,7 +359,20 @@ __global__ __launch_bounds__(kFusedWaves * 64) void k_attn_fused(const be42_kv_p
 
     const int rsub = lane / RL, rl = lane % RL;   // row within the step, lane within the row
     const int T = ns * kPg;
-    const int rows_per_iter = kFusedWaves * RPW;
+    constexpr int rows_per_iter = WAVES * RPW;
+
+    auto load_raw = [&](const void *base, int r, float &sc_out) -> Raw {
+        const int rr = r < T ? r : T - 1;
+        const int pg = rr / kPg, t = rr % kPg;
+        const size_t slot = ((size_t)pphys[pg] * n_kv + kvh) * kPg + t;
+        if constexpr (BF16) {
+            sc_out = 1.0f;
+            return *(const Raw *)((const uint16_t *)base + slot * HD + rl * 8);
+        } else {
+            sc_out = (base == P.k ? P.k_scale : P.v_scale)[slot];
+            return *(const Raw *)((const int8_t *)base + slot * HD + rl * 8);
+        }
+    };
 
     // A. scores
     float qv[G][8];
@@ -316,29 +382,24 @@ __global__ __launch_bounds__(kFusedWaves * 64) void k_attn_fused(const be42_kv_p
         for (int j = 0; j < 8; j++)
             qv[g][j] = qs[g][rl * 8 + j];
     for (int r0 = wave * RPW; r0 < T; r0 += rows_per_iter * UNR) {
-        float kv[UNR][8];
+        Raw kr[UNR];
+        float ks[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; u++)
+            kr[u] = load_raw(P.k, r0 + u * rows_per_iter + rsub, ks[u]);
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
             const int r = r0 + u * rows_per_iter + rsub;
-            const int rr = r < T ? r : T - 1;
-            const int pg = rr / kPg, t = rr % kPg;
-            const size_t slot = ((size_t)pphys[pg] * n_kv + kvh) * kPg + t;
-            load_row_f32(kv[u], P.k, slot * HD + rl * 8, 8, BF16, BF16 ? 1.0f : P.k_scale[slot]);
-        }
-#pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            const int r = r0 + u * rows_per_iter + rsub;
+            float kv[8];
+            raw_to_f32<BF16>(kv, kr[u], ks[u]);
             float acc[G];
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 float a = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 8; j++)
-                    a = __fmaf_rn(qv[g][j], kv[u][j], a);
-#pragma unroll
-                for (int x = 1; x < RL; x <<= 1)
-                    a += __shfl_xor(a, x, RL);
-                acc[g] = a;
+                    a = __fmaf_rn(qv[g][j], kv[j], a);
+                acc[g] = group_sum<RL>(a);
             }
             if (rl == 0 && r < T) {
                 const int pg = r / kPg, t = r % kPg;
@@ -351,7 +412,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void k_attn_fused(const be42_kv_p
     __syncthreads();
 
     // B. weights, wave g <-> head g, lane <-> page
-    for (int g = wave; g < G; g += kFusedWaves) {
+    for (int g = wave; g < G; g += WAVES) {
         float *s = sc[g];
         const int nt = lane < ns ? pnt[lane] : 0;
         float lm = -INFINITY;
@@ -415,27 +476,25 @@ __global__ __launch_bounds__(kFusedWaves * 64) void k_attn_fused(const be42_kv_p
         for (int j = 0; j < 8; j++)
             o[g][j] = 0.0f;
     for (int r0 = wave * RPW; r0 < T; r0 += rows_per_iter * UNR) {
-        float vv[UNR][8];
+        Raw vr[UNR];
+        float vsc[UNR];
 #pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            const int r = r0 + u * rows_per_iter + rsub;
-            const int rr = r < T ? r : T - 1;
-            const int pg = rr / kPg, t = rr % kPg;
-            const size_t slot = ((size_t)pphys[pg] * n_kv + kvh) * kPg + t;
-            load_row_f32(vv[u], P.v, slot * HD + rl * 8, 8, BF16, BF16 ? 1.0f : P.v_scale[slot]);
-        }
+        for (int u = 0; u < UNR; u++)
+            vr[u] = load_raw(P.v, r0 + u * rows_per_iter + rsub, vsc[u]);
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
             const int r = r0 + u * rows_per_iter + rsub;
             if (r < T) {
                 const int pg = r / kPg, t = r % kPg;
                 if (t < pnt[pg]) {
+                    float vv[8];
+                    raw_to_f32<BF16>(vv, vr[u], vsc[u]);
 #pragma unroll
                     for (int g = 0; g < G; g++) {
                         const float w = sc[g][pg * 17 + t];
 #pragma unroll
                         for (int j = 0; j < 8; j++)
-                            o[g][j] = __fmaf_rn(w, vv[u][j], o[g][j]);
+                            o[g][j] = __fmaf_rn(w, vv[j], o[g][j]);
                     }
                 }
             }
@@ -462,24 +521,37 @@ __global__ __launch_bounds__(kFusedWaves * 64) void k_attn_fused(const be42_kv_p
         const int g = i / HD, d = i % HD;
         float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kFusedWaves; w++)
+        for (int w = 0; w < WAVES; w++)
             v += red[w][g][d];
         const float l = lsh[g];
         out[((size_t)b * H + kvh * G + g) * HD + d] = l > 0.0f ? v * (1.0f / l) : v;
     }
 }
 
+// 16 waves when the grid is small (more loads in flight per workgroup), 8
+// waves once there are enough workgroups to fill the chip.
+template <bool BF16, int HD, int G>
+static void launch_fused_g(const be42_kv_pool &P, const float *q, const int *sel, const int *nsel, int sel_stride,
+                           int B, int H, float scale, float *out, hipStream_t s)
+{
+    const dim3 grid(B, P.n_kv);
+    if ((long)B * P.n_kv < 512)
+        hipLaunchKernelGGL((k_attn_fused<BF16, HD, G, 16, 8>), grid, dim3(1024), 0, s, P, q, sel, nsel, sel_stride,
+                           H, scale, out);
+    else
+        hipLaunchKernelGGL((k_attn_fused<BF16, HD, G, 8, 8>), grid, dim3(512), 0, s, P, q, sel, nsel, sel_stride, H,
+                           scale, out);
+}
+
 template <bool BF16, int HD>
 static bool launch_fused_hd(const be42_kv_pool &P, const float *q, const int *sel, const int *nsel, int sel_stride,
                             int B, int H, float scale, float *out, hipStream_t s)
 {
-    const int G = H / P.n_kv;
-    const dim3 grid(B, P.n_kv), blk(kFusedWaves * 64);
-    switch (G) {
-    case 1: hipLaunchKernelGGL((k_attn_fused<BF16, HD, 1>), grid, blk, 0, s, P, q, sel, nsel, sel_stride, H, scale, out); return true;
-    case 2: hipLaunchKernelGGL((k_attn_fused<BF16, HD, 2>), grid, blk, 0, s, P, q, sel, nsel, sel_stride, H, scale, out); return true;
-    case 3: hipLaunchKernelGGL((k_attn_fused<BF16, HD, 3>), grid, blk, 0, s, P, q, sel, nsel, sel_stride, H, scale, out); return true;
-    case 4: hipLaunchKernelGGL((k_attn_fused<BF16, HD, 4>), grid, blk, 0, s, P, q, sel, nsel, sel_stride, H, scale, out); return true;
+    switch (H / P.n_kv) {
+    case 1: launch_fused_g<BF16, HD, 1>(P, q, sel, nsel, sel_stride, B, H, scale, out, s); return true;
+    case 2: launch_fused_g<BF16, HD, 2>(P, q, sel, nsel, sel_stride, B, H, scale, out, s); return true;
+    case 3: launch_fused_g<BF16, HD, 3>(P, q, sel, nsel, sel_stride, B, H, scale, out, s); return true;
+    case 4: launch_fused_g<BF16, HD, 4>(P, q, sel, nsel, sel_stride, B, H, scale, out, s); return true;
     default: return false;
     }
 }

@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "be42_common.h"
+#include "xdigits.h"
 
 namespace be42 {
 
@@ -48,16 +49,58 @@ __global__ __launch_bounds__(256) void k_embed(float *__restrict__ x, const uint
     x[(size_t)b * dim + i] = v * emb_s[tok];
 }
 
-// out = rmsnorm(x [+ delta]) per row; with delta, x is updated in place first
-// (the residual add of inference.c:525/:577 fused with the next norm).
-__global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ out, float *__restrict__ x,
-                                                 const float *__restrict__ delta, const uint16_t *__restrict__ w,
-                                                 int dim, float eps)
+// block-wide max of non-negative values (blockDim.x a multiple of 64, <= 1024)
+__device__ __forceinline__ float block_max(float v, float *red)
+{
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0)
+        red[wave] = v;
+    __syncthreads();
+    float r = 0.0f;
+    for (int w = 0; w < nw; w++)
+        r = fmaxf(r, red[w]);
+    return r;
+}
+
+// Write row b of the GEMV digit planes from LDS values v[0..K) (zero past K).
+template <bool FP8>
+__device__ __forceinline__ void row_digits(const float *v, int K, uint8_t *dig, int B, int b, float *red)
+{
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < K; i += blockDim.x)
+        m = fmaxf(m, fabsf(v[i]));
+    const float amax = block_max(m, red);
+    const float s = digit_scale<FP8>(amax);
+    const int Kp = (int)xdig_kp(K, FP8);
+    if (threadIdx.x == 0)
+        xdig_scales(dig, K, B, FP8)[b] = s;
+    for (int k0 = threadIdx.x * 4; k0 < Kp; k0 += blockDim.x * 4) {
+        float xe[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            xe[e] = k0 + e < K ? v[k0 + e] : 0.0f;
+        store_digit_words<FP8>(xe, s, dig, B, Kp, b, k0);
+    }
+}
+
+// xn = rmsnorm(x [+ delta]) per row b, written as GEMV digit planes (and, if
+// out != NULL, as fp32); with delta, x is updated in place first (the
+// residual add of inference.c:525/:577 fused with the next norm).  The sum
+// of squares follows compute_rms_f32_avx2: 8 FMA chains (chain l over
+// i = l (mod 8), in order), ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7)), fused
+// scalar remainder; ss / dim; inv = 1 / sqrtf(ss + eps); (x * inv) * w.
+template <bool FP8>
+__global__ __launch_bounds__(1024) void k_rmsnorm(float *__restrict__ out, uint8_t *__restrict__ dig,
+                                                 float *__restrict__ x, const float *__restrict__ delta,
+                                                 const uint16_t *__restrict__ w, int dim, int B, float eps)
 {
     extern __shared__ float xs[];
-    __shared__ float inv_s;
-    float *xr = x + (size_t)blockIdx.x * dim;
-    const float *dr = delta ? delta + (size_t)blockIdx.x * dim : nullptr;
+    __shared__ float inv_s, red[16];
+    const int b = blockIdx.x;
+    float *xr = x + (size_t)b * dim;
+    const float *dr = delta ? delta + (size_t)b * dim : nullptr;
     for (int i = threadIdx.x; i < dim; i += blockDim.x) {
         float v = xr[i];
         if (dr) {
@@ -72,11 +115,19 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ out, float 
         const int main = dim & ~7;
         float s = 0.0f;
         if (lane < 8) {
-#pragma unroll 16
-            for (int i = lane; i < main; i += 8)
-                s = __fmaf_rn(xs[i], xs[i], s);
+            // 32 elements of the chain are loaded before their 32 dependent FMAs
+            for (int c0 = 0; c0 < main; c0 += 8 * 32) {
+                float v[32];
+#pragma unroll
+                for (int j = 0; j < 32; j++) {
+                    const int i = c0 + lane + 8 * j;
+                    v[j] = i < main ? xs[i] : 0.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < 32; j++)
+                    s = __fmaf_rn(v[j], v[j], s);      // the zero padding adds exact zeros
+            }
         }
-        // ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7))
         const float t = s + __shfl_down(s, 4, 8);
         const float u = t + __shfl_down(t, 1, 8);
         float ss = u + __shfl_down(u, 2, 8);
@@ -89,9 +140,14 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ out, float 
     }
     __syncthreads();
     const float inv = inv_s;
-    float *orow = out + (size_t)blockIdx.x * dim;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x)
-        orow[i] = (xs[i] * inv) * bf16_to_f32(w[i]);
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+        const float v = (xs[i] * inv) * bf16_to_f32(w[i]);
+        xs[i] = v;
+        if (out)
+            out[(size_t)b * dim + i] = v;
+    }
+    __syncthreads();
+    row_digits<FP8>(xs, dim, dig, B, b, red);
 }
 
 // q [B][nq*hd], k [B][nk*hd] rotated at position pos (table rows [pos][hd/2])
@@ -111,27 +167,37 @@ __global__ __launch_bounds__(256) void k_rope(float *__restrict__ q, float *__re
     base[j + half] = __fmaf_rn(x0, s, x1 * c);
 }
 
-// out = (g * sigmoid(g)) * u over rows of n: blocks of 8 use the vector
-// Schraudolph exp (round to nearest), the n % 8 remainder the scalar one.
-__global__ __launch_bounds__(256) void k_silu_mul(float *__restrict__ out, const float *__restrict__ g,
-                                                  const float *__restrict__ u, int n, int rows)
+// h = (g * sigmoid(g)) * u for row b (op_silu_mul_fused_f32): blocks of 8 use
+// the vector Schraudolph exp (clamp, fused multiply-add, round to nearest),
+// the n % 8 remainder the scalar one; written as GEMV digit planes of the
+// down projection (and to out if not NULL).
+template <bool FP8>
+__global__ __launch_bounds__(1024) void k_silu_mul(float *__restrict__ out, uint8_t *__restrict__ dig,
+                                                   const float *__restrict__ g, const float *__restrict__ u, int n,
+                                                   int B)
 {
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)n * rows)
-        return;
-    const int i = (int)(idx % n);
-    const float gv = g[idx], uv = u[idx];
-    float e;
-    if (i < (n & ~7)) {
-        float x = 0.0f - gv;
-        x = fmaxf(x, -87.0f);
-        x = fminf(x, 87.0f);
-        e = __int_as_float(__float2int_rn(__fmaf_rn(x, 12102203.0f, 1065353216.0f)));
-    } else {
-        e = fast_expf(-gv);
+    extern __shared__ float hs[];
+    __shared__ float red[16];
+    const int b = blockIdx.x;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float gv = g[(size_t)b * n + i], uv = u[(size_t)b * n + i];
+        float e;
+        if (i < (n & ~7)) {
+            float xv = 0.0f - gv;
+            xv = fmaxf(xv, -87.0f);
+            xv = fminf(xv, 87.0f);
+            e = __int_as_float(__float2int_rn(__fmaf_rn(xv, 12102203.0f, 1065353216.0f)));
+        } else {
+            e = fast_expf(-gv);
+        }
+        const float sig = __fdiv_rn(1.0f, 1.0f + e);
+        const float h = (gv * sig) * uv;
+        hs[i] = h;
+        if (out)
+            out[(size_t)b * n + i] = h;
     }
-    const float sig = __fdiv_rn(1.0f, 1.0f + e);
-    out[idx] = (gv * sig) * uv;
+    __syncthreads();
+    row_digits<FP8>(hs, n, dig, B, b, red);
 }
 
 // argmax_simd_f32: the maximum value wins; among equal maxima in the
@@ -234,7 +300,8 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
     const be42_decoder_config &c = *cfg;
     BE42_CHECK(c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0 &&
                    c.head_dim > 0 && c.head_dim % 8 == 0 && c.hidden_dim > 0 && c.vocab > 0 && c.max_seq > 0 &&
-                   c.max_batch > 0 && c.max_batch <= kMaxBatch && c.dim % 16 == 0 && c.hidden_dim % 16 == 0 &&
+                   c.max_batch > 0 && c.max_batch <= 16 && c.dim % 16 == 0 && c.hidden_dim % 16 == 0 &&
+                   c.hidden_dim <= 40960 && c.dim <= 40960 &&
                    (c.n_heads * c.head_dim) % 16 == 0,
                "be42_decoder_create: unsupported shape");
     BE42_CHECK(c.wkind == 0 || c.wkind == 1, "be42_decoder_create: weight kind %d", c.wkind);
@@ -302,6 +369,26 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
         be42_decoder_destroy(d);
         return hip_fail(e, "be42_decoder_create", __FILE__, __LINE__);
     }
+    if ((size_t)c.hidden_dim * 4 > 65536) {
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)k_silu_mul<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    c.hidden_dim * 4);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)k_silu_mul<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    c.hidden_dim * 4);
+    }
+    if ((size_t)c.dim * 4 > 65536) {
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)k_rmsnorm<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    c.dim * 4);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)k_rmsnorm<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    c.dim * 4);
+    }
+    if (e != hipSuccess) {
+        be42_decoder_destroy(d);
+        return hip_fail(e, "be42_decoder_create", __FILE__, __LINE__);
+    }
     *out = d;
     return BE42_OK;
 }
@@ -364,7 +451,18 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
         hipLaunchKernelGGL(k_embed<false>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, ta,
                            dev_tok, dim);
     BE42_LAUNCH_CHECK();
-    const size_t norm_lds = (size_t)dim * 4;
+    const size_t norm_lds = (size_t)dim * 4, silu_lds = (size_t)c.hidden_dim * 4;
+    uint8_t *dig = (uint8_t *)d->xdig;
+    // RMSNorm (+ residual) straight into the GEMV digit planes
+    auto norm = [&](const uint16_t *wn, const float *delta) {
+        if (fp8)
+            hipLaunchKernelGGL(k_rmsnorm<true>, dim3(B), dim3(1024), norm_lds, st, nullptr, dig, d->x, delta, wn,
+                               dim, B, c.norm_eps);
+        else
+            hipLaunchKernelGGL(k_rmsnorm<false>, dim3(B), dim3(1024), norm_lds, st, nullptr, dig, d->x, delta, wn,
+                               dim, B, c.norm_eps);
+        return hipGetLastError();
+    };
     const float scale = 1.0f / sqrtf((float)hd);
     const float *pending = nullptr;   // residual delta not yet added to x
     int slot_ids[kMaxBatch], positions[kMaxBatch];
@@ -373,10 +471,7 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
     const int pages = pos / 16 + 1;
     for (int l = 0; l < c.n_layers; l++) {
         const be42_decoder_layer &L = d->w.layers[l];
-        hipLaunchKernelGGL(k_rmsnorm, dim3(B), dim3(256), norm_lds, st, d->xb, d->x, pending, L.attn_norm, dim,
-                           c.norm_eps);
-        BE42_LAUNCH_CHECK();
-        DEC_TRY(be42_gemv_prepare(d->xdig, d->xb, dim, B, fp8, st));
+        BE42_HIP(norm(L.attn_norm, pending));
         DEC_TRY(gemv(d, d->q, L.wq, L.sq, qd, dim, B, st));
         DEC_TRY(gemv(d, d->k, L.wk, L.sk, kd, dim, B, st));
         DEC_TRY(gemv(d, d->v, L.wv, L.sv, kd, dim, B, st));
@@ -412,26 +507,21 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
         }
         DEC_TRY(be42_gemv_prepare(d->xdig, d->att, qd, B, fp8, st));
         DEC_TRY(gemv(d, d->xb, L.wo, L.so, dim, qd, B, st));
-        // x += xb; xn = rmsnorm(x)
-        hipLaunchKernelGGL(k_rmsnorm, dim3(B), dim3(256), norm_lds, st, d->xn, d->x, d->xb, L.ffn_norm, dim,
-                           c.norm_eps);
-        BE42_LAUNCH_CHECK();
-        DEC_TRY(be42_gemv_prepare(d->xdig, d->xn, dim, B, fp8, st));
+        BE42_HIP(norm(L.ffn_norm, d->xb));                 // x += attention output
         DEC_TRY(gemv(d, d->hb, L.w1, L.s1, c.hidden_dim, dim, B, st));
         DEC_TRY(gemv(d, d->hb2, L.w3, L.s3, c.hidden_dim, dim, B, st));
-        const size_t nh = (size_t)B * c.hidden_dim;
-        hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((nh + 255) / 256)), dim3(256), 0, st, d->hb, d->hb, d->hb2,
-                           c.hidden_dim, B);
+        if (fp8)
+            hipLaunchKernelGGL(k_silu_mul<true>, dim3(B), dim3(1024), silu_lds, st, nullptr, dig, d->hb, d->hb2,
+                               c.hidden_dim, B);
+        else
+            hipLaunchKernelGGL(k_silu_mul<false>, dim3(B), dim3(1024), silu_lds, st, nullptr, dig, d->hb, d->hb2,
+                               c.hidden_dim, B);
         BE42_LAUNCH_CHECK();
-        DEC_TRY(be42_gemv_prepare(d->xdig, d->hb, c.hidden_dim, B, fp8, st));
         DEC_TRY(gemv(d, d->xb, L.w2, L.s2, dim, c.hidden_dim, B, st));
         pending = d->xb;
     }
     // final residual + norm, lm_head, argmax
-    hipLaunchKernelGGL(k_rmsnorm, dim3(B), dim3(256), norm_lds, st, d->xn, d->x, pending, d->w.final_norm, dim,
-                       c.norm_eps);
-    BE42_LAUNCH_CHECK();
-    DEC_TRY(be42_gemv_prepare(d->xdig, d->xn, dim, B, fp8, st));
+    BE42_HIP(norm(d->w.final_norm, pending));
     float *lg = logits_out ? logits_out : d->logits;
     DEC_TRY(gemv(d, lg, d->w.out, d->w.out_s, c.vocab, dim, B, st));
     hipLaunchKernelGGL(k_argmax, dim3(B), dim3(1024), 0, st, d->next, lg, c.vocab);

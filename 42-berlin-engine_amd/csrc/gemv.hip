@@ -23,25 +23,9 @@
 #include <type_traits>
 
 #include "be42_common.h"
+#include "xdigits.h"
 
 namespace be42 {
-
-constexpr int kI8Digits = 3;
-constexpr int kI8Base = 254;
-constexpr int kF8Digits = 5;
-constexpr int kF8Base = 30;
-
-// integer in [-15, 15] -> exact E4M3 code
-__device__ __forceinline__ uint8_t small_int_to_e4m3(int n)
-{
-    const uint32_t s = n < 0 ? 0x80u : 0u;
-    int a = n < 0 ? -n : n;
-    if (a == 0)
-        return 0;
-    int e = 31 - __clz(a);               // floor(log2 a), 0..3
-    int m = (a << (3 - e)) & 7;          // 3 mantissa bits below the leading one
-    return (uint8_t)(s | ((uint32_t)(e + 7) << 3) | (uint32_t)m);
-}
 
 // Digit planes of the activations.  Grid (chunks of kPrepChunk k, batch):
 // every block recomputes the row absmax (x is small and L2-resident), then
@@ -83,36 +67,15 @@ __global__ __launch_bounds__(256) void k_gemv_prep(const float *__restrict__ x, 
         red[threadIdx.x >> 6] = m;
     __syncthreads();
     const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    constexpr int R0 = FP8 ? 15 : 127;
-    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
-    constexpr float BASE = FP8 ? (float)kF8Base : (float)kI8Base;
-    const float s = amax > 0.0f ? amax / (float)R0 : 1.0f;
+    const float s = digit_scale<FP8>(amax);
     if (blockIdx.x == 0 && threadIdx.x == 0)
         sx[b] = s;
     const int k0 = blockIdx.x * kPrepChunk + threadIdx.x * 4;
     if (k0 >= Kp)
         return;
-    uint32_t word[ND];
-#pragma unroll
-    for (int d = 0; d < ND; d++)
-        word[d] = 0;
     const float4 xv4 = k0 < K ? *(const float4 *)(xr + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
     const float xe[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        float v = xe[e] / s;
-#pragma unroll
-        for (int d = 0; d < ND; d++) {
-            float dv = rintf(v);
-            dv = fminf(fmaxf(dv, -(float)R0), (float)R0);
-            v = (v - dv) * BASE;
-            const uint32_t code = FP8 ? small_int_to_e4m3((int)dv) : (uint32_t)(uint8_t)(int8_t)(int)dv;
-            word[d] |= code << (8 * e);
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < ND; d++)
-        *(uint32_t *)(dig + ((size_t)d * B + b) * Kp + k0) = word[d];
+    store_digit_words<FP8>(xe, s, dig, B, Kp, b, k0);
 }
 
 __constant__ double kF8Weight[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 27000, 1.0 / 810000};
@@ -217,9 +180,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(
                     }
                 }
     };
-    // Ping-pong over two register sets: the loads of burst i+1 are issued
-    // before the MFMAs of burst i (the scheduling barriers keep that order),
-    // so a wave always has one burst in flight while it computes.
+    // One burst in flight per wave; the latency is hidden by the other
+    // resident waves (occupancy), not by software pipelining.
     for (int bi = b0; bi < b1; bi++) {
         load(bi, wv, xv);
         compute(wv, xv);
@@ -298,27 +260,6 @@ __global__ __launch_bounds__(256) void k_gemv_generic(float *y, const uint8_t *W
             y[(size_t)b * N + row] = ((red[0] + red[1]) + (red[2] + red[3])) * sw[row];
         __syncthreads();
     }
-}
-
-// Activation digit planes: layout of the buffer filled by be42_gemv_prepare.
-// Kp is K rounded up to the largest burst any tile configuration uses.
-struct XDigits {
-    int nd, step, burst;
-};
-static XDigits xdig_layout(bool fp8)
-{
-    return fp8 ? XDigits{kF8Digits, 128, 128 * 8} : XDigits{kI8Digits, 64, 64 * 16};
-}
-static size_t xdig_kp(int k, bool fp8)
-{
-    const XDigits L = xdig_layout(fp8);
-    return ((size_t)(k + L.burst - 1) / L.burst) * L.burst;
-}
-// digits first, then 16 float scales on a 256-byte boundary
-static size_t xdig_bytes(int k, int batch, bool fp8)
-{
-    const size_t dig = (size_t)xdig_layout(fp8).nd * batch * xdig_kp(k, fp8);
-    return ((dig + 255) & ~(size_t)255) + 16 * sizeof(float);
 }
 
 static int prepare_launch(void *buf, const float *x, int k, int batch, bool fp8, hipStream_t s)

@@ -1,0 +1,96 @@
+// xdigits.h -- activation digit planes of the MFMA GEMV.
+//
+// The GEMV feeds raw INT8 / E4M3 weight codes to the matrix cores; the fp32
+// activations are split once per call into exact fixed-point digits of the
+// MFMA input type:
+//     x[b][k] = s_b * sum_d digit_d[b][k] * R^-d
+//   INT8: 3 digits in [-127, 127], R = 254, s_b = max|x_b| / 127
+//   FP8:  5 integer digits in [-15, 15] stored as exact E4M3 codes, R = 30,
+//         s_b = max|x_b| / 15
+// (to ~2^-24 relative to max|x_b|).  Buffer layout: digit planes
+// dig[d][b][0..Kp) bytes (zero past K), then, on a 256-byte boundary, 16
+// floats s_b.  Kp is K rounded up to the largest burst a GEMV tile uses.
+#pragma once
+
+#include "be42_common.h"
+
+namespace be42 {
+
+constexpr int kI8Digits = 3;
+constexpr int kI8Base = 254;
+constexpr int kF8Digits = 5;
+constexpr int kF8Base = 30;
+
+// integer in [-15, 15] -> exact E4M3 code
+__device__ __forceinline__ uint8_t small_int_to_e4m3(int n)
+{
+    const uint32_t s = n < 0 ? 0x80u : 0u;
+    int a = n < 0 ? -n : n;
+    if (a == 0)
+        return 0;
+    int e = 31 - __clz(a);               // floor(log2 a), 0..3
+    int m = (a << (3 - e)) & 7;          // 3 mantissa bits below the leading one
+    return (uint8_t)(s | ((uint32_t)(e + 7) << 3) | (uint32_t)m);
+}
+
+template <bool FP8>
+__device__ __forceinline__ float digit_scale(float amax)
+{
+    return amax > 0.0f ? amax / (FP8 ? 15.0f : 127.0f) : 1.0f;
+}
+
+// digits of x[b][k0 .. k0+4) (xe), one 32-bit word per plane
+template <bool FP8>
+__device__ __forceinline__ void store_digit_words(const float xe[4], float s, uint8_t *__restrict__ dig, int B,
+                                                  int Kp, int b, int k0)
+{
+    constexpr int R0 = FP8 ? 15 : 127;
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr float BASE = FP8 ? (float)kF8Base : (float)kI8Base;
+    uint32_t word[ND];
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+        word[d] = 0;
+    const float rs = 1.0f / s;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float v = xe[e] * rs;
+#pragma unroll
+        for (int d = 0; d < ND; d++) {
+            float dv = rintf(v);
+            dv = fminf(fmaxf(dv, -(float)R0), (float)R0);
+            v = (v - dv) * BASE;
+            const uint32_t code = FP8 ? small_int_to_e4m3((int)dv) : (uint32_t)(uint8_t)(int8_t)(int)dv;
+            word[d] |= code << (8 * e);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+        *(uint32_t *)(dig + ((size_t)d * B + b) * Kp + k0) = word[d];
+}
+
+struct XDigits {
+    int nd, step, burst;
+};
+__host__ __device__ inline XDigits xdig_layout(bool fp8)
+{
+    return fp8 ? XDigits{kF8Digits, 128, 128 * 8} : XDigits{kI8Digits, 64, 64 * 16};
+}
+__host__ __device__ inline size_t xdig_kp(int k, bool fp8)
+{
+    const XDigits L = xdig_layout(fp8);
+    return ((size_t)(k + L.burst - 1) / L.burst) * L.burst;
+}
+// digits first, then 16 float scales on a 256-byte boundary
+__host__ __device__ inline size_t xdig_bytes(int k, int batch, bool fp8)
+{
+    const size_t dig = (size_t)xdig_layout(fp8).nd * batch * xdig_kp(k, fp8);
+    return ((dig + 255) & ~(size_t)255) + 16 * sizeof(float);
+}
+__host__ __device__ inline float *xdig_scales(void *buf, int k, int batch, bool fp8)
+{
+    const size_t dig = (size_t)xdig_layout(fp8).nd * batch * xdig_kp(k, fp8);
+    return (float *)((uint8_t *)buf + ((dig + 255) & ~(size_t)255));
+}
+
+}  // namespace be42
