@@ -39,6 +39,7 @@ SIGNATURES = {
     "be42_gemv_prepare": (i32, [vp, vp, i32, i32, i32, vp]),
     "be42_gemv_q8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemv_fp8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "be42_gemv_prepared_multi": (i32, [vp, i32, vp, i32, i32, i32, vp]),
     "be42_gemm_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_decoder_create": (i32, [vp, vp, vp, vp]),
@@ -66,6 +67,10 @@ SIGNATURES = {
 }
 
 KV_INT8, KV_BF16 = 0, 1
+
+
+class GemvSeg(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("w_scale", C.c_void_p), ("y", C.c_void_p), ("n", C.c_int)]
 
 
 class DecoderConfig(C.Structure):
@@ -203,6 +208,17 @@ class Lib:
         name = "be42_gemv_q8_prepared" if kind == "int8" else "be42_gemv_fp8_prepared"
         self._call(name, self.p(out), self.p(w), self.p(sw), self.p(xdig), n, k, batch, self.stream(stream))
         return out
+
+    def gemv_prepared_multi(self, segs, xdig, batch, kind, stream=None):
+        """segs: [(w [n][k], w_scale [n], out [batch][n])], up to 3, one launch."""
+        k = segs[0][0].shape[1]
+        arr = (GemvSeg * len(segs))()
+        for i, (w, sw, out) in enumerate(segs):
+            assert w.shape[1] == k
+            arr[i] = GemvSeg(self.p(w), self.p(sw), self.p(out), w.shape[0])
+        self._call("be42_gemv_prepared_multi", C.addressof(arr), len(segs), self.p(xdig), k, batch,
+                   1 if kind == "fp8" else 0, self.stream(stream))
+        return [s[2] for s in segs]
 
 
     # -- prefill GEMM -----------------------------------------------------------

@@ -18,32 +18,40 @@
 // MFMA GEMVs (fp32-accurate), attention is the fused paged attention (dense
 // while a layer has <= sparse_k pages, else the LSH route).
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <vector>
 
 #include "be42_common.h"
+#include "paged_step.h"
 #include "xdigits.h"
 
 namespace be42 {
 
-constexpr int kMaxBatch = 64;
+constexpr int kMaxBatch = 16;
 
-struct TokArgs {
-    int tok[kMaxBatch];
+// Parameters of one step, written by the host into pinned memory and copied
+// to the device at the start of the step: with them in device memory the
+// launch sequence of a step is the same for every position, so it is
+// captured once as a HIP graph and replayed.
+struct StepHead {
+    int pos;
+    int tokens[kMaxBatch];
 };
 
-// tokens from the kernel argument, or (dev_tok != NULL) from the device
-// argmax of the previous step
+// tokens from device memory: the step's parameters, or the previous step's
+// argmax
 template <bool FP8>
 __global__ __launch_bounds__(256) void k_embed(float *__restrict__ x, const uint8_t *__restrict__ emb,
-                                               const float *__restrict__ emb_s, const TokArgs t,
-                                               const int *__restrict__ dev_tok, int dim)
+                                               const float *__restrict__ emb_s, const int *__restrict__ tok_p,
+                                               int dim)
 {
     const int b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= dim)
         return;
-    const int tok = dev_tok ? dev_tok[b] : t.tok[b];
+    const int tok = tok_p[b];
     const uint8_t c = emb[(size_t)tok * dim + i];
     const float v = FP8 ? fp8_to_f32(c) : (float)(int8_t)c;
     x[(size_t)b * dim + i] = v * emb_s[tok];
@@ -64,24 +72,36 @@ __device__ __forceinline__ float block_max(float v, float *red)
     return r;
 }
 
-// Write row b of the GEMV digit planes from LDS values v[0..K) (zero past K).
-template <bool FP8>
-__device__ __forceinline__ void row_digits(const float *v, int K, uint8_t *dig, int B, int b, float *red)
+// Row kernels (one block of kRowThreads per batch row) keep the row in
+// registers: thread t owns the float4 number t + kRowThreads * j (j < NV) of
+// the row, and every global load of the row is issued before the first is
+// waited on -- one memory round trip per kernel instead of one per loop trip.
+// NV = ceil(n / 4096) covers rows up to kRowMax elements (n % 16 == 0).
+constexpr int kRowThreads = 1024;
+constexpr int kRowMax = 4 * 4 * kRowThreads;
+
+__device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// Write row b of the GEMV digit planes from the row's registers (zero past n).
+template <bool FP8, int NV>
+__device__ __forceinline__ void row_digits_reg(const float4 (&h)[NV], int n, uint8_t *dig, int B, int b, float *red)
 {
     float m = 0.0f;
-    for (int i = threadIdx.x; i < K; i += blockDim.x)
-        m = fmaxf(m, fabsf(v[i]));
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(h[j].x), fabsf(h[j].y)), fmaxf(fabsf(h[j].z), fabsf(h[j].w))));
     const float amax = block_max(m, red);
     const float s = digit_scale<FP8>(amax);
-    const int Kp = (int)xdig_kp(K, FP8);
+    const int Kp = (int)xdig_kp(n, FP8);
     if (threadIdx.x == 0)
-        xdig_scales(dig, K, B, FP8)[b] = s;
-    for (int k0 = threadIdx.x * 4; k0 < Kp; k0 += blockDim.x * 4) {
-        float xe[4];
+        xdig_scales(dig, n, B, FP8)[b] = s;
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            xe[e] = k0 + e < K ? v[k0 + e] : 0.0f;
-        store_digit_words<FP8>(xe, s, dig, B, Kp, b, k0);
+    for (int j = 0; j < NV; j++) {
+        const int k0 = 4 * ((int)threadIdx.x + kRowThreads * j);
+        if (k0 < Kp) {
+            const float xe[4] = {h[j].x, h[j].y, h[j].z, h[j].w};
+            store_digit_words<FP8>(xe, s, dig, B, Kp, b, k0);
+        }
     }
 }
 
@@ -91,48 +111,62 @@ __device__ __forceinline__ void row_digits(const float *v, int K, uint8_t *dig, 
 // of squares follows compute_rms_f32_avx2: 8 FMA chains (chain l over
 // i = l (mod 8), in order), ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7)), fused
 // scalar remainder; ss / dim; inv = 1 / sqrtf(ss + eps); (x * inv) * w.
-template <bool FP8>
-__global__ __launch_bounds__(1024) void k_rmsnorm(float *__restrict__ out, uint8_t *__restrict__ dig,
-                                                 float *__restrict__ x, const float *__restrict__ delta,
-                                                 const uint16_t *__restrict__ w, int dim, int B, float eps)
+// The chains run on 8 lanes from LDS (xs, dim rounded up to 256 with zeros,
+// whose products add exact zeros), 32 loads ahead of their FMAs.
+template <bool FP8, int NV>
+__global__ __launch_bounds__(kRowThreads) void k_rmsnorm(float *__restrict__ out, uint8_t *__restrict__ dig,
+                                                        float *__restrict__ x, const float *__restrict__ delta,
+                                                        const uint16_t *__restrict__ w, int dim, int B, float eps)
 {
     extern __shared__ float xs[];
     __shared__ float inv_s, red[16];
-    const int b = blockIdx.x;
-    float *xr = x + (size_t)b * dim;
-    const float *dr = delta ? delta + (size_t)b * dim : nullptr;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
-        float v = xr[i];
-        if (dr) {
-            v = v + dr[i];
-            xr[i] = v;
+    const int b = blockIdx.x, n4 = dim >> 2, dimp = (dim + 255) & ~255;
+    float4 *x4 = (float4 *)(x + (size_t)b * dim);
+    const float4 *d4 = delta ? (const float4 *)(delta + (size_t)b * dim) : nullptr;
+    const uint2 *w4 = (const uint2 *)w;
+    float4 v[NV], dv[NV];
+    uint2 wv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = min((int)threadIdx.x + kRowThreads * j, n4 - 1);
+        v[j] = x4[i];
+        wv[j] = w4[i];
+        if (d4)
+            dv[j] = d4[i];
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + kRowThreads * j;
+        if (d4) {
+            v[j] = make_float4(v[j].x + dv[j].x, v[j].y + dv[j].y, v[j].z + dv[j].z, v[j].w + dv[j].w);
+            if (i < n4)
+                x4[i] = v[j];
         }
-        xs[i] = v;
+        if (i >= n4)
+            v[j] = f4_zero();
+        if (4 * i < dimp)
+            ((float4 *)xs)[i] = v[j];
     }
     __syncthreads();
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
-        const int main = dim & ~7;
         float s = 0.0f;
         if (lane < 8) {
-            // 32 elements of the chain are loaded before their 32 dependent FMAs
-            for (int c0 = 0; c0 < main; c0 += 8 * 32) {
-                float v[32];
-#pragma unroll
-                for (int j = 0; j < 32; j++) {
-                    const int i = c0 + lane + 8 * j;
-                    v[j] = i < main ? xs[i] : 0.0f;
-                }
+            for (int c0 = 0; c0 < dimp; c0 += 8 * 32) {
+                float t[32];
 #pragma unroll
                 for (int j = 0; j < 32; j++)
-                    s = __fmaf_rn(v[j], v[j], s);      // the zero padding adds exact zeros
+                    t[j] = xs[c0 + lane + 8 * j];
+#pragma unroll
+                for (int j = 0; j < 32; j++)
+                    s = __fmaf_rn(t[j], t[j], s);
             }
         }
         const float t = s + __shfl_down(s, 4, 8);
         const float u = t + __shfl_down(t, 1, 8);
         float ss = u + __shfl_down(u, 2, 8);
         if (lane == 0) {
-            for (int i = main; i < dim; i++)
+            for (int i = dim & ~7; i < dim; i++)
                 ss = __fmaf_rn(xs[i], xs[i], ss);
             ss = __fdiv_rn(ss, (float)dim);
             inv_s = __fdiv_rn(1.0f, __fsqrt_rn(ss + eps));
@@ -140,21 +174,32 @@ __global__ __launch_bounds__(1024) void k_rmsnorm(float *__restrict__ out, uint8
     }
     __syncthreads();
     const float inv = inv_s;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
-        const float v = (xs[i] * inv) * bf16_to_f32(w[i]);
-        xs[i] = v;
-        if (out)
-            out[(size_t)b * dim + i] = v;
+    float4 h[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + kRowThreads * j;
+        const uint2 wj = wv[j];
+        h[j] = make_float4((v[j].x * inv) * bf16_to_f32((uint16_t)(wj.x & 0xFFFF)),
+                           (v[j].y * inv) * bf16_to_f32((uint16_t)(wj.x >> 16)),
+                           (v[j].z * inv) * bf16_to_f32((uint16_t)(wj.y & 0xFFFF)),
+                           (v[j].w * inv) * bf16_to_f32((uint16_t)(wj.y >> 16)));
+        if (i >= n4)
+            h[j] = f4_zero();
+        else if (out)
+            ((float4 *)(out + (size_t)b * dim))[i] = h[j];
     }
-    __syncthreads();
-    row_digits<FP8>(xs, dim, dig, B, b, red);
+    row_digits_reg<FP8, NV>(h, dim, dig, B, b, red);
 }
 
-// q [B][nq*hd], k [B][nk*hd] rotated at position pos (table rows [pos][hd/2])
+// q [B][nq*hd], k [B][nk*hd] rotated at position *pos (table rows
+// [pos][hd/2]); positions at or past the table (rope_len) are not rotated.
 __global__ __launch_bounds__(256) void k_rope(float *__restrict__ q, float *__restrict__ k,
                                               const float *__restrict__ cos_t, const float *__restrict__ sin_t,
-                                              int pos, int nq, int nk, int hd)
+                                              const int *__restrict__ pos_p, int rope_len, int nq, int nk, int hd)
 {
+    const int pos = *pos_p;
+    if (pos >= rope_len)
+        return;
     const int half = hd / 2, b = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (nq + nk) * half)
@@ -171,33 +216,48 @@ __global__ __launch_bounds__(256) void k_rope(float *__restrict__ q, float *__re
 // the vector Schraudolph exp (clamp, fused multiply-add, round to nearest),
 // the n % 8 remainder the scalar one; written as GEMV digit planes of the
 // down projection (and to out if not NULL).
-template <bool FP8>
-__global__ __launch_bounds__(1024) void k_silu_mul(float *__restrict__ out, uint8_t *__restrict__ dig,
-                                                   const float *__restrict__ g, const float *__restrict__ u, int n,
-                                                   int B)
+__device__ __forceinline__ float silu_mul1(float gv, float uv, bool vec)
 {
-    extern __shared__ float hs[];
-    __shared__ float red[16];
-    const int b = blockIdx.x;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float gv = g[(size_t)b * n + i], uv = u[(size_t)b * n + i];
-        float e;
-        if (i < (n & ~7)) {
-            float xv = 0.0f - gv;
-            xv = fmaxf(xv, -87.0f);
-            xv = fminf(xv, 87.0f);
-            e = __int_as_float(__float2int_rn(__fmaf_rn(xv, 12102203.0f, 1065353216.0f)));
-        } else {
-            e = fast_expf(-gv);
-        }
-        const float sig = __fdiv_rn(1.0f, 1.0f + e);
-        const float h = (gv * sig) * uv;
-        hs[i] = h;
-        if (out)
-            out[(size_t)b * n + i] = h;
+    float e;
+    if (vec) {
+        float xv = 0.0f - gv;
+        xv = fmaxf(xv, -87.0f);
+        xv = fminf(xv, 87.0f);
+        e = __int_as_float(__float2int_rn(__fmaf_rn(xv, 12102203.0f, 1065353216.0f)));
+    } else {
+        e = fast_expf(-gv);
     }
-    __syncthreads();
-    row_digits<FP8>(hs, n, dig, B, b, red);
+    const float sig = __fdiv_rn(1.0f, 1.0f + e);
+    return (gv * sig) * uv;
+}
+
+template <bool FP8, int NV>
+__global__ __launch_bounds__(kRowThreads) void k_silu_mul(float *__restrict__ out, uint8_t *__restrict__ dig,
+                                                         const float *__restrict__ g, const float *__restrict__ u,
+                                                         int n, int B)
+{
+    __shared__ float red[16];
+    const int b = blockIdx.x, n4 = n >> 2, nvec = n & ~7;
+    const float4 *g4 = (const float4 *)(g + (size_t)b * n), *u4 = (const float4 *)(u + (size_t)b * n);
+    float4 gv[NV], uv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = min((int)threadIdx.x + kRowThreads * j, n4 - 1);
+        gv[j] = g4[i];
+        uv[j] = u4[i];
+    }
+    float4 h[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + kRowThreads * j, e0 = 4 * i;
+        h[j] = make_float4(silu_mul1(gv[j].x, uv[j].x, e0 < nvec), silu_mul1(gv[j].y, uv[j].y, e0 + 1 < nvec),
+                           silu_mul1(gv[j].z, uv[j].z, e0 + 2 < nvec), silu_mul1(gv[j].w, uv[j].w, e0 + 3 < nvec));
+        if (i >= n4)
+            h[j] = f4_zero();
+        else if (out)
+            ((float4 *)(out + (size_t)b * n))[i] = h[j];
+    }
+    row_digits_reg<FP8, NV>(h, n, dig, B, b, red);
 }
 
 // argmax_simd_f32: the maximum value wins; among equal maxima in the
@@ -284,6 +344,29 @@ struct be42_decoder {
     int *cand = nullptr, *ncand = nullptr;
     float *capture_q = nullptr;   // optional [n_layers][max_batch][n_heads * head_dim]
     int *capture_nsel = nullptr;  // optional [n_layers][max_batch] pages attended
+    // step parameters: StepHead then AppendStepArgs[n_layers], two pinned host
+    // copies (steps alternate, so the host never rewrites a buffer a queued
+    // step still has to read) and their device copies
+    size_t params_bytes = 0;
+    void *params_host[2] = {nullptr, nullptr}, *params_dev[2] = {nullptr, nullptr};
+    hipEvent_t params_free[2] = {nullptr, nullptr};
+    int parity = 0;
+    int *next_host = nullptr;     // pinned copy of the argmax
+    hipStream_t gstream = nullptr;
+    hipEvent_t ev_in = nullptr, ev_out = nullptr;
+    struct Key {
+        int batch = -1, sparse = -1, dev_tokens = -1;
+        const float *logits = nullptr;
+        const float *cq = nullptr;
+        const int *cn = nullptr;
+        bool operator==(const Key &o) const
+        {
+            return batch == o.batch && sparse == o.sparse && dev_tokens == o.dev_tokens && logits == o.logits &&
+                   cq == o.cq && cn == o.cn;
+        }
+    } key[2];
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
+    bool use_graph = true;
 };
 
 static int dec_fail(be42_decoder *d, int rc)
@@ -300,7 +383,7 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
     const be42_decoder_config &c = *cfg;
     BE42_CHECK(c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0 &&
                    c.head_dim > 0 && c.head_dim % 8 == 0 && c.hidden_dim > 0 && c.vocab > 0 && c.max_seq > 0 &&
-                   c.max_batch > 0 && c.max_batch <= 16 && c.dim % 16 == 0 && c.hidden_dim % 16 == 0 &&
+                   c.max_batch > 0 && c.max_batch <= 16 && c.dim % 16 == 0 && c.hidden_dim % 16 == 0 && c.dim <= kRowMax && c.hidden_dim <= kRowMax &&
                    c.hidden_dim <= 40960 && c.dim <= 40960 &&
                    (c.n_heads * c.head_dim) % 16 == 0,
                "be42_decoder_create: unsupported shape");
@@ -369,21 +452,27 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
         be42_decoder_destroy(d);
         return hip_fail(e, "be42_decoder_create", __FILE__, __LINE__);
     }
-    if ((size_t)c.hidden_dim * 4 > 65536) {
+    d->params_bytes = sizeof(StepHead) + (size_t)c.n_layers * sizeof(AppendStepArgs);
+    for (int i = 0; i < 2; i++) {
         if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *)k_silu_mul<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    c.hidden_dim * 4);
+            e = hipHostMalloc(&d->params_host[i], d->params_bytes, hipHostMallocDefault);
+        alloc(&d->params_dev[i], d->params_bytes);
         if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *)k_silu_mul<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    c.hidden_dim * 4);
+            e = hipEventCreateWithFlags(&d->params_free[i], hipEventDisableTiming);
     }
-    if ((size_t)c.dim * 4 > 65536) {
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *)k_rmsnorm<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    c.dim * 4);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *)k_rmsnorm<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    c.dim * 4);
+    if (e == hipSuccess)
+        e = hipHostMalloc((void **)&d->next_host, kMaxBatch * sizeof(int), hipHostMallocDefault);
+    if (e == hipSuccess)
+        e = hipStreamCreateWithFlags(&d->gstream, hipStreamNonBlocking);
+    if (e == hipSuccess)
+        e = hipEventCreateWithFlags(&d->ev_in, hipEventDisableTiming);
+    if (e == hipSuccess)
+        e = hipEventCreateWithFlags(&d->ev_out, hipEventDisableTiming);
+    if (e == hipSuccess)
+        e = hipMemset(d->next, 0, (size_t)B * 4);
+    {
+        const char *ng = getenv("BE42_DECODE_NO_GRAPH");
+        d->use_graph = !(ng && ng[0] == '1');
     }
     if (e != hipSuccess) {
         be42_decoder_destroy(d);
@@ -397,6 +486,26 @@ extern "C" void be42_decoder_destroy(be42_decoder *d)
 {
     if (!d)
         return;
+    if (d->gstream)
+        (void)hipStreamSynchronize(d->gstream);
+    for (int i = 0; i < 2; i++) {
+        if (d->exec[i])
+            (void)hipGraphExecDestroy(d->exec[i]);
+        if (d->params_host[i])
+            (void)hipHostFree(d->params_host[i]);
+        if (d->params_dev[i])
+            (void)hipFree(d->params_dev[i]);
+        if (d->params_free[i])
+            (void)hipEventDestroy(d->params_free[i]);
+    }
+    if (d->next_host)
+        (void)hipHostFree(d->next_host);
+    if (d->ev_in)
+        (void)hipEventDestroy(d->ev_in);
+    if (d->ev_out)
+        (void)hipEventDestroy(d->ev_out);
+    if (d->gstream)
+        (void)hipStreamDestroy(d->gstream);
     if (d->pool)
         be42_kv_destroy(d->pool);
     void *ptrs[] = {d->cos_t, d->sin_t, d->x, d->xb, d->xn, d->q, d->k, d->v, d->att, d->hb, d->hb2, d->logits, d->sel,
@@ -418,6 +527,12 @@ static int gemv(be42_decoder *d, float *y, const void *w, const float *s, int n,
                            : be42_gemv_fp8_prepared(y, (const uint8_t *)w, s, d->xdig, n, k, B, st);
 }
 
+// projections that share one input, in one launch
+static int gemv_multi(be42_decoder *d, std::initializer_list<be42_gemv_seg> segs, int k, int B, hipStream_t st)
+{
+    return be42_gemv_prepared_multi(segs.begin(), (int)segs.size(), d->xdig, k, B, d->c.wkind, st);
+}
+
 #define DEC_TRY(x)                                                                                                 \
     do {                                                                                                           \
         const int rc_ = (x);                                                                                       \
@@ -425,74 +540,84 @@ static int gemv(be42_decoder *d, float *y, const void *w, const float *s, int n,
             return rc_;                                                                                            \
     } while (0)
 
-extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
-                                 float *logits_out, void *stream)
+// Calls f(integral_constant FP8, integral_constant NV) for a row of n
+// elements (n <= kRowMax).
+template <class F>
+static void launch_rows(bool fp8, int n, F &&f)
 {
-    BE42_CHECK(d, "be42_decoder_step: null decoder");
+    using T = std::true_type;
+    using Fa = std::false_type;
+    const int nv = (n + 4095) / 4096;
+    auto pick = [&](auto f8) {
+        switch (nv) {
+        case 1: f(f8, std::integral_constant<int, 1>()); break;
+        case 2: f(f8, std::integral_constant<int, 2>()); break;
+        case 3: f(f8, std::integral_constant<int, 3>()); break;
+        default: f(f8, std::integral_constant<int, 4>()); break;
+        }
+    };
+    if (fp8)
+        pick(T());
+    else
+        pick(Fa());
+}
+
+// The launches of one step.  Everything that changes from step to step (the
+// position, the tokens, the page bookkeeping of the appends) is read from
+// device memory at params_dev, so this sequence depends only on the key
+// (batch, dense or sparse attention, token source, output buffers).
+static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, float *logits_out, int parity,
+                        hipStream_t st)
+{
     const be42_decoder_config &c = d->c;
-    BE42_CHECK(batch > 0 && batch <= c.max_batch, "be42_decoder_step: batch %d (max %d)", batch, c.max_batch);
-    BE42_CHECK(pos >= 0 && pos < c.max_seq, "be42_decoder_step: position %d (max %d)", pos, c.max_seq);
-    hipStream_t st = as_stream(stream);
-    const int B = batch, dim = c.dim, hd = c.head_dim, H = c.n_heads, KV = c.n_kv_heads;
+    const int dim = c.dim, hd = c.head_dim, H = c.n_heads, KV = c.n_kv_heads;
     const int qd = H * hd, kd = KV * hd, fp8 = c.wkind;
-    TokArgs ta;
-    memset(&ta, 0, sizeof ta);
-    for (int b = 0; tokens && b < B; b++) {
-        BE42_CHECK(tokens[b] >= 0 && tokens[b] < c.vocab, "be42_decoder_step: token %d out of range", tokens[b]);
-        ta.tok[b] = tokens[b];
-    }
-    // the device argmax of the previous step is always in [0, vocab)
-    const int *dev_tok = tokens ? nullptr : d->next;
+    uint8_t *params = (uint8_t *)d->params_dev[parity];
+    const StepHead *head = (const StepHead *)params;
+    const AppendStepArgs *app = (const AppendStepArgs *)(params + sizeof(StepHead));
+    BE42_HIP(hipMemcpyAsync(params, d->params_host[parity], d->params_bytes, hipMemcpyHostToDevice, st));
+    const int *tok = dev_tokens ? d->next : head->tokens;
     const dim3 eg((dim + 255) / 256, B);
     if (fp8)
-        hipLaunchKernelGGL(k_embed<true>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, ta,
-                           dev_tok, dim);
+        hipLaunchKernelGGL(k_embed<true>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, tok,
+                           dim);
     else
-        hipLaunchKernelGGL(k_embed<false>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, ta,
-                           dev_tok, dim);
+        hipLaunchKernelGGL(k_embed<false>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, tok,
+                           dim);
     BE42_LAUNCH_CHECK();
-    const size_t norm_lds = (size_t)dim * 4, silu_lds = (size_t)c.hidden_dim * 4;
+    const size_t norm_lds = (size_t)((dim + 255) & ~255) * 4;
     uint8_t *dig = (uint8_t *)d->xdig;
     // RMSNorm (+ residual) straight into the GEMV digit planes
     auto norm = [&](const uint16_t *wn, const float *delta) {
-        if (fp8)
-            hipLaunchKernelGGL(k_rmsnorm<true>, dim3(B), dim3(1024), norm_lds, st, nullptr, dig, d->x, delta, wn,
-                               dim, B, c.norm_eps);
-        else
-            hipLaunchKernelGGL(k_rmsnorm<false>, dim3(B), dim3(1024), norm_lds, st, nullptr, dig, d->x, delta, wn,
-                               dim, B, c.norm_eps);
+        launch_rows(fp8, dim, [&](auto f8, auto nv) {
+            hipLaunchKernelGGL((k_rmsnorm<decltype(f8)::value, decltype(nv)::value>), dim3(B), dim3(kRowThreads),
+                               norm_lds, st, nullptr, dig, d->x, delta, wn, dim, B, c.norm_eps);
+        });
         return hipGetLastError();
     };
     const float scale = 1.0f / sqrtf((float)hd);
+    const int rope_len = c.rope_len > 0 ? c.rope_len : c.max_seq;
+    const be42_kv_pool &P = *d->pool;
+    // dense: every page in logical order from the device page table; the
+    // fused kernel reads each sequence's page count from the device
+    const int dense_max = std::min(c.sparse_k, P.max_logical);
     const float *pending = nullptr;   // residual delta not yet added to x
-    int slot_ids[kMaxBatch], positions[kMaxBatch];
-    for (int b = 0; b < B; b++)
-        positions[b] = pos;
-    const int pages = pos / 16 + 1;
     for (int l = 0; l < c.n_layers; l++) {
         const be42_decoder_layer &L = d->w.layers[l];
         BE42_HIP(norm(L.attn_norm, pending));
-        DEC_TRY(gemv(d, d->q, L.wq, L.sq, qd, dim, B, st));
-        DEC_TRY(gemv(d, d->k, L.wk, L.sk, kd, dim, B, st));
-        DEC_TRY(gemv(d, d->v, L.wv, L.sv, kd, dim, B, st));
-        if (pos < (c.rope_len > 0 ? c.rope_len : c.max_seq)) {   // no rotation past the table
-            hipLaunchKernelGGL(k_rope, dim3(((H + KV) * (hd / 2) + 255) / 256, B), dim3(256), 0, st, d->q, d->k,
-                               d->cos_t, d->sin_t, pos, H, KV, hd);
-            BE42_LAUNCH_CHECK();
-        }
+        DEC_TRY(gemv_multi(d, {{L.wq, L.sq, d->q, qd}, {L.wk, L.sk, d->k, kd}, {L.wv, L.sv, d->v, kd}}, dim, B, st));
+        hipLaunchKernelGGL(k_rope, dim3(((H + KV) * (hd / 2) + 255) / 256, B), dim3(256), 0, st, d->q, d->k,
+                           d->cos_t, d->sin_t, &head->pos, rope_len, H, KV, hd);
+        BE42_LAUNCH_CHECK();
         if (d->capture_q)
             BE42_HIP(hipMemcpyAsync(d->capture_q + (size_t)l * c.max_batch * qd, d->q, (size_t)B * qd * 4,
                                     hipMemcpyDeviceToDevice, st));
-        for (int b = 0; b < B; b++)
-            slot_ids[b] = l * c.max_batch + b;
-        DEC_TRY(be42_kv_append_step(d->pool, slot_ids, positions, B, d->k, d->v, st));
+        DEC_TRY(launch_append_step_dev(P, app + l, B, d->k, d->v, st));
         const int *lslots = d->slots + (size_t)l * c.max_batch;
-        if (pages <= c.sparse_k) {
-            // dense: every page in logical order, straight from the device page table
-            const be42_kv_pool &P = *d->pool;
+        if (!sparse) {
             DEC_TRY(be42_paged_attention(d->pool, d->q, B, H, P.page_table + (size_t)l * c.max_batch * P.max_logical,
-                                         P.n_logical + (size_t)l * c.max_batch, P.max_logical, pages, scale,
-                                         d->att, pages <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
+                                         P.n_logical + (size_t)l * c.max_batch, P.max_logical, dense_max, scale,
+                                         d->att, dense_max <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
         } else {
             const int stride = std::max(c.sparse_k, 64);
             DEC_TRY(be42_lsh_route(d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, d->sel, d->nsel, stride,
@@ -501,21 +626,18 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
                                          c.sparse_k <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
         }
         if (d->capture_nsel) {
-            const int *src = pages <= c.sparse_k ? d->pool->n_logical + (size_t)l * c.max_batch : d->nsel;
+            const int *src = !sparse ? P.n_logical + (size_t)l * c.max_batch : d->nsel;
             BE42_HIP(hipMemcpyAsync(d->capture_nsel + (size_t)l * c.max_batch, src, (size_t)B * 4,
                                     hipMemcpyDeviceToDevice, st));
         }
         DEC_TRY(be42_gemv_prepare(d->xdig, d->att, qd, B, fp8, st));
         DEC_TRY(gemv(d, d->xb, L.wo, L.so, dim, qd, B, st));
         BE42_HIP(norm(L.ffn_norm, d->xb));                 // x += attention output
-        DEC_TRY(gemv(d, d->hb, L.w1, L.s1, c.hidden_dim, dim, B, st));
-        DEC_TRY(gemv(d, d->hb2, L.w3, L.s3, c.hidden_dim, dim, B, st));
-        if (fp8)
-            hipLaunchKernelGGL(k_silu_mul<true>, dim3(B), dim3(1024), silu_lds, st, nullptr, dig, d->hb, d->hb2,
-                               c.hidden_dim, B);
-        else
-            hipLaunchKernelGGL(k_silu_mul<false>, dim3(B), dim3(1024), silu_lds, st, nullptr, dig, d->hb, d->hb2,
-                               c.hidden_dim, B);
+        DEC_TRY(gemv_multi(d, {{L.w1, L.s1, d->hb, c.hidden_dim}, {L.w3, L.s3, d->hb2, c.hidden_dim}}, dim, B, st));
+        launch_rows(fp8, c.hidden_dim, [&](auto f8, auto nv) {
+            hipLaunchKernelGGL((k_silu_mul<decltype(f8)::value, decltype(nv)::value>), dim3(B), dim3(kRowThreads),
+                               0, st, nullptr, dig, d->hb, d->hb2, c.hidden_dim, B);
+        });
         BE42_LAUNCH_CHECK();
         DEC_TRY(gemv(d, d->xb, L.w2, L.s2, dim, c.hidden_dim, B, st));
         pending = d->xb;
@@ -526,10 +648,85 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
     DEC_TRY(gemv(d, lg, d->w.out, d->w.out_s, c.vocab, dim, B, st));
     hipLaunchKernelGGL(k_argmax, dim3(B), dim3(1024), 0, st, d->next, lg, c.vocab);
     BE42_LAUNCH_CHECK();
-    if (next_tokens)
-        BE42_HIP(hipMemcpyAsync(next_tokens, d->next, (size_t)B * 4, hipMemcpyDeviceToHost, st));
-    if (next_tokens)
-        BE42_HIP(hipStreamSynchronize(st));
+    BE42_HIP(hipMemcpyAsync(d->next_host, d->next, (size_t)B * 4, hipMemcpyDeviceToHost, st));
+    return BE42_OK;
+}
+
+extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
+                                 float *logits_out, void *stream)
+{
+    BE42_CHECK(d, "be42_decoder_step: null decoder");
+    const be42_decoder_config &c = d->c;
+    BE42_CHECK(batch > 0 && batch <= c.max_batch, "be42_decoder_step: batch %d (max %d)", batch, c.max_batch);
+    BE42_CHECK(pos >= 0 && pos < c.max_seq, "be42_decoder_step: position %d (max %d)", pos, c.max_seq);
+    hipStream_t caller = as_stream(stream);
+    const int B = batch;
+    for (int b = 0; tokens && b < B; b++)
+        BE42_CHECK(tokens[b] >= 0 && tokens[b] < c.vocab, "be42_decoder_step: token %d out of range", tokens[b]);
+    // host parameters of this step into the pinned buffer of this parity,
+    // once the step that used it last has copied it
+    const int par = d->parity;
+    BE42_HIP(hipEventSynchronize(d->params_free[par]));
+    uint8_t *ph = (uint8_t *)d->params_host[par];
+    StepHead *head = (StepHead *)ph;
+    AppendStepArgs *app = (AppendStepArgs *)(ph + sizeof(StepHead));
+    head->pos = pos;
+    for (int b = 0; b < kMaxBatch; b++)
+        head->tokens[b] = tokens && b < B ? tokens[b] : 0;
+    int slot_ids[kMaxBatch], positions[kMaxBatch];
+    for (int b = 0; b < B; b++)
+        positions[b] = pos;
+    for (int l = 0; l < c.n_layers; l++) {
+        for (int b = 0; b < B; b++)
+            slot_ids[b] = l * c.max_batch + b;
+        DEC_TRY(plan_append_step(d->pool, slot_ids, positions, B, app + l));
+    }
+    const int pages = pos / 16 + 1;
+    be42_decoder::Key key;
+    key.batch = B;
+    key.sparse = pages > c.sparse_k ? 1 : 0;
+    key.dev_tokens = tokens ? 0 : 1;
+    key.logits = logits_out;
+    key.cq = d->capture_q;
+    key.cn = d->capture_nsel;
+    // the step runs on the decoder's own stream, ordered after the caller's work
+    hipStream_t st = d->gstream;
+    BE42_HIP(hipEventRecord(d->ev_in, caller));
+    BE42_HIP(hipStreamWaitEvent(st, d->ev_in, 0));
+    if (!d->use_graph) {
+        DEC_TRY(enqueue_step(d, B, key.sparse, key.dev_tokens, logits_out, par, st));
+    } else {
+        if (!d->exec[par] || !(d->key[par] == key)) {
+            if (d->exec[par]) {
+                BE42_HIP(hipStreamSynchronize(st));
+                BE42_HIP(hipGraphExecDestroy(d->exec[par]));
+                d->exec[par] = nullptr;
+            }
+            hipGraph_t graph = nullptr;
+            BE42_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            const int rc = enqueue_step(d, B, key.sparse, key.dev_tokens, logits_out, par, st);
+            const hipError_t ce = hipStreamEndCapture(st, &graph);
+            if (rc) {
+                if (graph)
+                    (void)hipGraphDestroy(graph);
+                return rc;
+            }
+            BE42_HIP(ce);
+            const hipError_t ie = hipGraphInstantiate(&d->exec[par], graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            BE42_HIP(ie);
+            d->key[par] = key;
+        }
+        BE42_HIP(hipGraphLaunch(d->exec[par], st));
+    }
+    BE42_HIP(hipEventRecord(d->params_free[par], st));
+    d->parity ^= 1;
+    BE42_HIP(hipEventRecord(d->ev_out, st));
+    BE42_HIP(hipStreamWaitEvent(caller, d->ev_out, 0));
+    if (next_tokens) {
+        BE42_HIP(hipEventSynchronize(d->ev_out));
+        memcpy(next_tokens, d->next_host, (size_t)B * sizeof(int));
+    }
     return BE42_OK;
 }
 

@@ -80,6 +80,31 @@ __global__ __launch_bounds__(256) void k_gemv_prep(const float *__restrict__ x, 
 
 __constant__ double kF8Weight[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 27000, 1.0 / 810000};
 
+// Up to three weight matrices that share one input (the q/k/v or gate/up
+// projections of a decode step) stream in one launch: their rows are
+// numbered one after another, and a row tile may straddle two of them.
+constexpr int kMaxSegs = 3;
+struct GemvSegs {
+    const uint8_t *w[kMaxSegs];
+    const float *sw[kMaxSegs];
+    float *y[kMaxSegs];
+    int n[kMaxSegs];
+    int nseg, total;
+};
+
+__device__ __forceinline__ int seg_of(const GemvSegs &S, int row, int *local)
+{
+    int sg = 0, r = row;
+#pragma unroll
+    for (int i = 0; i < kMaxSegs - 1; i++)
+        if (sg == i && i + 1 < S.nseg && r >= S.n[i]) {
+            r -= S.n[i];
+            sg = i + 1;
+        }
+    *local = r;
+    return sg;
+}
+
 // Main GEMV kernel.
 // Operands of one MFMA: A = 16 weight rows x STEP k (row r = lane % 16, k
 // slice lane / 16), B = STEP k x 16 columns, where column c of column group nc
@@ -91,14 +116,16 @@ __constant__ double kF8Weight[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 2700
 // A block holds WAVES waves in WAVES/KS groups; a group owns one tile of
 // 16*RT rows and its KS waves split K into contiguous slices.  A wave loads a
 // burst of U MFMA steps (RT*U KiB of INT8 weights) with unconditional 16-byte
-// loads, then runs its MFMAs; latency is hidden by the other resident waves
-// (MFMA time per burst is a few percent of the memory latency).  Epilogue: raw accumulators go through LDS one row tile at
-// a time and the group's first wave sums slices and digit columns per output,
-// weighting digit d by 254^(2-d) in exact int64 (INT8) or 30^-d in fp64 (FP8).
-template <bool FP8, int RT, int U, int KS, int NC, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void k_gemv(
-    float *__restrict__ y, const uint8_t *__restrict__ W, const float *__restrict__ sw,
-    const uint8_t *__restrict__ dig, const float *__restrict__ sx, int N, int K, int Kp, int B)
+// loads, then runs its MFMAs.  With PF the next burst is loaded into a
+// second register set before the MFMAs of the current one, so a wave keeps
+// one burst in flight while it computes; without PF the latency is hidden by
+// the other resident waves alone.  Epilogue: raw accumulators go through LDS
+// one row tile at a time and the group's first wave sums slices and digit
+// columns per output, weighting digit d by 254^(2-d) in exact int64 (INT8) or
+// 30^-d in fp64 (FP8).
+template <bool FP8, int RT, int U, int KS, int NC, int WAVES, bool PF>
+__global__ __launch_bounds__(WAVES * 64) void k_gemv(const GemvSegs S, const uint8_t *__restrict__ dig,
+                                                     const float *__restrict__ sx, int K, int Kp, int B)
 {
     constexpr int ND = FP8 ? kF8Digits : kI8Digits;
     constexpr int STEP = FP8 ? 128 : 64;
@@ -125,14 +152,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(
 
     // Every load is unconditional and in bounds, so the loop carries no
     // branches and the next burst stays in flight across the MFMAs: rows past
-    // N read row N-1 and columns past the batch read plane 0 (neither is ever
-    // written out); k past K reads the row's last 16 bytes against digits that
-    // are zero there.
+    // the last read the last row and columns past the batch read plane 0
+    // (neither is ever written out); k past K reads the row's last 16 bytes
+    // against digits that are zero there.
     const uint8_t *wrow[RT];
 #pragma unroll
     for (int t = 0; t < RT; t++) {
-        const int row = min(row0 + t * 16 + r, N - 1);
-        wrow[t] = W + (size_t)row * K;
+        int local;
+        const int sg = seg_of(S, min(row0 + t * 16 + r, S.total - 1), &local);
+        wrow[t] = S.w[sg] + (size_t)local * K;
     }
     const uint8_t *xcolp[NC];
 #pragma unroll
@@ -142,7 +170,6 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(
     }
     const int klast = K - 16;
 
-    v4i wv[RT][U][NV], xv[NC][U][NV];
     auto load = [&](int bi, v4i (&wd)[RT][U][NV], v4i (&xd)[NC][U][NV]) {
         const int kb = bi * STEP * U + g * 16 * NV;
 #pragma unroll
@@ -180,11 +207,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(
                     }
                 }
     };
-    // One burst in flight per wave; the latency is hidden by the other
-    // resident waves (occupancy), not by software pipelining.
-    for (int bi = b0; bi < b1; bi++) {
-        load(bi, wv, xv);
-        compute(wv, xv);
+    if constexpr (PF) {
+        v4i wa[RT][U][NV], xa[NC][U][NV], wb[RT][U][NV], xb[NC][U][NV];
+        if (b0 < b1)
+            load(b0, wa, xa);
+        for (int bi = b0; bi < b1; bi += 2) {
+            if (bi + 1 < b1)
+                load(bi + 1, wb, xb);
+            compute(wa, xa);
+            if (bi + 1 >= b1)
+                break;
+            if (bi + 2 < b1)
+                load(bi + 2, wa, xa);
+            compute(wb, xb);
+        }
+    } else {
+        v4i wv[RT][U][NV], xv[NC][U][NV];
+        for (int bi = b0; bi < b1; bi++) {
+            load(bi, wv, xv);
+            compute(wv, xv);
+        }
     }
 
     // C layout of a 16x16 MFMA: lane holds rows 4*(lane/16)+j of column lane%16.
@@ -205,7 +247,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(
             for (int o = lane; o < 16 * B; o += kWave) {
                 const int bb = o / 16, i = o % 16;
                 const int row = row0 + t * 16 + i;
-                if (row >= N)
+                if (row >= S.total)
                     continue;
                 Tot tot = 0;
 #pragma unroll
@@ -220,7 +262,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(
                     else
                         tot = tot + dsum * (Tot)(d == 0 ? kI8Base * kI8Base : (d == 1 ? kI8Base : 1));
                 }
-                y[(size_t)bb * N + row] = (float)((double)tot * ((double)sx[bb] * sxw * (double)sw[row]));
+                int local;
+                const int sg = seg_of(S, row, &local);
+                S.y[sg][(size_t)bb * S.n[sg] + local] =
+                    (float)((double)tot * ((double)sx[bb] * sxw * (double)S.sw[sg][local]));
             }
         }
     }
@@ -277,112 +322,141 @@ static int prepare_launch(void *buf, const float *x, int k, int batch, bool fp8,
     return BE42_OK;
 }
 
-template <bool FP8, int RT, int U, int NC, int KS>
-static void launch_ks(float *y, const uint8_t *w, const float *sw, const uint8_t *dig, const float *sx, int n,
-                      int k, int Kp, int batch, hipStream_t s)
+template <bool FP8, int RT, int U, int NC, int KS, int WAVES, bool PF>
+static void launch_cfg(const GemvSegs &S, const uint8_t *dig, const float *sx, int k, int Kp, int batch,
+                       hipStream_t s)
 {
-    constexpr int WAVES = KS > 4 ? KS : 4;
-    const int tiles = (n + 16 * RT - 1) / (16 * RT);
+    static_assert(WAVES % KS == 0, "a row group is KS whole waves");
     constexpr int GROUPS = WAVES / KS;
+    const int tiles = (S.total + 16 * RT - 1) / (16 * RT);
     const int blocks = (tiles + GROUPS - 1) / GROUPS;
-    hipLaunchKernelGGL((k_gemv<FP8, RT, U, KS, NC, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, y, w, sw, dig,
-                       sx, n, k, Kp, batch);
+    hipLaunchKernelGGL((k_gemv<FP8, RT, U, KS, NC, WAVES, PF>), dim3(blocks), dim3(WAVES * 64), 0, s, S, dig, sx, k,
+                       Kp, batch);
 }
 
-// K-split factor: the fewest waves per row tile that still give >= target
-// waves, and no more slices than there are bursts.
-template <bool FP8, int RT, int U, int NC>
-static int launch_shape(float *y, const uint8_t *w, const float *sw, const uint8_t *dig, const float *sx,
-                        int n, int k, int Kp, int batch, hipStream_t s, int ks_force)
+// Launch shape per (dtype, column groups NC, rows n, k), measured on MI355X
+// over the decode projections of configs[0] and configs[4] and the four
+// configs[1] shapes at batch 1 / 4 / 8 / 16 (rows n count all segments of a
+// launch).  RT row tiles of 16 per wave, U MFMA steps per burst, KS waves
+// splitting K per row group, WAVES per block, PF register double buffering.
+struct TileCfg {
+    int rt, u, ks, waves, pf;
+};
+
+static TileCfg pick_tile(bool fp8, int nc, int n, int k)
 {
-    const int tiles = (n + 16 * RT - 1) / (16 * RT);
-    const int nburst = Kp / ((FP8 ? 128 : 64) * U);
-    int ks = 1;
-    while (ks < 8 && tiles * ks < 4096 && ks * 2 <= nburst)
-        ks *= 2;
-    if (ks_force > 0) {
-        ks = ks_force;
-        while (ks > 1 && ks > nburst)
-            ks /= 2;
+    if (fp8) {
+        if (nc == 1) {
+            if (n <= 4096)
+                return k <= 4096 ? TileCfg{1, 4, 4, 4, 1} : TileCfg{1, 2, 8, 8, 0};
+            if (n <= 8192)
+                return {2, 2, 8, 8, 1};
+            return n <= 32768 ? TileCfg{2, 1, 4, 8, 1} : TileCfg{2, 1, 4, 4, 1};
+        }
+        if (nc == 2) {
+            if (n <= 4096)
+                return k <= 4096 ? TileCfg{1, 1, 8, 8, 1} : TileCfg{1, 1, 8, 8, 0};
+            return n <= 32768 ? TileCfg{2, 4, 2, 4, 0} : TileCfg{4, 1, 2, 4, 0};
+        }
+        if (nc == 3) {
+            if (n <= 4096)
+                return {1, 1, 4, 4, 1};
+            if (n <= 8192)
+                return {2, 2, 4, 4, 0};
+            return n <= 32768 ? TileCfg{4, 1, 4, 4, 0} : TileCfg{4, 2, 1, 4, 0};
+        }
+        if (n <= 4096)
+            return k <= 4096 ? TileCfg{1, 1, 4, 4, 0} : TileCfg{1, 2, 4, 4, 1};
+        return n <= 32768 ? TileCfg{4, 2, 4, 4, 0} : TileCfg{4, 2, 1, 4, 0};
     }
-    switch (ks) {
-    case 1: launch_ks<FP8, RT, U, NC, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s); break;
-    case 2: launch_ks<FP8, RT, U, NC, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s); break;
-    case 4: launch_ks<FP8, RT, U, NC, 4>(y, w, sw, dig, sx, n, k, Kp, batch, s); break;
-    default: launch_ks<FP8, RT, U, NC, 8>(y, w, sw, dig, sx, n, k, Kp, batch, s); break;
+    if (nc == 1) {
+        if (n <= 2048)
+            return k <= 1024 ? TileCfg{1, 8, 8, 8, 1} : TileCfg{1, 4, 8, 8, 1};
+        if (n <= 4096)
+            return k <= 4096 ? TileCfg{1, 8, 4, 4, 1} : TileCfg{1, 2, 8, 8, 1};
+        return n <= 32768 ? TileCfg{2, 2, 4, 4, 0} : TileCfg{2, 2, 4, 4, 1};
     }
-    BE42_LAUNCH_CHECK();
-    return BE42_OK;
+    if (n <= 4096)
+        return k <= 4096 ? TileCfg{1, 2, 4, 4, 0} : TileCfg{1, 2, 8, 8, 1};
+    return n <= 32768 ? TileCfg{4, 2, 4, 4, 1} : TileCfg{4, 2, 2, 8, 1};
 }
 
-// Tile override for tuning: BE42_GEMV_TILE="<variant>,<ks>".
-static int tile_override(int *ks)
+#define BE42_TILE(RT, U, KS, W, PF)                                                                                \
+    if (c.rt == RT && c.u == U && c.ks == KS && c.waves == W && c.pf == PF)                                      \
+        return launch_cfg<FP8, RT, U, NC, KS, W, PF>(S, dig, sx, k, Kp, batch, s), true;
+
+// The shapes pick_tile returns for each (dtype, NC); false if c is not one.
+template <bool FP8, int NC>
+static bool launch_tile(const TileCfg &c, const GemvSegs &S, const uint8_t *dig, const float *sx, int k, int Kp,
+                        int batch, hipStream_t s)
 {
-    int variant = -1, ksv = 0;
-    const char *e = getenv("BE42_GEMV_TILE");
-    if (e && sscanf(e, "%d,%d", &variant, &ksv) < 1)
-        variant = -1;
-    *ks = ksv;
-    return variant;
+    if constexpr (FP8 && NC == 1) {
+        BE42_TILE(1, 4, 4, 4, 1) BE42_TILE(1, 2, 8, 8, 0) BE42_TILE(2, 2, 8, 8, 1) BE42_TILE(2, 1, 4, 8, 1)
+        BE42_TILE(2, 1, 4, 4, 1)
+    } else if constexpr (FP8 && NC == 2) {
+        BE42_TILE(1, 1, 8, 8, 1) BE42_TILE(1, 1, 8, 8, 0) BE42_TILE(2, 4, 2, 4, 0) BE42_TILE(4, 1, 2, 4, 0)
+    } else if constexpr (FP8 && NC == 3) {
+        BE42_TILE(1, 1, 4, 4, 1) BE42_TILE(2, 2, 4, 4, 0) BE42_TILE(4, 1, 4, 4, 0) BE42_TILE(4, 2, 1, 4, 0)
+    } else if constexpr (FP8) {
+        BE42_TILE(1, 1, 4, 4, 0) BE42_TILE(1, 2, 4, 4, 1) BE42_TILE(4, 2, 4, 4, 0) BE42_TILE(4, 2, 1, 4, 0)
+    } else if constexpr (NC == 1) {
+        BE42_TILE(1, 8, 8, 8, 1) BE42_TILE(1, 4, 8, 8, 1) BE42_TILE(1, 8, 4, 4, 1) BE42_TILE(1, 2, 8, 8, 1)
+        BE42_TILE(2, 2, 4, 4, 0) BE42_TILE(2, 2, 4, 4, 1)
+    } else {
+        BE42_TILE(1, 2, 4, 4, 0) BE42_TILE(1, 2, 8, 8, 1) BE42_TILE(4, 2, 4, 4, 1) BE42_TILE(4, 2, 2, 8, 1)
+    }
+    return false;
 }
+#undef BE42_TILE
 
-// Tile choice.  NC = ceil(batch*ND/16) MFMA column groups.  Variant 0 (one
-// row tile, deep bursts) maximises the number of waves for small n; variant 1
-// (four row tiles) amortises the activation operand over more weight rows
-// and keeps VGPRs low for large n.
+// NC = ceil(batch * digits / 16) MFMA column groups.
 template <bool FP8>
-static int prepared_launch(float *y, const uint8_t *w, const float *sw, const void *buf, int n, int k,
-                           int batch, hipStream_t s)
+static int segs_launch(const GemvSegs &S, const void *buf, int k, int batch, hipStream_t s)
 {
     const int Kp = (int)xdig_kp(k, FP8);
     const uint8_t *dig = (const uint8_t *)buf;
     const size_t dbytes = (size_t)xdig_layout(FP8).nd * batch * Kp;
     const float *sx = (const float *)(dig + ((dbytes + 255) & ~(size_t)255));
     const int nc = (batch * (FP8 ? kF8Digits : kI8Digits) + 15) / 16;
-    int ksf = 0;
-    int variant = tile_override(&ksf);
-    if (variant < 0) {
-        // measured on MI355X over the 4 shapes x batch {1,4,16} x both dtypes
-        if (n <= 8192) {
-            variant = 0;
-            ksf = nc == 1 ? 8 : 4;
-        } else if (n <= 32768) {
-            variant = 1;
-            ksf = FP8 ? (nc == 1 ? 8 : 4) : (nc == 1 ? 4 : 8);
-        } else {
-            variant = 1;
-            ksf = FP8 ? (nc == 1 ? 8 : 2) : (nc == 1 ? 4 : 2);
-        }
-    }
+    const TileCfg c = pick_tile(FP8, nc, S.total, k);
+    bool ok;
     if constexpr (FP8) {
-        if (variant == 0) {
-            switch (nc) {
-            case 1: return launch_shape<true, 1, 8, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-            case 2: return launch_shape<true, 1, 4, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-            default: return launch_shape<true, 2, 1, 5>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-            }
-        }
         switch (nc) {
-        case 1: return launch_shape<true, 4, 2, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-        case 2: return launch_shape<true, 4, 2, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-        case 3: return launch_shape<true, 4, 1, 3>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-        case 4: return launch_shape<true, 4, 1, 4>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-        default: return launch_shape<true, 4, 1, 5>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        case 1: ok = launch_tile<true, 1>(c, S, dig, sx, k, Kp, batch, s); break;
+        case 2: ok = launch_tile<true, 2>(c, S, dig, sx, k, Kp, batch, s); break;
+        case 3: ok = launch_tile<true, 3>(c, S, dig, sx, k, Kp, batch, s); break;
+        case 4: ok = launch_tile<true, 4>(c, S, dig, sx, k, Kp, batch, s); break;
+        default: ok = launch_tile<true, 5>(c, S, dig, sx, k, Kp, batch, s); break;
         }
     } else {
-        if (variant == 0) {
-            switch (nc) {
-            case 1: return launch_shape<false, 1, 16, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-            case 2: return launch_shape<false, 1, 8, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-            default: return launch_shape<false, 2, 4, 3>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-            }
-        }
         switch (nc) {
-        case 1: return launch_shape<false, 4, 4, 1>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-        case 2: return launch_shape<false, 4, 4, 2>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
-        default: return launch_shape<false, 4, 4, 3>(y, w, sw, dig, sx, n, k, Kp, batch, s, ksf);
+        case 1: ok = launch_tile<false, 1>(c, S, dig, sx, k, Kp, batch, s); break;
+        case 2: ok = launch_tile<false, 2>(c, S, dig, sx, k, Kp, batch, s); break;
+        default: ok = launch_tile<false, 3>(c, S, dig, sx, k, Kp, batch, s); break;
         }
     }
+    BE42_CHECK(ok, "be42 gemv: no kernel for tile (%d,%d,%d,%d,%d) at nc %d", c.rt, c.u, c.ks, c.waves, c.pf, nc);
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
+static GemvSegs one_seg(float *y, const uint8_t *w, const float *sw, int n)
+{
+    GemvSegs S{};
+    S.w[0] = w;
+    S.sw[0] = sw;
+    S.y[0] = y;
+    S.n[0] = n;
+    S.nseg = 1;
+    S.total = n;
+    return S;
+}
+
+template <bool FP8>
+static int prepared_launch(float *y, const uint8_t *w, const float *sw, const void *buf, int n, int k,
+                           int batch, hipStream_t s)
+{
+    return segs_launch<FP8>(one_seg(y, w, sw, n), buf, k, batch, s);
 }
 
 static bool fast_path(const void *w, int k, int batch)
@@ -468,4 +542,27 @@ extern "C" int be42_gemv_fp8_prepared(float *y, const uint8_t *w, const float *w
     if (n == 0)
         return BE42_OK;
     return prepared_launch<true>(y, w, w_scale, xdig, n, k, batch, as_stream(stream));
+}
+
+extern "C" int be42_gemv_prepared_multi(const be42_gemv_seg *segs, int nseg, const void *xdig, int k, int batch,
+                                        int fp8, void *stream)
+{
+    BE42_CHECK(segs && xdig && nseg >= 1 && nseg <= kMaxSegs, "be42_gemv_prepared_multi: bad arguments");
+    BE42_CHECK(k > 0 && k % 16 == 0 && batch > 0 && batch <= 16,
+               "be42_gemv_prepared_multi: needs k %% 16 == 0 and 1 <= batch <= 16 (k=%d batch=%d)", k, batch);
+    GemvSegs S{};
+    S.nseg = nseg;
+    for (int i = 0; i < nseg; i++) {
+        BE42_CHECK(segs[i].w && segs[i].w_scale && segs[i].y && segs[i].n > 0 &&
+                       (((uintptr_t)segs[i].w) & 15) == 0,
+                   "be42_gemv_prepared_multi: segment %d needs weights (16-byte aligned), scales, output, n > 0", i);
+        BE42_CHECK(S.total <= INT32_MAX - segs[i].n, "be42_gemv_prepared_multi: too many rows");
+        S.w[i] = (const uint8_t *)segs[i].w;
+        S.sw[i] = segs[i].w_scale;
+        S.y[i] = segs[i].y;
+        S.n[i] = segs[i].n;
+        S.total += segs[i].n;
+    }
+    hipStream_t s = as_stream(stream);
+    return fp8 ? segs_launch<true>(S, xdig, k, batch, s) : segs_launch<false>(S, xdig, k, batch, s);
 }

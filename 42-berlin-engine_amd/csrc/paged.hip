@@ -26,6 +26,7 @@
 #include <vector>
 
 #include "be42_common.h"
+#include "paged_step.h"
 
 namespace be42 {
 
@@ -33,7 +34,6 @@ constexpr int kPage = 16;
 
 // Bookkeeping of one append of up to kArgTok tokens, passed by value as a
 // kernel argument so that a decode step needs no host-to-device copy.
-constexpr int kArgTok = 64;
 constexpr int kArgPages = kArgTok / 16 + 2;
 struct AppendArgs {
     int pos0, n_tok, layer_base;
@@ -134,22 +134,18 @@ __global__ __launch_bounds__(64) void k_kv_append(void *__restrict__ kdst, void 
 
 // One token for each of n layer slots (a decode step of a batch): the same
 // store, with per-token slot, position and page bookkeeping.
-struct AppendStepArgs {
-    int n, max_logical;
-    int pos[kArgTok], phys[kArgTok], slot[kArgTok], publish[kArgTok];
-    int n_seal;
-    int seal_phys[kArgTok], seal_slot[kArgTok], seal_logical[kArgTok], seal_nidx[kArgTok];
-};
 
 template <bool BF16>
-__global__ __launch_bounds__(64) void k_kv_append_step(void *__restrict__ kdst, void *__restrict__ vdst,
-                                                       float *__restrict__ kscale, float *__restrict__ vscale,
-                                                       int *__restrict__ ntok, int *__restrict__ page_table,
-                                                       int *__restrict__ n_logical, const AppendStepArgs a,
-                                                       const float *__restrict__ k, const float *__restrict__ v,
-                                                       int n_kv, int hd)
+__device__ __forceinline__ void append_step_body(void *__restrict__ kdst, void *__restrict__ vdst,
+                                                 float *__restrict__ kscale, float *__restrict__ vscale,
+                                                 int *__restrict__ ntok, int *__restrict__ page_table,
+                                                 int *__restrict__ n_logical, const AppendStepArgs &a,
+                                                 const float *__restrict__ k, const float *__restrict__ v, int n_kv,
+                                                 int hd)
 {
     const int tok = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    if (tok >= a.n)
+        return;
     const int pos = a.pos[tok], off = pos % kPage, blk = pos / kPage, phys = a.phys[tok];
     if (h == 0 && lane == 0) {
         if (a.publish[tok]) {
@@ -161,6 +157,30 @@ __global__ __launch_bounds__(64) void k_kv_append_step(void *__restrict__ kdst, 
     const size_t slot = ((size_t)phys * n_kv + h) * kPage + off;
     store_kv_row<BF16>(kdst, vdst, kscale, vscale, slot, k + (size_t)tok * n_kv * hd + (size_t)h * hd,
                        v + (size_t)tok * n_kv * hd + (size_t)h * hd, hd, lane);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_kv_append_step(void *__restrict__ kdst, void *__restrict__ vdst,
+                                                       float *__restrict__ kscale, float *__restrict__ vscale,
+                                                       int *__restrict__ ntok, int *__restrict__ page_table,
+                                                       int *__restrict__ n_logical, const AppendStepArgs a,
+                                                       const float *__restrict__ k, const float *__restrict__ v,
+                                                       int n_kv, int hd)
+{
+    append_step_body<BF16>(kdst, vdst, kscale, vscale, ntok, page_table, n_logical, a, k, v, n_kv, hd);
+}
+
+// the same with the bookkeeping read from device memory (graph replays)
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_kv_append_step_dev(void *__restrict__ kdst, void *__restrict__ vdst,
+                                                           float *__restrict__ kscale, float *__restrict__ vscale,
+                                                           int *__restrict__ ntok, int *__restrict__ page_table,
+                                                           int *__restrict__ n_logical,
+                                                           const AppendStepArgs *__restrict__ a,
+                                                           const float *__restrict__ k, const float *__restrict__ v,
+                                                           int n_kv, int hd)
+{
+    append_step_body<BF16>(kdst, vdst, kscale, vscale, ntok, page_table, n_logical, *a, k, v, n_kv, hd);
 }
 
 // One block per page that became full: centroid of the head-0 keys (per
@@ -214,17 +234,41 @@ __global__ __launch_bounds__(256) void k_kv_seal(const void *__restrict__ kpool,
 }
 
 template <bool BF16>
+__device__ __forceinline__ void seal_step_body(const void *__restrict__ kpool, const float *__restrict__ kscale,
+                                               float *__restrict__ centroid, uint16_t *__restrict__ page_hash,
+                                               int *__restrict__ n_indexed, const AppendStepArgs &a,
+                                               const float *__restrict__ hpT, int n_kv, int hd)
+{
+    __shared__ float c[256];
+    const int i = blockIdx.x;
+    if (i >= a.n_seal)
+        return;
+    const int slot = a.seal_slot[i];
+    if (threadIdx.x == 0)
+        n_indexed[slot] = a.seal_nidx[i];
+    seal_page<BF16>(kpool, kscale, centroid, page_hash + (size_t)slot * a.max_logical + a.seal_logical[i],
+                    a.seal_phys[i], hpT, n_kv, hd, c);
+}
+
+template <bool BF16>
 __global__ __launch_bounds__(256) void k_kv_seal_step(const void *__restrict__ kpool, const float *__restrict__ kscale,
                                                       float *__restrict__ centroid, uint16_t *__restrict__ page_hash,
                                                       int *__restrict__ n_indexed, const AppendStepArgs a,
                                                       const float *__restrict__ hpT, int n_kv, int hd)
 {
-    __shared__ float c[256];
-    const int i = blockIdx.x, slot = a.seal_slot[i];
-    if (threadIdx.x == 0)
-        n_indexed[slot] = a.seal_nidx[i];
-    seal_page<BF16>(kpool, kscale, centroid, page_hash + (size_t)slot * a.max_logical + a.seal_logical[i],
-                    a.seal_phys[i], hpT, n_kv, hd, c);
+    seal_step_body<BF16>(kpool, kscale, centroid, page_hash, n_indexed, a, hpT, n_kv, hd);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_kv_seal_step_dev(const void *__restrict__ kpool,
+                                                          const float *__restrict__ kscale,
+                                                          float *__restrict__ centroid,
+                                                          uint16_t *__restrict__ page_hash,
+                                                          int *__restrict__ n_indexed,
+                                                          const AppendStepArgs *__restrict__ a,
+                                                          const float *__restrict__ hpT, int n_kv, int hd)
+{
+    seal_step_body<BF16>(kpool, kscale, centroid, page_hash, n_indexed, *a, hpT, n_kv, hd);
 }
 
 }  // namespace be42
@@ -489,17 +533,16 @@ extern "C" int be42_kv_export(const be42_kv_pool *pool, int *page_table, int *fr
     return BE42_OK;
 }
 
-// One decode token for each of n layer slots (paged.c:195-272 per slot).
-extern "C" int be42_kv_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, const float *k,
-                                   const float *v, void *stream)
+namespace be42 {
+
+// Host bookkeeping of one decode token for each of n distinct layer slots
+// (paged.c:195-272 per slot): page allocation, page table, seal list.
+int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, AppendStepArgs *out)
 {
-    BE42_CHECK(pool && slots && pos && k && v, "be42_kv_append_step: null pointer");
     BE42_CHECK(n >= 0 && n <= kArgTok, "be42_kv_append_step: %d slots (at most %d)", n, kArgTok);
-    if (n == 0)
-        return BE42_OK;
     PoolImpl *p = impl(pool);
     be42_kv_pool &P = p->pub;
-    AppendStepArgs a;
+    AppendStepArgs &a = *out;
     memset(&a, 0, sizeof a);
     a.n = n;
     a.max_logical = P.max_logical;
@@ -539,6 +582,44 @@ extern "C" int be42_kv_append_step(be42_kv_pool *pool, const int *slots, const i
             a.n_seal++;
         }
     }
+    return BE42_OK;
+}
+
+// Launch the append (and seal) of n tokens whose bookkeeping is in device
+// memory (a_dev): grids sized for n tokens and up to n seals.
+int launch_append_step_dev(const be42_kv_pool &P, const AppendStepArgs *a_dev, int n, const float *k, const float *v,
+                           hipStream_t st)
+{
+    const dim3 grid(n, P.n_kv);
+    if (P.kind == BE42_KV_BF16) {
+        hipLaunchKernelGGL(k_kv_append_step_dev<true>, grid, dim3(64), 0, st, P.k, P.v, P.k_scale, P.v_scale,
+                           P.ntok, P.page_table, P.n_logical, a_dev, k, v, P.n_kv, P.head_dim);
+        hipLaunchKernelGGL(k_kv_seal_step_dev<true>, dim3(n), dim3(256), 0, st, P.k, P.k_scale, P.centroid,
+                           P.page_hash, P.n_indexed, a_dev, P.hpT, P.n_kv, P.head_dim);
+    } else {
+        hipLaunchKernelGGL(k_kv_append_step_dev<false>, grid, dim3(64), 0, st, P.k, P.v, P.k_scale, P.v_scale,
+                           P.ntok, P.page_table, P.n_logical, a_dev, k, v, P.n_kv, P.head_dim);
+        hipLaunchKernelGGL(k_kv_seal_step_dev<false>, dim3(n), dim3(256), 0, st, P.k, P.k_scale, P.centroid,
+                           P.page_hash, P.n_indexed, a_dev, P.hpT, P.n_kv, P.head_dim);
+    }
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
+}  // namespace be42
+
+// One decode token for each of n layer slots (paged.c:195-272 per slot).
+extern "C" int be42_kv_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, const float *k,
+                                   const float *v, void *stream)
+{
+    BE42_CHECK(pool && slots && pos && k && v, "be42_kv_append_step: null pointer");
+    if (n == 0)
+        return BE42_OK;
+    AppendStepArgs a;
+    const int rc = plan_append_step(pool, slots, pos, n, &a);
+    if (rc)
+        return rc;
+    const be42_kv_pool &P = *pool;
     hipStream_t st = as_stream(stream);
     const dim3 grid(n, P.n_kv);
     if (P.kind == BE42_KV_BF16)

@@ -370,6 +370,12 @@ def decode_3b_bench(lib, batches=(1, 8), steps=10):
     rows = []
     for B in batches:
         toks = tok0[:B]
+        # one step that records the attended page counts, then the timed
+        # steps without the inspection copies
+        dec.capture(cq, cn)
+        dec.step(toks, T, sync=True)
+        nsel = cn[:, :B].cpu().numpy()
+        dec.capture(None, None)
         for _ in range(2):
             dec.step(toks, T, sync=False)
         torch.cuda.synchronize()
@@ -380,7 +386,6 @@ def decode_3b_bench(lib, batches=(1, 8), steps=10):
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
-        nsel = cn[:, :B].cpu().numpy()
         kv_bytes = int(nsel.sum()) * 16 * KVH * hd * 2 * 2
         wb = weight_bytes(A)
         rows.append({"batch": B, "tokens_per_s": round(B / (ms * 1e-3), 1), "ms_per_step": round(ms, 3),
@@ -523,6 +528,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-gemv", action="store_true",
+                    help="skip the GEMV sweep (value is then null; for profiling the other legs)")
     ap.add_argument("--no-lsh", action="store_true", help="skip the LSH attention leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step leg")
@@ -545,97 +552,109 @@ def main():
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
 
-    # ---- data: rotated weight pools per (kind, shape) -------------------------
-    configs = []
-    for kind in KINDS:
-        for (n, k) in SHAPES:
-            copies = max(2, min(64, -(-POOL_BYTES // (n * k))))
-            w32 = torch.randn(n, k, device=dev) * 0.02
-            q0, s0 = lib.quant_rows_int8(w32) if kind == "int8" else lib.quant_rows_fp8(w32)
-            del w32
-            pool = [q0] + [q0.roll(shifts=i * 7, dims=1).contiguous() for i in range(1, copies)]
-            for b in BATCHES:
-                x = torch.randn(b, k, device=dev)
-                xdig = lib.gemv_prepare(x, kind)
-                y = torch.empty(b, n, device=dev)
-                configs.append(dict(kind=kind, n=n, k=k, b=b, pool=pool, s=s0, x=x, xdig=xdig, y=y, i=0))
-    torch.cuda.synchronize()
+    def gemv_sweep():
+        # ---- data: rotated weight pools per (kind, shape) -------------------------
+        configs = []
+        for kind in KINDS:
+            for (n, k) in SHAPES:
+                copies = max(2, min(64, -(-POOL_BYTES // (n * k))))
+                w32 = torch.randn(n, k, device=dev) * 0.02
+                q0, s0 = lib.quant_rows_int8(w32) if kind == "int8" else lib.quant_rows_fp8(w32)
+                del w32
+                pool = [q0] + [q0.roll(shifts=i * 7, dims=1).contiguous() for i in range(1, copies)]
+                for b in BATCHES:
+                    x = torch.randn(b, k, device=dev)
+                    xdig = lib.gemv_prepare(x, kind)
+                    y = torch.empty(b, n, device=dev)
+                    configs.append(dict(kind=kind, n=n, k=k, b=b, pool=pool, s=s0, x=x, xdig=xdig, y=y, i=0))
+        torch.cuda.synchronize()
 
-    def run_step(ev=None):
+        def run_step(ev=None):
+            for ci, c in enumerate(configs):
+                w = c["pool"][c["i"] % len(c["pool"])]
+                c["i"] += 1
+                if ev is not None:
+                    ev[ci][0].record()
+                lib.gemv_prepare(c["x"], c["kind"], buf=c["xdig"])
+                if ev is not None:
+                    ev[ci][1].record()
+                lib.gemv_prepared(w, c["s"], c["xdig"], c["b"], c["kind"], c["y"])
+                if ev is not None:
+                    ev[ci][2].record()
+
+        for _ in range(args.warmup):
+            run_step()
+        torch.cuda.synchronize()
+
+        evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in configs]
+               for _ in range(args.steps)]
+        t0 = time.perf_counter()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for s in range(args.steps):
+            run_step(evs[s])
+        stop.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        total_ms = start.elapsed_time(stop)
+
+        step_bytes = sum(gemv_bytes(c["n"], c["k"], c["b"]) for c in configs)
+        ms_per_step = total_ms / args.steps
+        value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+        sweep = []
+        dominant = None
         for ci, c in enumerate(configs):
-            w = c["pool"][c["i"] % len(c["pool"])]
-            c["i"] += 1
-            if ev is not None:
-                ev[ci][0].record()
-            lib.gemv_prepare(c["x"], c["kind"], buf=c["xdig"])
-            if ev is not None:
-                ev[ci][1].record()
-            lib.gemv_prepared(w, c["s"], c["xdig"], c["b"], c["kind"], c["y"])
-            if ev is not None:
-                ev[ci][2].record()
+            op_ms = sum(evs[s][ci][0].elapsed_time(evs[s][ci][2]) for s in range(args.steps)) / args.steps
+            main_ms = sum(evs[s][ci][1].elapsed_time(evs[s][ci][2]) for s in range(args.steps)) / args.steps
+            nb = gemv_bytes(c["n"], c["k"], c["b"])
+            row = {"dtype": c["kind"], "n": c["n"], "k": c["k"], "batch": c["b"],
+                   "op_us": round(op_ms * 1e3, 2), "kernel_us": round(main_ms * 1e3, 2),
+                   "op_GBps": round(nb / (op_ms * 1e-3) / 1e9, 1),
+                   "kernel_GBps": round(nb / (main_ms * 1e-3) / 1e9, 1)}
+            sweep.append(row)
+            if dominant is None or main_ms > dominant[0]:
+                dominant = (main_ms, c, nb)
 
-    for _ in range(args.warmup):
-        run_step()
-    torch.cuda.synchronize()
+        dm, dc, dnb = dominant
+        achieved = dnb / (dm * 1e-3) / 1e9
+        kname = "be42::k_gemv (%s)" % dc["kind"]
+        out = {
+            "metric": "decode tokens/s; quant GEMV HBM GB/s (% of peak); LSH attn µs/token @32k",
+            "value": round(value, 1),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "int8/fp8 weights, fp32 activations",
+            "data": "synthetic",
+            "config": {"workload": "configs[1]: quantized GEMV sweep, INT8+FP8 per-row weights, "
+                                   "shapes 4096x4096/14336x4096/4096x14336/128256x4096, batch 1/4/16",
+                       "pool_bytes_per_shape": POOL_BYTES, "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "kernel": kname,
+                         "workload": f"{dc['kind']} {dc['n']}x{dc['k']} batch {dc['b']}",
+                         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dc),
+                         "bytes_per_launch": dnb},
+            "gemv_sweep": sweep,
+            "wall_s": round(wall, 2),
+        }
+        return out, configs
 
-    evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in configs]
-           for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for s in range(args.steps):
-        run_step(evs[s])
-    stop.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    total_ms = start.elapsed_time(stop)
-
-    step_bytes = sum(gemv_bytes(c["n"], c["k"], c["b"]) for c in configs)
-    ms_per_step = total_ms / args.steps
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
-
-    sweep = []
-    dominant = None
-    for ci, c in enumerate(configs):
-        op_ms = sum(evs[s][ci][0].elapsed_time(evs[s][ci][2]) for s in range(args.steps)) / args.steps
-        main_ms = sum(evs[s][ci][1].elapsed_time(evs[s][ci][2]) for s in range(args.steps)) / args.steps
-        nb = gemv_bytes(c["n"], c["k"], c["b"])
-        row = {"dtype": c["kind"], "n": c["n"], "k": c["k"], "batch": c["b"],
-               "op_us": round(op_ms * 1e3, 2), "kernel_us": round(main_ms * 1e3, 2),
-               "op_GBps": round(nb / (op_ms * 1e-3) / 1e9, 1),
-               "kernel_GBps": round(nb / (main_ms * 1e-3) / 1e9, 1)}
-        sweep.append(row)
-        if dominant is None or main_ms > dominant[0]:
-            dominant = (main_ms, c, nb)
-
-    dm, dc, dnb = dominant
-    achieved = dnb / (dm * 1e-3) / 1e9
-    kname = "be42::k_gemv (%s)" % dc["kind"]
-    out = {
-        "metric": "decode tokens/s; quant GEMV HBM GB/s (% of peak); LSH attn µs/token @32k",
-        "value": round(value, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8/fp8 weights, fp32 activations",
-        "data": "synthetic",
-        "config": {"workload": "configs[1]: quantized GEMV sweep, INT8+FP8 per-row weights, "
-                               "shapes 4096x4096/14336x4096/4096x14336/128256x4096, batch 1/4/16",
-                   "pool_bytes_per_shape": POOL_BYTES, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": kname,
-                     "workload": f"{dc['kind']} {dc['n']}x{dc['k']} batch {dc['b']}",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dc),
-                     "bytes_per_launch": dnb},
-        "gemv_sweep": sweep,
-        "wall_s": round(wall, 2),
-    }
+    if args.no_gemv:
+        configs = []
+        out = {"metric": "decode tokens/s; quant GEMV HBM GB/s (% of peak); LSH attn µs/token @32k",
+               "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+               "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+               "dtype": "int8/fp8 weights, fp32 activations", "data": "synthetic",
+               "config": {"workload": "GEMV sweep skipped (--no-gemv)", "parallelism": "single GPU"}}
+    else:
+        out, configs = gemv_sweep()
     if not args.no_decode:
         configs.clear()
         torch.cuda.empty_cache()

@@ -9,7 +9,7 @@
  *
  * The reference-signature entry points built on top of these (op_matmul,
  * paged_kv_append, lsh_hash, op_paged_attention_sparse, ...) are declared in
- * be42_ref_abi.h.
+ * be42_engine.h.
  */
 #ifndef BE42_HIP_H
 #define BE42_HIP_H
@@ -73,6 +73,17 @@ int be42_gemv_q8_prepared(float *y, const int8_t *w, const float *w_scale, const
                           int n, int k, int batch, void *stream);
 int be42_gemv_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, const void *xdig,
                            int n, int k, int batch, void *stream);
+/* Several weight matrices of one kind and one k that share a prepared input
+ * (the q/k/v or gate/up projections of a decode step), streamed in one
+ * launch: up to 3 segments, segment i writes y [batch][n]. */
+typedef struct be42_gemv_seg {
+    const void  *w;        /* [n][k] INT8 or E4M3 codes, 16-byte aligned */
+    const float *w_scale;  /* [n] */
+    float       *y;        /* [batch][n] */
+    int          n;
+} be42_gemv_seg;
+int be42_gemv_prepared_multi(const be42_gemv_seg *segs, int nseg, const void *xdig, int k, int batch, int fp8,
+                             void *stream);
 
 /* ---- prefill GEMM ---------------------------------------------------------------
  * Y[m][n] for m < M tokens, n < N features, both operands K-contiguous
@@ -231,7 +242,13 @@ be42_kv_pool *be42_decoder_pool(be42_decoder *d);
  * device argmax (greedy decoding with no host round trip); next_tokens may be
  * NULL (the argmax stays on the device, be42_decoder_next_tokens);
  * logits_out (device, [batch][vocab]) may be NULL.  Re-running a position
- * overwrites that position's K/V. */
+ * overwrites that position's K/V.
+ * The step's kernels run on the decoder's own stream, after the work already
+ * queued on `stream`, and `stream` waits for them; they are captured once per
+ * (batch, dense or routed attention, token source, output buffers) and replayed
+ * as a HIP graph (environment BE42_DECODE_NO_GRAPH=1 launches them one by one).
+ * The call returns once the host side of the step is queued; it blocks only
+ * for next_tokens, or when the step before the last still runs. */
 int  be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
                        float *logits_out, void *stream);
 int  be42_decoder_next_tokens(be42_decoder *d, const int **dev_ptr);

@@ -92,3 +92,32 @@ def test_gemv_outliers_and_zero(be, orc):
                     torch.from_numpy(x).cuda(), kind).cpu().numpy()
         assert np.all(y[1] == 0.0)
         _check(y, want)
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("b", [1, 5, 16])
+def test_gemv_multi_segments(be, orc, kind, b):
+    """Three matrices sharing one prepared input in one launch (ragged row
+    counts, so row tiles straddle segments) against the oracle per segment
+    and against one launch per matrix."""
+    rng = np.random.default_rng(31 + b)
+    k = 1024
+    ns = (300, 64, 77)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    xdig = be.gemv_prepare(xt, kind)
+    segs, wants, singles = [], [], []
+    for n in ns:
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        wq, ws = orc.quantize_rows(w, kind)
+        wants.append(orc.gemv(wq, ws, x, kind))
+        wt, st = torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda()
+        segs.append((wt, st, torch.full((b, n), float("nan"), device="cuda")))
+        singles.append(be.gemv_prepared(wt, st, xdig, b, kind, torch.empty((b, n), device="cuda")))
+    outs = be.gemv_prepared_multi(segs, xdig, b, kind)
+    for y, want, one in zip(outs, wants, singles):
+        y = y.cpu().numpy()
+        _check(y, want)
+        # the digit-split path is far inside the north-star tolerance
+        assert rel_err(y, one.cpu().numpy()) <= 1e-6
+        assert rel_err(y, want) <= 1e-5
