@@ -18,6 +18,7 @@
 // A lane (r = lane % 16, g = lane / 16) loads 16 (INT8) or 32 (FP8)
 // contiguous bytes of weight row r per MFMA; the same k positions of digit
 // column r form the B operand.  Tiling and K-split are described at k_gemv.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <type_traits>
@@ -271,6 +272,211 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(const GemvSegs S, const uin
     }
 }
 
+// s_waitcnt immediate that waits until at most n vector-memory operations of
+// this wave are outstanding (expcnt and lgkmcnt left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Streaming GEMV with the weights and the digit planes moved HBM -> LDS by
+// the direct-to-LDS loads of gfx950 (global_load_lds_dwordx4), P stages deep,
+// so the bytes in flight sit in LDS instead of VGPRs.  A block is WAVES waves
+// (one or two per SIMD); wave w owns RT row tiles of 16 rows over the whole of K.
+// A stage is 128 k-bytes: per row tile 2 KB of weights (two wave-wide loads,
+// lane l writing LDS bytes [16l, 16l+16) of each, and later reading exactly
+// those back as its MFMA A operand) in a ring private to the wave, and
+// NC*2 KB of digit planes in a ring shared by the block.  Digit load j covers
+// column group j/2 and 16-byte pieces 4*(j%2)..+3 of the stage, lane l
+// carrying column 16*(j/2) + l%16 and piece 4*(j%2) + l/16, so that each
+// 16-lane group of a B-operand read touches 256 contiguous bytes.  The
+// block's 2*NC digit loads are spread over its waves (DI per wave; a wave
+// past the last one reloads piece 0 into a spare 1 KB, keeping the per-stage
+// load count uniform for the wait counts).
+// Iteration s: wait for this wave's loads of stage s, barrier (all waves'
+// loads of stage s are in LDS and every wave is done with stage s-1), issue
+// stage s+P-1 into the slot stage s-1 used, run stage s's MFMAs.
+template <bool FP8, int RT, int NC, int P, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const uint8_t *__restrict__ dig,
+                                                         const float *__restrict__ sx, int K, int Kp, int B)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr int COLS = NC * 16;
+    constexpr int WI = 2 * RT;                       // weight loads per wave per stage
+    constexpr int NDL = 2 * NC;                      // digit loads per block per stage
+    constexpr int DI = (NDL + WAVES - 1) / WAVES;    // digit loads per wave per stage
+    constexpr int PER = WI + DI;
+    constexpr int WRING = WAVES * P * WI * 1024;
+    constexpr int DRING = P * NDL * 1024;
+    constexpr int PART = WAVES * 16 * COLS * 4;
+    constexpr int LDS_BYTES = (WRING + DRING + 1024) > PART ? (WRING + DRING + 1024) : PART;
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    static_assert(P >= 2 && (P - 2) * PER < 64, "stages");
+    using Tot = typename std::conditional<FP8, double, long long>::type;
+    using Acc = typename std::conditional<FP8, v4f, v4i>::type;
+    using Raw = typename std::conditional<FP8, float, int>::type;
+    __shared__ __align__(1024) uint8_t lds[LDS_BYTES];
+    uint8_t *wring = lds, *dring = lds + WRING, *spare = lds + WRING + DRING;
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
+    const int row0 = (blockIdx.x * WAVES + wave) * 16 * RT;
+    const int nst = Kp / 128;
+
+    Acc acc[RT][NC];
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+            acc[t][c] = Acc{0, 0, 0, 0};
+
+    // per-lane sources: weight rows (rows past the end read the last row)
+    // and digit columns (columns past the batch read plane 0 of row 0)
+    const uint8_t *wrow[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        int local;
+        const int sg = seg_of(S, min(row0 + t * 16 + r, S.total - 1), &local);
+        wrow[t] = S.w[sg] + (size_t)local * K;
+    }
+    const int klast = K - 16;
+    // weight load v of a tile: FP8 bytes 32g + 16v (one MFMA step, two loads);
+    // INT8 bytes 64v + 16g (MFMA step v)
+    const int woff0 = FP8 ? 32 * g : 16 * g, woff1 = FP8 ? 32 * g + 16 : 64 + 16 * g;
+    const uint8_t *dsrc[DI];
+    uint8_t *ddst[DI];
+#pragma unroll
+    for (int i = 0; i < DI; i++) {
+        const int j = wave * DI + i;
+        const int jj = j < NDL ? j : 0;
+        const int col = 16 * (jj / 2) + r, q = 4 * (jj % 2) + g;
+        const int bb = col / ND, d = col % ND;
+        dsrc[i] = dig + ((size_t)d * B + (bb < B ? bb : 0)) * Kp + 16 * q;
+        ddst[i] = j < NDL ? dring + j * 1024 : spare;
+    }
+
+    auto issue = [&](int st) {
+        const int slot = st % P;
+        uint8_t *wbase = wring + ((wave * P + slot) * WI) * 1024;
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+            __builtin_amdgcn_global_load_lds((const void *)(wrow[t] + min(st * 128 + woff0, klast)),
+                                             (lds_void *)(wbase + (2 * t) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(wrow[t] + min(st * 128 + woff1, klast)),
+                                             (lds_void *)(wbase + (2 * t + 1) * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < DI; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(dsrc[i] + (size_t)st * 128),
+                                             (lds_void *)(ddst[i] == spare ? spare : ddst[i] + slot * NDL * 1024),
+                                             16, 0, 0);
+    };
+    auto compute = [&](int st) {
+        const int slot = st % P;
+        const uint8_t *wbase = wring + ((wave * P + slot) * WI) * 1024 + lane * 16;
+        const uint8_t *dbase = dring + slot * NDL * 1024;
+        if constexpr (FP8) {
+            v8i a[RT];
+#pragma unroll
+            for (int t = 0; t < RT; t++) {
+                const v4i a0 = *(const v4i *)(wbase + (2 * t) * 1024), a1 = *(const v4i *)(wbase + (2 * t + 1) * 1024);
+                a[t] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            }
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                // pieces 2g and 2g+1 of column 16c + r: load 2c + g/2, lanes r + 16*((2g) % 4) and +16
+                const uint8_t *xp = dbase + (2 * c + (g >> 1)) * 1024 + (r + 16 * ((2 * g) & 3)) * 16;
+                const v4i b0 = *(const v4i *)xp, b1 = *(const v4i *)(xp + 256);
+                const v8i bb = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+#pragma unroll
+                for (int t = 0; t < RT; t++)
+                    acc[t][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[t], bb, acc[t][c], 0, 0, 0, 127,
+                                                                                 0, 127);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                v4i a[RT];
+#pragma unroll
+                for (int t = 0; t < RT; t++)
+                    a[t] = *(const v4i *)(wbase + (2 * t + u) * 1024);
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const v4i bb = *(const v4i *)(dbase + (2 * c + u) * 1024 + lane * 16);
+#pragma unroll
+                    for (int t = 0; t < RT; t++)
+                        acc[t][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], bb, acc[t][c], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int st = 0; st < P - 1; st++)
+        if (st < nst)
+            issue(st);
+    for (int st = 0; st < nst; st++) {
+        if (st + P - 2 < nst)
+            wait_vmcnt<(P - 2) * PER>();
+        else
+            wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (st + P - 1 < nst)
+            issue(st + P - 1);
+        compute(st);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    // epilogue: each wave combines the digit columns of its own rows
+    Raw(*part)[16][COLS] = (Raw(*)[16][COLS])lds;
+    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        if (t > 0)
+            __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                part[wave][4 * g + j][16 * c + r] = acc[t][c][j];
+        __syncthreads();
+        for (int o = lane; o < 16 * B; o += kWave) {
+            const int bb = o / 16, i = o % 16;
+            const int row = row0 + t * 16 + i;
+            if (row >= S.total)
+                continue;
+            Tot tot = 0;
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                const Tot dsum = (Tot)part[wave][i][bb * ND + d];
+                if constexpr (FP8)
+                    tot = tot + dsum * kF8Weight[d];
+                else
+                    tot = tot + dsum * (Tot)(d == 0 ? kI8Base * kI8Base : (d == 1 ? kI8Base : 1));
+            }
+            int local;
+            const int sg = seg_of(S, row, &local);
+            S.y[sg][(size_t)bb * S.n[sg] + local] =
+                (float)((double)tot * ((double)sx[bb] * sxw * (double)S.sw[sg][local]));
+        }
+    }
+}
+
+template <bool FP8, int RT, int NC, int P, int WAVES>
+static void launch_dma(const GemvSegs &S, const uint8_t *dig, const float *sx, int k, int Kp, int batch,
+                       hipStream_t s)
+{
+    const int tiles = (S.total + 16 * RT - 1) / (16 * RT);
+    const int blocks = (tiles + WAVES - 1) / WAVES;
+    hipLaunchKernelGGL((k_gemv_dma<FP8, RT, NC, P, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, S, dig, sx, k,
+                       Kp, batch);
+}
+
 // Generic path for shapes the MFMA path does not take (k % 16 != 0, unaligned
 // pointers, batch > 16): one block per output row, fp32 dot of the
 // dequantized row, reduction through LDS.
@@ -341,7 +547,9 @@ static void launch_cfg(const GemvSegs &S, const uint8_t *dig, const float *sx, i
 // splitting K per row group, WAVES per block, PF register double buffering.
 struct TileCfg {
     int rt, u, ks, waves, pf;
+    int dma;   // 1: k_gemv_dma with u = pipeline stages (ks, pf unused)
 };
+constexpr TileCfg dma_tile(int rt, int stages, int waves) { return TileCfg{rt, stages, 0, waves, 0, 1}; }
 
 static TileCfg pick_tile(bool fp8, int nc, int n, int k)
 {
@@ -356,18 +564,20 @@ static TileCfg pick_tile(bool fp8, int nc, int n, int k)
         if (nc == 2) {
             if (n <= 4096)
                 return k <= 4096 ? TileCfg{1, 1, 8, 8, 1} : TileCfg{1, 1, 8, 8, 0};
-            return n <= 32768 ? TileCfg{2, 4, 2, 4, 0} : TileCfg{4, 1, 2, 4, 0};
+            return n <= 8192 ? TileCfg{2, 4, 2, 4, 0} : dma_tile(1, 4, 4);
         }
         if (nc == 3) {
             if (n <= 4096)
                 return {1, 1, 4, 4, 1};
             if (n <= 8192)
                 return {2, 2, 4, 4, 0};
-            return n <= 32768 ? TileCfg{4, 1, 4, 4, 0} : TileCfg{4, 2, 1, 4, 0};
+            return n <= 32768 ? dma_tile(1, 4, 4) : dma_tile(2, 3, 8);
         }
         if (n <= 4096)
             return k <= 4096 ? TileCfg{1, 1, 4, 4, 0} : TileCfg{1, 2, 4, 4, 1};
-        return n <= 32768 ? TileCfg{4, 2, 4, 4, 0} : TileCfg{4, 2, 1, 4, 0};
+        if (n <= 8192)
+            return {4, 2, 4, 4, 0};
+        return n <= 32768 ? dma_tile(1, 4, 4) : dma_tile(2, 3, 4);
     }
     if (nc == 1) {
         if (n <= 2048)
@@ -378,12 +588,17 @@ static TileCfg pick_tile(bool fp8, int nc, int n, int k)
     }
     if (n <= 4096)
         return k <= 4096 ? TileCfg{1, 2, 4, 4, 0} : TileCfg{1, 2, 8, 8, 1};
-    return n <= 32768 ? TileCfg{4, 2, 4, 4, 1} : TileCfg{4, 2, 2, 8, 1};
+    if (n <= 8192)
+        return {4, 2, 4, 4, 1};
+    return n <= 32768 ? dma_tile(1, 5, 4) : dma_tile(1, 3, 8);
 }
 
 #define BE42_TILE(RT, U, KS, W, PF)                                                                                \
-    if (c.rt == RT && c.u == U && c.ks == KS && c.waves == W && c.pf == PF)                                      \
+    if (!c.dma && c.rt == RT && c.u == U && c.ks == KS && c.waves == W && c.pf == PF)                            \
         return launch_cfg<FP8, RT, U, NC, KS, W, PF>(S, dig, sx, k, Kp, batch, s), true;
+#define BE42_DMA(RT, P, W)                                                                                         \
+    if (c.dma && c.rt == RT && c.u == P && c.waves == W)                                                          \
+        return launch_dma<FP8, RT, NC, P, W>(S, dig, sx, k, Kp, batch, s), true;
 
 // The shapes pick_tile returns for each (dtype, NC); false if c is not one.
 template <bool FP8, int NC>
@@ -394,20 +609,23 @@ static bool launch_tile(const TileCfg &c, const GemvSegs &S, const uint8_t *dig,
         BE42_TILE(1, 4, 4, 4, 1) BE42_TILE(1, 2, 8, 8, 0) BE42_TILE(2, 2, 8, 8, 1) BE42_TILE(2, 1, 4, 8, 1)
         BE42_TILE(2, 1, 4, 4, 1)
     } else if constexpr (FP8 && NC == 2) {
-        BE42_TILE(1, 1, 8, 8, 1) BE42_TILE(1, 1, 8, 8, 0) BE42_TILE(2, 4, 2, 4, 0) BE42_TILE(4, 1, 2, 4, 0)
+        BE42_TILE(1, 1, 8, 8, 1) BE42_TILE(1, 1, 8, 8, 0) BE42_TILE(2, 4, 2, 4, 0) BE42_DMA(1, 4, 4)
     } else if constexpr (FP8 && NC == 3) {
-        BE42_TILE(1, 1, 4, 4, 1) BE42_TILE(2, 2, 4, 4, 0) BE42_TILE(4, 1, 4, 4, 0) BE42_TILE(4, 2, 1, 4, 0)
+        BE42_TILE(1, 1, 4, 4, 1) BE42_TILE(2, 2, 4, 4, 0) BE42_DMA(1, 4, 4) BE42_DMA(2, 3, 8)
     } else if constexpr (FP8) {
-        BE42_TILE(1, 1, 4, 4, 0) BE42_TILE(1, 2, 4, 4, 1) BE42_TILE(4, 2, 4, 4, 0) BE42_TILE(4, 2, 1, 4, 0)
+        BE42_TILE(1, 1, 4, 4, 0) BE42_TILE(1, 2, 4, 4, 1) BE42_TILE(4, 2, 4, 4, 0) BE42_DMA(1, 4, 4)
+        BE42_DMA(2, 3, 4)
     } else if constexpr (NC == 1) {
         BE42_TILE(1, 8, 8, 8, 1) BE42_TILE(1, 4, 8, 8, 1) BE42_TILE(1, 8, 4, 4, 1) BE42_TILE(1, 2, 8, 8, 1)
         BE42_TILE(2, 2, 4, 4, 0) BE42_TILE(2, 2, 4, 4, 1)
     } else {
-        BE42_TILE(1, 2, 4, 4, 0) BE42_TILE(1, 2, 8, 8, 1) BE42_TILE(4, 2, 4, 4, 1) BE42_TILE(4, 2, 2, 8, 1)
+        BE42_TILE(1, 2, 4, 4, 0) BE42_TILE(1, 2, 8, 8, 1) BE42_TILE(4, 2, 4, 4, 1) BE42_DMA(1, 5, 4)
+        BE42_DMA(1, 3, 8)
     }
     return false;
 }
 #undef BE42_TILE
+#undef BE42_DMA
 
 // NC = ceil(batch * digits / 16) MFMA column groups.
 template <bool FP8>
@@ -435,7 +653,8 @@ static int segs_launch(const GemvSegs &S, const void *buf, int k, int batch, hip
         default: ok = launch_tile<false, 3>(c, S, dig, sx, k, Kp, batch, s); break;
         }
     }
-    BE42_CHECK(ok, "be42 gemv: no kernel for tile (%d,%d,%d,%d,%d) at nc %d", c.rt, c.u, c.ks, c.waves, c.pf, nc);
+    BE42_CHECK(ok, "be42 gemv: no kernel for tile (%d,%d,%d,%d,%d,%d) at nc %d", c.rt, c.u, c.ks, c.waves, c.pf,
+               c.dma, nc);
     BE42_LAUNCH_CHECK();
     return BE42_OK;
 }

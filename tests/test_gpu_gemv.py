@@ -121,3 +121,43 @@ def test_gemv_multi_segments(be, orc, kind, b):
         # the digit-split path is far inside the north-star tolerance
         assert rel_err(y, one.cpu().numpy()) <= 1e-6
         assert rel_err(y, want) <= 1e-5
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("b", [4, 8, 16])
+def test_gemv_lds_stream_shapes(be, orc, kind, b):
+    """Row counts past 8192 at batch >= 4 take the LDS-staged streaming
+    kernel: a ragged row count (not a multiple of any tile), k not a multiple
+    of the 128-byte stage, and three segments whose row tiles straddle."""
+    rng = np.random.default_rng(400 + b)
+    k = 1040
+    ns = (20011, 5000, 8002)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    xdig = be.gemv_prepare(xt, kind)
+    segs, wants = [], []
+    for n in ns:
+        if kind == "int8":
+            wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+            ws = rng.uniform(0.005, 0.02, n).astype(np.float32)
+        else:
+            wq = rng.integers(0, 256, (n, k), dtype=np.uint8)
+            wq[(wq & 0x7F) == 0x7F] = 0x7E
+            ws = rng.uniform(0.005, 0.02, n).astype(np.float32) / 200.0
+        wants.append(orc.gemv(wq, ws, x, kind))
+        segs.append((torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda(),
+                     torch.full((b, n), float("nan"), device="cuda")))
+    # INT8 digit sums are exact int32; FP8 sums accumulate in fp32 inside the
+    # MFMA, and codes drawn uniformly over all 256 (|w| up to 448) put that
+    # rounding at ~1e-5 relative -- inside the north-star 1e-3, bounded at 1e-4
+    tight = 1e-5 if kind == "int8" else 1e-4
+    outs = be.gemv_prepared_multi(segs, xdig, b, kind)
+    for y, want in zip(outs, wants):
+        y = y.cpu().numpy()
+        _check(y, want)
+        assert rel_err(y, want) <= tight
+    # one matrix alone (33013 rows)
+    w_all = torch.cat([s[0] for s in segs]).contiguous()
+    s_all = torch.cat([s[1] for s in segs]).contiguous()
+    y1 = be.gemv_prepared(w_all, s_all, xdig, b, kind, torch.empty((b, sum(ns)), device="cuda")).cpu().numpy()
+    assert rel_err(y1, np.concatenate(wants, axis=1)) <= tight
