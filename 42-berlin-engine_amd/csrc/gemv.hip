@@ -106,6 +106,71 @@ __device__ __forceinline__ int seg_of(const GemvSegs &S, int row, int *local)
     return sg;
 }
 
+// Epilogue operands of a lane, loaded at kernel start so their latency hides
+// under the weight stream.  In the epilogue loop over o = lane + 64 j the
+// lane's output row within a tile is always r = lane % 16 and its batch rows
+// are g + 4 j (g = lane / 16), j < 4.
+template <int RT>
+struct EpiOps {
+    float sw[RT];
+    float *y[RT];
+    int n[RT];
+    float sx[4];
+};
+
+template <int RT>
+__device__ __forceinline__ void epi_load(EpiOps<RT> &E, const GemvSegs &S, const float *sx, int row0, int r, int g,
+                                         int B)
+{
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const int row = row0 + t * 16 + r;
+        if (row < S.total) {
+            int local;
+            const int sg = seg_of(S, row, &local);
+            E.sw[t] = S.sw[sg][local];
+            E.y[t] = S.y[sg] + local;
+            E.n[t] = S.n[sg];
+        } else {
+            E.sw[t] = 0.0f;
+            E.y[t] = nullptr;
+            E.n[t] = 0;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        E.sx[j] = g + 4 * j < B ? sx[g + 4 * j] : 0.0f;
+}
+
+// y for row tile t from the digit sums of each (row, batch row): raw(d, bb)
+// returns the sum of digit plane d of batch row bb for the lane's row.
+template <bool FP8, int RT, class RawAt>
+__device__ __forceinline__ void epi_store(const EpiOps<RT> &E, int t, int g, int B, RawAt raw)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    using Tot = typename std::conditional<FP8, double, long long>::type;
+    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
+    if (!E.y[t])
+        return;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int bb = g + 4 * j;
+        if (bb >= B)
+            break;
+        Tot tot = 0;
+#pragma unroll
+        for (int d = 0; d < ND; d++) {
+            const Tot dsum = raw(d, bb);
+            // digit weights: INT8 254^(2-d) (exact in int64), FP8 30^-d
+            if constexpr (FP8)
+                tot = tot + dsum * kF8Weight[d];
+            else
+                tot = tot + dsum * (Tot)(d == 0 ? kI8Base * kI8Base : (d == 1 ? kI8Base : 1));
+        }
+        E.y[t][(size_t)bb * E.n[t]] = (float)((double)tot * ((double)E.sx[j] * sxw * (double)E.sw[t]));
+    }
+}
+
 // Main GEMV kernel.
 // Operands of one MFMA: A = 16 weight rows x STEP k (row r = lane % 16, k
 // slice lane / 16), B = STEP k x 16 columns, where column c of column group nc
@@ -143,6 +208,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(const GemvSegs S, const uin
     const int row0 = (blockIdx.x * GROUPS + group) * 16 * RT;
     const int nburst = Kp / (STEP * U);
     const int b0 = (nburst * slice) / KS, b1 = (nburst * (slice + 1)) / KS;
+    EpiOps<RT> E;
+    if (slice == 0)
+        epi_load<RT>(E, S, sx, row0, r, g, B);
 
     Acc acc[RT][NC];
 #pragma unroll
@@ -233,7 +301,6 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(const GemvSegs S, const uin
     // C layout of a 16x16 MFMA: lane holds rows 4*(lane/16)+j of column lane%16.
     // One row tile at a time through LDS: slices and digit columns are summed
     // per output by the group's first wave.
-    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
 #pragma unroll
     for (int t = 0; t < RT; t++) {
         if (t > 0)
@@ -244,31 +311,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(const GemvSegs S, const uin
             for (int j = 0; j < 4; j++)
                 part[wave][4 * g + j][16 * c + r] = acc[t][c][j];
         __syncthreads();
-        if (slice == 0) {
-            for (int o = lane; o < 16 * B; o += kWave) {
-                const int bb = o / 16, i = o % 16;
-                const int row = row0 + t * 16 + i;
-                if (row >= S.total)
-                    continue;
-                Tot tot = 0;
+        if (slice == 0)
+            epi_store<FP8, RT>(E, t, g, B, [&](int d, int bb) {
+                Tot dsum = 0;
 #pragma unroll
-                for (int d = 0; d < ND; d++) {
-                    Tot dsum = 0;
-#pragma unroll
-                    for (int s = 0; s < KS; s++)
-                        dsum += (Tot)part[group * KS + s][i][bb * ND + d];
-                    // digit weights: INT8 254^(2-d) (exact in int64), FP8 30^-d
-                    if constexpr (FP8)
-                        tot = tot + dsum * kF8Weight[d];
-                    else
-                        tot = tot + dsum * (Tot)(d == 0 ? kI8Base * kI8Base : (d == 1 ? kI8Base : 1));
-                }
-                int local;
-                const int sg = seg_of(S, row, &local);
-                S.y[sg][(size_t)bb * S.n[sg] + local] =
-                    (float)((double)tot * ((double)sx[bb] * sxw * (double)S.sw[sg][local]));
-            }
-        }
+                for (int sl = 0; sl < KS; sl++)
+                    dsum += (Tot)part[group * KS + sl][r][bb * ND + d];
+                return dsum;
+            });
     }
 }
 
@@ -326,6 +376,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
     const int r = lane & 15, g = lane >> 4;
     const int row0 = (blockIdx.x * WAVES + wave) * 16 * RT;
     const int nst = Kp / 128;
+    EpiOps<RT> E;
+    epi_load<RT>(E, S, sx, row0, r, g, B);
 
     Acc acc[RT][NC];
 #pragma unroll
@@ -434,7 +486,6 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
 
     // epilogue: each wave combines the digit columns of its own rows
     Raw(*part)[16][COLS] = (Raw(*)[16][COLS])lds;
-    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
 #pragma unroll
     for (int t = 0; t < RT; t++) {
         if (t > 0)
@@ -445,25 +496,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
             for (int j = 0; j < 4; j++)
                 part[wave][4 * g + j][16 * c + r] = acc[t][c][j];
         __syncthreads();
-        for (int o = lane; o < 16 * B; o += kWave) {
-            const int bb = o / 16, i = o % 16;
-            const int row = row0 + t * 16 + i;
-            if (row >= S.total)
-                continue;
-            Tot tot = 0;
-#pragma unroll
-            for (int d = 0; d < ND; d++) {
-                const Tot dsum = (Tot)part[wave][i][bb * ND + d];
-                if constexpr (FP8)
-                    tot = tot + dsum * kF8Weight[d];
-                else
-                    tot = tot + dsum * (Tot)(d == 0 ? kI8Base * kI8Base : (d == 1 ? kI8Base : 1));
-            }
-            int local;
-            const int sg = seg_of(S, row, &local);
-            S.y[sg][(size_t)bb * S.n[sg] + local] =
-                (float)((double)tot * ((double)sx[bb] * sxw * (double)S.sw[sg][local]));
-        }
+        epi_store<FP8, RT>(E, t, g, B, [&](int d, int bb) { return (Tot)part[wave][r][bb * ND + d]; });
     }
 }
 
