@@ -263,63 +263,105 @@ __global__ __launch_bounds__(kRowThreads) void k_silu_mul(float *__restrict__ ou
 // argmax_simd_f32: the maximum value wins; among equal maxima in the
 // 8-lane part (indices below 8*floor(n/8), n >= 8) the lowest lane (i % 8),
 // then the first index; tail entries win only with a strictly larger value.
-__global__ __launch_bounds__(1024) void k_argmax(int *__restrict__ out, const float *__restrict__ logits, int n)
+// In one pass: (max, smallest key (i % 8, i) among the elements equal to
+// it) is an associative pair, so kArgChunks blocks per row reduce their
+// chunks of the 8-lane part, and the last block of the row to finish
+// (counted with an atomic in cnt[row], which it resets for the next call)
+// combines the chunks in order and applies the tail rule.
+constexpr int kArgChunks = 64;
+struct ArgPart {
+    float vm;
+    int pad;
+    unsigned long long key;
+};
+
+__device__ __forceinline__ void arg_merge(float &vm, unsigned long long &key, float v2, unsigned long long k2)
 {
-    __shared__ float redv[16], redt[16];
-    __shared__ unsigned long long redk[16];
-    __shared__ float vmax_s, tmax_s;
-    const float *x = logits + (size_t)blockIdx.x * n;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (v2 > vm || (v2 == vm && k2 < key)) {
+        vm = v2;
+        key = k2;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_argmax(int *__restrict__ out, const float *__restrict__ logits, int n,
+                                                ArgPart *__restrict__ parts, int *__restrict__ cnt)
+{
+    __shared__ float rv[4];
+    __shared__ unsigned long long rk[4];
+    __shared__ int last;
+    const int row = blockIdx.y, c = blockIdx.x;
+    const float *x = logits + (size_t)row * n;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int main = n < 8 ? 0 : (n & ~7);
-    float vm = -INFINITY, tm = -INFINITY;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        if (i < main)
-            vm = fmaxf(vm, x[i]);
-        else
-            tm = fmaxf(tm, x[i]);
-    }
-    vm = wave_max(vm);
-    tm = wave_max(tm);
-    if (lane == 0) {
-        redv[wave] = vm;
-        redt[wave] = tm;
-    }
-    __syncthreads();
-    if (wave == 0) {
-        float a = lane < nw ? redv[lane] : -INFINITY, t = lane < nw ? redt[lane] : -INFINITY;
-        a = wave_max(a);
-        t = wave_max(t);
-        if (lane == 0) {
-            vmax_s = a;
-            tmax_s = t;
-        }
-    }
-    __syncthreads();
-    const float vmax = vmax_s, tmax = tmax_s;
-    const bool tail_wins = main == 0 || tmax > vmax;
-    const float target = tail_wins ? tmax : vmax;
-    // smallest key among the winners: (lane, index) in the vector part, index in the tail
+    const int cs = ((main + kArgChunks - 1) / kArgChunks + 7) & ~7;
+    const int lo = min(c * cs, main), hi = min(lo + cs, main);
+    float vm = -INFINITY;
     unsigned long long key = ~0ull;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const bool in_vec = i < main;
-        if (in_vec != tail_wins && x[i] == target) {
-            const unsigned long long k =
-                tail_wins ? (unsigned long long)i : ((unsigned long long)(i & 7) << 32) | (unsigned)i;
-            key = k < key ? k : key;
+    for (int i0 = lo; i0 < hi; i0 += 8 * 256) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = i0 + j * 256 + threadIdx.x;
+            v[j] = i < hi ? x[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = i0 + j * 256 + threadIdx.x;
+            if (i < hi)
+                arg_merge(vm, key, v[j], ((unsigned long long)(i & 7) << 32) | (unsigned)i);
         }
     }
     for (int o = 32; o > 0; o >>= 1) {
-        const unsigned long long other = __shfl_xor(key, o);
-        key = other < key ? other : key;
+        const float v2 = __shfl_xor(vm, o);
+        const unsigned long long k2 = __shfl_xor(key, o);
+        arg_merge(vm, key, v2, k2);
     }
-    if (lane == 0)
-        redk[wave] = key;
+    if (lane == 0) {
+        rv[wave] = vm;
+        rk[wave] = key;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        unsigned long long k = ~0ull;
-        for (int w = 0; w < nw; w++)
-            k = redk[w] < k ? redk[w] : k;
-        out[blockIdx.x] = k == ~0ull ? 0 : (int)(k & 0xFFFFFFFFu);
+        for (int w = 1; w < 4; w++)
+            arg_merge(vm, key, rv[w], rk[w]);
+        parts[(size_t)row * kArgChunks + c] = ArgPart{vm, 0, key};
+        __threadfence();
+        last = atomicAdd(&cnt[row], 1) == kArgChunks - 1;
+    }
+    __syncthreads();
+    if (!last)
+        return;
+    __threadfence();
+    if (wave == 0) {
+        float cv = -INFINITY;
+        unsigned long long ck = ~0ull;
+        if (lane < kArgChunks) {
+            const ArgPart p = parts[(size_t)row * kArgChunks + lane];
+            cv = p.vm;
+            ck = p.key;
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float v2 = __shfl_xor(cv, o);
+            const unsigned long long k2 = __shfl_xor(ck, o);
+            arg_merge(cv, ck, v2, k2);
+        }
+        if (lane == 0) {
+            // tail: first index of the largest value; wins only if strictly larger
+            float tm = -INFINITY;
+            int ti = -1;
+            for (int i = main; i < n; i++)
+                if (ti < 0 || x[i] > tm) {
+                    tm = x[i];
+                    ti = i;
+                }
+            int res;
+            if (main == 0 || (ti >= 0 && tm > cv))
+                res = ti >= 0 ? ti : 0;
+            else
+                res = ck == ~0ull ? 0 : (int)(ck & 0xFFFFFFFFu);
+            out[row] = res;
+            cnt[row] = 0;
+        }
     }
 }
 
@@ -339,6 +381,8 @@ struct be42_decoder {
     void *xdig = nullptr;
     size_t xdig_bytes = 0;
     int *sel = nullptr, *nsel = nullptr, *slots = nullptr, *next = nullptr;
+    ArgPart *arg_parts = nullptr;   // [max_batch][kArgChunks] argmax partials
+    int *arg_cnt = nullptr;         // [max_batch] chunk counters, zero between calls
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     int *cand = nullptr, *ncand = nullptr;
@@ -433,6 +477,8 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
     alloc((void **)&d->nsel, (size_t)B * 4);
     alloc((void **)&d->slots, (size_t)c.n_layers * B * 4);
     alloc((void **)&d->next, (size_t)B * 4);
+    alloc((void **)&d->arg_parts, (size_t)B * kArgChunks * sizeof(ArgPart));
+    alloc((void **)&d->arg_cnt, (size_t)B * 4);
     alloc((void **)&d->cand, (size_t)B * std::max(c.cand_cap, 1) * 4);
     alloc((void **)&d->ncand, (size_t)B * 4);
     d->xdig_bytes = std::max(be42_gemv_xdig_bytes(wide, B, c.wkind), be42_gemv_xdig_bytes(c.dim, B, c.wkind));
@@ -470,6 +516,8 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
         e = hipEventCreateWithFlags(&d->ev_out, hipEventDisableTiming);
     if (e == hipSuccess)
         e = hipMemset(d->next, 0, (size_t)B * 4);
+    if (e == hipSuccess)
+        e = hipMemset(d->arg_cnt, 0, (size_t)B * 4);
     {
         const char *ng = getenv("BE42_DECODE_NO_GRAPH");
         d->use_graph = !(ng && ng[0] == '1');
@@ -509,7 +557,7 @@ extern "C" void be42_decoder_destroy(be42_decoder *d)
     if (d->pool)
         be42_kv_destroy(d->pool);
     void *ptrs[] = {d->cos_t, d->sin_t, d->x, d->xb, d->xn, d->q, d->k, d->v, d->att, d->hb, d->hb2, d->logits, d->sel,
-                    d->nsel, d->slots, d->next, d->cand, d->ncand, d->xdig, d->attn_ws};
+                    d->nsel, d->slots, d->next, d->cand, d->ncand, d->xdig, d->attn_ws, d->arg_parts, d->arg_cnt};
     for (void *p : ptrs)
         if (p)
             (void)hipFree(p);
@@ -646,7 +694,8 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     BE42_HIP(norm(d->w.final_norm, pending));
     float *lg = logits_out ? logits_out : d->logits;
     DEC_TRY(gemv(d, lg, d->w.out, d->w.out_s, c.vocab, dim, B, st));
-    hipLaunchKernelGGL(k_argmax, dim3(B), dim3(1024), 0, st, d->next, lg, c.vocab);
+    hipLaunchKernelGGL(k_argmax, dim3(kArgChunks, B), dim3(256), 0, st, d->next, lg, c.vocab, d->arg_parts,
+                       d->arg_cnt);
     BE42_LAUNCH_CHECK();
     BE42_HIP(hipMemcpyAsync(d->next_host, d->next, (size_t)B * 4, hipMemcpyDeviceToHost, st));
     return BE42_OK;

@@ -42,12 +42,12 @@ constexpr int kMaxCandList = 512;   // be42_lsh_candidates cap
 constexpr int kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
 
 struct RouteSmem {
-    int off_qm, off_q0, off_hp, off_list, off_cnt, off_offs, off_cand, off_mid, off_sc, off_pt, off_ph, stage, bytes;
+    int off_qm, off_q0, off_hp, off_list, off_cnt, off_offs, off_cand, off_mid, off_sc, off_mpt, off_ph, stage, bytes;
 };
 
 // LDS layout of the router.  When they fit in the workgroup's LDS, the
-// layer's page table and page hashes are staged there (stage = max_logical),
-// else read from HBM (stage = 0).
+// layer's page hashes are staged there (stage = max_logical), else read from
+// HBM (stage = 0).
 __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical)
 {
     RouteSmem r;
@@ -61,8 +61,8 @@ __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical
     r.off_cand = o; o += cap * 4;
     r.off_mid = o;  o += cap * 4;
     r.off_sc = o;   o += cap * 4;
-    r.stage = o + max_logical * 6 + 16 <= kLdsBytes ? max_logical : 0;
-    r.off_pt = o;   o += r.stage * 4;
+    r.off_mpt = o;  o += cap * 4 + 4 * 4;
+    r.stage = o + max_logical * 2 + 16 <= kLdsBytes ? max_logical : 0;
     r.off_ph = o;   o += (r.stage * 2 + 15) & ~15;
     r.bytes = o;
     return r;
@@ -93,7 +93,6 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     int *cand = (int *)(smem + L.off_cand);
     int *mid = (int *)(smem + L.off_mid);
     float *sc = (float *)(smem + L.off_sc);
-    int *pt_s = (int *)(smem + L.off_pt);
     uint16_t *ph_s = (uint16_t *)(smem + L.off_ph);
 
     const int b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -116,18 +115,45 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     }
     const int nidx = min(P.n_indexed[layer], P.max_logical);
 
-    // 0. loads that do not depend on the query hash are issued together:
-    //    page table and page hashes (staged), projection, q
+    // 0. loads that do not depend on the query hash, each thread's share
+    //    issued before any is stored: page hashes (staged), projection, the
+    //    first and last page of the table
+    int *mpt = (int *)(smem + L.off_mpt);      // [cap] physical page of mid[e]; [cap], [cap+1]: first, last
     if (STAGE) {
-        for (int i = tid; i < n; i += blockDim.x)
-            pt_s[i] = P.page_table[base + i];
-        for (int i = tid; i < nidx; i += blockDim.x)
-            ph_s[i] = P.page_hash[base + i];
+        for (int i0 = 0; i0 < nidx; i0 += 8 * 256) {
+            uint16_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + j * 256 + tid;
+                v[j] = i < nidx ? P.page_hash[base + i] : (uint16_t)0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + j * 256 + tid;
+                if (i < nidx)
+                    ph_s[i] = v[j];
+            }
+        }
     }
-    const int *pt = STAGE ? pt_s : P.page_table + base;
     const uint16_t *ph = STAGE ? ph_s : P.page_hash + base;
-    for (int i = tid; i < hd * 16; i += blockDim.x)
-        hp[i] = P.hpT[i];
+    for (int i0 = 0; i0 < hd * 16; i0 += 8 * 256) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = i0 + j * 256 + tid;
+            v[j] = i < hd * 16 ? P.hpT[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = i0 + j * 256 + tid;
+            if (i < hd * 16)
+                hp[i] = v[j];
+        }
+    }
+    if (tid == 0) {
+        mpt[cap] = P.page_table[base];
+        mpt[cap + 1] = P.page_table[base + n - 1];
+    }
 
     // 1. q_mean (inference.c:291-295): sum in head order, then / n_heads;
     //    32 heads' loads are issued before the sum consumes them
@@ -258,10 +284,12 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     for (int e0 = 0; e0 < nm; e0 += 128) {
         const int e = e0 + (tid >> 1), half = tid & 1;
         const int ee = e < nm ? e : nm - 1;
-        const int phys = pt[mid[ee]];
+        const int phys = P.page_table[base + mid[ee]];
         const float s = dot_ref8x2(q0, P.centroid + (size_t)phys * hd, hd, half);
-        if (half == 0 && e < nm)
+        if (half == 0 && e < nm) {
             sc[e] = s;
+            mpt[e] = phys;
+        }
     }
     __syncthreads();
 
@@ -269,7 +297,7 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     //    min(k-2, #middle, 62), strict replacement) run by wave 0
     if (wave != 0)
         return;
-    const int first = pt[0], last = pt[n - 1];
+    const int first = mpt[cap], last = mpt[cap + 1];
     int ns = 0;
     if (lane == 0)
         selb[0] = first;
@@ -291,7 +319,7 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     }
     const int size = heap.size, hi = heap.hi;
     if (lane < size)
-        selb[ns + lane] = pt[mid[hi]];
+        selb[ns + lane] = mpt[hi];
     if (lane == 0)
         nsel[b] = ns + size;
 }
