@@ -40,6 +40,7 @@ SIGNATURES = {
     "be42_gemv_q8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemv_fp8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemv_prepared_multi": (i32, [vp, i32, vp, i32, i32, i32, vp]),
+    "be42_lsh_attention": (i32, [vp, vp, vp, i32, i32, i32, i32, f32, vp, vp, vp, i32, vp]),
     "be42_gemm_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_decoder_create": (i32, [vp, vp, vp, vp]),
@@ -271,6 +272,21 @@ class Lib:
         self._call("be42_lsh_route", pool.handle, self.p(q), self.p(slots), B, H, k_sel, cap, self.p(sel),
                    self.p(nsel), sel_stride, self.p(cand), self.p(ncand), self.p(qh), self.stream())
         return sel, nsel, cand, ncand, qh
+
+    def lsh_attention(self, pool, q, k_sel, cap, scale, slots=None, out=None, want_sel=True):
+        """Route + sparse attention in one launch; returns (out, sel, nsel)
+        (sel, nsel None when want_sel is False)."""
+        t = self.torch
+        B, H, hd = q.shape
+        out = out if out is not None else t.empty((B, H, hd), dtype=t.float32, device=q.device)
+        sel = nsel = None
+        stride = max(k_sel, 64)
+        if want_sel:
+            sel = t.full((B, stride), -1, dtype=t.int32, device=q.device)
+            nsel = t.zeros(B, dtype=t.int32, device=q.device)
+        self._call("be42_lsh_attention", pool.handle, self.p(q), self.p(slots), B, H, k_sel, cap, float(scale),
+                   self.p(out), self.p(sel), self.p(nsel), stride, self.stream())
+        return out, sel, nsel
 
     def paged_attention(self, pool, q, sel, nsel, max_sel, scale, n_split=1, out=None, workspace=None):
         t = self.torch

@@ -27,9 +27,11 @@
 //                   l = sum w_t;
 //   k_attn_apply    partial o = sum_t w_t v_t over the split's pages;
 //   k_attn_combine  out = (sum over splits) * (1 / l).
+#include <algorithm>
 #include <type_traits>
 
 #include "be42_common.h"
+#include "route.h"
 
 namespace be42 {
 
@@ -328,60 +330,59 @@ __device__ __forceinline__ float group_sum(float a)
     return a;
 }
 
+// LDS of the fused attention: per selected page ("slot") its physical page
+// and token count, the scores / weights of the G heads per slot, and the
+// cross-wave reduction of o.
+template <int HD, int G, int WAVES>
+struct AttnShared {
+    float qs[G][HD];
+    float sc[G][kFusedMaxPages * 17];
+    float red[WAVES][G][HD];
+    float lsh[G];
+    int pphys[kFusedMaxPages], pnt[kFusedMaxPages], order[kFusedMaxPages];
+};
+
+template <int HD, int G, int WAVES>
+__device__ __forceinline__ void attn_load_q(AttnShared<HD, G, WAVES> &S, const float *__restrict__ q, int b, int kvh,
+                                            int H)
+{
+    for (int i = threadIdx.x; i < G * HD; i += blockDim.x)
+        S.qs[i / HD][i % HD] = q[((size_t)b * H + kvh * G + i / HD) * HD + i % HD];
+}
+
+// A. scores of the ns pages of S.pphys (slot order) for the G heads, by
+// waves w0 .. w0+nw-1.
 template <bool BF16, int HD, int G, int WAVES, int UNR>
-__global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P, const float *__restrict__ q,
-                                                           const int *__restrict__ sel,
-                                                           const int *__restrict__ nsel, int sel_stride, int H,
-                                                           float scale, float *__restrict__ out)
+__device__ __forceinline__ void attn_scores(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
+                                            float scale, int w0, int nw)
 {
     constexpr int RL = HD / 8;                 // lanes per row
     constexpr int RPW = kWave / RL;            // rows per wave per step
     using Raw = typename RawRow<BF16>::T;
-    __shared__ float qs[G][HD];
-    __shared__ float sc[G][kFusedMaxPages * 17];
-    __shared__ float red[WAVES][G][HD];
-    __shared__ float lsh[G];
-    __shared__ int pphys[kFusedMaxPages], pnt[kFusedMaxPages];
-
-    const int b = blockIdx.x, kvh = blockIdx.y;
     const int n_kv = P.n_kv;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int ns = min(nsel[b], kFusedMaxPages);
-    const int *selb = sel + (size_t)b * sel_stride;
-    for (int i = tid; i < G * HD; i += blockDim.x)
-        qs[i / HD][i % HD] = q[((size_t)b * H + kvh * G + i / HD) * HD + i % HD];
-    for (int i = tid; i < ns; i += blockDim.x) {
-        const int ph = selb[i];
-        pphys[i] = ph;
-        pnt[i] = P.ntok[ph];
-    }
-    __syncthreads();
-
-    const int rsub = lane / RL, rl = lane % RL;   // row within the step, lane within the row
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rsub = lane / RL, rl = lane % RL;
     const int T = ns * kPg;
-    constexpr int rows_per_iter = WAVES * RPW;
-
+    const int rows_per_iter = nw * RPW;
     auto load_raw = [&](const void *base, int r, float &sc_out) -> Raw {
         const int rr = r < T ? r : T - 1;
         const int pg = rr / kPg, t = rr % kPg;
-        const size_t slot = ((size_t)pphys[pg] * n_kv + kvh) * kPg + t;
+        const size_t slot = ((size_t)S.pphys[pg] * n_kv + kvh) * kPg + t;
         if constexpr (BF16) {
             sc_out = 1.0f;
             return *(const Raw *)((const uint16_t *)base + slot * HD + rl * 8);
         } else {
-            sc_out = (base == P.k ? P.k_scale : P.v_scale)[slot];
+            sc_out = P.k_scale[slot];
             return *(const Raw *)((const int8_t *)base + slot * HD + rl * 8);
         }
     };
-
-    // A. scores
     float qv[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            qv[g][j] = qs[g][rl * 8 + j];
-    for (int r0 = wave * RPW; r0 < T; r0 += rows_per_iter * UNR) {
+            qv[g][j] = S.qs[g][rl * 8 + j];
+    for (int r0 = (wave - w0) * RPW; r0 < T; r0 += rows_per_iter * UNR) {
         Raw kr[UNR];
         float ks[UNR];
 #pragma unroll
@@ -405,19 +406,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
                 const int pg = r / kPg, t = r % kPg;
 #pragma unroll
                 for (int g = 0; g < G; g++)
-                    sc[g][pg * 17 + t] = acc[g] * scale;
+                    S.sc[g][pg * 17 + t] = acc[g] * scale;
             }
         }
     }
-    __syncthreads();
+}
 
-    // B. weights, wave g <-> head g, lane <-> page
+// B. weights: wave g <-> head g, lane <-> selection position p (slot
+// order[p], or p when order is NULL), the closed-form online softmax of the
+// file header over the selection order; l = sum w.
+template <int HD, int G, int WAVES>
+__device__ __forceinline__ void attn_weights(AttnShared<HD, G, WAVES> &S, int ns, const int *order)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int g = wave; g < G; g += WAVES) {
-        float *s = sc[g];
-        const int nt = lane < ns ? pnt[lane] : 0;
+        float *s = S.sc[g];
+        const int slot = lane < ns ? (order ? order[lane] : lane) : 0;
+        const int nt = lane < ns ? S.pnt[slot] : 0;
         float lm = -INFINITY;
         for (int t = 0; t < nt; t++)
-            lm = fmaxf(lm, s[lane * 17 + t]);
+            lm = fmaxf(lm, s[slot * 17 + t]);
         float inc = lm;
 #pragma unroll
         for (int o = 1; o < kWave; o <<= 1) {
@@ -433,11 +441,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
         for (int t = 0; t < kPg; t++) {
             av[t] = 1.0f;
             if (t < nt) {
-                const float st = s[lane * 17 + t];
+                const float st = s[slot * 17 + t];
                 const float mprev = m;
                 m = fmaxf(m, st);
                 const float at = mprev == -INFINITY ? 1.0f : fast_expf(mprev - m);
-                s[lane * 17 + t] = fast_expf(st - m);
+                s[slot * 17 + t] = fast_expf(st - m);
                 av[t] = at;
                 lprod *= at;
             }
@@ -456,19 +464,44 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
 #pragma unroll
         for (int t = kPg - 1; t >= 0; t--) {
             if (t < nt) {
-                const float w = s[lane * 17 + t] * pr;
-                s[lane * 17 + t] = w;
+                const float w = s[slot * 17 + t] * pr;
+                s[slot * 17 + t] = w;
                 ls += w;
                 pr *= av[t];
             }
         }
         ls = wave_sum(ls);
         if (lane == 0)
-            lsh[g] = ls;
+            S.lsh[g] = ls;
     }
-    __syncthreads();
+}
 
-    // C. o = sum_t w_t v_t
+// C. o = sum_t w_t v_t over the slots (the order of the sum is free), then
+// out = o * (1 / l).
+template <bool BF16, int HD, int G, int WAVES, int UNR>
+__device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int b, int kvh,
+                                            int ns, int H, float *__restrict__ out)
+{
+    constexpr int RL = HD / 8;
+    constexpr int RPW = kWave / RL;
+    using Raw = typename RawRow<BF16>::T;
+    const int n_kv = P.n_kv;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int rsub = lane / RL, rl = lane % RL;
+    const int T = ns * kPg;
+    constexpr int rows_per_iter = WAVES * RPW;
+    auto load_raw = [&](const void *base, int r, float &sc_out) -> Raw {
+        const int rr = r < T ? r : T - 1;
+        const int pg = rr / kPg, t = rr % kPg;
+        const size_t slot = ((size_t)S.pphys[pg] * n_kv + kvh) * kPg + t;
+        if constexpr (BF16) {
+            sc_out = 1.0f;
+            return *(const Raw *)((const uint16_t *)base + slot * HD + rl * 8);
+        } else {
+            sc_out = P.v_scale[slot];
+            return *(const Raw *)((const int8_t *)base + slot * HD + rl * 8);
+        }
+    };
     float o[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
@@ -486,12 +519,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
             const int r = r0 + u * rows_per_iter + rsub;
             if (r < T) {
                 const int pg = r / kPg, t = r % kPg;
-                if (t < pnt[pg]) {
+                if (t < S.pnt[pg]) {
                     float vv[8];
                     raw_to_f32<BF16>(vv, vr[u], vsc[u]);
 #pragma unroll
                     for (int g = 0; g < G; g++) {
-                        const float w = sc[g][pg * 17 + t];
+                        const float w = S.sc[g][pg * 17 + t];
 #pragma unroll
                         for (int j = 0; j < 8; j++)
                             o[g][j] = __fmaf_rn(w, vv[j], o[g][j]);
@@ -515,17 +548,141 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
         for (int g = 0; g < G; g++)
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                red[wave][g][rl * 8 + j] = o[g][j];
+                S.red[wave][g][rl * 8 + j] = o[g][j];
     __syncthreads();
     for (int i = tid; i < G * HD; i += blockDim.x) {
         const int g = i / HD, d = i % HD;
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < WAVES; w++)
-            v += red[w][g][d];
-        const float l = lsh[g];
+            v += S.red[w][g][d];
+        const float l = S.lsh[g];
         out[((size_t)b * H + kvh * G + g) * HD + d] = l > 0.0f ? v * (1.0f / l) : v;
     }
+}
+
+template <bool BF16, int HD, int G, int WAVES, int UNR>
+__global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P, const float *__restrict__ q,
+                                                           const int *__restrict__ sel,
+                                                           const int *__restrict__ nsel, int sel_stride, int H,
+                                                           float scale, float *__restrict__ out)
+{
+    __shared__ AttnShared<HD, G, WAVES> S;
+    const int b = blockIdx.x, kvh = blockIdx.y;
+    const int ns = min(nsel[b], kFusedMaxPages);
+    const int *selb = sel + (size_t)b * sel_stride;
+    attn_load_q(S, q, b, kvh, H);
+    for (int i = threadIdx.x; i < ns; i += blockDim.x) {
+        const int ph = selb[i];
+        S.pphys[i] = ph;
+        S.pnt[i] = P.ntok[ph];
+    }
+    __syncthreads();
+    attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns, scale, 0, WAVES);
+    __syncthreads();
+    attn_weights(S, ns, nullptr);
+    __syncthreads();
+    attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out);
+}
+
+// LSH route + sparse attention of one query in one kernel: workgroup
+// (query b, KV head kvh) runs the router's phases 0-4 itself (every KV head
+// of a query repeats them: a few KiB of hashes and centroids from L2), so
+// the attention needs no second launch.  When every middle entry is
+// selected (#middle <= heap capacity, the usual case), the selected set is
+// known before the heap has ordered it: wave 0 runs the heap while the other
+// waves already compute the scores of the set, stored by set slot; the
+// weights then follow the heap's order through S.order.  With fewer heap
+// slots than middle entries the scores wait for the heap.  The workgroup of
+// KV head 0 writes the selection to sel / nsel (when given).
+template <bool BF16, int HD, int G, int WAVES, int UNR, bool STAGE>
+__global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, const float *__restrict__ q,
+                                                         const int *__restrict__ slots, int H, int k_sel, int cap,
+                                                         float scale, float *__restrict__ out, int *__restrict__ sel,
+                                                         int *__restrict__ nsel, int sel_stride)
+{
+    static_assert(WAVES * 64 >= kRouteThreads, "the router needs 4 waves");
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ AttnShared<HD, G, WAVES> S;
+    __shared__ int set_n;
+    const RouteView V = route_view(smem, route_smem(HD, cap, P.max_logical));
+    const int b = blockIdx.x, kvh = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int layer = slots ? slots[b] : b;
+    const int base = layer * P.max_logical;
+    const int n = P.n_logical[layer];
+    int *selb = sel && kvh == 0 ? sel + (size_t)b * sel_stride : nullptr;
+    attn_load_q(S, q, b, kvh, H);
+
+    if (n <= k_sel) {
+        // dense: every page in logical order
+        const int ns = n > 0 ? n : 0;
+        for (int i = tid; i < ns; i += blockDim.x) {
+            const int ph = P.page_table[base + i];
+            S.pphys[i] = ph;
+            S.pnt[i] = P.ntok[ph];
+            if (selb)
+                selb[i] = ph;
+        }
+        if (tid == 0 && selb)
+            nsel[b] = ns;
+        __syncthreads();
+        if (ns == 0) {
+            for (int i = tid; i < G * HD; i += blockDim.x)
+                out[((size_t)b * H + kvh * G) * HD + i] = 0.0f;
+            return;
+        }
+        attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns, scale, 0, WAVES);
+        __syncthreads();
+        attn_weights(S, ns, nullptr);
+        __syncthreads();
+        attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out);
+        return;
+    }
+    const int nidx = min(P.n_indexed[layer], P.max_logical);
+    route_prepare<STAGE>(P, q + (size_t)b * H * HD, base, n, nidx, H, cap, V, nullptr, nullptr, nullptr);
+    const int nm = route_middles(V);
+    const int ns0 = V.mpt[cap + 1] != V.mpt[cap] ? 2 : 1;
+    int ak = min(k_sel - 2, min(nm, kHeapMax));
+    if (k_sel <= 2 || nm == 0)
+        ak = 0;
+    const bool known = nm <= ak;             // every middle entry is selected
+    if (known) {
+        const int nset = ns0 + nm;
+        for (int i = tid; i < nset; i += blockDim.x) {
+            const int ph = i == 0 ? V.mpt[cap] : (i < ns0 ? V.mpt[cap + 1] : V.mpt[i - ns0]);
+            S.pphys[i] = ph;
+            S.pnt[i] = P.ntok[ph];
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int ns = route_select(k_sel, cap, V, selb, S.order);
+        if (lane == 0) {
+            set_n = ns;
+            if (selb)
+                nsel[b] = ns;
+        }
+    } else if (known) {
+        attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns0 + nm, scale, 1, WAVES - 1);
+    }
+    __syncthreads();
+    const int ns = set_n;
+    if (!known) {
+        // the heap replaced entries: slots follow the selection order
+        for (int i = tid; i < ns; i += blockDim.x) {
+            const int slot = S.order[i];
+            const int ph = slot == 0 ? V.mpt[cap] : (slot < ns0 ? V.mpt[cap + 1] : V.mpt[slot - ns0]);
+            S.pphys[i] = ph;
+            S.pnt[i] = P.ntok[ph];
+        }
+        __syncthreads();
+        attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns, scale, 0, WAVES);
+        __syncthreads();
+    }
+    attn_weights(S, ns, known ? S.order : nullptr);
+    __syncthreads();
+    attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out);
 }
 
 // 16 waves when the grid is small (more loads in flight per workgroup), 8
@@ -567,6 +724,55 @@ static bool launch_fused(const be42_kv_pool &P, const float *q, const int *sel, 
         return bf16 ? launch_fused_hd<true, 64>(P, q, sel, nsel, sel_stride, B, H, scale, out, s)
                     : launch_fused_hd<false, 64>(P, q, sel, nsel, sel_stride, B, H, scale, out, s);
     return false;
+}
+
+template <bool BF16, int HD, int G, bool STAGE>
+static void launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
+                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride, size_t lds,
+                              hipStream_t s)
+{
+    const dim3 grid(B, P.n_kv);
+    if ((long)B * P.n_kv < 512)
+        hipLaunchKernelGGL((k_lsh_attn<BF16, HD, G, 16, 8, STAGE>), grid, dim3(1024), lds, s, P, q, slots, H, k_sel,
+                           cap, scale, out, sel, nsel, sel_stride);
+    else
+        hipLaunchKernelGGL((k_lsh_attn<BF16, HD, G, 8, 8, STAGE>), grid, dim3(512), lds, s, P, q, slots, H, k_sel,
+                           cap, scale, out, sel, nsel, sel_stride);
+}
+
+template <bool BF16, int HD, int G>
+static int launch_lsh_attn_g(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
+                             int cap, float scale, float *out, int *sel, int *nsel, int sel_stride, hipStream_t s)
+{
+    const RouteSmem L = route_smem(HD, cap, P.max_logical);
+    if (L.bytes > 65536) {
+        const void *fns[4] = {(const void *)k_lsh_attn<BF16, HD, G, 16, 8, true>,
+                              (const void *)k_lsh_attn<BF16, HD, G, 8, 8, true>,
+                              (const void *)k_lsh_attn<BF16, HD, G, 16, 8, false>,
+                              (const void *)k_lsh_attn<BF16, HD, G, 8, 8, false>};
+        for (const void *f : fns)
+            BE42_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes));
+    }
+    if (L.stage)
+        launch_lsh_attn_s<BF16, HD, G, true>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride,
+                                             (size_t)L.bytes, s);
+    else
+        launch_lsh_attn_s<BF16, HD, G, false>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride,
+                                              (size_t)L.bytes, s);
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
+template <bool BF16, int HD>
+static int launch_lsh_attn_hd(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
+                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride, hipStream_t s)
+{
+    switch (H / P.n_kv) {
+    case 1: return launch_lsh_attn_g<BF16, HD, 1>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, s);
+    case 2: return launch_lsh_attn_g<BF16, HD, 2>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, s);
+    case 3: return launch_lsh_attn_g<BF16, HD, 3>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, s);
+    default: return launch_lsh_attn_g<BF16, HD, 4>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, s);
+    }
 }
 
 }  // namespace be42
@@ -645,4 +851,55 @@ extern "C" int be42_paged_attention(const be42_kv_pool *pool, const float *q, in
                        (int)bh, P.head_dim, n_split);
     BE42_LAUNCH_CHECK();
     return BE42_OK;
+}
+
+extern "C" int be42_lsh_attention(const be42_kv_pool *pool, const float *q, const int *slots, int n_queries,
+                                  int n_heads, int k_sel, int cand_cap, float scale, float *out, int *sel,
+                                  int *n_sel, int sel_stride, void *stream)
+{
+    BE42_CHECK(pool && q && out, "be42_lsh_attention: null pointer");
+    const be42_kv_pool &P = *pool;
+    BE42_CHECK(k_sel > 0 && k_sel <= kFusedMaxPages && cand_cap > 0 && cand_cap <= kMaxCand,
+               "be42_lsh_attention: k %d (1..%d), cap %d (1..%d)", k_sel, kFusedMaxPages, cand_cap, kMaxCand);
+    BE42_CHECK(n_heads > 0 && n_heads % P.n_kv == 0 && n_heads / P.n_kv <= 4,
+               "be42_lsh_attention: %d heads over %d kv heads (groups of 1..4)", n_heads, P.n_kv);
+    BE42_CHECK(P.head_dim == 64 || P.head_dim == 128, "be42_lsh_attention: head_dim %d (64 or 128)", P.head_dim);
+    BE42_CHECK((sel == nullptr) == (n_sel == nullptr), "be42_lsh_attention: sel and n_sel go together");
+    BE42_CHECK(!sel || (sel_stride >= k_sel && sel_stride >= kHeapMax + 2),
+               "be42_lsh_attention: sel_stride %d must be >= max(k, 64)", sel_stride);
+    if (n_queries <= 0)
+        return BE42_OK;
+    hipStream_t s = as_stream(stream);
+    if ((long)n_queries * P.n_kv > 512) {
+        // Enough workgroups to fill the chip: the router's latency is better
+        // spent once per query in its own launch than once per KV head in
+        // the attention's workgroups (measured on MI355X).  The selection
+        // goes through the library workspace when the caller wants none.
+        int *ws_sel = sel, *ws_n = n_sel, stride = sel_stride;
+        if (!sel) {
+            stride = std::max(k_sel, kHeapMax + 2);
+            int *w = (int *)workspace((size_t)n_queries * (stride + 1) * sizeof(int), s);
+            if (!w)
+                return BE42_ENOMEM;
+            ws_sel = w;
+            ws_n = w + (size_t)n_queries * stride;
+        }
+        const int rc = be42_lsh_route(pool, q, slots, n_queries, n_heads, k_sel, cand_cap, ws_sel, ws_n, stride,
+                                      nullptr, nullptr, nullptr, stream);
+        if (rc)
+            return rc;
+        // <= 64 pages, no split: the fused attention kernel, which takes no workspace
+        return be42_paged_attention(pool, q, n_queries, n_heads, ws_sel, ws_n, stride, k_sel, scale, out, 1, nullptr,
+                                    0, stream);
+    }
+    const bool bf16 = P.kind == BE42_KV_BF16;
+    if (P.head_dim == 128)
+        return bf16 ? launch_lsh_attn_hd<true, 128>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out,
+                                                    sel, n_sel, sel_stride, s)
+                    : launch_lsh_attn_hd<false, 128>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out,
+                                                     sel, n_sel, sel_stride, s);
+    return bf16 ? launch_lsh_attn_hd<true, 64>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, sel,
+                                               n_sel, sel_stride, s)
+                : launch_lsh_attn_hd<false, 64>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, sel,
+                                                n_sel, sel_stride, s);
 }

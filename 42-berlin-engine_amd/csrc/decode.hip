@@ -650,6 +650,7 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     // fused kernel reads each sequence's page count from the device
     const int dense_max = std::min(c.sparse_k, P.max_logical);
     const float *pending = nullptr;   // residual delta not yet added to x
+    const bool fused_route = c.sparse_k <= 64 && c.cand_cap <= 256 && H / KV <= 4 && (hd == 64 || hd == 128);
     for (int l = 0; l < c.n_layers; l++) {
         const be42_decoder_layer &L = d->w.layers[l];
         BE42_HIP(norm(L.attn_norm, pending));
@@ -666,6 +667,10 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
             DEC_TRY(be42_paged_attention(d->pool, d->q, B, H, P.page_table + (size_t)l * c.max_batch * P.max_logical,
                                          P.n_logical + (size_t)l * c.max_batch, P.max_logical, dense_max, scale,
                                          d->att, dense_max <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
+        } else if (fused_route) {
+            // route + attention in one launch
+            DEC_TRY(be42_lsh_attention(d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, scale, d->att, d->sel,
+                                       d->nsel, std::max(c.sparse_k, 64), st));
         } else {
             const int stride = std::max(c.sparse_k, 64);
             DEC_TRY(be42_lsh_route(d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, d->sel, d->nsel, stride,

@@ -31,48 +31,9 @@
 #include <cmath>
 
 #include "be42_common.h"
-#include "heap_wave.h"
+#include "route.h"
 
 namespace be42 {
-
-constexpr int kProbes = 17;
-constexpr int kMaxCand = 256;       // router candidate cap
-constexpr int kMaxCandList = 512;   // be42_lsh_candidates cap
-
-constexpr int kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
-
-struct RouteSmem {
-    int off_qm, off_q0, off_hp, off_list, off_cnt, off_offs, off_cand, off_mid, off_sc, off_mpt, off_ph, stage, bytes;
-};
-
-// LDS layout of the router.  When they fit in the workgroup's LDS, the
-// layer's page hashes are staged there (stage = max_logical), else read from
-// HBM (stage = 0).
-__host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical)
-{
-    RouteSmem r;
-    int o = 0;
-    r.off_qm = o;   o += 256 * 4;
-    r.off_q0 = o;   o += 256 * 4;
-    r.off_hp = o;   o += hd * 16 * 4;
-    r.off_list = o; o += 4 * kProbes * cap * 4;
-    r.off_cnt = o;  o += 4 * kProbes * 4 + 4 * 4;
-    r.off_offs = o; o += 4 * kProbes * 4 + 4 * 4;
-    r.off_cand = o; o += cap * 4;
-    r.off_mid = o;  o += cap * 4;
-    r.off_sc = o;   o += cap * 4;
-    r.off_mpt = o;  o += cap * 4 + 4 * 4;
-    r.stage = o + max_logical * 2 + 16 <= kLdsBytes ? max_logical : 0;
-    r.off_ph = o;   o += (r.stage * 2 + 15) & ~15;
-    r.bytes = o;
-    return r;
-}
-
-__device__ __forceinline__ int rl(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
-__device__ __forceinline__ float rlf(float v, int lane)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
 
 template <bool STAGE>
 __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float *__restrict__ q,
@@ -82,24 +43,11 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
                                                uint16_t *__restrict__ qhash_out)
 {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int hd = P.head_dim;
-    const RouteSmem L = route_smem(hd, cap, P.max_logical);
-    float *qm = (float *)(smem + L.off_qm);
-    float *q0 = (float *)(smem + L.off_q0);
-    float *hp = (float *)(smem + L.off_hp);
-    int *list = (int *)(smem + L.off_list);
-    int *cnt = (int *)(smem + L.off_cnt);
-    int *offs = (int *)(smem + L.off_offs);
-    int *cand = (int *)(smem + L.off_cand);
-    int *mid = (int *)(smem + L.off_mid);
-    float *sc = (float *)(smem + L.off_sc);
-    uint16_t *ph_s = (uint16_t *)(smem + L.off_ph);
-
-    const int b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const RouteView V = route_view(smem, route_smem(P.head_dim, cap, P.max_logical));
+    const int b = blockIdx.x, tid = threadIdx.x;
     const int layer = slots ? slots[b] : b;
     const int base = layer * P.max_logical;
     const int n = P.n_logical[layer];
-    const float *qb = q + (size_t)b * H * hd;
     int *selb = sel + (size_t)b * sel_stride;
 
     if (n <= 0 || n <= k_sel) {
@@ -114,214 +62,14 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
         return;
     }
     const int nidx = min(P.n_indexed[layer], P.max_logical);
-
-    // 0. loads that do not depend on the query hash, each thread's share
-    //    issued before any is stored: page hashes (staged), projection, the
-    //    first and last page of the table
-    int *mpt = (int *)(smem + L.off_mpt);      // [cap] physical page of mid[e]; [cap], [cap+1]: first, last
-    if (STAGE) {
-        for (int i0 = 0; i0 < nidx; i0 += 8 * 256) {
-            uint16_t v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + j * 256 + tid;
-                v[j] = i < nidx ? P.page_hash[base + i] : (uint16_t)0;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + j * 256 + tid;
-                if (i < nidx)
-                    ph_s[i] = v[j];
-            }
-        }
-    }
-    const uint16_t *ph = STAGE ? ph_s : P.page_hash + base;
-    for (int i0 = 0; i0 < hd * 16; i0 += 8 * 256) {
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int i = i0 + j * 256 + tid;
-            v[j] = i < hd * 16 ? P.hpT[i] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int i = i0 + j * 256 + tid;
-            if (i < hd * 16)
-                hp[i] = v[j];
-        }
-    }
-    if (tid == 0) {
-        mpt[cap] = P.page_table[base];
-        mpt[cap + 1] = P.page_table[base + n - 1];
-    }
-
-    // 1. q_mean (inference.c:291-295): sum in head order, then / n_heads;
-    //    32 heads' loads are issued before the sum consumes them
-    for (int d = tid; d < hd; d += blockDim.x) {
-        float s = 0.0f;
-        for (int h0 = 0; h0 < H; h0 += 32) {
-            float v[32];
-#pragma unroll
-            for (int j = 0; j < 32; j++)
-                v[j] = h0 + j < H ? qb[(h0 + j) * hd + d] : 0.0f;
-#pragma unroll
-            for (int j = 0; j < 32; j++)
-                if (h0 + j < H)
-                    s = s + v[j];
-        }
-        qm[d] = s / (float)H;
-        q0[d] = qb[d];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        float s = 0.0f;
-        if (lane < 16) {
-#pragma unroll 16
-            for (int i = 0; i < hd; i++)
-                s = __fmaf_rn(qm[i], hp[i * 16 + lane], s);
-        }
-        const unsigned long long m = __ballot(lane < 16 && s > 0.0f);
-        if (lane == 0)
-            cnt[4 * kProbes] = (int)(m & 0xFFFFu);
-    }
-    __syncthreads();
-    const int qh = cnt[4 * kProbes];
-    if (tid == 0 && qhash_out)
-        qhash_out[b] = (uint16_t)qh;
-
-    // 2. candidate scan: wave w owns ids [lo, hi), scanned from hi-1 down
-    {
-        const int part = (nidx + 3) / 4;
-        const int hi = max(nidx - wave * part, 0), lo = max(nidx - (wave + 1) * part, 0);
-        int cntv = 0;    // lane p < 17 holds the hit count of probe p
-        int *mylist = list + wave * kProbes * cap;
-        for (int top = hi - 1; top >= lo; top -= kWave) {
-            const int id = top - lane;
-            const bool valid = id >= lo;
-            int p = kProbes;
-            if (valid) {
-                const int dd = (int)ph[id] ^ qh;
-                p = dd == 0 ? 0 : (((dd & (dd - 1)) == 0) ? __ffs(dd) : kProbes);
-            }
-            unsigned long long hits = __ballot(p < kProbes);
-            while (hits) {
-                const int l0 = __ffsll((long long)hits) - 1;
-                const int pp = rl(p, l0);
-                const unsigned long long m = __ballot(p == pp);
-                const int basec = rl(cntv, pp);
-                if (p == pp) {
-                    const int rank = __popcll(m & ((1ull << lane) - 1ull));
-                    if (basec + rank < cap)
-                        mylist[pp * cap + basec + rank] = id;
-                }
-                if (lane == pp)
-                    cntv += __popcll(m);
-                hits &= ~m;
-            }
-        }
-        if (lane < kProbes)
-            cnt[wave * kProbes + lane] = cntv;
-    }
-    __syncthreads();
-
-    // 3. concatenation: list j = 4 * probe + wave (probe order, then
-    //    descending id) starts at offs[j]; lane l of wave 0 owns lists 2l, 2l+1
-    if (wave == 0) {
-        int c0 = 0, c1 = 0;
-        if (lane < 2 * kProbes) {
-            const int j0 = 2 * lane, j1 = j0 + 1;
-            c0 = min(cnt[(j0 & 3) * kProbes + (j0 >> 2)], cap);
-            c1 = min(cnt[(j1 & 3) * kProbes + (j1 >> 2)], cap);
-        }
-        int inc = c0 + c1;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int v = __shfl_up(inc, o, kWave);
-            if (lane >= o)
-                inc += v;
-        }
-        if (lane < 2 * kProbes) {
-            offs[2 * lane] = inc - c0 - c1;
-            offs[2 * lane + 1] = inc - c1;
-        }
-        if (lane == kWave - 1)
-            cnt[4 * kProbes + 1] = min(inc, cap);
-    }
-    __syncthreads();
-    for (int j = wave; j < 4 * kProbes; j += 4) {
-        const int off = offs[j];
-        const int *src = list + ((j & 3) * kProbes + (j >> 2)) * cap;
-        const int take = min(min(cnt[(j & 3) * kProbes + (j >> 2)], cap), cap - off);
-        for (int i = lane; i < take; i += kWave)
-            cand[off + i] = src[i];
-    }
-    __syncthreads();
-    const int total = cnt[4 * kProbes + 1];
-    if (cand_out)
-        for (int i = tid; i < total; i += blockDim.x)
-            cand_out[(size_t)b * cap + i] = cand[i];
-    if (tid == 0 && ncand_out)
-        ncand_out[b] = total;
-    // middle entries: candidates other than the first and last page
-    if (wave == 0) {
-        int nm = 0;
-        for (int i0 = 0; i0 < total; i0 += kWave) {
-            const int i = i0 + lane;
-            const int id = i < total ? cand[i] : -1;
-            const bool keep = i < total && id != 0 && id != n - 1 && id < n;
-            const unsigned long long m = __ballot(keep);
-            if (keep)
-                mid[nm + __popcll(m & ((1ull << lane) - 1ull))] = id;
-            nm += __popcll(m);
-        }
-        if (lane == 0)
-            cnt[4 * kProbes + 2] = nm;
-    }
-    __syncthreads();
-    const int nm = cnt[4 * kProbes + 2];
-
-    // 4. scores of the middle entries (score_blocks semantics), a lane pair each
-    for (int e0 = 0; e0 < nm; e0 += 128) {
-        const int e = e0 + (tid >> 1), half = tid & 1;
-        const int ee = e < nm ? e : nm - 1;
-        const int phys = P.page_table[base + mid[ee]];
-        const float s = dot_ref8x2(q0, P.centroid + (size_t)phys * hd, hd, half);
-        if (half == 0 && e < nm) {
-            sc[e] = s;
-            mpt[e] = phys;
-        }
-    }
-    __syncthreads();
-
-    // 5. selection: anchors, then the reference min-heap (capacity
-    //    min(k-2, #middle, 62), strict replacement) run by wave 0
-    if (wave != 0)
+    route_prepare<STAGE>(P, q + (size_t)b * H * P.head_dim, base, n, nidx, H, cap, V,
+                         qhash_out ? qhash_out + b : nullptr, cand_out ? cand_out + (size_t)b * cap : nullptr,
+                         ncand_out ? ncand_out + b : nullptr);
+    if ((tid >> 6) != 0)
         return;
-    const int first = mpt[cap], last = mpt[cap + 1];
-    int ns = 0;
-    if (lane == 0)
-        selb[0] = first;
-    ns = 1;
-    if (last != first) {
-        if (lane == 0)
-            selb[1] = last;
-        ns = 2;
-    }
-    int ak = min(k_sel - 2, min(nm, kHeapMax));
-    if (k_sel <= 2 || nm == 0)
-        ak = 0;
-    WaveHeap heap(ak);
-    for (int e0 = 0; e0 < nm && ak > 0; e0 += kWave) {
-        const float sv = e0 + lane < nm ? sc[e0 + lane] : 0.0f;
-        const int ecnt = min(kWave, nm - e0);
-        for (int u = 0; u < ecnt; u++)
-            heap.push(rlf(sv, u), e0 + u);
-    }
-    const int size = heap.size, hi = heap.hi;
-    if (lane < size)
-        selb[ns + lane] = mpt[hi];
-    if (lane == 0)
-        nsel[b] = ns + size;
+    const int ns = route_select(k_sel, cap, V, selb, nullptr);
+    if ((tid & 63) == 0)
+        nsel[b] = ns;
 }
 
 // Hash of n vectors: each wave hashes 4 vectors, 16 lanes per vector, one

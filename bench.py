@@ -148,7 +148,7 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
         ws = torch.empty(max(1, lib.lib.be42_attn_workspace_bytes(B, H, hd, cfg["k_sel"], n_split)),
                          dtype=torch.uint8, device="cuda")
 
-        def step(ev=None):
+        def step_split(ev=None):
             if ev is not None:
                 ev[0].record()
             lib._call("be42_lsh_route", pool.handle, lib.p(qd), None, B, H, cfg["k_sel"], cfg["cap"], lib.p(sel),
@@ -159,22 +159,42 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
             if ev is not None:
                 ev[2].record()
 
+        fsel = torch.empty((B, sel_stride), dtype=torch.int32, device="cuda")
+        fnsel = torch.empty(B, dtype=torch.int32, device="cuda")
+        fout = torch.empty((B, H, hd), device="cuda")
+
+        def step_fused():
+            lib._call("be42_lsh_attention", pool.handle, lib.p(qd), None, B, H, cfg["k_sel"], cfg["cap"], scale,
+                      lib.p(fout), lib.p(fsel), lib.p(fnsel), sel_stride, lib.stream())
+
         for _ in range(warmup):
-            step()
+            step_split()
+            step_fused()
         torch.cuda.synchronize()
+        # the decode path: route + attention in one launch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            step_fused()
+        e1.record()
+        torch.cuda.synchronize()
+        tot_ms = e0.elapsed_time(e1) / steps
+        # breakdown: the same work as two launches (router, then attention)
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
         for i in range(steps):
-            step(evs[i])
+            step_split(evs[i])
         torch.cuda.synchronize()
         route_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
         attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
-        tot_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / steps
-        ns = nsel.cpu().numpy()
+        split_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / steps
+        assert torch.equal(fsel, sel) and torch.equal(fnsel, nsel), "fused and two-launch selections differ"
+        ns = fnsel.cpu().numpy()
         nc = ncand.cpu().numpy()
         nbytes = sum(lsh_bytes(int(a), int(c)) for a, c in zip(ns, nc))
         kv_bytes = sum(int(a) * cfg["page"] * KVH * hd * 2 * 2 for a in ns)
         rows.append({"batch": B, "us_per_token": round(tot_ms * 1e3 / B, 3), "step_us": round(tot_ms * 1e3, 2),
-                     "route_us": round(route_ms * 1e3, 2), "attention_us": round(attn_ms * 1e3, 2),
+                     "two_launch_us": round(split_ms * 1e3, 2), "route_us": round(route_ms * 1e3, 2),
+                     "attention_us": round(attn_ms * 1e3, 2),
                      "n_sel_mean": float(ns.mean()), "n_cand_mean": float(nc.mean()),
                      "bytes_per_step": nbytes, "GBps": round(nbytes / (tot_ms * 1e-3) / 1e9, 1),
                      "frac_of_hbm_peak": round(nbytes / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -183,7 +203,9 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
     head = max(rows, key=lambda r: r["batch"])
     return {"workload": f"configs[3]: B sequences x {T}-token bf16 paged KV (page 16), {H} heads / {KVH} KV heads, "
                         f"head_dim {hd}, top-K {cfg['k_sel']} pages, candidate cap {cfg['cap']}, 5% planted pages; "
-                        f"one step = route + sparse attention of one decode token per sequence",
+                        f"one step = route + sparse attention of one decode token per sequence "
+                        f"(be42_lsh_attention: one launch up to 512 query x KV-head pairs, two above; "
+                        f"route_us / attention_us time the work as two launches)",
             "us_per_token": head["us_per_token"], "batch": head["batch"],
             "frac_of_hbm_peak": head["frac_of_hbm_peak"], "by_batch": rows}
 

@@ -194,6 +194,18 @@ size_t be42_attn_workspace_bytes(int n_queries, int n_heads, int head_dim, int m
 int  be42_paged_attention(const be42_kv_pool *pool, const float *q, int n_queries, int n_heads,
                           const int *sel, const int *n_sel, int sel_stride, int max_sel, float scale,
                           float *out, int n_split, void *workspace, size_t workspace_bytes, void *stream);
+/* be42_lsh_route followed by be42_paged_attention over its selection, in one
+ * launch (the decode step's sparse path, inference.c:447-494 with
+ * op_paged_attention_sparse, ops_attention.c:443-461): the same selection,
+ * bit for bit, and the same attention up to the order of the V sum.
+ * k_sel <= 64, cand_cap <= 256, n_heads / n_kv <= 4, head_dim 64 or 128.
+ * sel / n_sel (both or neither) receive the selection as be42_lsh_route
+ * writes it (sel_stride >= 64).  Above 512 (query, KV head) pairs it runs as
+ * the two launches (the library workspace holds the selection when sel is
+ * NULL). */
+int  be42_lsh_attention(const be42_kv_pool *pool, const float *q, const int *slots, int n_queries,
+                        int n_heads, int k_sel, int cand_cap, float scale, float *out, int *sel, int *n_sel,
+                        int sel_stride, void *stream);
 
 /* ---- decode step ------------------------------------------------------------------
  * transformer_forward (src/inference/inference.c:60-696) on the paged path for a

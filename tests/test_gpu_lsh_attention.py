@@ -292,3 +292,61 @@ def test_lsh_attention_pipeline_c4_shape(be, orc):
     want = op.attention_pages(q[0], want_sel, H, scale)
     assert rel_err(out.ravel(), want) <= TOL
     gp.close()
+
+
+@pytest.mark.parametrize("kind", [OR_KV_INT8, OR_KV_BF16])
+@pytest.mark.parametrize("cap,k_sel", [(64, 64), (16, 8), (64, 40)])
+@pytest.mark.parametrize("n_kv,H,hd", [(4, 8, 64), (2, 8, 128)])
+def test_lsh_attention_fused_matches_oracle(be, orc, kind, cap, k_sel, n_kv, H, hd):
+    """Route + attention in one launch: the selection is the oracle's route
+    (bit-exact) and the output its attention over that selection.  k 64 with
+    cap 64 selects every middle candidate (the scores start while the heap
+    orders them); k 8 / cap 16 and k 40 / cap 64 replace heap entries (the
+    scores wait for the heap); the 3-page layers take the dense path."""
+    rng = np.random.default_rng(900 + cap + k_sel + kind + hd)
+    n_layers = 4
+    lens = (70 * PAGE + 5, 130 * PAGE, 3 * PAGE, 2 * PAGE + 1)
+    _, hpT = orc.lsh_init(hd, 42)
+    q = rng.standard_normal((n_layers, H, hd)).astype(np.float32)
+    gp, op, idx = _build(be, orc, kind, n_layers, n_kv, hd, 140, lens, rng, hpT,
+                         planted=_planter(orc, hpT, hd, H, q, 0.1, rng), chunks=(64, 3, 17))
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    out, sel, nsel = be.lsh_attention(gp, torch.from_numpy(q).cuda(), k_sel, cap, scale)
+    out, sel, nsel = out.cpu().numpy(), sel.cpu().numpy(), nsel.cpu().numpy()
+    for layer in range(n_layers):
+        want_sel, _ = op.route(layer, q[layer], H, hpT, idx[layer], cap, k_sel)
+        np.testing.assert_array_equal(sel[layer, :nsel[layer]], want_sel)
+        want = op.attention_pages(q[layer], list(want_sel), H, scale)
+        assert rel_err(out[layer].ravel(), want) <= 2e-5, layer
+    # the same as the two-launch path
+    s2, n2, _, _, _ = be.route(gp, torch.from_numpy(q).cuda(), k_sel, cap)
+    o2 = be.paged_attention(gp, torch.from_numpy(q).cuda(), s2, n2, k_sel, scale, n_split=1).cpu().numpy()
+    assert rel_err(out.ravel(), o2.ravel()) <= 1e-6
+    gp.close()
+
+
+def test_lsh_attention_many_queries(be, orc):
+    """65 queries x 8 KV heads (> 512 pairs): be42_lsh_attention runs the
+    router and the attention as two launches; the result equals those two
+    calls, with and without a selection output."""
+    rng = np.random.default_rng(990)
+    n_kv, hd, H = 8, 64, 16
+    lens = (70 * PAGE + 5, 130 * PAGE, 3 * PAGE, 90 * PAGE)
+    _, hpT = orc.lsh_init(hd, 42)
+    q4 = rng.standard_normal((4, H, hd)).astype(np.float32)
+    gp, op, idx = _build(be, orc, OR_KV_BF16, 4, n_kv, hd, 140, lens, rng, hpT,
+                         planted=_planter(orc, hpT, hd, H, q4, 0.1, rng), chunks=(64,))
+    B = 65
+    slots = torch.tensor([b % 4 for b in range(B)], dtype=torch.int32, device="cuda")
+    q = torch.from_numpy(rng.standard_normal((B, H, hd)).astype(np.float32)).cuda()
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    out, sel, nsel = be.lsh_attention(gp, q, 64, 64, scale, slots=slots)
+    out2, _, _ = be.lsh_attention(gp, q, 64, 64, scale, slots=slots, want_sel=False)
+    s2, n2, _, _, _ = be.route(gp, q, 64, 64, slots=slots)
+    o2 = be.paged_attention(gp, q, s2, n2, 64, scale, n_split=1)
+    assert torch.equal(sel[:, :64], s2[:, :64]) and torch.equal(nsel, n2)
+    assert torch.equal(out, o2) and torch.equal(out2, o2)
+    for b in (0, 1, 3, 64):
+        want_sel, _ = op.route(b % 4, q[b].cpu().numpy(), H, hpT, idx[b % 4], 64, 64)
+        np.testing.assert_array_equal(sel[b, :nsel[b]].cpu().numpy(), want_sel)
+    gp.close()
