@@ -278,6 +278,10 @@ static void launch_scores_apply(const be42_kv_pool &P, const float *q, const int
 //     out = o * (1 / l).
 // Every K and V row of the selected pages is read once per KV head.
 constexpr int kFusedMaxPages = 64;
+// Slots whose scores the fused route + attention computes while the heap
+// orders them: the two anchors and every middle candidate, when they number
+// at most this many.
+constexpr int kSetMax = 80;
 
 template <bool BF16>
 struct RawRow {
@@ -336,10 +340,10 @@ __device__ __forceinline__ float group_sum(float a)
 template <int HD, int G, int WAVES>
 struct AttnShared {
     float qs[G][HD];
-    float sc[G][kFusedMaxPages * 17];
+    float sc[G][kSetMax * 17];
     float red[WAVES][G][HD];
     float lsh[G];
-    int pphys[kFusedMaxPages], pnt[kFusedMaxPages], order[kFusedMaxPages];
+    int pphys[kSetMax], pnt[kSetMax], order[kFusedMaxPages];
 };
 
 template <int HD, int G, int WAVES>
@@ -476,32 +480,51 @@ __device__ __forceinline__ void attn_weights(AttnShared<HD, G, WAVES> &S, int ns
     }
 }
 
-// C. o = sum_t w_t v_t over the slots (the order of the sum is free), then
-// out = o * (1 / l).
+// A batch of V rows of a wave (UNR row steps).
+template <bool BF16, int UNR>
+struct VBatch {
+    typename RawRow<BF16>::T vr[UNR];
+    float vsc[UNR];
+};
+
 template <bool BF16, int HD, int G, int WAVES, int UNR>
-__device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int b, int kvh,
-                                            int ns, int H, float *__restrict__ out)
+__device__ __forceinline__ void attn_values_load(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
+                                                 const int *order, int r0, VBatch<BF16, UNR> &vb)
 {
     constexpr int RL = HD / 8;
     constexpr int RPW = kWave / RL;
     using Raw = typename RawRow<BF16>::T;
-    const int n_kv = P.n_kv;
+    constexpr int rows_per_iter = WAVES * RPW;
+    const int lane = threadIdx.x & 63, rsub = lane / RL, rl = lane % RL;
+    const int T = ns * kPg;
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        const int r = r0 + u * rows_per_iter + rsub;
+        const int rr = r < T ? r : T - 1;
+        const int pg = rr / kPg, t = rr % kPg;
+        const size_t slot = ((size_t)S.pphys[order ? order[pg] : pg] * P.n_kv + kvh) * kPg + t;
+        if constexpr (BF16) {
+            vb.vsc[u] = 1.0f;
+            vb.vr[u] = *(const Raw *)((const uint16_t *)P.v + slot * HD + rl * 8);
+        } else {
+            vb.vsc[u] = P.v_scale[slot];
+            vb.vr[u] = *(const Raw *)((const int8_t *)P.v + slot * HD + rl * 8);
+        }
+    }
+}
+
+// C. o = sum_t w_t v_t over the slots (the order of the sum is free), then
+// out = o * (1 / l).
+template <bool BF16, int HD, int G, int WAVES, int UNR>
+__device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int b, int kvh,
+                                            int ns, int H, float *__restrict__ out, const int *order)
+{
+    constexpr int RL = HD / 8;
+    constexpr int RPW = kWave / RL;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int rsub = lane / RL, rl = lane % RL;
     const int T = ns * kPg;
     constexpr int rows_per_iter = WAVES * RPW;
-    auto load_raw = [&](const void *base, int r, float &sc_out) -> Raw {
-        const int rr = r < T ? r : T - 1;
-        const int pg = rr / kPg, t = rr % kPg;
-        const size_t slot = ((size_t)S.pphys[pg] * n_kv + kvh) * kPg + t;
-        if constexpr (BF16) {
-            sc_out = 1.0f;
-            return *(const Raw *)((const uint16_t *)base + slot * HD + rl * 8);
-        } else {
-            sc_out = P.v_scale[slot];
-            return *(const Raw *)((const int8_t *)base + slot * HD + rl * 8);
-        }
-    };
     float o[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
@@ -509,22 +532,20 @@ __device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD
         for (int j = 0; j < 8; j++)
             o[g][j] = 0.0f;
     for (int r0 = wave * RPW; r0 < T; r0 += rows_per_iter * UNR) {
-        Raw vr[UNR];
-        float vsc[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; u++)
-            vr[u] = load_raw(P.v, r0 + u * rows_per_iter + rsub, vsc[u]);
+        VBatch<BF16, UNR> vb;
+        attn_values_load<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns, order, r0, vb);
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
             const int r = r0 + u * rows_per_iter + rsub;
             if (r < T) {
                 const int pg = r / kPg, t = r % kPg;
-                if (t < S.pnt[pg]) {
+                const int sl = order ? order[pg] : pg;
+                if (t < S.pnt[sl]) {
                     float vv[8];
-                    raw_to_f32<BF16>(vv, vr[u], vsc[u]);
+                    raw_to_f32<BF16>(vv, vb.vr[u], vb.vsc[u]);
 #pragma unroll
                     for (int g = 0; g < G; g++) {
-                        const float w = S.sc[g][pg * 17 + t];
+                        const float w = S.sc[g][sl * 17 + t];
 #pragma unroll
                         for (int j = 0; j < 8; j++)
                             o[g][j] = __fmaf_rn(w, vv[j], o[g][j]);
@@ -582,19 +603,19 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
     __syncthreads();
     attn_weights(S, ns, nullptr);
     __syncthreads();
-    attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out);
+    attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out, nullptr);
 }
 
 // LSH route + sparse attention of one query in one kernel: workgroup
 // (query b, KV head kvh) runs the router's phases 0-4 itself (every KV head
 // of a query repeats them: a few KiB of hashes and centroids from L2), so
-// the attention needs no second launch.  When every middle entry is
-// selected (#middle <= heap capacity, the usual case), the selected set is
-// known before the heap has ordered it: wave 0 runs the heap while the other
-// waves already compute the scores of the set, stored by set slot; the
-// weights then follow the heap's order through S.order.  With fewer heap
-// slots than middle entries the scores wait for the heap.  The workgroup of
-// KV head 0 writes the selection to sel / nsel (when given).
+// the attention needs no second launch.  The selection is a subset of the
+// anchors and the middle candidates, so while wave 0 runs the heap the
+// other waves already compute the scores of all of them (up to kSetMax
+// "set slots": at cap 64 two candidates more than the 62 heap slots); the
+// weights and V then follow the heap's order through S.order.  With more
+// candidates the scores wait for the heap.  The workgroup of KV head 0
+// writes the selection to sel / nsel (when given).
 template <bool BF16, int HD, int G, int WAVES, int UNR, bool STAGE>
 __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, const float *__restrict__ q,
                                                          const int *__restrict__ slots, int H, int k_sel, int cap,
@@ -636,19 +657,16 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
         __syncthreads();
         attn_weights(S, ns, nullptr);
         __syncthreads();
-        attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out);
+        attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out, nullptr);
         return;
     }
     const int nidx = min(P.n_indexed[layer], P.max_logical);
     route_prepare<STAGE>(P, q + (size_t)b * H * HD, base, n, nidx, H, cap, V, nullptr, nullptr, nullptr);
     const int nm = route_middles(V);
     const int ns0 = V.mpt[cap + 1] != V.mpt[cap] ? 2 : 1;
-    int ak = min(k_sel - 2, min(nm, kHeapMax));
-    if (k_sel <= 2 || nm == 0)
-        ak = 0;
-    const bool known = nm <= ak;             // every middle entry is selected
-    if (known) {
-        const int nset = ns0 + nm;
+    const int nset = ns0 + nm;
+    const bool early = nset <= kSetMax;      // score every candidate while the heap runs
+    if (early) {
         for (int i = tid; i < nset; i += blockDim.x) {
             const int ph = i == 0 ? V.mpt[cap] : (i < ns0 ? V.mpt[cap + 1] : V.mpt[i - ns0]);
             S.pphys[i] = ph;
@@ -663,13 +681,13 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
             if (selb)
                 nsel[b] = ns;
         }
-    } else if (known) {
-        attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns0 + nm, scale, 1, WAVES - 1);
+    } else if (early) {
+        attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, nset, scale, 1, WAVES - 1);
     }
     __syncthreads();
     const int ns = set_n;
-    if (!known) {
-        // the heap replaced entries: slots follow the selection order
+    if (!early) {
+        // too many candidates: score only the selection, in selection order
         for (int i = tid; i < ns; i += blockDim.x) {
             const int slot = S.order[i];
             const int ph = slot == 0 ? V.mpt[cap] : (slot < ns0 ? V.mpt[cap + 1] : V.mpt[slot - ns0]);
@@ -680,9 +698,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
         attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns, scale, 0, WAVES);
         __syncthreads();
     }
-    attn_weights(S, ns, known ? S.order : nullptr);
+    attn_weights(S, ns, early ? S.order : nullptr);
     __syncthreads();
-    attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out);
+    attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out, early ? S.order : nullptr);
 }
 
 // 16 waves when the grid is small (more loads in flight per workgroup), 8
