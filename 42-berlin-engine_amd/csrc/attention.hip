@@ -888,7 +888,7 @@ extern "C" int be42_lsh_attention(const be42_kv_pool *pool, const float *q, cons
     if (n_queries <= 0)
         return BE42_OK;
     hipStream_t s = as_stream(stream);
-    if ((long)n_queries * P.n_kv > 512) {
+    if ((long)n_queries * P.n_kv > 1024) {
         // Enough workgroups to fill the chip: the router's latency is better
         // spent once per query in its own launch than once per KV head in
         // the attention's workgroups (measured on MI355X).  The selection
