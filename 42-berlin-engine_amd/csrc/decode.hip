@@ -191,27 +191,6 @@ __global__ __launch_bounds__(kRowThreads) void k_rmsnorm(float *__restrict__ out
     row_digits_reg<FP8, NV>(h, dim, dig, B, b, red);
 }
 
-// q [B][nq*hd], k [B][nk*hd] rotated at position *pos (table rows
-// [pos][hd/2]); positions at or past the table (rope_len) are not rotated.
-__global__ __launch_bounds__(256) void k_rope(float *__restrict__ q, float *__restrict__ k,
-                                              const float *__restrict__ cos_t, const float *__restrict__ sin_t,
-                                              const int *__restrict__ pos_p, int rope_len, int nq, int nk, int hd)
-{
-    const int pos = *pos_p;
-    if (pos >= rope_len)
-        return;
-    const int half = hd / 2, b = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (nq + nk) * half)
-        return;
-    const int h = i / half, j = i % half;
-    float *base = h < nq ? q + ((size_t)b * nq + h) * hd : k + ((size_t)b * nk + (h - nq)) * hd;
-    const float c = cos_t[(size_t)pos * half + j], s = sin_t[(size_t)pos * half + j];
-    const float x0 = base[j], x1 = base[j + half];
-    base[j] = __fmaf_rn(x0, c, -(x1 * s));
-    base[j + half] = __fmaf_rn(x0, s, x1 * c);
-}
-
 // h = (g * sigmoid(g)) * u for row b (op_silu_mul_fused_f32): blocks of 8 use
 // the vector Schraudolph exp (clamp, fused multiply-add, round to nearest),
 // the n % 8 remainder the scalar one; written as GEMV digit planes of the
@@ -655,13 +634,12 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         const be42_decoder_layer &L = d->w.layers[l];
         BE42_HIP(norm(L.attn_norm, pending));
         DEC_TRY(gemv_multi(d, {{L.wq, L.sq, d->q, qd}, {L.wk, L.sk, d->k, kd}, {L.wv, L.sv, d->v, kd}}, dim, B, st));
-        hipLaunchKernelGGL(k_rope, dim3(((H + KV) * (hd / 2) + 255) / 256, B), dim3(256), 0, st, d->q, d->k,
-                           d->cos_t, d->sin_t, &head->pos, rope_len, H, KV, hd);
-        BE42_LAUNCH_CHECK();
+        // RoPE of q and k, the K/V append and the seal of filled pages: one launch
+        DEC_TRY(launch_rope_append_step_dev(P, app + l, B, d->q, d->k, d->v, d->cos_t, d->sin_t, &head->pos, rope_len,
+                                            H, st));
         if (d->capture_q)
             BE42_HIP(hipMemcpyAsync(d->capture_q + (size_t)l * c.max_batch * qd, d->q, (size_t)B * qd * 4,
                                     hipMemcpyDeviceToDevice, st));
-        DEC_TRY(launch_append_step_dev(P, app + l, B, d->k, d->v, st));
         const int *lslots = d->slots + (size_t)l * c.max_batch;
         if (!sparse) {
             DEC_TRY(be42_paged_attention(d->pool, d->q, B, H, P.page_table + (size_t)l * c.max_batch * P.max_logical,

@@ -170,19 +170,6 @@ __global__ __launch_bounds__(64) void k_kv_append_step(void *__restrict__ kdst, 
     append_step_body<BF16>(kdst, vdst, kscale, vscale, ntok, page_table, n_logical, a, k, v, n_kv, hd);
 }
 
-// the same with the bookkeeping read from device memory (graph replays)
-template <bool BF16>
-__global__ __launch_bounds__(64) void k_kv_append_step_dev(void *__restrict__ kdst, void *__restrict__ vdst,
-                                                           float *__restrict__ kscale, float *__restrict__ vscale,
-                                                           int *__restrict__ ntok, int *__restrict__ page_table,
-                                                           int *__restrict__ n_logical,
-                                                           const AppendStepArgs *__restrict__ a,
-                                                           const float *__restrict__ k, const float *__restrict__ v,
-                                                           int n_kv, int hd)
-{
-    append_step_body<BF16>(kdst, vdst, kscale, vscale, ntok, page_table, n_logical, *a, k, v, n_kv, hd);
-}
-
 // One block per page that became full: centroid of the head-0 keys (per
 // dimension, tokens summed in order, then * (1.0f/16)), then its hash: 16
 // lanes each run the FMA chain over d ascending from +0 (bit h = sum > 0).
@@ -259,16 +246,68 @@ __global__ __launch_bounds__(256) void k_kv_seal_step(const void *__restrict__ k
     seal_step_body<BF16>(kpool, kscale, centroid, page_hash, n_indexed, a, hpT, n_kv, hd);
 }
 
+// RoPE + append + seal of one decode token of one layer slot, for KV head h
+// (block (token, h), 256 threads): the q heads of h's group and k head h are
+// rotated in place (the RoPE of inference.c / ops_rope.c:192 as k_rope does
+// it), the rotated k row and the v row are stored into the page, and block
+// h == 0 seals the page when this token fills it.
 template <bool BF16>
-__global__ __launch_bounds__(256) void k_kv_seal_step_dev(const void *__restrict__ kpool,
-                                                          const float *__restrict__ kscale,
-                                                          float *__restrict__ centroid,
-                                                          uint16_t *__restrict__ page_hash,
-                                                          int *__restrict__ n_indexed,
-                                                          const AppendStepArgs *__restrict__ a,
-                                                          const float *__restrict__ hpT, int n_kv, int hd)
+__global__ __launch_bounds__(256) void k_rope_append_dev(const be42_kv_pool P, const AppendStepArgs *__restrict__ ap,
+                                                         float *__restrict__ q, float *__restrict__ k,
+                                                         const float *__restrict__ v,
+                                                         const float *__restrict__ cos_t,
+                                                         const float *__restrict__ sin_t,
+                                                         const int *__restrict__ pos_p, int rope_len, int H)
 {
-    seal_step_body<BF16>(kpool, kscale, centroid, page_hash, n_indexed, *a, hpT, n_kv, hd);
+    __shared__ float ks[256];
+    __shared__ float c[256];
+    const AppendStepArgs &a = *ap;
+    const int tok = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    if (tok >= a.n)
+        return;
+    const int n_kv = P.n_kv, hd = P.head_dim, half = hd / 2, G = H / n_kv;
+    const int pos = *pos_p;
+    float *krow = k + ((size_t)tok * n_kv + h) * hd;
+    if (pos < rope_len) {
+        for (int i = tid; i < (G + 1) * half; i += blockDim.x) {
+            const int j = i / half, pr = i % half;
+            float *base = j < G ? q + ((size_t)tok * H + h * G + j) * hd : krow;
+            const float cs = cos_t[(size_t)pos * half + pr], sn = sin_t[(size_t)pos * half + pr];
+            const float x0 = base[pr], x1 = base[pr + half];
+            const float y0 = __fmaf_rn(x0, cs, -(x1 * sn)), y1 = __fmaf_rn(x0, sn, x1 * cs);
+            base[pr] = y0;
+            base[pr + half] = y1;
+            if (j == G) {
+                ks[pr] = y0;
+                ks[pr + half] = y1;
+            }
+        }
+    } else {
+        for (int i = tid; i < hd; i += blockDim.x)
+            ks[i] = krow[i];
+    }
+    __syncthreads();
+    const int off = a.pos[tok] % kPage, blk = a.pos[tok] / kPage, phys = a.phys[tok];
+    if (tid < kWave) {
+        if (h == 0 && tid == 0) {
+            if (a.publish[tok]) {
+                P.page_table[(size_t)a.slot[tok] * a.max_logical + blk] = phys;
+                P.n_logical[a.slot[tok]] = blk + 1;
+            }
+            P.ntok[phys] = off + 1;
+        }
+        const size_t slot = ((size_t)phys * n_kv + h) * kPage + off;
+        store_kv_row<BF16>(P.k, P.v, P.k_scale, P.v_scale, slot, ks, v + ((size_t)tok * n_kv + h) * hd, hd, tid);
+    }
+    const int si = a.seal_of[tok];
+    if (h != 0 || si < 0)
+        return;
+    __syncthreads();                       // the page's last row is in memory
+    if (tid == 0)
+        P.n_indexed[a.seal_slot[si]] = a.seal_nidx[si];
+    seal_page<BF16>(P.k, P.k_scale, P.centroid,
+                    P.page_hash + (size_t)a.seal_slot[si] * a.max_logical + a.seal_logical[si], a.seal_phys[si],
+                    P.hpT, n_kv, hd, c);
 }
 
 }  // namespace be42
@@ -571,7 +610,9 @@ int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n
         a.pos[t] = ps;
         a.phys[t] = phys;
         a.slot[t] = s;
+        a.seal_of[t] = -1;
         if (ps % kPage == kPage - 1 && !p->registered[phys]) {
+            a.seal_of[t] = a.n_seal;
             p->registered[phys] = 1;
             if (blk + 1 > p->n_indexed[s])
                 p->n_indexed[s] = blk + 1;
@@ -585,23 +626,19 @@ int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n
     return BE42_OK;
 }
 
-// Launch the append (and seal) of n tokens whose bookkeeping is in device
-// memory (a_dev): grids sized for n tokens and up to n seals.
-int launch_append_step_dev(const be42_kv_pool &P, const AppendStepArgs *a_dev, int n, const float *k, const float *v,
-                           hipStream_t st)
+int launch_rope_append_step_dev(const be42_kv_pool &P, const AppendStepArgs *a_dev, int n, float *q, float *k,
+                                const float *v, const float *cos_t, const float *sin_t, const int *pos_p,
+                                int rope_len, int n_heads, hipStream_t st)
 {
+    BE42_CHECK(P.head_dim <= 256 && n_heads % P.n_kv == 0, "rope+append: head_dim %d, %d heads over %d kv heads",
+               P.head_dim, n_heads, P.n_kv);
     const dim3 grid(n, P.n_kv);
-    if (P.kind == BE42_KV_BF16) {
-        hipLaunchKernelGGL(k_kv_append_step_dev<true>, grid, dim3(64), 0, st, P.k, P.v, P.k_scale, P.v_scale,
-                           P.ntok, P.page_table, P.n_logical, a_dev, k, v, P.n_kv, P.head_dim);
-        hipLaunchKernelGGL(k_kv_seal_step_dev<true>, dim3(n), dim3(256), 0, st, P.k, P.k_scale, P.centroid,
-                           P.page_hash, P.n_indexed, a_dev, P.hpT, P.n_kv, P.head_dim);
-    } else {
-        hipLaunchKernelGGL(k_kv_append_step_dev<false>, grid, dim3(64), 0, st, P.k, P.v, P.k_scale, P.v_scale,
-                           P.ntok, P.page_table, P.n_logical, a_dev, k, v, P.n_kv, P.head_dim);
-        hipLaunchKernelGGL(k_kv_seal_step_dev<false>, dim3(n), dim3(256), 0, st, P.k, P.k_scale, P.centroid,
-                           P.page_hash, P.n_indexed, a_dev, P.hpT, P.n_kv, P.head_dim);
-    }
+    if (P.kind == BE42_KV_BF16)
+        hipLaunchKernelGGL(k_rope_append_dev<true>, grid, dim3(256), 0, st, P, a_dev, q, k, v, cos_t, sin_t, pos_p,
+                           rope_len, n_heads);
+    else
+        hipLaunchKernelGGL(k_rope_append_dev<false>, grid, dim3(256), 0, st, P, a_dev, q, k, v, cos_t, sin_t, pos_p,
+                           rope_len, n_heads);
     BE42_LAUNCH_CHECK();
     return BE42_OK;
 }
