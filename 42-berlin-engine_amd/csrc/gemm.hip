@@ -13,7 +13,11 @@
 // xq / sx come from the per-token quantizers (quant_f32_to_int8,
 // ops_quant.c:229, and the amax/224 E4M3 encoder, ops_quant.c:103).
 //
-// Tiling.  A workgroup computes a BM x BN tile of Y (tokens x features) with
+// Two kernels: k_gemm_dma (K a multiple of 128, the prefill shapes), whose
+// stages go global -> LDS by the direct-to-LDS loads and whose tiles run on
+// the 32x32 matrix-core steps (described at the kernel), and k_gemm for any
+// K that is a multiple of 16:
+// A workgroup computes a BM x BN tile of Y (tokens x features) with
 // WGM x WGN waves, each owning (BM/WGM) x (BN/WGN) = TM x TN tiles of 16x16.
 // K advances in stages of 128 bytes: the stage's X rows and W rows are
 // copied global -> registers -> LDS (rows padded to 144 bytes so that the
@@ -27,6 +31,8 @@
 // A and B fragments use the same k assignment, so every product pairs equal
 // k.  The accumulator of a 16x16 tile holds, in lane l, rows 4*(l/16)+j
 // (j = 0..3) of column l%16.
+#include <cstdlib>
+
 #include "be42_common.h"
 
 namespace be42 {
@@ -181,6 +187,252 @@ __global__ __launch_bounds__(WGM *WGN * 64) void k_gemm(float *__restrict__ Y, c
     }
 }
 
+// Chunk slot of 16-byte chunk c in LDS row R of the DMA-staged GEMM: rows
+// are 128 bytes, chunks XOR-permuted so that 16 consecutive rows read at the
+// same chunk fall on 16 distinct (row parity, slot) pairs, i.e. on distinct
+// banks whether the LDS serves 8 lanes x 16 bytes over 32 banks or 16 lanes
+// over 64 banks per cycle.
+__device__ __forceinline__ int dma_slot(int R, int c) { return c ^ ((R & 7) ^ ((R >> 3) & 1)); }
+
+// Scheduling hint: NM matrix-core instructions, each followed by its share of
+// ND LDS reads (the first ND % NM take one more).
+template <int NM, int ND, int I = 0>
+__device__ __forceinline__ void sched_interleave()
+{
+    if constexpr (I < NM) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        constexpr int d = ND / NM + (I < ND % NM ? 1 : 0);
+        if constexpr (d > 0)
+            __builtin_amdgcn_sched_group_barrier(0x100, d, 0);
+        sched_interleave<NM, ND, I + 1>();
+    }
+}
+
+// Large-tile GEMM whose stages move global -> LDS through the direct-to-LDS
+// loads of gfx950 (global_load_lds_dwordx4), so no VGPRs or LDS-store
+// instructions are spent on staging.  A workgroup of WGM x WGN waves owns a
+// BM x BN tile of Y, each wave (BM/WGM) x (BN/WGN) = TM x TN tiles of 32x32
+// on the 32x32 matrix-core instructions, which do twice the work of the
+// 16x16 ones per operand byte read from LDS:
+//   FP8:  v_mfma_scale_f32_32x32x64_f8f6f4 with unit scales, lane
+//         (r = lane%32, h = lane/32) supplying 32 bytes of row r;
+//   INT8: two v_mfma_i32_32x32x32_i8, 16 bytes each.
+// The accumulator of a 32x32 tile holds, in lane l, rows
+// 8*(i/4) + 4*(l/32) + i%4 (i = 0..15) of column l%32.
+// A stage is 128 k-bytes of the BM + BN rows (X rows first, then W rows),
+// laid out in LDS as 128-byte rows with chunks placed by dma_slot; one load
+// instruction fills 1 KB = 8 rows, lane l writing LDS bytes [16l, 16l+16),
+// i.e. row l/8, slot l%8, so each lane fetches global chunk
+// dma_slot(row, l%8) and the 8 lanes of a row read one full 128-byte line.
+// NS stages are resident in a ring (see the main loop).  Within a stage the
+// LDS reads of step 1 are interleaved with the matrix-core instructions of
+// step 0, and those of the next stage's step 0 with step 1.  Workgroup ids
+// are spread over the 8 XCDs round-robin by the hardware; they are remapped
+// so that each XCD walks a contiguous run of the grouped tile order.
+// K must be a multiple of 128 and M*K, N*K below 2^32 (32-bit offsets);
+// rows past M or N read the last row and are not stored.
+template <bool FP8, int BM, int BN, int WGM, int WGN, int NS>
+__global__ __launch_bounds__(WGM *WGN * 64) void k_gemm_dma(float *__restrict__ Y, const uint8_t *__restrict__ X,
+                                                            const float *__restrict__ sx,
+                                                            const uint8_t *__restrict__ W,
+                                                            const float *__restrict__ sw, int M, int N, int K,
+                                                            int tiles_m, int tiles_n, int tiles)
+{
+    constexpr int NW = WGM * WGN;
+    constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;
+    constexpr int SBYTES = (BM + BN) * 128;              // one stage
+    constexpr int DPW = (BM + BN) / 8 / NW;              // 1 KB loads per wave per stage
+    static_assert((BM + BN) % (8 * NW) == 0, "stage loads must divide over the waves");
+    static_assert(BM % 32 == 0 && BN % 32 == 0, "32-row blocks");
+    using AccT = typename std::conditional<FP8, v16f, v16i>::type;
+    extern __shared__ __align__(1024) uint8_t lds_dyn[];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int per = nb / 8, rem = nb % 8, x = b % 8, i8 = b / 8;
+    const int tile = (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + i8;
+    if (tile >= tiles)
+        return;
+    // grouped order: runs of 8 M-tiles, N-tiles within a run, so that the
+    // 32 workgroups an XCD holds at once cover 8 x 4 tiles and share their X
+    // and W slabs in its L2
+    int bm, bn;
+    {
+        constexpr int GM = 8;
+        const int span = GM * tiles_n;
+        const int first = tile / span * GM, gsz = min(tiles_m - first, GM), t = tile % span;
+        bm = first + t % gsz;
+        bn = t / gsz;
+    }
+
+    const int m0 = bm * BM, n0 = bn * BN;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    // byte offsets of this lane's 16-byte chunk in X or W (which one is
+    // uniform over each load: BM is a multiple of 8); the host keeps M*K
+    // and N*K below 2^32
+    uint32_t src[DPW];
+#pragma unroll
+    for (int j = 0; j < DPW; j++) {
+        const int row = (wave * DPW + j) * 8 + (lane >> 3);
+        const uint32_t off = dma_slot(row, lane & 7) * 16;
+        if (row < BM)
+            src[j] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)K + off;
+        else
+            src[j] = (uint32_t)min(n0 + row - BM, N - 1) * (uint32_t)K + off;
+    }
+    auto issue = [&](int st) {
+        uint8_t *base = lds_dyn + (st % NS) * SBYTES + wave * DPW * 1024;
+#pragma unroll
+        for (int j = 0; j < DPW; j++) {
+            const uint8_t *g = (wave * DPW + j) * 8 < BM ? X : W;
+            __builtin_amdgcn_global_load_lds((const void *)(g + src[j] + (size_t)st * 128),
+                                             (lds_void *)(base + j * 1024), 16, 0, 0);
+        }
+    };
+
+    AccT acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            acc[i][j] = AccT{};
+
+    const int r = lane & 31, h = lane >> 5;
+    // row r of every 32-row block has the same slot permutation
+    const int arow = (wm * TM * 32 + r) * 128, brow = (BM + wn * TN * 32 + r) * 128;
+    // a stage is two steps of 64 k-bytes; a step's fragment is 32 bytes a
+    // lane, chunks c0 and c1 of its row:
+    //   FP8  one 32x32x64 instruction, k = 64u + 32h .. +31: c0 = 4u + 2h, c1 = c0 + 1
+    //   INT8 two 32x32x32 instructions, k = 64u + 16h .. +15 (c0 = 4u + h) and
+    //        k = 64u + 32 + 16h .. +15 (c1 = 4u + 2 + h)
+    struct Frags {
+        v8i a[TM], b[TN];
+    };
+    const int c0 = FP8 ? 2 * h : h, c1 = FP8 ? 2 * h + 1 : 2 + h;
+    auto load = [&](int buf, int u, Frags &f) {
+        const uint8_t *L = lds_dyn + buf * SBYTES;
+        auto rd = [&](int rowoff, int c) -> v4i { return *(const v4i *)(L + rowoff + dma_slot(r, c) * 16); };
+#pragma unroll
+        for (int i = 0; i < TM + TN; i++) {
+            const int ro = i < TM ? arow + i * 32 * 128 : brow + (i - TM) * 32 * 128;
+            const v4i lo = rd(ro, 4 * u + c0), hi = rd(ro, 4 * u + c1);
+            const v8i v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if (i < TM)
+                f.a[i] = v;
+            else
+                f.b[i - TM] = v;
+        }
+    };
+    auto mfma = [&](const Frags &f) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                if constexpr (FP8) {
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0, 0,
+                                                                                127, 0, 127);
+                } else {
+                    const v4i alo = {f.a[i][0], f.a[i][1], f.a[i][2], f.a[i][3]};
+                    const v4i ahi = {f.a[i][4], f.a[i][5], f.a[i][6], f.a[i][7]};
+                    const v4i blo = {f.b[j][0], f.b[j][1], f.b[j][2], f.b[j][3]};
+                    const v4i bhi = {f.b[j][4], f.b[j][5], f.b[j][6], f.b[j][7]};
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(alo, blo, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ahi, bhi, acc[i][j], 0, 0, 0);
+                }
+            }
+    };
+    // the LDS reads of the next step go between the matrix-core instructions
+    // of this one
+    auto interleave = [&]() {
+        if constexpr (FP8)
+            sched_interleave<TM * TN, (TM + TN) * 2>();
+    };
+
+    // Stages s .. s+NS-1 are resident (the first NS issued up front).  The
+    // loads of stage s+NS are issued once every wave has read its last
+    // fragments of stage s (the barrier before the last step of s), which is
+    // also where stage s+1 is waited for (NS-2 later stages may still be in
+    // flight).
+    const int nk = K / 128;
+#pragma unroll
+    for (int st = 0; st < NS; st++)
+        if (st < nk)
+            issue(st);
+    if (nk >= NS)
+        wait_vmcnt<(NS - 1) * DPW>();
+    else
+        wait_vmcnt<0>();
+    __syncthreads();
+    Frags F[2];
+    load(0, 0, F[0]);
+    for (int st = 0; st < nk; st++) {
+        const int buf = st % NS, nbuf = (st + 1) % NS;
+        // step 0: read step 1's fragments while the matrix cores run step 0
+        __builtin_amdgcn_sched_barrier(0);
+        load(buf, 1, F[1]);
+        mfma(F[0]);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        // step 1: stage st+1 must have landed and every wave be done with
+        // stage st before its buffer takes stage st+NS; then read stage
+        // st+1's first fragments (past the last stage the read is of stale
+        // LDS and unused)
+        if (st + 1 < nk) {
+            if (st + NS - 1 < nk)
+                wait_vmcnt<(NS - 2) * DPW>();
+            else
+                wait_vmcnt<0>();
+            __syncthreads();
+            if (st + NS < nk)
+                issue(st + NS);
+        }
+        load(nbuf, 0, F[0]);
+        mfma(F[1]);
+        interleave();
+    }
+
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = n0 + wn * (TN * 32) + j * 32 + r;
+        if (n >= N)
+            continue;
+        const float swn = sw[n];
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = m0 + wm * (TM * 32) + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (m < M) {
+                    float v;
+                    if constexpr (FP8)
+                        v = acc[i][j][e];
+                    else
+                        v = (float)acc[i][j][e];
+                    Y[(size_t)m * N + n] = (v * sx[m]) * swn;
+                }
+            }
+        }
+    }
+}
+
+template <bool FP8, int BM, int BN, int WGM, int WGN, int NS>
+static void launch_gemm_dma(float *Y, const uint8_t *X, const float *sx, const uint8_t *W, const float *sw, int M,
+                            int N, int K, hipStream_t s)
+{
+    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+    const size_t lds = (size_t)NS * (BM + BN) * 128;
+    static_assert(NS * (BM + BN) * 128 <= 160 * 1024, "LDS budget");
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void *)k_gemm_dma<FP8, BM, BN, WGM, WGN, NS>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_gemm_dma<FP8, BM, BN, WGM, WGN, NS>), dim3(tm * tn), dim3(WGM * WGN * 64), lds, s, Y, X, sx,
+                       W, sw, M, N, K, tm, tn, tm * tn);
+}
+
 template <bool FP8, int BM, int BN, int WGM, int WGN>
 static void launch_gemm(float *Y, const uint8_t *X, const float *sx, const uint8_t *W, const float *sw, int M,
                         int N, int K, hipStream_t s)
@@ -190,14 +442,25 @@ static void launch_gemm(float *Y, const uint8_t *X, const float *sx, const uint8
                        M, N, K, tn);
 }
 
-// Tile choice: 128 x 128 workgroups of 4 waves (2 x 2, 64 x 64 per wave)
-// when the grid fills the chip, else 64 x 128.
+// Kernel and tile choice.  K a multiple of 128 (and operands under 4 GiB):
+// the direct-to-LDS kernel, at 256 x 256 when that grid alone fills the 256
+// CUs, else at 128 x 128.  Otherwise the register-staged 16x16 kernel at
+// 128 x 128 when its grid holds two workgroups per CU, else 64 x 128.
+// BE42_GEMM_TILE = 1..4 forces one of the four (1 and 2 only where K allows).
 template <bool FP8>
 static void gemm_dispatch(float *Y, const uint8_t *X, const float *sx, const uint8_t *W, const float *sw, int M,
                           int N, int K, hipStream_t s)
 {
     const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles128 >= 512)
+    const long tiles256 = (long)((M + 255) / 256) * ((N + 255) / 256);
+    const bool dma = K % 128 == 0 && (size_t)M * K < (1ull << 32) && (size_t)N * K < (1ull << 32);
+    const char *e = getenv("BE42_GEMM_TILE");
+    const int force = e ? atoi(e) : 0;
+    if (dma && (force == 1 || (!force && tiles256 >= 256)))
+        launch_gemm_dma<FP8, 256, 256, 2, 4, 2>(Y, X, sx, W, sw, M, N, K, s);
+    else if (dma && (force == 2 || !force))
+        launch_gemm_dma<FP8, 128, 128, 2, 2, 2>(Y, X, sx, W, sw, M, N, K, s);
+    else if (force == 3 || (!force && tiles128 >= 512))
         launch_gemm<FP8, 128, 128, 2, 2>(Y, X, sx, W, sw, M, N, K, s);
     else
         launch_gemm<FP8, 64, 128, 2, 2>(Y, X, sx, W, sw, M, N, K, s);

@@ -322,17 +322,6 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(const GemvSegs S, const uin
     }
 }
 
-// s_waitcnt immediate that waits until at most n vector-memory operations of
-// this wave are outstanding (expcnt and lgkmcnt left unconstrained).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt()
-{
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-typedef __attribute__((address_space(3))) void lds_void;
-
 // Streaming GEMV with the weights and the digit planes moved HBM -> LDS by
 // the direct-to-LDS loads of gfx950 (global_load_lds_dwordx4), P stages deep,
 // so the bytes in flight sit in LDS instead of VGPRs.  A block is WAVES waves

@@ -124,3 +124,27 @@ def test_gemm_rejects_bad_shapes(be):
     y = torch.zeros(64, dtype=torch.float32, device="cuda")
     rc = be.lib.be42_gemm_i8(be.p(y), be.p(t), be.p(f), be.p(t), be.p(f), 2, 2, 24, None)
     assert rc != 0 and "multiple of 16" in be.last_error()
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("tile", ["1", "2", "3", "4"])
+def test_gemm_every_tile(be, orc, kind, tile, monkeypatch):
+    """Each kernel and workgroup tiling (BE42_GEMM_TILE: 1 = 256x256 and
+    2 = 128x128 on the direct-to-LDS 32x32 kernel, which needs k a multiple
+    of 128; 3 = 128x128 and 4 = 64x128 on the 16x16 kernel, here with k not
+    a multiple of the 128-byte stage) on a ragged shape whose edges cut
+    every tile."""
+    monkeypatch.setenv("BE42_GEMM_TILE", tile)
+    rng = np.random.default_rng(77 + int(tile))
+    m, n, k = (300, 520, 1152) if tile in ("1", "2") else (300, 520, 1040)
+    x, w = _inputs(rng, m, n, k)
+    xq, sx = orc.quantize_rows(x, kind)
+    wq, sw = orc.quantize_rows(w, kind)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    y = be.gemm(t(xq), t(sx), t(wq), t(sw), kind).cpu().numpy()
+    want = orc.gemm(xq, sx, wq, sw, kind)
+    if kind == "int8":
+        np.testing.assert_array_equal(y, want)
+    else:
+        assert rel_err(y, want) <= TOL
+        assert rel_err(y.astype(np.float64), _exact_fp8(orc, xq, sx, wq, sw)) <= 2e-4
