@@ -76,6 +76,24 @@ __device__ __forceinline__ void wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Stage boundary of a direct-to-LDS ring shared by the waves of a block:
+// wait until at most N vector-memory operations of this wave are outstanding
+// and until every LDS read this wave issued has returned, then s_barrier.
+// After it, every wave's loads older than its N newest are in LDS, and no
+// wave still has a read of a ring slot in flight, so the slot the previous
+// stage used may be refilled.  (A raw s_barrier, unlike __syncthreads, does
+// not drain the loads still in flight for later stages.)  The empty asm
+// statements keep the compiler from moving memory operations across it.
+template <int N>
+__device__ __forceinline__ void stage_barrier()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ float wave_max(float v)

@@ -289,6 +289,9 @@ __global__ __launch_bounds__(WGM *WGN * 64) void k_gemm_dma(float *__restrict__ 
             __builtin_amdgcn_global_load_lds((const void *)(g + src[j] + (size_t)st * 128),
                                              (lds_void *)(base + j * 1024), 16, 0, 0);
         }
+        // the wait counts assume every load of stage st is issued before any
+        // load of a later stage: keep the compiler from interleaving stages
+        asm volatile("" ::: "memory");
     };
 
     AccT acc[TM][TN];

@@ -415,6 +415,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
             __builtin_amdgcn_global_load_lds((const void *)(dsrc[i] + (size_t)st * 128),
                                              (lds_void *)(ddst[i] == spare ? spare : ddst[i] + slot * NDL * 1024),
                                              16, 0, 0);
+        // the wait counts assume every load of stage st is issued before any
+        // load of a later stage: keep the compiler from interleaving stages
+        asm volatile("" ::: "memory");
     };
     auto compute = [&](int st) {
         const int slot = st % P;
@@ -462,10 +465,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
             issue(st);
     for (int st = 0; st < nst; st++) {
         if (st + P - 2 < nst)
-            wait_vmcnt<(P - 2) * PER>();
+            stage_barrier<(P - 2) * PER>();
         else
-            wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
+            stage_barrier<0>();
         if (st + P - 1 < nst)
             issue(st + P - 1);
         compute(st);
@@ -487,6 +489,244 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
         __syncthreads();
         epi_store<FP8, RT>(E, t, g, B, [&](int d, int bb) { return (Tot)part[wave][r][bb * ND + d]; });
     }
+}
+
+// Streaming GEMV for many rows (the lm_head) with the digit planes resident in
+// LDS one K-slice at a time.
+// Operand roles are the transpose of k_gemv's: A = one digit plane (16 batch
+// rows x 128 k; lane (r, g) holds batch row r, k bytes 32g .. 32g+31 for FP8,
+// 64v + 16g .. +15 for the two INT8 sub-steps v), B = 16 weight rows (lane
+// (r, g) holds row r at the same k).  A lane's accumulator j is then the sum
+// of batch row 4g + j for weight row r, so it holds every digit plane of its
+// own outputs and recombines them in registers: no LDS epilogue.
+// A block of WAVES waves owns 16*RT*WAVES rows over the whole of K.  K is cut
+// into slices of KSL bytes; the digits of a slice (ND planes x 16 batch rows x
+// KSL, 2 KB per plane and 128-byte step, laid out [piece p][batch row][16
+// bytes] so that each 16-lane read is one 256-byte run) are moved HBM -> LDS
+// once per block by direct-to-LDS loads, double buffered, so a block crosses
+// one barrier per slice instead of one per stage.  A wave streams its weights
+// into a register ring of D stages; a stage is one row tile over SB steps of
+// 128 k, i.e. 16 rows x 128*SB contiguous bytes each.  Stage order: slice,
+// then tile, then step; the ring runs across tile and slice boundaries.
+template <bool FP8, int RT, int SB, int KSL, int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, const uint8_t *__restrict__ dig,
+                                                          const float *__restrict__ sx, int K, int Kp, int B)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr int STEPS = KSL / 128;                 // 128-k steps per slice
+    constexpr int SPT = STEPS / SB;                  // stages per tile per slice
+    constexpr int NST = RT * SPT;                    // stages per slice per wave
+    constexpr int WL = 2 * SB;                       // weight loads per stage
+    constexpr int SLB = ND * STEPS * 2048;           // LDS bytes per slice
+    constexpr int NDMA = ND * STEPS * 2;             // 1 KB loads per slice
+    constexpr int DI = NDMA / WAVES;                 // of them per wave
+    static_assert(STEPS % SB == 0 && NST % D == 0 && D >= 2 && D <= NST, "stage ring");
+    static_assert(NDMA % WAVES == 0, "slice loads split evenly over the waves");
+    static_assert(2 * SLB <= 160 * 1024, "LDS budget");
+    static_assert((D - 1) * WL < 64, "vmcnt");
+    using Acc = typename std::conditional<FP8, v4f, v4i>::type;
+    __shared__ __align__(1024) uint8_t lds[2 * SLB];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
+    const int row0 = (blockIdx.x * WAVES + wave) * 16 * RT;
+    const int nsl = Kp / KSL;
+
+    Acc acc[RT][ND];
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+            acc[t][d] = Acc{0, 0, 0, 0};
+
+    const uint8_t *wrow[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        int local;
+        const int sg = seg_of(S, min(row0 + t * 16 + r, S.total - 1), &local);
+        wrow[t] = S.w[sg] + (size_t)local * K;
+    }
+    const int klast = K - 16;
+    const int woff0 = FP8 ? 32 * g : 16 * g, woff1 = FP8 ? 32 * g + 16 : 64 + 16 * g;
+
+    // slice loads: load j of a slice carries plane d, step st, half h; lane
+    // l brings batch row l % 16 (clamped to the batch), piece l / 16 + 4h
+    const uint8_t *dsrc[DI];
+    int ddst[DI];
+#pragma unroll
+    for (int i = 0; i < DI; i++) {
+        const int j = wave * DI + i;
+        const int d = j / (STEPS * 2), st = (j / 2) % STEPS, h = j % 2;
+        const int b = min(r, B - 1);
+        dsrc[i] = dig + ((size_t)d * B + b) * Kp + st * 128 + 16 * (g + 4 * h);
+        ddst[i] = (d * STEPS + st) * 2048 + h * 1024;
+    }
+    // Blocks start at different slices (slice s of block b covers k bytes
+    // KSL * ((s + b) mod nsl) ..), so that at any moment the blocks read
+    // spread-out k ranges of their rows rather than all the same one.
+    const int sk0 = blockIdx.x % nsl;
+    auto kslice = [&](int s) { return (s + sk0 < nsl ? s + sk0 : s + sk0 - nsl) * KSL; };
+    auto issue_slice = [&](int s) {
+        uint8_t *buf = lds + (s & 1) * SLB;
+        const int kb = kslice(s);
+#pragma unroll
+        for (int i = 0; i < DI; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(dsrc[i] + kb), (lds_void *)(buf + ddst[i]), 16, 0, 0);
+        asm volatile("" ::: "memory");
+    };
+
+    // A stage's weights, one 32-byte MFMA operand per step: FP8 bytes 32g ..
+    // 32g+31 of the step, INT8 bytes 16g .. +15 (low half) and 64+16g .. +15
+    // (high half).  Held as 8-dword vectors so each operand sits in
+    // consecutive registers from the load on.
+    v8i wr[D][SB];
+    // weights of stage i (tile i / SPT, step group i % SPT) of slice s
+    auto issue = [&](int s, int i, v8i (&w)[SB]) {
+        const int t = i / SPT, q = i % SPT;
+        const int kb = kslice(s) + q * SB * 128;
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const v4i lo = *(const v4i *)(wrow[t] + min(kb + u * 128 + woff0, klast));
+            const v4i hi = *(const v4i *)(wrow[t] + min(kb + u * 128 + woff1, klast));
+            w[u] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+        asm volatile("" ::: "memory");
+    };
+    // stage i of slice s, digits from LDS buffer s & 1
+    auto compute = [&](const v8i (&w)[SB], int i, int s) {
+        const int t = i / SPT, q = i % SPT;
+        const uint8_t *buf = lds + (s & 1) * SLB;
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const int st = q * SB + u;
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                const uint8_t *pl = buf + (d * STEPS + st) * 2048 + r * 16;
+                if constexpr (FP8) {
+                    const v4i a0 = *(const v4i *)(pl + (2 * g) * 256), a1 = *(const v4i *)(pl + (2 * g + 1) * 256);
+                    const v8i a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+                    acc[t][d] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, w[u], acc[t][d], 0, 0, 0, 127, 0,
+                                                                                 127);
+                } else {
+                    const v4i a0 = *(const v4i *)(pl + g * 256), a1 = *(const v4i *)(pl + (4 + g) * 256);
+                    const v4i w0 = __builtin_shufflevector(w[u], w[u], 0, 1, 2, 3);
+                    const v4i w1 = __builtin_shufflevector(w[u], w[u], 4, 5, 6, 7);
+                    acc[t][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0, acc[t][d], 0, 0, 0);
+                    acc[t][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1, acc[t][d], 0, 0, 0);
+                }
+            }
+            // keep each step's LDS reads next to its matrix instructions:
+            // merging the identical reads of different tiles, or gathering a
+            // whole slice's reads ahead of its matrix instructions, would not
+            // fit the registers (the empty asm ties the accumulators here)
+#pragma unroll
+            for (int d = 0; d < ND; d++)
+                asm volatile("" : "+v"(acc[t][d]));
+            asm volatile("" ::: "memory");
+        }
+    };
+    // one slice: stage i computes while stage i + D - 1 (of this slice or
+    // the next) is issued; the ring slot of a stage is its number mod D,
+    // static because NST is a multiple of D.  The last slice issues its own
+    // last stage again in place of the stages past the end (same addresses
+    // as the load just before, served by the L2), so that every slice runs
+    // the same code and keeps the same number of loads in flight.
+    auto slice = [&](int s, int snext) {
+#pragma unroll
+        for (int i = 0; i < NST; i++) {
+            const int ii = i + D - 1;
+            if (ii < NST)
+                issue(s, ii, wr[ii % D]);
+            else if (snext > s)
+                issue(snext, ii - NST, wr[ii % D]);
+            else
+                issue(s, NST - 1, wr[ii % D]);
+            compute(wr[i % D], i, s);
+        }
+    };
+
+    issue_slice(0);
+    if (nsl > 1)
+        issue_slice(1);
+#pragma unroll
+    for (int j = 0; j < D - 1; j++)
+        issue(0, j, wr[j]);
+    // Slice s is in LDS once this wave's loads older than the D-1 weight
+    // stages in flight have landed: at s = 0 everything but slice 1's loads
+    // and those stages; later, slice s's loads were issued a whole slice
+    // (NST >= D stages) ago.  Every wave is then done with slice s-1, whose
+    // buffer takes slice s+1.
+    if (nsl > 1)
+        stage_barrier<DI + (D - 1) * WL>();
+    else
+        stage_barrier<(D - 1) * WL>();
+    for (int s = 0; s < nsl; s++) {
+        if (s > 0) {
+            stage_barrier<(D - 1) * WL>();
+            if (s + 1 < nsl)
+                issue_slice(s + 1);
+        }
+        slice(s, min(s + 1, nsl - 1));
+    }
+    wait_vmcnt<0>();
+
+    // epilogue operands
+    float e_sw[RT], e_sx[4];
+    float *e_y[RT];
+    int e_n[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const int row = row0 + t * 16 + r;
+        e_y[t] = nullptr;
+        e_sw[t] = 0.0f;
+        e_n[t] = 0;
+        if (row < S.total) {
+            int local;
+            const int sg = seg_of(S, row, &local);
+            e_sw[t] = S.sw[sg][local];
+            e_y[t] = S.y[sg] + local;
+            e_n[t] = S.n[sg];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        e_sx[j] = 4 * g + j < B ? sx[4 * g + j] : 0.0f;
+
+    constexpr double kI8W[3] = {(double)(kI8Base * kI8Base), (double)kI8Base, 1.0};
+    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        if (!e_y[t])
+            continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int b = 4 * g + j;
+            if (b >= B)
+                break;
+            double tot = 0.0;
+            if constexpr (FP8) {
+#pragma unroll
+                for (int d = 0; d < ND; d++)
+                    tot += (double)acc[t][d][j] * kF8Weight[d];
+            } else {
+                long long it = 0;
+#pragma unroll
+                for (int d = 0; d < ND; d++)
+                    it += (long long)acc[t][d][j] * (long long)kI8W[d];
+                tot = (double)it;
+            }
+            e_y[t][(size_t)b * e_n[t]] = (float)(tot * ((double)e_sx[j] * sxw * (double)e_sw[t]));
+        }
+    }
+}
+
+template <bool FP8, int RT, int SB, int KSL, int D, int WAVES>
+static void launch_slab(const GemvSegs &S, const uint8_t *dig, const float *sx, int k, int Kp, int batch,
+                        hipStream_t s)
+{
+    const int blocks = (S.total + 16 * RT * WAVES - 1) / (16 * RT * WAVES);
+    hipLaunchKernelGGL((k_gemv_slab<FP8, RT, SB, KSL, D, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, S, dig, sx,
+                       k, Kp, batch);
 }
 
 template <bool FP8, int RT, int NC, int P, int WAVES>
@@ -569,12 +809,20 @@ static void launch_cfg(const GemvSegs &S, const uint8_t *dig, const float *sx, i
 // splitting K per row group, WAVES per block, PF register double buffering.
 struct TileCfg {
     int rt, u, ks, waves, pf;
-    int dma;   // 1: k_gemv_dma with u = pipeline stages (ks, pf unused)
+    int dma;   // 1: k_gemv_dma with u = pipeline stages (ks, pf unused); 3: k_gemv_slab
 };
 constexpr TileCfg dma_tile(int rt, int stages, int waves) { return TileCfg{rt, stages, 0, waves, 0, 1}; }
+constexpr TileCfg slab_tile(int rt, int stages, int waves, int slice_steps)
+{
+    return TileCfg{rt, stages, 1, waves, slice_steps, 3};
+}
 
 static TileCfg pick_tile(bool fp8, int nc, int n, int k)
 {
+    // many rows at 3+ column groups (FP8 batch >= 7, INT8 batch >= 11): the
+    // LDS-resident-digit slab kernel, one block of 8 waves x 4 row tiles
+    if (n > 32768 && nc >= 3)
+        return slab_tile(4, 4, 8, 4);
     if (fp8) {
         if (nc == 1) {
             if (n <= 4096)
@@ -619,7 +867,7 @@ static TileCfg pick_tile(bool fp8, int nc, int n, int k)
     if (!c.dma && c.rt == RT && c.u == U && c.ks == KS && c.waves == W && c.pf == PF)                            \
         return launch_cfg<FP8, RT, U, NC, KS, W, PF>(S, dig, sx, k, Kp, batch, s), true;
 #define BE42_DMA(RT, P, W)                                                                                         \
-    if (c.dma && c.rt == RT && c.u == P && c.waves == W)                                                          \
+    if (c.dma == 1 && c.rt == RT && c.u == P && c.waves == W)                                                     \
         return launch_dma<FP8, RT, NC, P, W>(S, dig, sx, k, Kp, batch, s), true;
 
 // The shapes pick_tile returns for each (dtype, NC); false if c is not one.
@@ -658,8 +906,28 @@ static int segs_launch(const GemvSegs &S, const void *buf, int k, int batch, hip
     const size_t dbytes = (size_t)xdig_layout(FP8).nd * batch * Kp;
     const float *sx = (const float *)(dig + ((dbytes + 255) & ~(size_t)255));
     const int nc = (batch * (FP8 ? kF8Digits : kI8Digits) + 15) / 16;
-    const TileCfg c = pick_tile(FP8, nc, S.total, k);
-    bool ok;
+    TileCfg c = pick_tile(FP8, nc, S.total, k);
+    // BE42_GEMV_TILE = "kind,rt,u,ks,waves,pf" forces one launch shape
+    // (kind 0 register path, 1 k_gemv_dma, 3 k_gemv_slab with u = ring
+    // stages, ks = steps per stage, pf = steps per slice)
+    if (const char *e = getenv("BE42_GEMV_TILE")) {
+        TileCfg f{};
+        if (sscanf(e, "%d,%d,%d,%d,%d,%d", &f.dma, &f.rt, &f.u, &f.ks, &f.waves, &f.pf) == 6)
+            c = f;
+    }
+    bool ok = false;
+    if (c.dma == 3) {
+#define BE42_SLAB(RT, SB, KSL, D, W)                                                                               \
+    if (!ok && c.rt == RT && c.ks == SB && c.pf * 128 == KSL && c.u == D && c.waves == W && Kp % KSL == 0) {      \
+        launch_slab<FP8, RT, SB, KSL, D, W>(S, dig, sx, k, Kp, batch, s);                                          \
+        ok = true;                                                                                                 \
+    }
+        BE42_SLAB(4, 1, 512, 4, 8) BE42_SLAB(2, 1, 512, 4, 8) BE42_SLAB(4, 1, 1024, 8, 8)
+#undef BE42_SLAB
+        BE42_CHECK(ok, "be42 gemv: no slab kernel for (%d,%d,%d,%d,%d)", c.rt, c.u, c.ks, c.waves, c.pf);
+        BE42_LAUNCH_CHECK();
+        return BE42_OK;
+    }
     if constexpr (FP8) {
         switch (nc) {
         case 1: ok = launch_tile<true, 1>(c, S, dig, sx, k, Kp, batch, s); break;

@@ -161,3 +161,49 @@ def test_gemv_lds_stream_shapes(be, orc, kind, b):
     s_all = torch.cat([s[1] for s in segs]).contiguous()
     y1 = be.gemv_prepared(w_all, s_all, xdig, b, kind, torch.empty((b, sum(ns)), device="cuda")).cpu().numpy()
     assert rel_err(y1, np.concatenate(wants, axis=1)) <= tight
+
+
+# Launch shapes forced through BE42_GEMV_TILE ("kind,rt,u,ks,waves,pf"):
+# every slab configuration the dispatcher can name, and the direct-to-LDS
+# ones at their column-group count, each run several times on one input.
+FORCED = [
+    ("slab", "3,4,4,1,8,4", None), ("slab", "3,2,4,1,8,4", None), ("slab", "3,4,8,1,8,8", None),
+    ("dma", "1,2,3,0,4,0", ("fp8", 16)), ("dma", "1,1,4,0,4,0", ("fp8", 16)),
+    ("dma", "1,1,5,0,4,0", ("int8", 16)), ("dma", "1,1,3,0,8,0", ("int8", 16)),
+]
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("b", [1, 5, 16])
+@pytest.mark.parametrize("name,tile,only", FORCED)
+def test_gemv_forced_tiles(be, orc, monkeypatch, kind, b, name, tile, only):
+    """Each launch shape against the oracle on a ragged row count with k not
+    a multiple of the 128-byte stage, five times in a row: the results must
+    be identical every time (the direct-to-LDS rings and their barriers
+    leave no read of a slot in flight when it is refilled)."""
+    if only is not None and only != (kind, b):
+        pytest.skip("launch shape instantiated for another column-group count")
+    rng = np.random.default_rng(900 + b)
+    n, k = 20011, 1040
+    if kind == "int8":
+        wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        ws = rng.uniform(0.005, 0.02, n).astype(np.float32)
+    else:
+        wq = rng.integers(0, 256, (n, k), dtype=np.uint8)
+        wq[(wq & 0x7F) == 0x7F] = 0x7E
+        ws = rng.uniform(0.005, 0.02, n).astype(np.float32) / 200.0
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    want = orc.gemv(wq, ws, x, kind)
+    wt, st = torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda()
+    xdig = be.gemv_prepare(torch.from_numpy(x).cuda(), kind)
+    monkeypatch.setenv("BE42_GEMV_TILE", tile)
+    first = None
+    for _ in range(5):
+        y = be.gemv_prepared(wt, st, xdig, b, kind, torch.full((b, n), float("nan"), device="cuda"))
+        y = y.cpu().numpy()
+        if first is None:
+            first = y
+            _check(y, want)
+            assert rel_err(y, want) <= (1e-5 if kind == "int8" else 1e-4)
+        else:
+            assert np.array_equal(y, first)
