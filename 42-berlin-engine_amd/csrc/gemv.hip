@@ -491,6 +491,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
     }
 }
 
+// Partial sums of split-K slab launches, [ks][b][row] floats, added up by a
+// second launch (k_gemv_part_sum).  Shared by every launch on the device, so
+// split-K GEMVs on one device must not run concurrently (one stream).
+constexpr size_t kGemvPartFloats = (size_t)1 << 20;   // 4 MiB
+__device__ float g_gemv_part[kGemvPartFloats];
+
 // Streaming GEMV for many rows (the lm_head) with the digit planes resident in
 // LDS one K-slice at a time.
 // Operand roles are the transpose of k_gemv's: A = one digit plane (16 batch
@@ -510,7 +516,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
 // then tile, then step; the ring runs across tile and slice boundaries.
 template <bool FP8, int RT, int SB, int KSL, int D, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, const uint8_t *__restrict__ dig,
-                                                          const float *__restrict__ sx, int K, int Kp, int B)
+                                                          const float *__restrict__ sx, int K, int Kp, int B,
+                                                          int nsl)
 {
     constexpr int ND = FP8 ? kF8Digits : kI8Digits;
     constexpr int STEPS = KSL / 128;                 // 128-k steps per slice
@@ -530,7 +537,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
     const int row0 = (blockIdx.x * WAVES + wave) * 16 * RT;
-    const int nsl = Kp / KSL;
+    // blockIdx.y = ks: this block covers slices ks*nsl .. ks*nsl + nsl-1 of K
+    const int ks = blockIdx.y, ksplit = gridDim.y;
 
     Acc acc[RT][ND];
 #pragma unroll
@@ -565,7 +573,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
     // KSL * ((s + b) mod nsl) ..), so that at any moment the blocks read
     // spread-out k ranges of their rows rather than all the same one.
     const int sk0 = blockIdx.x % nsl;
-    auto kslice = [&](int s) { return (s + sk0 < nsl ? s + sk0 : s + sk0 - nsl) * KSL; };
+    auto kslice = [&](int s) { return (ks * nsl + (s + sk0 < nsl ? s + sk0 : s + sk0 - nsl)) * KSL; };
     auto issue_slice = [&](int s) {
         uint8_t *buf = lds + (s & 1) * SLB;
         const int kb = kslice(s);
@@ -694,6 +702,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
 
     constexpr double kI8W[3] = {(double)(kI8Base * kI8Base), (double)kI8Base, 1.0};
     const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
+    // one K range's share of y[b][row]; with a K split it goes to the
+    // partial buffer [ks][b][row] instead of y
 #pragma unroll
     for (int t = 0; t < RT; t++) {
         if (!e_y[t])
@@ -715,18 +725,39 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
                     it += (long long)acc[t][d][j] * (long long)kI8W[d];
                 tot = (double)it;
             }
-            e_y[t][(size_t)b * e_n[t]] = (float)(tot * ((double)e_sx[j] * sxw * (double)e_sw[t]));
+            const float v = (float)(tot * ((double)e_sx[j] * sxw * (double)e_sw[t]));
+            if (ksplit == 1)
+                e_y[t][(size_t)b * e_n[t]] = v;
+            else
+                g_gemv_part[((size_t)ks * B + b) * S.total + row0 + t * 16 + r] = v;
         }
     }
 }
 
+// y[b][row] = sum over the K ranges of a split slab launch, in K order.
+__global__ __launch_bounds__(256) void k_gemv_part_sum(const GemvSegs S, int B, int ksplit)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= B * S.total)
+        return;
+    const int b = i / S.total, row = i % S.total;
+    float v = 0.0f;
+    for (int q = 0; q < ksplit; q++)
+        v += g_gemv_part[((size_t)q * B + b) * S.total + row];
+    int local;
+    const int sg = seg_of(S, row, &local);
+    S.y[sg][(size_t)b * S.n[sg] + local] = v;
+}
+
 template <bool FP8, int RT, int SB, int KSL, int D, int WAVES>
-static void launch_slab(const GemvSegs &S, const uint8_t *dig, const float *sx, int k, int Kp, int batch,
+static void launch_slab(const GemvSegs &S, const uint8_t *dig, const float *sx, int k, int Kp, int batch, int ksplit,
                         hipStream_t s)
 {
     const int blocks = (S.total + 16 * RT * WAVES - 1) / (16 * RT * WAVES);
-    hipLaunchKernelGGL((k_gemv_slab<FP8, RT, SB, KSL, D, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, S, dig, sx,
-                       k, Kp, batch);
+    hipLaunchKernelGGL((k_gemv_slab<FP8, RT, SB, KSL, D, WAVES>), dim3(blocks, ksplit), dim3(WAVES * 64), 0, s, S,
+                       dig, sx, k, Kp, batch, Kp / KSL / ksplit);
+    if (ksplit > 1)
+        hipLaunchKernelGGL(k_gemv_part_sum, dim3((batch * S.total + 255) / 256), dim3(256), 0, s, S, batch, ksplit);
 }
 
 template <bool FP8, int RT, int NC, int P, int WAVES>
@@ -809,20 +840,44 @@ static void launch_cfg(const GemvSegs &S, const uint8_t *dig, const float *sx, i
 // splitting K per row group, WAVES per block, PF register double buffering.
 struct TileCfg {
     int rt, u, ks, waves, pf;
-    int dma;   // 1: k_gemv_dma with u = pipeline stages (ks, pf unused); 3: k_gemv_slab
+    int dma;        // 1: k_gemv_dma with u = pipeline stages (ks, pf unused); 3: k_gemv_slab
+    int split = 1;  // k_gemv_slab: K ranges per row range
 };
 constexpr TileCfg dma_tile(int rt, int stages, int waves) { return TileCfg{rt, stages, 0, waves, 0, 1}; }
-constexpr TileCfg slab_tile(int rt, int stages, int waves, int slice_steps)
+constexpr TileCfg slab_tile(int rt, int stages, int waves, int slice_steps, int split = 1)
 {
-    return TileCfg{rt, stages, 1, waves, slice_steps, 3};
+    return TileCfg{rt, stages, 1, waves, slice_steps, 3, split};
 }
 
-static TileCfg pick_tile(bool fp8, int nc, int n, int k)
+// Split-K slab shape for n rows: 128 (or, past 8192 rows, 256) rows per
+// range and the largest split of the 512-byte slices that keeps the grid
+// within 256 blocks and the partials within their buffer; split 0 if none.
+static TileCfg split_slab_tile(int n, int k, int batch, bool fp8)
 {
-    // many rows at 3+ column groups (FP8 batch >= 7, INT8 batch >= 11): the
-    // LDS-resident-digit slab kernel, one block of 8 waves x 4 row tiles
-    if (n > 32768 && nc >= 3)
-        return slab_tile(4, 4, 8, 4);
+    const int rt = n > 8192 ? 2 : 1;
+    const int ranges = (n + 128 * rt - 1) / (128 * rt);
+    const int nsl = (int)(xdig_kp(k, fp8) / 512);
+    for (int d = nsl; d >= 2; d--)
+        if (nsl % d == 0 && ranges * d <= 256 && (size_t)d * batch * n <= kGemvPartFloats)
+            return slab_tile(rt, 4, 8, 4, d);
+    return slab_tile(rt, 4, 8, 4, 0);
+}
+
+static TileCfg pick_tile(bool fp8, int nc, int n, int k, int batch)
+{
+    // 3+ column groups (FP8 batch >= 7, INT8 batch >= 11): the LDS-resident
+    // digit slab kernel; many rows: one block of 8 waves x 4 row tiles per
+    // row range; long rows, or FP8 at 4096 .. 14336 rows: split K, partials
+    // added by a second launch
+    if (nc >= 3) {
+        if (n > 32768)
+            return slab_tile(4, 4, 8, 4);
+        if (k >= 8192 || (fp8 && n >= 4096 && n <= 14336)) {
+            const TileCfg c = split_slab_tile(n, k, batch, fp8);
+            if (c.split > 1)
+                return c;
+        }
+    }
     if (fp8) {
         if (nc == 1) {
             if (n <= 4096)
@@ -906,23 +961,29 @@ static int segs_launch(const GemvSegs &S, const void *buf, int k, int batch, hip
     const size_t dbytes = (size_t)xdig_layout(FP8).nd * batch * Kp;
     const float *sx = (const float *)(dig + ((dbytes + 255) & ~(size_t)255));
     const int nc = (batch * (FP8 ? kF8Digits : kI8Digits) + 15) / 16;
-    TileCfg c = pick_tile(FP8, nc, S.total, k);
-    // BE42_GEMV_TILE = "kind,rt,u,ks,waves,pf" forces one launch shape
-    // (kind 0 register path, 1 k_gemv_dma, 3 k_gemv_slab with u = ring
-    // stages, ks = steps per stage, pf = steps per slice)
+    TileCfg c = pick_tile(FP8, nc, S.total, k, batch);
+    // BE42_GEMV_TILE = "kind,rt,u,ks,waves,pf[,split]" forces one launch
+    // shape (kind 0 register path, 1 k_gemv_dma, 3 k_gemv_slab with u = ring
+    // stages, ks = steps per stage, pf = steps per slice, split = K ranges)
     if (const char *e = getenv("BE42_GEMV_TILE")) {
         TileCfg f{};
-        if (sscanf(e, "%d,%d,%d,%d,%d,%d", &f.dma, &f.rt, &f.u, &f.ks, &f.waves, &f.pf) == 6)
+        const int got = sscanf(e, "%d,%d,%d,%d,%d,%d,%d", &f.dma, &f.rt, &f.u, &f.ks, &f.waves, &f.pf, &f.split);
+        if (got == 6)
+            f.split = 1;
+        if (got >= 6)
             c = f;
     }
     bool ok = false;
     if (c.dma == 3) {
+        BE42_CHECK(c.split >= 1 && c.pf > 0 && Kp % (c.pf * 128 * c.split) == 0 &&
+                       (c.split == 1 || (size_t)c.split * batch * S.total <= kGemvPartFloats),
+                   "be42 gemv: slab split %d does not fit k=%d rows=%d batch=%d", c.split, k, S.total, batch);
 #define BE42_SLAB(RT, SB, KSL, D, W)                                                                               \
-    if (!ok && c.rt == RT && c.ks == SB && c.pf * 128 == KSL && c.u == D && c.waves == W && Kp % KSL == 0) {      \
-        launch_slab<FP8, RT, SB, KSL, D, W>(S, dig, sx, k, Kp, batch, s);                                          \
+    if (!ok && c.rt == RT && c.ks == SB && c.pf * 128 == KSL && c.u == D && c.waves == W) {                       \
+        launch_slab<FP8, RT, SB, KSL, D, W>(S, dig, sx, k, Kp, batch, c.split, s);                                 \
         ok = true;                                                                                                 \
     }
-        BE42_SLAB(4, 1, 512, 4, 8) BE42_SLAB(2, 1, 512, 4, 8) BE42_SLAB(4, 1, 1024, 8, 8)
+        BE42_SLAB(4, 1, 512, 4, 8) BE42_SLAB(2, 1, 512, 4, 8) BE42_SLAB(1, 1, 512, 4, 8) BE42_SLAB(4, 1, 1024, 8, 8)
 #undef BE42_SLAB
         BE42_CHECK(ok, "be42 gemv: no slab kernel for (%d,%d,%d,%d,%d)", c.rt, c.u, c.ks, c.waves, c.pf);
         BE42_LAUNCH_CHECK();

@@ -167,7 +167,9 @@ def test_gemv_lds_stream_shapes(be, orc, kind, b):
 # every slab configuration the dispatcher can name, and the direct-to-LDS
 # ones at their column-group count, each run several times on one input.
 FORCED = [
-    ("slab", "3,4,4,1,8,4", None), ("slab", "3,2,4,1,8,4", None), ("slab", "3,4,8,1,8,8", None),
+    ("slab", "3,4,4,1,8,4", None), ("slab", "3,2,4,1,8,4", None), ("slab", "3,1,4,1,8,4", None),
+    ("slab", "3,4,8,1,8,8", None), ("slab split", "3,1,4,1,8,4,2", None), ("slab split", "3,2,4,1,8,4,2", None),
+    ("slab split", "3,1,4,1,8,4,4", ("fp8", 5)),
     ("dma", "1,2,3,0,4,0", ("fp8", 16)), ("dma", "1,1,4,0,4,0", ("fp8", 16)),
     ("dma", "1,1,5,0,4,0", ("int8", 16)), ("dma", "1,1,3,0,8,0", ("int8", 16)),
 ]
@@ -207,3 +209,30 @@ def test_gemv_forced_tiles(be, orc, monkeypatch, kind, b, name, tile, only):
             assert rel_err(y, want) <= (1e-5 if kind == "int8" else 1e-4)
         else:
             assert np.array_equal(y, first)
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("b", [8, 16])
+def test_gemv_split_k_segments(be, orc, kind, b):
+    """The split-K slab path (partials added by a second launch) on the
+    decode projections of configs[4] at batch 8 / 16: q/k/v as three
+    segments (5120 rows over k = 3072) and the down projection (3072 rows
+    over k = 8192), against the oracle and one launch per matrix."""
+    rng = np.random.default_rng(1200 + b)
+    for ns, k in (((3072, 1024, 1024), 3072), ((3072,), 8192)):
+        x = rng.standard_normal((b, k)).astype(np.float32)
+        xdig = be.gemv_prepare(torch.from_numpy(x).cuda(), kind)
+        segs, wants = [], []
+        for n in ns:
+            w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+            wq, ws = orc.quantize_rows(w, kind)
+            wants.append(orc.gemv(wq, ws, x, kind))
+            segs.append((torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda(),
+                         torch.full((b, n), float("nan"), device="cuda")))
+        outs = be.gemv_prepared_multi(segs, xdig, b, kind)
+        for (wt, st, _), y, want in zip(segs, outs, wants):
+            y = y.cpu().numpy()
+            _check(y, want)
+            assert rel_err(y, want) <= 1e-5
+            one = be.gemv_prepared(wt, st, xdig, b, kind, torch.empty((b, wt.shape[0]), device="cuda"))
+            assert rel_err(one.cpu().numpy(), want) <= 1e-5
