@@ -227,12 +227,22 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
             cnt[4 * kProbes + 1] = min(inc, cap);
     }
     __syncthreads();
-    for (int j = wave; wave < 4 && j < 4 * kProbes; j += 4) {
-        const int off = offs[j];
-        const int *src = list + ((j & 3) * kProbes + (j >> 2)) * cap;
-        const int take = min(min(cnt[(j & 3) * kProbes + (j >> 2)], cap), cap - off);
-        for (int i = lane; i < take; i += kWave)
-            cand[off + i] = src[i];
+    // candidate i belongs to the last list j with offs[j] <= i (lists are
+    // concatenated, empty ones share the next list's offset)
+    {
+        const int tot = cnt[4 * kProbes + 1];
+        for (int i = tid; i < tot; i += blockDim.x) {
+            int lo = 0, hi = 4 * kProbes - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (offs[mid] <= i)
+                    lo = mid;
+                else
+                    hi = mid - 1;
+            }
+            const int j = lo;
+            cand[i] = list[((j & 3) * kProbes + (j >> 2)) * cap + (i - offs[j])];
+        }
     }
     __syncthreads();
     const int total = cnt[4 * kProbes + 1];
