@@ -427,54 +427,45 @@ __device__ __forceinline__ void attn_weights(AttnShared<HD, G, WAVES> &S, int ns
         float *s = S.sc[g];
         const int slot = lane < ns ? (order ? order[lane] : lane) : 0;
         const int nt = lane < ns ? S.pnt[slot] : 0;
-        float lm = -INFINITY;
-        for (int t = 0; t < nt; t++)
-            lm = fmaxf(lm, s[slot * 17 + t]);
-        float inc = lm;
+        // the slot's 16 scores in registers (one LDS round trip)
+        float sv[kPg];
 #pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const float v = __shfl_up(inc, o, kWave);
-            if (lane >= o)
-                inc = fmaxf(inc, v);
-        }
-        float m = __shfl_up(inc, 1, kWave);
-        if (lane == 0)
-            m = -INFINITY;
+        for (int t = 0; t < kPg; t++)
+            sv[t] = s[slot * 17 + t];
+        float lm = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < kPg; t++)
+            if (t < nt)
+                lm = fmaxf(lm, sv[t]);
+        // running max before this slot: exclusive prefix max over the lanes
+        float m = wave_shift_up1(wave_prefix_max(lm), -INFINITY);
         float av[kPg], lprod = 1.0f;
 #pragma unroll
         for (int t = 0; t < kPg; t++) {
             av[t] = 1.0f;
             if (t < nt) {
-                const float st = s[slot * 17 + t];
+                const float st = sv[t];
                 const float mprev = m;
                 m = fmaxf(m, st);
                 const float at = mprev == -INFINITY ? 1.0f : fast_expf(mprev - m);
-                s[slot * 17 + t] = fast_expf(st - m);
+                sv[t] = fast_expf(st - m);
                 av[t] = at;
                 lprod *= at;
             }
         }
-        float suf = lprod;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const float v = __shfl_down(suf, o, kWave);
-            if (lane + o < kWave)
-                suf *= v;
-        }
-        float pr = __shfl_down(suf, 1, kWave);
-        if (lane == kWave - 1)
-            pr = 1.0f;
+        // rescales of all later slots: exclusive suffix product over the lanes
+        float pr = wave_shift_down1(wave_suffix_prod(lprod), 1.0f);
         float ls = 0.0f;
 #pragma unroll
         for (int t = kPg - 1; t >= 0; t--) {
             if (t < nt) {
-                const float w = s[slot * 17 + t] * pr;
+                const float w = sv[t] * pr;
                 s[slot * 17 + t] = w;
                 ls += w;
                 pr *= av[t];
             }
         }
-        ls = wave_sum(ls);
+        ls = wave_sum_dpp(ls);
         if (lane == 0)
             S.lsh[g] = ls;
     }

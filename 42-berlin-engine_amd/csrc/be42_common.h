@@ -112,6 +112,61 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
+// Wave-wide scans with DPP lane moves (no LDS crossbar round trips):
+// row_shr / row_shl steps within each 16-lane row, then row_bcast:15 / :31
+// (or readlane of the row totals) across rows.
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ float dpp_mov(float old, float v)
+{
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWMASK, 0xF, false));
+}
+
+// inclusive prefix max over lanes 0 .. lane
+__device__ __forceinline__ float wave_prefix_max(float v)
+{
+    const float ninf = -INFINITY;
+    v = fmaxf(v, dpp_mov<0x111>(ninf, v));          // row_shr:1
+    v = fmaxf(v, dpp_mov<0x112>(ninf, v));          // row_shr:2
+    v = fmaxf(v, dpp_mov<0x114>(ninf, v));          // row_shr:4
+    v = fmaxf(v, dpp_mov<0x118>(ninf, v));          // row_shr:8
+    v = fmaxf(v, dpp_mov<0x142, 0xA>(ninf, v));     // row_bcast:15 into rows 1, 3
+    v = fmaxf(v, dpp_mov<0x143, 0xC>(ninf, v));     // row_bcast:31 into rows 2, 3
+    return v;
+}
+
+// inclusive suffix product over lanes lane .. 63
+__device__ __forceinline__ float wave_suffix_prod(float v)
+{
+    v = v * dpp_mov<0x101>(1.0f, v);                // row_shl:1
+    v = v * dpp_mov<0x102>(1.0f, v);                // row_shl:2
+    v = v * dpp_mov<0x104>(1.0f, v);                // row_shl:4
+    v = v * dpp_mov<0x108>(1.0f, v);                // row_shl:8
+    // lane 16 r now holds the product of row r
+    const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    const int row = (threadIdx.x & 63) >> 4;
+    const float t23 = t2 * t3;
+    return row == 0 ? v * (t1 * t23) : row == 1 ? v * t23 : row == 2 ? v * t3 : v;
+}
+
+// the value of lane - 1 (fill in lane 0) / of lane + 1 (fill in lane 63)
+__device__ __forceinline__ float wave_shift_up1(float v, float fill) { return dpp_mov<0x138>(fill, v); }
+__device__ __forceinline__ float wave_shift_down1(float v, float fill) { return dpp_mov<0x130>(fill, v); }
+
+// sum over the wave (any order), in every lane
+__device__ __forceinline__ float wave_sum_dpp(float v)
+{
+    v = v + dpp_mov<0x111>(0.0f, v);
+    v = v + dpp_mov<0x112>(0.0f, v);
+    v = v + dpp_mov<0x114>(0.0f, v);
+    v = v + dpp_mov<0x118>(0.0f, v);
+    v = v + dpp_mov<0x142, 0xA>(0.0f, v);
+    v = v + dpp_mov<0x143, 0xC>(0.0f, v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ int wave_sum_i(int v)
 {
 #pragma unroll
