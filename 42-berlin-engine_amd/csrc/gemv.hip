@@ -106,6 +106,39 @@ __device__ __forceinline__ int seg_of(const GemvSegs &S, int row, int *local)
     return sg;
 }
 
+// a[sg] for a lane-varying segment number, by selects over the kernel
+// argument's entries (uniform, so scalar loads): indexing the by-value
+// argument with sg itself costs dependent vector loads from the argument
+// buffer before the first weight load can be addressed.
+// Accesses through global-address-space pointers.  A pointer that went
+// through seg_pick is no longer known to be global, and a plain dereference
+// becomes a flat access, which also counts against the LDS / scalar counter
+// (stage barriers wait on that one to drain) and makes the compiler wait on
+// it early.
+__device__ __forceinline__ float ld_global(const float *p)
+{
+    return *(const __attribute__((address_space(1))) float *)p;
+}
+__device__ __forceinline__ v4i ld_global_v4(const uint8_t *p)
+{
+    return *(const __attribute__((address_space(1))) v4i *)p;
+}
+__device__ __forceinline__ void st_global(float *p, float v) { *(__attribute__((address_space(1))) float *)p = v; }
+
+template <class T>
+__device__ __forceinline__ T seg_pick(const T (&a)[kMaxSegs], int sg)
+{
+    T v = a[0];
+    asm volatile("" : "+s"(v));   // each entry its own scalar value: not re-fused into a[sg]
+#pragma unroll
+    for (int i = 1; i < kMaxSegs; i++) {
+        T ai = a[i];
+        asm volatile("" : "+s"(ai));
+        v = sg == i ? ai : v;
+    }
+    return v;
+}
+
 // Epilogue operands of a lane, loaded at kernel start so their latency hides
 // under the weight stream.  In the epilogue loop over o = lane + 64 j the
 // lane's output row within a tile is always r = lane % 16 and its batch rows
@@ -128,9 +161,9 @@ __device__ __forceinline__ void epi_load(EpiOps<RT> &E, const GemvSegs &S, const
         if (row < S.total) {
             int local;
             const int sg = seg_of(S, row, &local);
-            E.sw[t] = S.sw[sg][local];
-            E.y[t] = S.y[sg] + local;
-            E.n[t] = S.n[sg];
+            E.sw[t] = ld_global(seg_pick(S.sw, sg) + local);
+            E.y[t] = seg_pick(S.y, sg) + local;
+            E.n[t] = seg_pick(S.n, sg);
         } else {
             E.sw[t] = 0.0f;
             E.y[t] = nullptr;
@@ -167,7 +200,7 @@ __device__ __forceinline__ void epi_store(const EpiOps<RT> &E, int t, int g, int
             else
                 tot = tot + dsum * (Tot)(d == 0 ? kI8Base * kI8Base : (d == 1 ? kI8Base : 1));
         }
-        E.y[t][(size_t)bb * E.n[t]] = (float)((double)tot * ((double)E.sx[j] * sxw * (double)E.sw[t]));
+        st_global(E.y[t] + (size_t)bb * E.n[t], (float)((double)tot * ((double)E.sx[j] * sxw * (double)E.sw[t])));
     }
 }
 
@@ -229,7 +262,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(const GemvSegs S, const uin
     for (int t = 0; t < RT; t++) {
         int local;
         const int sg = seg_of(S, min(row0 + t * 16 + r, S.total - 1), &local);
-        wrow[t] = S.w[sg] + (size_t)local * K;
+        wrow[t] = seg_pick(S.w, sg) + (size_t)local * K;
     }
     const uint8_t *xcolp[NC];
 #pragma unroll
@@ -247,7 +280,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv(const GemvSegs S, const uin
             for (int u = 0; u < U; u++)
 #pragma unroll
                 for (int v = 0; v < NV; v++)
-                    wd[t][u][v] = *(const v4i *)(wrow[t] + min(kb + u * STEP + 16 * v, klast));
+                    wd[t][u][v] = ld_global_v4(wrow[t] + min(kb + u * STEP + 16 * v, klast));
 #pragma unroll
         for (int c = 0; c < NC; c++)
 #pragma unroll
@@ -382,7 +415,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
     for (int t = 0; t < RT; t++) {
         int local;
         const int sg = seg_of(S, min(row0 + t * 16 + r, S.total - 1), &local);
-        wrow[t] = S.w[sg] + (size_t)local * K;
+        wrow[t] = seg_pick(S.w, sg) + (size_t)local * K;
     }
     const int klast = K - 16;
     // weight load v of a tile: FP8 bytes 32g + 16v (one MFMA step, two loads);
@@ -552,10 +585,33 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
     for (int t = 0; t < RT; t++) {
         int local;
         const int sg = seg_of(S, min(row0 + t * 16 + r, S.total - 1), &local);
-        wrow[t] = S.w[sg] + (size_t)local * K;
+        wrow[t] = seg_pick(S.w, sg) + (size_t)local * K;
     }
     const int klast = K - 16;
     const int woff0 = FP8 ? 32 * g : 16 * g, woff1 = FP8 ? 32 * g + 16 : 64 + 16 * g;
+
+    // epilogue operands, loaded up front and without branches (rows and
+    // batch rows past the end read the last one and are masked): fetched
+    // after the last weight stage, their loads would add a few microseconds
+    // to every block
+    float e_sw[RT], e_sx[4];
+    float *e_y[RT];
+    int e_n[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const int row = row0 + t * 16 + r;
+        const bool in = row < S.total;
+        int local;
+        const int sg = seg_of(S, in ? row : S.total - 1, &local);
+        e_sw[t] = ld_global(seg_pick(S.sw, sg) + local);
+        e_y[t] = in ? seg_pick(S.y, sg) + local : nullptr;
+        e_n[t] = seg_pick(S.n, sg);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float v = ld_global(sx + min(4 * g + j, B - 1));
+        e_sx[j] = 4 * g + j < B ? v : 0.0f;
+    }
 
     // slice loads: load j of a slice carries plane d, step st, half h; lane
     // l brings batch row l % 16 (clamped to the batch), piece l / 16 + 4h
@@ -594,8 +650,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
         const int kb = kslice(s) + q * SB * 128;
 #pragma unroll
         for (int u = 0; u < SB; u++) {
-            const v4i lo = *(const v4i *)(wrow[t] + min(kb + u * 128 + woff0, klast));
-            const v4i hi = *(const v4i *)(wrow[t] + min(kb + u * 128 + woff1, klast));
+            const v4i lo = ld_global_v4(wrow[t] + min(kb + u * 128 + woff0, klast));
+            const v4i hi = ld_global_v4(wrow[t] + min(kb + u * 128 + woff1, klast));
             w[u] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
         asm volatile("" ::: "memory");
@@ -678,28 +734,6 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
     }
     wait_vmcnt<0>();
 
-    // epilogue operands
-    float e_sw[RT], e_sx[4];
-    float *e_y[RT];
-    int e_n[RT];
-#pragma unroll
-    for (int t = 0; t < RT; t++) {
-        const int row = row0 + t * 16 + r;
-        e_y[t] = nullptr;
-        e_sw[t] = 0.0f;
-        e_n[t] = 0;
-        if (row < S.total) {
-            int local;
-            const int sg = seg_of(S, row, &local);
-            e_sw[t] = S.sw[sg][local];
-            e_y[t] = S.y[sg] + local;
-            e_n[t] = S.n[sg];
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-        e_sx[j] = 4 * g + j < B ? sx[4 * g + j] : 0.0f;
-
     constexpr double kI8W[3] = {(double)(kI8Base * kI8Base), (double)kI8Base, 1.0};
     const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
     // one K range's share of y[b][row]; with a K split it goes to the
@@ -727,7 +761,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
             }
             const float v = (float)(tot * ((double)e_sx[j] * sxw * (double)e_sw[t]));
             if (ksplit == 1)
-                e_y[t][(size_t)b * e_n[t]] = v;
+                st_global(e_y[t] + (size_t)b * e_n[t], v);
             else
                 g_gemv_part[((size_t)ks * B + b) * S.total + row0 + t * 16 + r] = v;
         }
@@ -746,7 +780,7 @@ __global__ __launch_bounds__(256) void k_gemv_part_sum(const GemvSegs S, int B, 
         v += g_gemv_part[((size_t)q * B + b) * S.total + row];
     int local;
     const int sg = seg_of(S, row, &local);
-    S.y[sg][(size_t)b * S.n[sg] + local] = v;
+    st_global(seg_pick(S.y, sg) + (size_t)b * seg_pick(S.n, sg) + local, v);
 }
 
 template <bool FP8, int RT, int SB, int KSL, int D, int WAVES>
@@ -844,14 +878,15 @@ struct TileCfg {
     int split = 1;  // k_gemv_slab: K ranges per row range
 };
 constexpr TileCfg dma_tile(int rt, int stages, int waves) { return TileCfg{rt, stages, 0, waves, 0, 1}; }
-constexpr TileCfg slab_tile(int rt, int stages, int waves, int slice_steps, int split = 1)
+constexpr TileCfg slab_tile(int rt, int stages, int steps, int waves, int slice_steps, int split = 1)
 {
-    return TileCfg{rt, stages, 1, waves, slice_steps, 3, split};
+    return TileCfg{rt, stages, steps, waves, slice_steps, 3, split};
 }
 
-// Split-K slab shape for n rows: 128 (or, past 8192 rows, 256) rows per
-// range and the largest split of the 512-byte slices that keeps the grid
-// within 256 blocks and the partials within their buffer; split 0 if none.
+// Split-K slab shape for n rows: 128 rows per range with 256-byte ring
+// stages (or, past 8192 rows, 256 rows with 512-byte stages) and the largest
+// split of the 512-byte slices that keeps the grid within 256 blocks and the
+// partials within their buffer; split 0 if none.
 static TileCfg split_slab_tile(int n, int k, int batch, bool fp8)
 {
     const int rt = n > 8192 ? 2 : 1;
@@ -859,19 +894,19 @@ static TileCfg split_slab_tile(int n, int k, int batch, bool fp8)
     const int nsl = (int)(xdig_kp(k, fp8) / 512);
     for (int d = nsl; d >= 2; d--)
         if (nsl % d == 0 && ranges * d <= 256 && (size_t)d * batch * n <= kGemvPartFloats)
-            return slab_tile(rt, 4, 8, 4, d);
-    return slab_tile(rt, 4, 8, 4, 0);
+            return slab_tile(rt, 2, 2 * rt, 8, 4, d);
+    return slab_tile(rt, 2, 2 * rt, 8, 4, 0);
 }
 
 static TileCfg pick_tile(bool fp8, int nc, int n, int k, int batch)
 {
     // 3+ column groups (FP8 batch >= 7, INT8 batch >= 11): the LDS-resident
     // digit slab kernel; many rows: one block of 8 waves x 4 row tiles per
-    // row range; long rows, or FP8 at 4096 .. 14336 rows: split K, partials
-    // added by a second launch
+    // row range, each ring stage 16 rows x 512 contiguous bytes; long rows,
+    // or FP8 at 4096 .. 14336 rows: split K, partials added by a second launch
     if (nc >= 3) {
         if (n > 32768)
-            return slab_tile(4, 4, 8, 4);
+            return slab_tile(4, 2, 4, 8, 4);
         if (k >= 8192 || (fp8 && n >= 4096 && n <= 14336)) {
             const TileCfg c = split_slab_tile(n, k, batch, fp8);
             if (c.split > 1)
@@ -983,7 +1018,8 @@ static int segs_launch(const GemvSegs &S, const void *buf, int k, int batch, hip
         launch_slab<FP8, RT, SB, KSL, D, W>(S, dig, sx, k, Kp, batch, c.split, s);                                 \
         ok = true;                                                                                                 \
     }
-        BE42_SLAB(4, 1, 512, 4, 8) BE42_SLAB(2, 1, 512, 4, 8) BE42_SLAB(1, 1, 512, 4, 8) BE42_SLAB(4, 1, 1024, 8, 8)
+        BE42_SLAB(4, 4, 512, 2, 8) BE42_SLAB(2, 4, 512, 2, 8) BE42_SLAB(1, 2, 512, 2, 8) BE42_SLAB(4, 1, 512, 4, 8)
+        BE42_SLAB(2, 1, 512, 4, 8) BE42_SLAB(1, 1, 512, 4, 8)
 #undef BE42_SLAB
         BE42_CHECK(ok, "be42 gemv: no slab kernel for (%d,%d,%d,%d,%d)", c.rt, c.u, c.ks, c.waves, c.pf);
         BE42_LAUNCH_CHECK();

@@ -167,9 +167,10 @@ def test_gemv_lds_stream_shapes(be, orc, kind, b):
 # every slab configuration the dispatcher can name, and the direct-to-LDS
 # ones at their column-group count, each run several times on one input.
 FORCED = [
+    ("slab", "3,4,2,4,8,4", None), ("slab", "3,2,2,4,8,4", None), ("slab", "3,1,2,2,8,4", None),
     ("slab", "3,4,4,1,8,4", None), ("slab", "3,2,4,1,8,4", None), ("slab", "3,1,4,1,8,4", None),
-    ("slab", "3,4,8,1,8,8", None), ("slab split", "3,1,4,1,8,4,2", None), ("slab split", "3,2,4,1,8,4,2", None),
-    ("slab split", "3,1,4,1,8,4,4", ("fp8", 5)),
+    ("slab split", "3,1,2,2,8,4,2", None), ("slab split", "3,2,2,4,8,4,2", None),
+    ("slab split", "3,1,4,1,8,4,2", None), ("slab split", "3,1,2,2,8,4,4", ("fp8", 5)),
     ("dma", "1,2,3,0,4,0", ("fp8", 16)), ("dma", "1,1,4,0,4,0", ("fp8", 16)),
     ("dma", "1,1,5,0,4,0", ("int8", 16)), ("dma", "1,1,3,0,8,0", ("int8", 16)),
 ]
