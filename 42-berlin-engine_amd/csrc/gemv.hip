@@ -95,15 +95,13 @@ struct GemvSegs {
 
 __device__ __forceinline__ int seg_of(const GemvSegs &S, int row, int *local)
 {
-    int sg = 0, r = row;
-#pragma unroll
-    for (int i = 0; i < kMaxSegs - 1; i++)
-        if (sg == i && i + 1 < S.nseg && r >= S.n[i]) {
-            r -= S.n[i];
-            sg = i + 1;
-        }
-    *local = r;
-    return sg;
+    static_assert(kMaxSegs == 3, "segment lookup written for three segments");
+    // branch-free: the segment ends are uniform, the row is per lane
+    const int e1 = S.n[0], e2 = S.n[0] + S.n[1];
+    const bool s1 = S.nseg > 1 && row >= e1;
+    const bool s2 = S.nseg > 2 && row >= e2;
+    *local = row - (s2 ? e2 : (s1 ? e1 : 0));
+    return (int)s1 + (int)s2;
 }
 
 // a[sg] for a lane-varying segment number, by selects over the kernel
@@ -783,6 +781,217 @@ __global__ __launch_bounds__(256) void k_gemv_part_sum(const GemvSegs S, int B, 
     st_global(seg_pick(S.y, sg) + (size_t)b * seg_pick(S.n, sg) + local, v);
 }
 
+// Block-cooperative streaming GEMV for many rows.
+// The 8 waves of a block read the same 16-row tile at the same time, wave w
+// taking its own SPW 128-byte steps of k, so that a block streams whole
+// 16-row x K regions (16 KiB .. 64 KiB of consecutive rows) one after
+// another: the DRAM pages of a region are read together, with every load
+// instruction covering whole 128-byte lines of 8 rows and the non-temporal
+// hint.  Loads go straight to LDS (global_load_lds), into a ring of D stages
+// per wave (a stage is 16 rows x 128 bytes); the matrix operands are read
+// back from LDS in the MFMA lane layout.  A wave's k range of the activation
+// digits stays in registers for the whole launch (A operand: batch row r,
+// k bytes 32g .. 32g+31 of the step for FP8; 16g .. and 64+16g .. for INT8),
+// so the block never re-reads them.  At the end of a tile each wave combines
+// its digit sums into one partial per (row, batch row) -- exact int64 for
+// INT8, fp64 for FP8 -- and after a barrier every wave adds up 32 of the
+// tile's 256 outputs over the 8 partials, in wave order, and writes y (or
+// the split-K partial).
+// Blocks cover tpb consecutive tiles; blockIdx.y selects a k range of a
+// split launch.
+constexpr int kCoopWaves = 8;
+constexpr int kCoopMaxTiles = 64;                // tiles per block (their weight scales sit in LDS)
+constexpr int kCoopHalf = 1040;                  // 8 rows x 128 bytes, + 16-byte pad
+constexpr int kCoopSlot = 2 * kCoopHalf;         // one stage: 16 rows x 128 bytes
+
+// LDS position of 16-byte chunk c of row rr (0..7 within a half): rows two
+// apart rotate their chunks by two, so that the 16 rows of an operand read
+// land in 16 different 16-byte bank groups (the pad shifts the second half)
+__device__ __forceinline__ int coop_pos(int c, int rr) { return (c + 2 * (rr >> 1)) & 7; }
+
+// LDS reads of this wave have completed, and the barrier leaves loads in
+// flight alone (a workgroup barrier from the language would drain them)
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <bool FP8, int SPW, int D>
+__global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S, const uint8_t *__restrict__ dig,
+                                                               const float *__restrict__ sx, int K, int Kp, int B,
+                                                               int tpb)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    static_assert(D >= 2 && (D - 1) * 2 < 64, "ring");
+    using Acc = typename std::conditional<FP8, v4f, v4i>::type;
+    using Tot = typename std::conditional<FP8, double, long long>::type;
+    __shared__ __align__(16) uint8_t ring[kCoopWaves * D * kCoopSlot];
+    __shared__ __align__(16) Tot red[2][kCoopWaves][64][4];
+    __shared__ float lsw[kCoopMaxTiles * 16];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
+    const int ks = blockIdx.y, ksplit = gridDim.y;
+    const int ntile = (S.total + 15) >> 4;
+    const int tile0 = blockIdx.x * tpb;
+    const int nst = tpb * SPW;
+    // first 128-byte step of k of this wave: the k ranges rotate with the
+    // block, so that at the start the blocks' waves do not all read the same
+    // digits at once
+    const int step0 = (ks * kCoopWaves + ((wave + blockIdx.x) & (kCoopWaves - 1))) * SPW;
+    const int klast = K - 16;
+    uint8_t *myring = ring + wave * D * kCoopSlot;
+
+    // stage i: tile i / SPW, step i % SPW, ring slot i % D; stages past the
+    // end load the last one again (into a free slot) so that every
+    // iteration keeps the same number of loads in flight
+    const int drr = lane >> 3;
+    const int dc = ((lane & 7) - 2 * (drr >> 1)) & 7;    // chunk this lane brings (inverse of coop_pos)
+    auto issue = [&](int i) {
+        const int ic = min(i, nst - 1);
+        const int t = ic / SPW, q = ic - t * SPW;
+        const int tile = min(tile0 + t, ntile - 1);
+        const int kb = min((step0 + q) * 128 + 16 * dc, klast);
+        uint8_t *dst = myring + (i % D) * kCoopSlot;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int local;
+            const int sg = seg_of(S, min(tile * 16 + 8 * h + drr, S.total - 1), &local);
+            const uint8_t *src = seg_pick(S.w, sg) + (size_t)local * K + kb;
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(dst + h * kCoopHalf), 16, 0, 2);
+        }
+        asm volatile("" ::: "memory");
+    };
+    // ring prologue first, so that weights stream while the digits load
+#pragma unroll
+    for (int j = 0; j < D - 1; j++)
+        issue(j);
+
+    // this wave's k range of the digits, kept for the whole launch
+    v8i a[SPW][ND];
+    {
+        const int b = min(r, B - 1);
+#pragma unroll
+        for (int q = 0; q < SPW; q++)
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                const uint8_t *p = dig + ((size_t)d * B + b) * Kp + (size_t)(step0 + q) * 128;
+                const v4i lo = ld_global_v4(p + (FP8 ? 32 * g : 16 * g));
+                const v4i hi = ld_global_v4(p + (FP8 ? 32 * g + 16 : 64 + 16 * g));
+                a[q][d] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+    }
+    // the output this lane adds up at the end of every tile (lanes < 32):
+    // number o = 32 * wave + lane, held by lane o / 4 of each wave
+    const int o_src = (32 * wave + lane) >> 2, o_j = lane & 3;
+    const int o_r = o_src & 15, o_b = 4 * (o_src >> 4) + o_j;
+    const double o_sx = (double)ld_global(sx + min(o_b, B - 1)) * (FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base));
+    // weight scales of the block's rows, staged in LDS before the loop: a
+    // plain load inside it would make the compiler wait for every load in
+    // flight (it cannot count plain loads apart from the ones into LDS);
+    // the first tile's barrier publishes them
+    for (int i = threadIdx.x; i < tpb * 16; i += kCoopWaves * 64) {
+        int local;
+        const int sg = seg_of(S, min(tile0 * 16 + i, S.total - 1), &local);
+        lsw[i] = ld_global(seg_pick(S.sw, sg) + local);
+    }
+
+    Acc acc[ND];
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+        acc[d] = Acc{0, 0, 0, 0};
+    const int rr = r & 7;
+    const int roff = (r >> 3) * kCoopHalf + rr * 128;
+    const int p0 = coop_pos(FP8 ? 2 * g : g, rr) * 16, p1 = coop_pos(FP8 ? 2 * g + 1 : 4 + g, rr) * 16;
+
+    constexpr long long kI8W[3] = {(long long)kI8Base * kI8Base, (long long)kI8Base, 1};
+    for (int t = 0; t < tpb; t++) {
+#pragma unroll
+        for (int q = 0; q < SPW; q++) {
+            const int i = t * SPW + q;
+            // the slot refilled next was read by stage i - 1, whose reads
+            // have returned (the matrix instructions used them)
+            issue(i + D - 1);
+            wait_vmcnt<(D - 1) * 2>();
+            asm volatile("" ::: "memory");
+            // operand reads as inline assembly: the compiler cannot tell the
+            // slot apart from the ones still being filled, and would wait for
+            // every load in flight before an LDS read it knows of
+            const uint32_t base = (uint32_t)(uintptr_t)(myring + (i % D) * kCoopSlot + roff);
+            v4i w0, w1;
+            asm volatile("ds_read_b128 %0, %1" : "=v"(w0) : "v"(base + p0));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(w1) : "v"(base + p1));
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w0), "+v"(w1));
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                if constexpr (FP8) {
+                    const v8i w = __builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7);
+                    acc[d] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[q][d], w, acc[d], 0, 0, 0, 127, 0,
+                                                                              127);
+                } else {
+                    const v4i a0 = __builtin_shufflevector(a[q][d], a[q][d], 0, 1, 2, 3);
+                    const v4i a1 = __builtin_shufflevector(a[q][d], a[q][d], 4, 5, 6, 7);
+                    acc[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0, acc[d], 0, 0, 0);
+                    acc[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1, acc[d], 0, 0, 0);
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        // this wave's share of the tile: digit sums combined per output
+        Tot *mine = &red[t & 1][wave][lane][0];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            Tot v = 0;
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                if constexpr (FP8)
+                    v += (double)acc[d][j] * kF8Weight[d];
+                else
+                    v += (long long)acc[d][j] * kI8W[d];
+            }
+            mine[j] = v;
+        }
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+            acc[d] = Acc{0, 0, 0, 0};
+        lds_barrier();
+        // the 256 outputs of the tile, 32 per wave: lane l < 32 of wave w
+        // adds up output 32w + l (held by lane o / 4, batch row 4g + o % 4 of
+        // that lane) over the 8 waves, in wave order
+        if (lane < 32) {
+            Tot tot = 0;
+#pragma unroll
+            for (int w = 0; w < kCoopWaves; w++)
+                tot += red[t & 1][w][o_src][o_j];
+            const int row = (tile0 + t) * 16 + o_r;
+            if (tile0 + t < ntile && row < S.total && o_b < B) {
+                // y[b][local] of the row's segment, or the partial [ks][b][row]
+                int local;
+                const int sg = seg_of(S, row, &local);
+                float *dst = ksplit == 1 ? seg_pick(S.y, sg) + (size_t)o_b * seg_pick(S.n, sg) + local
+                                         : g_gemv_part + ((size_t)ks * B + o_b) * S.total + row;
+                st_global(dst, (float)((double)tot * o_sx * (double)lsw[t * 16 + o_r]));
+            }
+        }
+    }
+    wait_vmcnt<0>();
+}
+
+template <bool FP8, int SPW, int D>
+static void launch_coop(const GemvSegs &S, const uint8_t *dig, const float *sx, int k, int Kp, int batch, int ksplit,
+                        int tpb, hipStream_t s)
+{
+    const int ntile = (S.total + 15) / 16;
+    const int blocks = (ntile + tpb - 1) / tpb;
+    hipLaunchKernelGGL((k_gemv_coop<FP8, SPW, D>), dim3(blocks, ksplit), dim3(kCoopWaves * 64), 0, s, S, dig, sx, k,
+                       Kp, batch, tpb);
+    if (ksplit > 1)
+        hipLaunchKernelGGL(k_gemv_part_sum, dim3((batch * S.total + 255) / 256), dim3(256), 0, s, S, batch, ksplit);
+}
+
 template <bool FP8, int RT, int SB, int KSL, int D, int WAVES>
 static void launch_slab(const GemvSegs &S, const uint8_t *dig, const float *sx, int k, int Kp, int batch, int ksplit,
                         hipStream_t s)
@@ -905,8 +1114,14 @@ static TileCfg pick_tile(bool fp8, int nc, int n, int k, int batch)
     // row range, each ring stage 16 rows x 512 contiguous bytes; long rows,
     // or FP8 at 4096 .. 14336 rows: split K, partials added by a second launch
     if (nc >= 3) {
-        if (n > 32768)
+        if (n > 32768) {
+            // block-cooperative kernel when k splits into 8 wave ranges of
+            // at most 4 steps (k <= 4096), else the slab kernel
+            const int steps = (int)(xdig_kp(k, fp8) / 128);
+            if (steps % kCoopWaves == 0 && steps / kCoopWaves <= 4)
+                return TileCfg{0, 6, 0, kCoopWaves, 0, 4, 1};
             return slab_tile(4, 2, 4, 8, 4);
+        }
         if (k >= 8192 || (fp8 && n >= 4096 && n <= 14336)) {
             const TileCfg c = split_slab_tile(n, k, batch, fp8);
             if (c.split > 1)
@@ -999,7 +1214,8 @@ static int segs_launch(const GemvSegs &S, const void *buf, int k, int batch, hip
     TileCfg c = pick_tile(FP8, nc, S.total, k, batch);
     // BE42_GEMV_TILE = "kind,rt,u,ks,waves,pf[,split]" forces one launch
     // shape (kind 0 register path, 1 k_gemv_dma, 3 k_gemv_slab with u = ring
-    // stages, ks = steps per stage, pf = steps per slice, split = K ranges)
+    // stages, ks = steps per stage, pf = steps per slice, split = K ranges;
+    // 4 k_gemv_coop with pf = tiles per block, 0 for the default)
     if (const char *e = getenv("BE42_GEMV_TILE")) {
         TileCfg f{};
         const int got = sscanf(e, "%d,%d,%d,%d,%d,%d,%d", &f.dma, &f.rt, &f.u, &f.ks, &f.waves, &f.pf, &f.split);
@@ -1009,6 +1225,26 @@ static int segs_launch(const GemvSegs &S, const void *buf, int k, int batch, hip
             c = f;
     }
     bool ok = false;
+    if (c.dma == 4) {
+        const int steps = Kp / 128;
+        BE42_CHECK(c.split >= 1 && steps % (kCoopWaves * c.split) == 0 && steps / (kCoopWaves * c.split) <= 4 &&
+                       (c.split == 1 || (size_t)c.split * batch * S.total <= kGemvPartFloats),
+                   "be42 gemv: cooperative split %d does not fit k=%d rows=%d batch=%d", c.split, k, S.total, batch);
+        const int spw = steps / (kCoopWaves * c.split);
+        const int ntile = (S.total + 15) / 16;
+        // tiles per block: about 256 blocks in all, unless forced (pf)
+        const int tpb = c.pf > 0 ? c.pf : std::max(1, (ntile * c.split + 255) / 256);
+        BE42_CHECK(tpb <= kCoopMaxTiles, "be42 gemv: %d tiles per block exceed %d (rows=%d)", tpb, kCoopMaxTiles,
+                   S.total);
+        switch (spw) {
+        case 1: launch_coop<FP8, 1, 6>(S, dig, sx, k, Kp, batch, c.split, tpb, s); break;
+        case 2: launch_coop<FP8, 2, 6>(S, dig, sx, k, Kp, batch, c.split, tpb, s); break;
+        case 3: launch_coop<FP8, 3, 6>(S, dig, sx, k, Kp, batch, c.split, tpb, s); break;
+        default: launch_coop<FP8, 4, 6>(S, dig, sx, k, Kp, batch, c.split, tpb, s); break;
+        }
+        BE42_LAUNCH_CHECK();
+        return BE42_OK;
+    }
     if (c.dma == 3) {
         BE42_CHECK(c.split >= 1 && c.pf > 0 && Kp % (c.pf * 128 * c.split) == 0 &&
                        (c.split == 1 || (size_t)c.split * batch * S.total <= kGemvPartFloats),

@@ -659,7 +659,7 @@ def main():
         torch.cuda.synchronize()
         dm = e0.elapsed_time(e1) / reps
         achieved = dnb / (dm * 1e-3) / 1e9
-        kname = "be42::k_gemv_slab (%s)" % dc["kind"]
+        kname = "be42::k_gemv_coop (%s)" % dc["kind"]
         out = {
             "metric": "decode tokens/s; quant GEMV HBM GB/s (% of peak); LSH attn µs/token @32k",
             "value": round(value, 1),

@@ -171,6 +171,7 @@ FORCED = [
     ("slab", "3,4,4,1,8,4", None), ("slab", "3,2,4,1,8,4", None), ("slab", "3,1,4,1,8,4", None),
     ("slab split", "3,1,2,2,8,4,2", None), ("slab split", "3,2,2,4,8,4,2", None),
     ("slab split", "3,1,4,1,8,4,2", None), ("slab split", "3,1,2,2,8,4,4", ("fp8", 5)),
+    ("coop", "4,0,6,0,8,0", None), ("coop", "4,0,6,0,8,1", None), ("coop split", "4,0,6,0,8,0,2", None),
     ("dma", "1,2,3,0,4,0", ("fp8", 16)), ("dma", "1,1,4,0,4,0", ("fp8", 16)),
     ("dma", "1,1,5,0,4,0", ("int8", 16)), ("dma", "1,1,3,0,8,0", ("int8", 16)),
 ]
@@ -237,3 +238,32 @@ def test_gemv_split_k_segments(be, orc, kind, b):
             assert rel_err(y, want) <= 1e-5
             one = be.gemv_prepared(wt, st, xdig, b, kind, torch.empty((b, wt.shape[0]), device="cuda"))
             assert rel_err(one.cpu().numpy(), want) <= 1e-5
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("b", [7, 16])
+def test_gemv_coop_segments(be, orc, monkeypatch, kind, b):
+    """The block-cooperative kernel over three segments whose boundaries fall
+    inside 16-row tiles (rows 3000 / 1000 / 1100 over k = 3072, three steps of
+    k per wave) and, split in two k ranges, over k = 8192 (four steps per
+    wave), against the oracle; then a row count that is not a multiple of 16
+    with forced tiles per block."""
+    rng = np.random.default_rng(1300 + b)
+    cases = (((3000, 1000, 1100), 3072, "4,0,6,0,8,0"), ((3000,), 8192, "4,0,6,0,8,0,2"),
+             ((4099,), 4096, "4,0,6,0,8,3"))
+    for ns, k, tile in cases:
+        monkeypatch.setenv("BE42_GEMV_TILE", tile)
+        x = rng.standard_normal((b, k)).astype(np.float32)
+        xdig = be.gemv_prepare(torch.from_numpy(x).cuda(), kind)
+        segs, wants = [], []
+        for n in ns:
+            w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+            wq, ws = orc.quantize_rows(w, kind)
+            wants.append(orc.gemv(wq, ws, x, kind))
+            segs.append((torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda(),
+                         torch.full((b, n), float("nan"), device="cuda")))
+        outs = be.gemv_prepared_multi(segs, xdig, b, kind)
+        for y, want in zip(outs, wants):
+            y = y.cpu().numpy()
+            _check(y, want)
+            assert rel_err(y, want) <= (1e-5 if kind == "int8" else 1e-4)
