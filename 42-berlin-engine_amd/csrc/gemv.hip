@@ -796,7 +796,8 @@ __global__ __launch_bounds__(256) void k_gemv_part_sum(const GemvSegs S, int B, 
 // its digit sums into one partial per (row, batch row) -- exact int64 for
 // INT8, fp64 for FP8 -- and after a barrier every wave adds up 32 of the
 // tile's 256 outputs over the 8 partials, in wave order, and writes y (or
-// the split-K partial).
+// the split-K partial).  Partials are double buffered (tile parity), with a
+// third buffer for tile 0, which is added up after tile 1's barrier.
 // Blocks cover tpb consecutive tiles; blockIdx.y selects a k range of a
 // split launch.
 constexpr int kCoopWaves = 8;
@@ -829,7 +830,7 @@ __global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S,
     using Acc = typename std::conditional<FP8, v4f, v4i>::type;
     using Tot = typename std::conditional<FP8, double, long long>::type;
     __shared__ __align__(16) uint8_t ring[kCoopWaves * D * kCoopSlot];
-    __shared__ __align__(16) Tot red[2][kCoopWaves][64][4];
+    __shared__ __align__(16) Tot red[3][kCoopWaves][64][4];
     __shared__ float lsw[kCoopMaxTiles * 16];
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -888,7 +889,7 @@ __global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S,
     // number o = 32 * wave + lane, held by lane o / 4 of each wave
     const int o_src = (32 * wave + lane) >> 2, o_j = lane & 3;
     const int o_r = o_src & 15, o_b = 4 * (o_src >> 4) + o_j;
-    const double o_sx = (double)ld_global(sx + min(o_b, B - 1)) * (FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base));
+    double o_sx = (double)ld_global(sx + min(o_b, B - 1)) * (FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base));
     // weight scales of the block's rows, staged in LDS before the loop: a
     // plain load inside it would make the compiler wait for every load in
     // flight (it cannot count plain loads apart from the ones into LDS);
@@ -898,6 +899,9 @@ __global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S,
         const int sg = seg_of(S, min(tile0 * 16 + i, S.total - 1), &local);
         lsw[i] = ld_global(seg_pick(S.sw, sg) + local);
     }
+    // the batch scale converted here, not next to its first use in the loop
+    // (where the compiler would wait for every load in flight first)
+    asm volatile("" : "+v"(o_sx));
 
     Acc acc[ND];
 #pragma unroll
@@ -908,6 +912,26 @@ __global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S,
     const int p0 = coop_pos(FP8 ? 2 * g : g, rr) * 16, p1 = coop_pos(FP8 ? 2 * g + 1 : 4 + g, rr) * 16;
 
     constexpr long long kI8W[3] = {(long long)kI8Base * kI8Base, (long long)kI8Base, 1};
+    // the 256 outputs of tile t, 32 per wave: lane l < 32 of wave w adds up
+    // output 32w + l (held by lane o / 4, batch row 4g + o % 4 of that lane)
+    // over the 8 waves' partials in buffer buf, in wave order
+    auto reduce_tile = [&](int t, int buf) {
+        if (lane < 32) {
+            Tot tot = 0;
+#pragma unroll
+            for (int w = 0; w < kCoopWaves; w++)
+                tot += red[buf][w][o_src][o_j];
+            const int row = (tile0 + t) * 16 + o_r;
+            if (tile0 + t < ntile && row < S.total && o_b < B) {
+                // y[b][local] of the row's segment, or the partial [ks][b][row]
+                int local;
+                const int sg = seg_of(S, row, &local);
+                float *dst = ksplit == 1 ? seg_pick(S.y, sg) + (size_t)o_b * seg_pick(S.n, sg) + local
+                                         : g_gemv_part + ((size_t)ks * B + o_b) * S.total + row;
+                st_global(dst, (float)((double)tot * o_sx * (double)lsw[t * 16 + o_r]));
+            }
+        }
+    };
     for (int t = 0; t < tpb; t++) {
 #pragma unroll
         for (int q = 0; q < SPW; q++) {
@@ -940,8 +964,13 @@ __global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S,
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
-        // this wave's share of the tile: digit sums combined per output
-        Tot *mine = &red[t & 1][wave][lane][0];
+        // this wave's share of the tile: digit sums combined per output.
+        // Tile 0 goes to a third buffer and is added up together with tile
+        // 1 after the second barrier: the waves start unevenly (each first
+        // waits for its k range of the digits), and the first tile then
+        // needs no barrier of its own.
+        const int buf = t == 0 ? 2 : (t & 1);
+        Tot *mine = &red[buf][wave][lane][0];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             Tot v = 0;
@@ -957,25 +986,12 @@ __global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S,
 #pragma unroll
         for (int d = 0; d < ND; d++)
             acc[d] = Acc{0, 0, 0, 0};
+        if (t == 0 && tpb > 1)
+            continue;
         lds_barrier();
-        // the 256 outputs of the tile, 32 per wave: lane l < 32 of wave w
-        // adds up output 32w + l (held by lane o / 4, batch row 4g + o % 4 of
-        // that lane) over the 8 waves, in wave order
-        if (lane < 32) {
-            Tot tot = 0;
-#pragma unroll
-            for (int w = 0; w < kCoopWaves; w++)
-                tot += red[t & 1][w][o_src][o_j];
-            const int row = (tile0 + t) * 16 + o_r;
-            if (tile0 + t < ntile && row < S.total && o_b < B) {
-                // y[b][local] of the row's segment, or the partial [ks][b][row]
-                int local;
-                const int sg = seg_of(S, row, &local);
-                float *dst = ksplit == 1 ? seg_pick(S.y, sg) + (size_t)o_b * seg_pick(S.n, sg) + local
-                                         : g_gemv_part + ((size_t)ks * B + o_b) * S.total + row;
-                st_global(dst, (float)((double)tot * o_sx * (double)lsw[t * 16 + o_r]));
-            }
-        }
+        if (t == 1)
+            reduce_tile(0, 2);
+        reduce_tile(t, buf);
     }
     wait_vmcnt<0>();
 }
