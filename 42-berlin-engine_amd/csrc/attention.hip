@@ -288,6 +288,20 @@ struct RawRow {
     using T = typename std::conditional<BF16, uint4, uint2>::type;
 };
 
+// K / V rows are read once per step: non-temporal loads (each wave
+// instruction covers whole 128-byte lines of 4 consecutive rows)
+__device__ __forceinline__ uint4 ld_row_nt(const uint16_t *p)
+{
+    const v4i v = __builtin_nontemporal_load((const v4i *)p);
+    return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+__device__ __forceinline__ uint2 ld_row_nt(const int8_t *p)
+{
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const v2i v = __builtin_nontemporal_load((const v2i *)p);
+    return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+}
+
 template <bool BF16>
 __device__ __forceinline__ void raw_to_f32(float *dst, const typename RawRow<BF16>::T &u, float scale)
 {
@@ -374,10 +388,10 @@ __device__ __forceinline__ void attn_scores(const be42_kv_pool &P, AttnShared<HD
         const size_t slot = ((size_t)S.pphys[pg] * n_kv + kvh) * kPg + t;
         if constexpr (BF16) {
             sc_out = 1.0f;
-            return *(const Raw *)((const uint16_t *)base + slot * HD + rl * 8);
+            return ld_row_nt((const uint16_t *)base + slot * HD + rl * 8);
         } else {
             sc_out = P.k_scale[slot];
-            return *(const Raw *)((const int8_t *)base + slot * HD + rl * 8);
+            return ld_row_nt((const int8_t *)base + slot * HD + rl * 8);
         }
     };
     float qv[G][8];
@@ -484,7 +498,6 @@ __device__ __forceinline__ void attn_values_load(const be42_kv_pool &P, AttnShar
 {
     constexpr int RL = HD / 8;
     constexpr int RPW = kWave / RL;
-    using Raw = typename RawRow<BF16>::T;
     constexpr int rows_per_iter = WAVES * RPW;
     const int lane = threadIdx.x & 63, rsub = lane / RL, rl = lane % RL;
     const int T = ns * kPg;
@@ -496,10 +509,10 @@ __device__ __forceinline__ void attn_values_load(const be42_kv_pool &P, AttnShar
         const size_t slot = ((size_t)S.pphys[order ? order[pg] : pg] * P.n_kv + kvh) * kPg + t;
         if constexpr (BF16) {
             vb.vsc[u] = 1.0f;
-            vb.vr[u] = *(const Raw *)((const uint16_t *)P.v + slot * HD + rl * 8);
+            vb.vr[u] = ld_row_nt((const uint16_t *)P.v + slot * HD + rl * 8);
         } else {
             vb.vsc[u] = P.v_scale[slot];
-            vb.vr[u] = *(const Raw *)((const int8_t *)P.v + slot * HD + rl * 8);
+            vb.vr[u] = ld_row_nt((const int8_t *)P.v + slot * HD + rl * 8);
         }
     }
 }
