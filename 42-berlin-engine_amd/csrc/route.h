@@ -30,7 +30,7 @@ __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical
     int o = 0;
     r.off_qm = o;   o += 256 * 4;
     r.off_q0 = o;   o += 256 * 4;
-    r.off_hp = o;   o += hd * 16 * 4;
+    r.off_hp = o;   o += 16 * (hd + 4) * 4;   // projection, bit-major, rows padded by 16 bytes
     r.off_list = o; o += 4 * kProbes * cap * 4;
     r.off_cnt = o;  o += 4 * kProbes * 4 + 4 * 4;
     r.off_offs = o; o += 4 * kProbes * 4 + 4 * 4;
@@ -126,7 +126,7 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
         for (int j = 0; j < 8; j++) {
             const int i = i0 + j * 256 + tid;
             if (i < hd * 16)
-                hp[i] = v[j];
+                hp[(i & 15) * (hd + 4) + (i >> 4)] = v[j];   // hpT[d][bit] -> hp[bit][d]
         }
     }
     if (tid == 0) {
@@ -155,9 +155,19 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
     if (wave == 0) {
         float s = 0.0f;
         if (lane < 16) {
-#pragma unroll 16
-            for (int i = 0; i < hd; i++)
-                s = __fmaf_rn(qm[i], hp[i * 16 + lane], s);
+            // the reference's order (d ascending, one fused multiply-add
+            // each), four terms per 16-byte LDS read: qm broadcast, the
+            // lane's projection row padded so the 16 rows hit different banks
+            const float4 *qm4 = (const float4 *)qm;
+            const float4 *hp4 = (const float4 *)(hp + lane * (hd + 4));
+#pragma unroll 8
+            for (int i4 = 0; i4 < hd / 4; i4++) {
+                const float4 a = qm4[i4], w = hp4[i4];
+                s = __fmaf_rn(a.x, w.x, s);
+                s = __fmaf_rn(a.y, w.y, s);
+                s = __fmaf_rn(a.z, w.z, s);
+                s = __fmaf_rn(a.w, w.w, s);
+            }
         }
         const unsigned long long m = __ballot(lane < 16 && s > 0.0f);
         if (lane == 0)
