@@ -1125,19 +1125,21 @@ static TileCfg split_slab_tile(int n, int k, int batch, bool fp8)
 
 static TileCfg pick_tile(bool fp8, int nc, int n, int k, int batch)
 {
-    // 3+ column groups (FP8 batch >= 7, INT8 batch >= 11): the LDS-resident
-    // digit slab kernel; many rows: one block of 8 waves x 4 row tiles per
-    // row range, each ring stage 16 rows x 512 contiguous bytes; long rows,
-    // or FP8 at 4096 .. 14336 rows: split K, partials added by a second launch
+    // 3+ column groups (FP8 batch >= 7, INT8 batch >= 11) otherwise: the
+    // LDS-resident digit slab kernel; many rows (k > 4096): one block of 8
+    // waves x 4 row tiles per row range, each ring stage 16 rows x 512
+    // contiguous bytes; long rows, or FP8 at 4096 .. 14336 rows: split K,
+    // partials added by a second launch
+    // many rows (the lm_head), any batch: the block-cooperative kernel when
+    // k splits into 8 wave ranges of at most 4 steps (k <= 4096)
+    if (n > 32768) {
+        const int steps = (int)(xdig_kp(k, fp8) / 128);
+        if (steps % kCoopWaves == 0 && steps / kCoopWaves <= 4)
+            return TileCfg{0, 6, 0, kCoopWaves, 0, 4, 1};
+    }
     if (nc >= 3) {
-        if (n > 32768) {
-            // block-cooperative kernel when k splits into 8 wave ranges of
-            // at most 4 steps (k <= 4096), else the slab kernel
-            const int steps = (int)(xdig_kp(k, fp8) / 128);
-            if (steps % kCoopWaves == 0 && steps / kCoopWaves <= 4)
-                return TileCfg{0, 6, 0, kCoopWaves, 0, 4, 1};
+        if (n > 32768)
             return slab_tile(4, 2, 4, 8, 4);
-        }
         if (k >= 8192 || (fp8 && n >= 4096 && n <= 14336)) {
             const TileCfg c = split_slab_tile(n, k, batch, fp8);
             if (c.split > 1)
