@@ -1130,9 +1130,11 @@ static TileCfg pick_tile(bool fp8, int nc, int n, int k, int batch)
     // waves x 4 row tiles per row range, each ring stage 16 rows x 512
     // contiguous bytes; long rows, or FP8 at 4096 .. 14336 rows: split K,
     // partials added by a second launch
-    // many rows (the lm_head), any batch: the block-cooperative kernel when
-    // k splits into 8 wave ranges of at most 4 steps (k <= 4096)
-    if (n > 32768) {
+    // the block-cooperative kernel when k splits into 8 wave ranges of at
+    // most 4 steps (k <= 4096): many rows (the lm_head) at any batch, and
+    // 8193 .. 32768 rows at 1-2 column groups (measured: 14336 x 4096 FP8
+    // batch 1 -6%, INT8 batch 4 -16%; at 3+ groups the split slab is faster)
+    if (n > 32768 || (n > 8192 && nc < 3)) {
         const int steps = (int)(xdig_kp(k, fp8) / 128);
         if (steps % kCoopWaves == 0 && steps / kCoopWaves <= 4)
             return TileCfg{0, 6, 0, kCoopWaves, 0, 4, 1};
