@@ -453,31 +453,36 @@ __device__ __forceinline__ void attn_weights(AttnShared<HD, G, WAVES> &S, int ns
                 lm = fmaxf(lm, sv[t]);
         // running max before this slot: exclusive prefix max over the lanes
         float m = wave_shift_up1(wave_prefix_max(lm), -INFINITY);
+        // the token steps without branches: every step is computed and
+        // selected (tokens past the page's count keep their state), which
+        // does the same operations for the valid tokens as the reference's
+        // loop; per-token branches cost more than the arithmetic
         float av[kPg], lprod = 1.0f;
 #pragma unroll
         for (int t = 0; t < kPg; t++) {
-            av[t] = 1.0f;
-            if (t < nt) {
-                const float st = sv[t];
-                const float mprev = m;
-                m = fmaxf(m, st);
-                const float at = mprev == -INFINITY ? 1.0f : fast_expf(mprev - m);
-                sv[t] = fast_expf(st - m);
-                av[t] = at;
-                lprod *= at;
-            }
+            const bool v = t < nt;
+            const float st = sv[t];
+            const float mprev = m;
+            const float mn = fmaxf(m, st);
+            const float ex = fast_expf(mprev - mn);
+            const float at = mprev == -INFINITY ? 1.0f : ex;
+            const float e = fast_expf(st - mn);
+            m = v ? mn : m;
+            sv[t] = v ? e : st;
+            av[t] = v ? at : 1.0f;
+            lprod = v ? lprod * at : lprod;
         }
         // rescales of all later slots: exclusive suffix product over the lanes
         float pr = wave_shift_down1(wave_suffix_prod(lprod), 1.0f);
         float ls = 0.0f;
 #pragma unroll
         for (int t = kPg - 1; t >= 0; t--) {
-            if (t < nt) {
-                const float w = sv[t] * pr;
+            const bool v = t < nt;
+            const float w = sv[t] * pr;
+            if (v)
                 s[slot * 17 + t] = w;
-                ls += w;
-                pr *= av[t];
-            }
+            ls = v ? ls + w : ls;
+            pr *= av[t];   // av = 1 past the count
         }
         ls = wave_sum_dpp(ls);
         if (lane == 0)
