@@ -566,7 +566,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              f"(the multi-GPU design is described in DESIGN.md)", file=sys.stderr)
+              f"(the hot path is built and measured on one GPU's share: GEMV rows, KV heads and "
+              f"queries would shard across GPUs, but no multi-GPU path is built)", file=sys.stderr)
         sys.exit(2)
 
     import torch
