@@ -49,6 +49,8 @@ SIGNATURES = {
     "be42_decoder_step": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "be42_decoder_next_tokens": (i32, [vp, vp]),
     "be42_decoder_capture": (i32, [vp, vp, vp]),
+    "be42_decoder_capture_kv": (i32, [vp, vp, vp]),
+    "be42_decoder_capture_sel": (i32, [vp, vp]),
     "be42_kv_create": (i32, [vp, i32, i32, i32, i32, i32, vp]),
     "be42_kv_destroy": (None, [vp]),
     "be42_kv_set_projection": (i32, [vp, vp]),
@@ -326,6 +328,25 @@ class KVPool:
     def reset(self, layer):
         self.lib._call("be42_kv_reset", self.handle, layer, self.lib.stream())
 
+    def export(self):
+        """Host bookkeeping: (page_table [n_layers*max_logical], free_stack,
+        free_top, logical_len)."""
+        import numpy as np
+        cap = self.s.capacity
+        pt = np.zeros(self.n_layers * self.max_logical, np.int32)
+        fs = np.zeros(max(cap, 1), np.int32)
+        top = C.c_int()
+        ll = np.zeros(self.n_layers, np.int32)
+        self.lib.check(self.lib.lib.be42_kv_export(self.handle, pt.ctypes.data, fs.ctypes.data, C.byref(top),
+                                                   ll.ctypes.data), "be42_kv_export")
+        return pt, fs[:cap], top.value, ll
+
+    def page_alloc(self):
+        return self.lib.lib.be42_kv_page_alloc(self.handle)
+
+    def page_free(self, phys):
+        self.lib.check(self.lib.lib.be42_kv_page_free(self.handle, phys), "be42_kv_page_free")
+
     def layer_pages(self, layer):
         import numpy as np
         out = np.zeros(self.max_logical, np.int32)
@@ -399,6 +420,12 @@ class Decoder:
 
     def capture(self, q=None, nsel=None):
         self.lib._call("be42_decoder_capture", self.handle, self.lib.p(q), self.lib.p(nsel))
+
+    def capture_kv(self, k=None, v=None):
+        self.lib._call("be42_decoder_capture_kv", self.handle, self.lib.p(k), self.lib.p(v))
+
+    def capture_sel(self, sel=None):
+        self.lib._call("be42_decoder_capture_sel", self.handle, self.lib.p(sel))
 
     def close(self):
         if self.handle:

@@ -366,6 +366,8 @@ struct be42_decoder {
     size_t attn_ws_bytes = 0;
     int *cand = nullptr, *ncand = nullptr;
     float *capture_q = nullptr;   // optional [n_layers][max_batch][n_heads * head_dim]
+    float *capture_k = nullptr, *capture_v = nullptr;   // optional [n_layers][max_batch][n_kv * head_dim]
+    int *capture_sel = nullptr;   // optional [n_layers][max_batch][sel stride]: routed selections
     int *capture_nsel = nullptr;  // optional [n_layers][max_batch] pages attended
     // step parameters: StepHead then AppendStepArgs[n_layers], two pinned host
     // copies (steps alternate, so the host never rewrites a buffer a queued
@@ -380,12 +382,12 @@ struct be42_decoder {
     struct Key {
         int batch = -1, sparse = -1, dev_tokens = -1;
         const float *logits = nullptr;
-        const float *cq = nullptr;
-        const int *cn = nullptr;
+        const float *cq = nullptr, *ck = nullptr, *cv = nullptr;
+        const int *cn = nullptr, *cs = nullptr;
         bool operator==(const Key &o) const
         {
             return batch == o.batch && sparse == o.sparse && dev_tokens == o.dev_tokens && logits == o.logits &&
-                   cq == o.cq && cn == o.cn;
+                   cq == o.cq && ck == o.ck && cv == o.cv && cn == o.cn && cs == o.cs;
         }
     } key[2];
     hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -640,6 +642,12 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         if (d->capture_q)
             BE42_HIP(hipMemcpyAsync(d->capture_q + (size_t)l * c.max_batch * qd, d->q, (size_t)B * qd * 4,
                                     hipMemcpyDeviceToDevice, st));
+        if (d->capture_k)
+            BE42_HIP(hipMemcpyAsync(d->capture_k + (size_t)l * c.max_batch * kd, d->k, (size_t)B * kd * 4,
+                                    hipMemcpyDeviceToDevice, st));
+        if (d->capture_v)
+            BE42_HIP(hipMemcpyAsync(d->capture_v + (size_t)l * c.max_batch * kd, d->v, (size_t)B * kd * 4,
+                                    hipMemcpyDeviceToDevice, st));
         const int *lslots = d->slots + (size_t)l * c.max_batch;
         if (!sparse) {
             DEC_TRY(be42_paged_attention(d->pool, d->q, B, H, P.page_table + (size_t)l * c.max_batch * P.max_logical,
@@ -655,6 +663,11 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
                                    d->cand, d->ncand, nullptr, st));
             DEC_TRY(be42_paged_attention(d->pool, d->q, B, H, d->sel, d->nsel, stride, c.sparse_k, scale, d->att,
                                          c.sparse_k <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
+        }
+        if (d->capture_sel && sparse) {
+            const int stride = std::max(c.sparse_k, 64);
+            BE42_HIP(hipMemcpyAsync(d->capture_sel + (size_t)l * c.max_batch * stride, d->sel,
+                                    (size_t)B * stride * 4, hipMemcpyDeviceToDevice, st));
         }
         if (d->capture_nsel) {
             const int *src = !sparse ? P.n_logical + (size_t)l * c.max_batch : d->nsel;
@@ -684,6 +697,9 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     return BE42_OK;
 }
 
+static int launch_step(be42_decoder *d, int B, int pos, bool host_tokens, float *logits_out, hipStream_t caller,
+                       bool *queued);
+
 extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
                                  float *logits_out, void *stream)
 {
@@ -708,24 +724,55 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
     int slot_ids[kMaxBatch], positions[kMaxBatch];
     for (int b = 0; b < B; b++)
         positions[b] = pos;
-    for (int l = 0; l < c.n_layers; l++) {
+    // the appends are planned on the host before anything is queued; a step
+    // that fails before its work is queued gives the pages back
+    PlanUndo undo;
+    int rc = BE42_OK;
+    for (int l = 0; l < c.n_layers && rc == BE42_OK; l++) {
         for (int b = 0; b < B; b++)
             slot_ids[b] = l * c.max_batch + b;
-        DEC_TRY(plan_append_step(d->pool, slot_ids, positions, B, app + l));
+        rc = plan_append_step(d->pool, slot_ids, positions, B, app + l, &undo);
     }
+    bool queued = false;
+    if (rc == BE42_OK)
+        rc = launch_step(d, B, pos, tokens != nullptr, logits_out, caller, &queued);
+    if (rc != BE42_OK) {
+        if (!queued)
+            undo_append_plans(d->pool, undo);
+        return rc;
+    }
+    if (next_tokens) {
+        BE42_HIP(hipEventSynchronize(d->ev_out));
+        memcpy(next_tokens, d->next_host, (size_t)B * sizeof(int));
+    }
+    return BE42_OK;
+}
+
+// Queue the planned step (parameters already in the pinned buffer of this
+// parity) on the decoder's stream, as a graph replay or kernel by kernel;
+// *queued tells whether any of its work reached the device.
+static int launch_step(be42_decoder *d, int B, int pos, bool host_tokens, float *logits_out, hipStream_t caller,
+                       bool *queued)
+{
+    const be42_decoder_config &c = d->c;
+    const int par = d->parity;
     const int pages = pos / 16 + 1;
     be42_decoder::Key key;
     key.batch = B;
     key.sparse = pages > c.sparse_k ? 1 : 0;
-    key.dev_tokens = tokens ? 0 : 1;
+    key.dev_tokens = host_tokens ? 0 : 1;
     key.logits = logits_out;
     key.cq = d->capture_q;
+    key.ck = d->capture_k;
+    key.cs = d->capture_sel;
+    key.cv = d->capture_v;
     key.cn = d->capture_nsel;
     // the step runs on the decoder's own stream, ordered after the caller's work
     hipStream_t st = d->gstream;
     BE42_HIP(hipEventRecord(d->ev_in, caller));
     BE42_HIP(hipStreamWaitEvent(st, d->ev_in, 0));
     if (!d->use_graph) {
+        *queued = true;   // launched one by one: a failure can come after some of them
         DEC_TRY(enqueue_step(d, B, key.sparse, key.dev_tokens, logits_out, par, st));
     } else {
         if (!d->exec[par] || !(d->key[par] == key)) {
@@ -749,16 +796,13 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
             BE42_HIP(ie);
             d->key[par] = key;
         }
+        *queued = true;
         BE42_HIP(hipGraphLaunch(d->exec[par], st));
     }
     BE42_HIP(hipEventRecord(d->params_free[par], st));
     d->parity ^= 1;
     BE42_HIP(hipEventRecord(d->ev_out, st));
     BE42_HIP(hipStreamWaitEvent(caller, d->ev_out, 0));
-    if (next_tokens) {
-        BE42_HIP(hipEventSynchronize(d->ev_out));
-        memcpy(next_tokens, d->next_host, (size_t)B * sizeof(int));
-    }
     return BE42_OK;
 }
 
@@ -777,5 +821,26 @@ extern "C" int be42_decoder_capture(be42_decoder *d, float *q_dst, int *nsel_dst
     BE42_CHECK(d, "be42_decoder_capture: null decoder");
     d->capture_q = q_dst;
     d->capture_nsel = nsel_dst;
+    return BE42_OK;
+}
+
+// Inspection: copy each layer's post-RoPE K and V rows of every step (the
+// values the step appends to the page pool, [n_layers][max_batch]
+// [n_kv * head_dim]) into device buffers; NULL stops either.
+extern "C" int be42_decoder_capture_kv(be42_decoder *d, float *k_dst, float *v_dst)
+{
+    BE42_CHECK(d, "be42_decoder_capture_kv: null decoder");
+    d->capture_k = k_dst;
+    d->capture_v = v_dst;
+    return BE42_OK;
+}
+
+// Inspection: on routed steps, copy each layer's selection (physical page
+// ids in attention order, [n_layers][max_batch][max(sparse_k, 64)]; the
+// counts are those of be42_decoder_capture) into a device buffer; NULL stops.
+extern "C" int be42_decoder_capture_sel(be42_decoder *d, int *sel_dst)
+{
+    BE42_CHECK(d, "be42_decoder_capture_sel: null decoder");
+    d->capture_sel = sel_dst;
     return BE42_OK;
 }

@@ -545,12 +545,31 @@ void paged_attention(float *output, const float *q, be42_kv_pool *pool, const in
     }
     const size_t qb = (size_t)n_heads * head_dim * 4;
     const float *dq = (const float *)in_dev(q, qb, kS0);
-    const int ns = n_sel > 0 ? n_sel : 0;
+    // attention_head_paged_sparse (ops_attention.c:403-411) skips entries < 0
+    // (score_blocks marks unmapped pages -1 and select_top_k_blocks keeps its
+    // anchors even then); an id past the pool is a caller error
+    std::vector<int> ids;
+    if (n_sel > 0) {
+        std::vector<int> raw((size_t)n_sel);
+        hip_ok(hipMemcpy(raw.data(), sel_host, (size_t)n_sel * 4,
+                         is_device(sel_host) ? hipMemcpyDeviceToHost : hipMemcpyHostToHost),
+               "stage selection");
+        ids.reserve(raw.size());
+        for (int id : raw) {
+            if (id < 0)
+                continue;
+            if (id >= pool->capacity) {
+                char msg[96];
+                snprintf(msg, sizeof msg, "page id %d outside the pool (capacity %d)", id, pool->capacity);
+                die(what, msg);
+            }
+            ids.push_back(id);
+        }
+    }
+    const int ns = (int)ids.size();
     int *dsel = (int *)scratch(kS4, (size_t)(ns + 1) * 4);
     if (ns)
-        hip_ok(hipMemcpy(dsel, sel_host, (size_t)ns * 4, is_device(sel_host) ? hipMemcpyDeviceToDevice
-                                                                              : hipMemcpyHostToDevice),
-               "stage selection");
+        hip_ok(hipMemcpy(dsel, ids.data(), (size_t)ns * 4, hipMemcpyHostToDevice), "stage selection");
     hip_ok(hipMemcpy(dsel + ns, &ns, 4, hipMemcpyHostToDevice), "stage selection");
     bool st;
     float *o = (float *)out_dev(output, qb, kS1, &st);

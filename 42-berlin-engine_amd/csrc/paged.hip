@@ -576,7 +576,8 @@ namespace be42 {
 
 // Host bookkeeping of one decode token for each of n distinct layer slots
 // (paged.c:195-272 per slot): page allocation, page table, seal list.
-int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, AppendStepArgs *out)
+int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, AppendStepArgs *out,
+                     PlanUndo *undo)
 {
     BE42_CHECK(n >= 0 && n <= kArgTok, "be42_kv_append_step: %d slots (at most %d)", n, kArgTok);
     PoolImpl *p = impl(pool);
@@ -585,12 +586,19 @@ int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n
     memset(&a, 0, sizeof a);
     a.n = n;
     a.max_logical = P.max_logical;
+    if (undo && undo->free_top == -2)
+        undo->free_top = p->free_top;
     for (int t = 0; t < n; t++) {
         const int s = slots[t], ps = pos[t];
         BE42_CHECK(s >= 0 && s < P.n_layers, "be42_kv_append_step: slot %d out of range", s);
         BE42_CHECK(ps >= 0 && ps / kPage < P.max_logical, "be42_kv_append_step: position %d out of range", ps);
         for (int u = 0; u < t; u++)
             BE42_CHECK(slots[u] != s, "be42_kv_append_step: slot %d given twice", s);
+        if (undo) {
+            undo->slot.push_back(s);
+            undo->len.push_back(p->logical_len[s]);
+            undo->nidx.push_back(p->n_indexed[s]);
+        }
         const int blk = ps / kPage, base = s * P.max_logical;
         if (blk >= p->logical_len[s]) {
             if (blk != p->logical_len[s]) {
@@ -614,6 +622,8 @@ int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n
         if (ps % kPage == kPage - 1 && !p->registered[phys]) {
             a.seal_of[t] = a.n_seal;
             p->registered[phys] = 1;
+            if (undo)
+                undo->sealed.push_back(phys);
             if (blk + 1 > p->n_indexed[s])
                 p->n_indexed[s] = blk + 1;
             a.seal_phys[a.n_seal] = phys;
@@ -624,6 +634,26 @@ int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n
         }
     }
     return BE42_OK;
+}
+
+void undo_append_plans(be42_kv_pool *pool, const PlanUndo &u)
+{
+    if (u.free_top == -2)
+        return;
+    PoolImpl *p = impl(pool);
+    const int ml = p->pub.max_logical;
+    for (int phys : u.sealed)
+        p->registered[phys] = 0;
+    // newest entry first: a slot logged twice ends at its oldest values
+    for (size_t i = u.slot.size(); i-- > 0;) {
+        const int s = u.slot[i];
+        for (int blk = u.len[i]; blk < p->logical_len[s]; blk++)
+            p->page_table[(size_t)s * ml + blk] = -1;
+        p->logical_len[s] = u.len[i];
+        p->n_indexed[s] = u.nidx[i];
+    }
+    // pops only move the top, so the stack's contents above it are intact
+    p->free_top = u.free_top;
 }
 
 int launch_rope_append_step_dev(const be42_kv_pool &P, const AppendStepArgs *a_dev, int n, float *q, float *k,

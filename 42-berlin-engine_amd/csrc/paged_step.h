@@ -2,6 +2,8 @@
 // pool (paged.hip) and the decode step (decode.hip).
 #pragma once
 
+#include <vector>
+
 #include "be42_common.h"
 
 namespace be42 {
@@ -19,8 +21,22 @@ struct AppendStepArgs {
     int seal_of[kArgTok];   // per token: its entry in the seal list, or -1
 };
 
-// host: allocate pages and fill the bookkeeping (paged.c:195-272 per slot)
-int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, AppendStepArgs *out);
+// What plan_append_step changed in the pool's host bookkeeping, so that a
+// step that fails before its launches are queued can give it back (the
+// device never saw those pages).  One log may span several plans.
+struct PlanUndo {
+    int free_top = -2;       // free-stack top before the first plan (-2: nothing logged)
+    std::vector<int> slot, len, nidx;   // per slot first touched: logical pages, pages indexed
+    std::vector<int> sealed;            // pages the plans marked registered
+};
+
+// host: allocate pages and fill the bookkeeping (paged.c:195-272 per slot);
+// undo (may be NULL) logs the changes
+int plan_append_step(be42_kv_pool *pool, const int *slots, const int *pos, int n, AppendStepArgs *out,
+                     PlanUndo *undo = nullptr);
+// restore the host bookkeeping logged in undo (pages back on the free stack
+// in their order, page-table entries unmapped, counters and flags reset)
+void undo_append_plans(be42_kv_pool *pool, const PlanUndo &undo);
 // device: RoPE of the n tokens' q [n][n_heads*hd] and k [n][n_kv*hd] at
 // position *pos_p (table rows [pos][hd/2]; not rotated at or past rope_len),
 // then the store of their K/V rows and the seal of the pages they fill, in

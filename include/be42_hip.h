@@ -7,6 +7,12 @@
  * the default stream) and returns without synchronising.  Return value:
  * BE42_OK or a negative BE42_E* code; be42_last_error() then holds a message.
  *
+ * One stream at a time per device: the library keeps one grow-only workspace
+ * and one split-K partial-sum buffer per process (used by the GEMVs, by
+ * be42_paged_attention / be42_lsh_attention without a caller workspace, and
+ * by the decoder's fallback paths), so calls that use them must not run
+ * concurrently on two streams.  Calls on one stream are always safe.
+ *
  * The reference-signature entry points built on top of these (op_matmul,
  * paged_kv_append, lsh_hash, op_paged_attention_sparse, ...) are declared in
  * be42_engine.h.
@@ -269,6 +275,14 @@ int  be42_decoder_next_tokens(be42_decoder *d, const int **dev_ptr);
  * each layer attended into nsel_dst ([n_layers][max_batch], device); NULL
  * stops either. */
 int  be42_decoder_capture(be42_decoder *d, float *q_dst, int *nsel_dst);
+/* Inspection: each step copies every layer's post-RoPE K and V rows (the
+ * values it appends to the page pool) into k_dst / v_dst ([n_layers]
+ * [max_batch][n_kv_heads * head_dim], device); NULL stops either. */
+int  be42_decoder_capture_kv(be42_decoder *d, float *k_dst, float *v_dst);
+/* Inspection: on routed steps (a layer past sparse_k pages) each step copies
+ * every layer's page selection (physical ids in attention order) into
+ * sel_dst ([n_layers][max_batch][max(sparse_k, 64)], device); NULL stops it. */
+int  be42_decoder_capture_sel(be42_decoder *d, int *sel_dst);
 
 #ifdef __cplusplus
 }

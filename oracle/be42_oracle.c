@@ -1068,6 +1068,18 @@ void or_decoder_free(or_decoder *d)
     memset(d, 0, sizeof *d);
 }
 
+void or_decoder_force_kv(or_decoder *d, const float *k, const float *v)
+{
+    d->kv_force_k = k;
+    d->kv_force_v = v;
+}
+
+void or_decoder_log_selection(or_decoder *d, int *sel, int *nsel)
+{
+    d->sel_log = sel;
+    d->nsel_log = nsel;
+}
+
 /* paged_kv_append plus the page index: a page that fills is hashed (its
  * centroid under the projection) and inserted as logical page id. */
 int or_decoder_kv_append(or_decoder *d, int layer, const float *k, const float *v, int pos)
@@ -1079,6 +1091,15 @@ int or_decoder_kv_append(or_decoder *d, int layer, const float *k, const float *
         uint16_t h = or_lsh_hash(d->hpT, d->c.hd, d->kv.centroid + (size_t)phys * d->c.hd);
         or_lsh_insert_block(&d->ix[layer], h, pos - OR_PAGE_TOKENS + 1, OR_PAGE_TOKENS);
     }
+    return 0;
+}
+
+int or_decoder_kv_append_n(or_decoder *d, int layer, const float *k, const float *v, int pos0, int n)
+{
+    const size_t kd = (size_t)d->c.n_kv * d->c.hd;
+    for (int t = 0; t < n; t++)
+        if (or_decoder_kv_append(d, layer, k + t * kd, v + t * kd, pos0 + t))
+            return -1;
     return 0;
 }
 
@@ -1113,18 +1134,30 @@ int or_decoder_step(or_decoder *d, int token, int pos, float *logits, int th)
         gemv_kind(d->v, c->wkind, L->wv, L->sv, d->xb, kd, dim, th);
         or_rope_apply(d->q, c->n_heads, hd, pos, c->max_seq, d->cos_t, d->sin_t);
         or_rope_apply(d->k, c->n_kv, hd, pos, c->max_seq, d->cos_t, d->sin_t);
-        if (or_decoder_kv_append(d, l, d->k, d->v, pos)) {
+        const float *kr = d->kv_force_k ? d->kv_force_k + (size_t)l * kd : d->k;
+        const float *vr = d->kv_force_v ? d->kv_force_v + (size_t)l * kd : d->v;
+        if (or_decoder_kv_append(d, l, kr, vr, pos)) {
             free(sel);
             return -1;
         }
         int nb = d->kv.logical_len[l];
         if (nb <= c->sparse_k) {
             or_paged_attention_dense(d->att, d->q, &d->kv, l, c->n_heads, scale, th);
+            if (d->sel_log) {
+                for (int i = 0; i < nb; i++)
+                    d->sel_log[(size_t)l * c->sparse_k + i] = i;
+                d->nsel_log[l] = nb;
+            }
         } else {
             int nc = 0;
             int ns = or_route_pages(sel, &nc, NULL, &d->kv, l, d->q, c->n_heads, d->hpT, &d->ix[l], c->cand_cap,
                                     c->sparse_k);
             or_paged_attention_pages(d->att, d->q, &d->kv, sel, ns, c->n_heads, scale, th);
+            if (d->sel_log) {
+                for (int i = 0; i < ns; i++)
+                    d->sel_log[(size_t)l * c->sparse_k + i] = d->kv.start_pos[sel[i]] / OR_PAGE_TOKENS;
+                d->nsel_log[l] = ns;
+            }
         }
         gemv_kind(d->xb, c->wkind, L->wo, L->so, d->att, dim, qd, th);
         for (int i = 0; i < dim; i++)
@@ -1138,6 +1171,7 @@ int or_decoder_step(or_decoder *d, int token, int pos, float *logits, int th)
             d->x[i] = d->x[i] + d->xb[i];
     }
     free(sel);
+    d->kv_force_k = d->kv_force_v = NULL;
     or_rmsnorm(d->x, d->x, d->w.final_norm, dim, c->eps);
     gemv_kind(logits, c->wkind, d->w.out, d->w.out_s, d->x, c->vocab, dim, th);
     return or_argmax(logits, c->vocab);

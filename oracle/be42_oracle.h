@@ -194,13 +194,27 @@ typedef struct or_decoder {
     or_lsh_index *ix;
     float *hpT, *cos_t, *sin_t;
     float *x, *xb, *q, *k, *v, *att, *hb, *hb2;
+    const float *kv_force_k, *kv_force_v;   /* [n_layers][n_kv*hd] rows for the next step's appends, or NULL */
+    int *sel_log, *nsel_log;                 /* optional [n_layers][sparse_k], [n_layers]: logical pages attended */
 } or_decoder;
 
 int  or_decoder_init(or_decoder *d, const or_decoder_cfg *c, const or_model_w *w, const float *hpT);
 void or_decoder_free(or_decoder *d);
 int  or_decoder_kv_append(or_decoder *d, int layer, const float *k, const float *v, int pos);
+/* n consecutive positions pos0.. of one layer, k and v [n][n_kv*hd] */
+int  or_decoder_kv_append_n(or_decoder *d, int layer, const float *k, const float *v, int pos0, int n);
 /* transformer_forward (inference.c:60-696), paged path; returns the argmax */
 int  or_decoder_step(or_decoder *d, int token, int pos, float *logits, int n_threads);
+/* Test hook (no reference counterpart): the next or_decoder_step appends the
+ * given post-RoPE K and V rows ([n_layers][n_kv*hd] each, kept by the caller
+ * until that step returns) instead of its own, so a checker can give the
+ * oracle exactly the K/V values another implementation stored and compare the
+ * rest of the step without code flips of the KV quantization. */
+void or_decoder_force_kv(or_decoder *d, const float *k, const float *v);
+/* Test hook: every step records, per layer, the logical ids of the pages it
+ * attended in attention order (sel [n_layers][sparse_k]) and their count
+ * (nsel [n_layers]); NULL stops it. */
+void or_decoder_log_selection(or_decoder *d, int *sel, int *nsel);
 
 #ifdef __cplusplus
 }

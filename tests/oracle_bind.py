@@ -107,8 +107,32 @@ class OracleDecoder:
         return self.o.lib.or_decoder_kv_append(self.buf, layer, np.ascontiguousarray(k, np.float32),
                                                np.ascontiguousarray(v, np.float32), pos)
 
-    def step(self, token, pos, threads=0):
+    def log_selection(self, on=True):
+        """Record each step's attended logical pages per layer (last_selection)."""
+        c = self.cfg
+        if on:
+            self.sel_log = np.zeros((c.n_layers, c.sparse_k), np.int32)
+            self.nsel_log = np.zeros(c.n_layers, np.int32)
+            self.o.lib.or_decoder_log_selection(self.buf, self.sel_log.ctypes.data, self.nsel_log.ctypes.data)
+        else:
+            self.o.lib.or_decoder_log_selection(self.buf, None, None)
+
+    def last_selection(self, layer):
+        return self.sel_log[layer, :self.nsel_log[layer]].copy()
+
+    def kv_append_n(self, layer, k, v, pos0):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        return self.o.lib.or_decoder_kv_append_n(self.buf, layer, k.ctypes.data, v.ctypes.data, pos0, k.shape[0])
+
+    def step(self, token, pos, threads=0, force_k=None, force_v=None):
+        """One step; force_k / force_v ([n_layers][n_kv*hd] fp32) replace the
+        K and V rows the step appends (or_decoder_force_kv)."""
         logits = np.zeros(self.vocab, np.float32)
+        if force_k is not None:
+            fk = np.ascontiguousarray(force_k, np.float32)
+            fv = np.ascontiguousarray(force_v, np.float32)
+            self.o.lib.or_decoder_force_kv(self.buf, fk.ctypes.data, fv.ctypes.data)
         nxt = self.o.lib.or_decoder_step(self.buf, int(token), int(pos), logits, threads)
         return nxt, logits
 
@@ -172,6 +196,9 @@ class Oracle:
         _sig(L, "or_decoder_free", None, C.c_void_p)
         _sig(L, "or_decoder_kv_append", C.c_int, C.c_void_p, C.c_int, f32p, f32p, C.c_int)
         _sig(L, "or_decoder_step", C.c_int, C.c_void_p, C.c_int, C.c_int, f32p, C.c_int)
+        _sig(L, "or_decoder_force_kv", None, C.c_void_p, C.c_void_p, C.c_void_p)
+        _sig(L, "or_decoder_kv_append_n", C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int)
+        _sig(L, "or_decoder_log_selection", None, C.c_void_p, C.c_void_p, C.c_void_p)
         _sig(L, "or_paged_alloc", C.c_int, C.POINTER(OrPaged))
         _sig(L, "or_paged_release", None, C.POINTER(OrPaged), C.c_int)
         _sig(L, "or_score_blocks", None, C.c_void_p, f32p, C.POINTER(OrPaged), C.c_int, C.c_int)

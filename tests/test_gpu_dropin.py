@@ -244,3 +244,42 @@ def test_paged_pipeline_drop_in(be, dl, orc):
     assert bm.free_top == op.free_top() and bm.free_stack[bm.free_top] == p
     dl.block_manager_free(C.byref(bm))
     assert bm.capacity == 0
+
+
+def test_sparse_attention_skips_unmapped_ids(be, dl, orc):
+    """attention_head_paged_sparse (ops_attention.c:403-411) skips selection
+    entries < 0: score_blocks marks unmapped pages -1 and
+    select_top_k_blocks keeps its anchors even then.  The drop-in drops them
+    on the host; an all -1 selection gives zeros, as the reference's
+    memset output with sum_exp == 0."""
+    rng = np.random.default_rng(5)
+    n_kv, hd, H, max_pages = 2, 64, 4, 8
+    bm, pkvs = _manager(dl, 1, n_kv, hd, max_pages)
+    op = OraclePaged(orc, 1, n_kv, hd, max_pages, OR_KV_INT8)
+    T = 5 * PAGE + 3
+    K = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    V = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    for t in range(T):
+        dl.paged_kv_append(C.byref(pkvs[0]), D.ptr(K[t]), D.ptr(V[t]), t)
+        op.append(0, K[t], V[t], t)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    phys = [op.phys(0, i) for i in range(op.n_blocks(0))]
+    sel = np.array([-1, phys[3], -1, phys[0], phys[5], -1], np.int32)
+    out = np.zeros(H * hd, np.float32)
+    dl.op_paged_attention_sparse(D.ptr(out), D.ptr(q), C.byref(bm), D.ptr(sel), len(sel), H, n_kv, hd,
+                                 C.c_float(scale))
+    want = op.attention_pages(q.reshape(H, hd), [phys[3], phys[0], phys[5]], H, scale)
+    assert rel_err(out, want) <= 2e-5
+    # the same selection from device memory
+    dsel = torch.from_numpy(sel).cuda()
+    out2 = np.zeros(H * hd, np.float32)
+    dl.op_paged_attention_sparse(D.ptr(out2), D.ptr(q), C.byref(bm), C.c_void_p(dsel.data_ptr()), len(sel), H,
+                                 n_kv, hd, C.c_float(scale))
+    assert np.array_equal(out, out2)
+    none = np.full(3, -1, np.int32)
+    out3 = np.full(H * hd, 7.0, np.float32)
+    dl.op_paged_attention_sparse(D.ptr(out3), D.ptr(q), C.byref(bm), D.ptr(none), 3, H, n_kv, hd,
+                                 C.c_float(scale))
+    assert not out3.any()
+    dl.block_manager_free(C.byref(bm))

@@ -74,10 +74,13 @@ def test_gemm_vs_oracle(be, orc, kind, m, n, k):
 
 
 @pytest.mark.parametrize("kind", ["int8", "fp8"])
-@pytest.mark.parametrize("m,n,k", [(512, 4096, 4096), (2048, 14336, 4096), (512, 4096, 14336)])
+@pytest.mark.parametrize("m,n,k", [(512, 4096, 4096), (2048, 14336, 4096), (512, 4096, 14336),
+                                   (8192, 4096, 14336), (2048, 128256, 4096), (8192, 128256, 4096)])
 def test_gemm_config_shapes_sampled(be, orc, kind, m, n, k):
-    """configs[2] shapes: the full product on the GPU, checked on 64 sampled
-    rows x 96 sampled columns against exact host arithmetic of the same codes."""
+    """configs[2] shapes up to M = 8192 and N = 128256: the full product on
+    the GPU, checked on 64 sampled rows x 96 sampled columns (the last row
+    and column always among them) against exact host arithmetic of the same
+    codes."""
     g = torch.Generator(device="cuda")
     g.manual_seed(m + n + k)
     x = torch.randn(m, k, generator=g, device="cuda")
@@ -92,9 +95,10 @@ def test_gemm_config_shapes_sampled(be, orc, kind, m, n, k):
     rows = np.sort(rng.choice(m, 64, replace=False))
     cols = np.sort(rng.choice(n, 96, replace=False))
     rows[-1], cols[-1] = m - 1, n - 1
-    xs, sxs = xq.cpu().numpy()[rows], sx.cpu().numpy()[rows]
-    ws, sws = wq.cpu().numpy()[cols], sw.cpu().numpy()[cols]
-    got = y.cpu().numpy()[np.ix_(rows, cols)]
+    r, c = torch.from_numpy(rows).cuda(), torch.from_numpy(cols).cuda()
+    xs, sxs = xq[r].cpu().numpy(), sx[r].cpu().numpy()
+    ws, sws = wq[c].cpu().numpy(), sw[c].cpu().numpy()
+    got = y[r][:, c].cpu().numpy()
     if kind == "int8":
         np.testing.assert_array_equal(got, _exact_int8(xs, sxs, ws, sws))
     else:

@@ -64,17 +64,27 @@ def test_gemv_config_shapes(be, orc, kind, n, k, b):
     _check(y, want)
 
 
-def test_gemv_lm_head_int8(be, orc):
-    """The largest config-2 shape (128256 x 4096) at batch 1."""
-    rng = np.random.default_rng(7)
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("b", [1, 4, 16])
+def test_gemv_lm_head(be, orc, kind, b):
+    """The largest config-2 shape (128256 x 4096) at every batch; FP8 at
+    batch 16 is the benchmark's roofline launch (the block-cooperative kernel
+    with 32 row tiles per block)."""
+    rng = np.random.default_rng(7 + b)
     n, k = 128256, 4096
-    wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
-    ws = rng.uniform(0.005, 0.02, n).astype(np.float32)
-    x = rng.standard_normal((1, k)).astype(np.float32)
-    want = orc.gemv(wq, ws, x, "int8")
+    if kind == "int8":
+        wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        ws = rng.uniform(0.005, 0.02, n).astype(np.float32)
+    else:
+        wq = rng.integers(0, 256, (n, k), dtype=np.uint8)
+        wq[(wq & 0x7F) == 0x7F] = 0x7E
+        ws = rng.uniform(0.005, 0.02, n).astype(np.float32) / 200.0
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    want = orc.gemv(wq, ws, x, kind)
     y = be.gemv(torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda(),
-                torch.from_numpy(x).cuda(), "int8").cpu().numpy()
+                torch.from_numpy(x).cuda(), kind).cpu().numpy()
     _check(y, want)
+    assert rel_err(y, want) <= (1e-5 if kind == "int8" else 1e-4)
 
 
 def test_gemv_outliers_and_zero(be, orc):

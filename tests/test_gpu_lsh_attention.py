@@ -273,24 +273,34 @@ def test_attention_fused_group_shapes(be, orc, kind, n_kv, H, hd):
     gp.close()
 
 
-def test_lsh_attention_pipeline_c4_shape(be, orc):
-    """Config-4 shape at 8k context: 32 query heads, 8 KV heads, head_dim 128,
-    bf16 pages, 5% planted pages, top-K 64 pages, candidate cap 64."""
-    rng = np.random.default_rng(600)
-    n_kv, hd, H, T = 8, 128, 32, 8192
+@pytest.mark.parametrize("T", [8192, 32768, 131072])
+def test_lsh_attention_pipeline_c4_shape(be, orc, T):
+    """configs[3] at each of its contexts (8k, 32k, 128k = 512 / 2048 / 8192
+    pages): 32 query heads, 8 KV heads, head_dim 128, bf16 pages, 5% planted
+    pages, top-K 64 pages, candidate cap 64.  The router (two launches) and
+    the fused route + attention launch both give the oracle's candidates and
+    selection bit for bit and its attention within 1e-3 (measured ~1e-6)."""
+    rng = np.random.default_rng(600 + T // 8192)
+    n_kv, hd, H = 8, 128, 32
     _, hpT = orc.lsh_init(hd, 42)
     q = rng.standard_normal((1, H, hd)).astype(np.float32)
     gp, op, idx = _build(be, orc, OR_KV_BF16, 1, n_kv, hd, T // PAGE + 1, (T,), rng, hpT,
                          planted=_planter(orc, hpT, hd, H, q, 0.05, rng), chunks=(64,))
+    print(f"c4 T={T}: built", flush=True)
     sel, nsel, cand, ncand, qh = be.route(gp, torch.from_numpy(q).cuda(), 64, 64)
     want_sel, want_cand = op.route(0, q[0], H, hpT, idx[0], 64, 64)
     s = sel.cpu().numpy()[0, :nsel.item()]
     np.testing.assert_array_equal(s, want_sel)
     np.testing.assert_array_equal(cand.cpu().numpy()[0, :ncand.item()], want_cand)
+    assert len(want_sel) == 64 and len(want_cand) == 64
     scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
     out = be.paged_attention(gp, torch.from_numpy(q).cuda(), sel, nsel, 64, scale, n_split=1).cpu().numpy()
     want = op.attention_pages(q[0], want_sel, H, scale)
     assert rel_err(out.ravel(), want) <= TOL
+    assert rel_err(out.ravel(), want) <= 2e-5
+    fo, fsel, fn = be.lsh_attention(gp, torch.from_numpy(q).cuda(), 64, 64, scale)
+    np.testing.assert_array_equal(fsel.cpu().numpy()[0, :fn.item()], want_sel)
+    assert rel_err(fo.cpu().numpy().ravel(), want) <= 2e-5
     gp.close()
 
 

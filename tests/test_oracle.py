@@ -342,6 +342,48 @@ def test_paged_centroid_closed_form(orc):
         np.testing.assert_array_equal(bits(c), bits(g["cen0"][i]))
 
 
+def test_paged_centroid_bf16_closed_form(orc):
+    """or_centroid_bf16: the bf16-page centroid (calc_block_centroid_int8,
+    paged.c:350-393, on bf16 rows) through the append path.  Closed form:
+    head 0's rows rounded to bf16 by an independent round-to-nearest-even
+    (torch), summed per dimension token by token in float32, then x (1/16);
+    bit-exact.  Page 1 holds +-2^20 around small values on head 0, where a
+    float32 sum in any other order (pairwise, reversed) rounds differently,
+    and head 1 differs from head 0, so a wrong head, a wrong token order or
+    a wrong divisor fails."""
+    rng = np.random.default_rng(11)
+    n_kv, hd = 2, 64
+    pk = OraclePaged(orc, 1, n_kv, hd, 4, OR_KV_BF16)
+    T = 3 * PAGE + 5
+    K = (rng.standard_normal((T, n_kv * hd)) * 3).astype(np.float32)
+    K[PAGE:2 * PAGE, :hd] = rng.uniform(0.1, 0.9, (PAGE, hd)).astype(np.float32)
+    K[PAGE, :hd] = 2.0 ** 20
+    K[2 * PAGE - 1, :hd] = -(2.0 ** 20)
+    V = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    for t in range(T):
+        pk.append(0, K[t], V[t], t)
+    bf = torch.from_numpy(K).to(torch.bfloat16).to(torch.float32).numpy()
+    for pg in range(pk.n_blocks(0)):
+        phys = pk.phys(0, pg)
+        kb = pk.page_arrays(phys)[0].reshape(n_kv, PAGE, hd)
+        n = min(PAGE, T - pg * PAGE)
+        # the stored rows are the independent bf16 rounding of the inputs
+        np.testing.assert_array_equal((kb[0, :n].astype(np.uint32) << 16).view(np.float32), bf[pg * PAGE:pg * PAGE + n, :hd])
+        if n < PAGE:
+            continue
+        c = np.zeros(hd, np.float32)
+        for t in range(PAGE):
+            c = (c + bf[pg * PAGE + t, :hd]).astype(np.float32)
+        c = (c * np.float32(1.0 / 16)).astype(np.float32)
+        np.testing.assert_array_equal(bits(pk.page_arrays(phys)[4]), bits(c))
+        if pg == 1:
+            rows = bf[PAGE:2 * PAGE, :hd]
+            pair = (rows.reshape(8, 2, hd).sum(1, dtype=np.float32))
+            while len(pair) > 1:
+                pair = pair.reshape(-1, 2, hd).sum(1, dtype=np.float32)
+            assert not np.array_equal(bits(pair[0] * np.float32(1.0 / 16)), bits(c))
+
+
 def _two_pass_attention(orc, q, K, V, scale):
     """Sequential-max softmax written as prefix max + suffix products of the
     rescale factors (the formulation the GPU kernel uses), in float64 sums."""

@@ -8,7 +8,7 @@ of the decoder loop, pinned without a GPU:
 import numpy as np
 import pytest
 
-from oracle_bind import OR_KV_INT8, OracleDecoder
+from oracle_bind import OR_KV_BF16, OR_KV_INT8, PAGE, OracleDecoder
 
 
 def _bf16(orc, x):
@@ -190,3 +190,197 @@ def test_decoder_matches_float64_forward(orc):
         assert nxt == orc.argmax(logits)
         err = np.max(np.abs(logits - want[pos])) / np.max(np.abs(want[pos]))
         assert err < 2e-3, (pos, err)
+
+
+# ------------------------------------------------------------------ routed FP8 / bf16 composition
+def _fp8_decode_independent(codes):
+    """E4M3 bytes -> float64 through torch's float8_e4m3fn (an independent
+    decoder; the reference encoder never emits 0x7F / 0xFF)."""
+    import torch
+    c = np.ascontiguousarray(codes, np.uint8)
+    assert not np.any((c & 0x7F) == 0x7F)
+    return torch.from_numpy(c).view(torch.float8_e4m3fn).to(torch.float64).numpy()
+
+
+def _bf16_round_independent(x):
+    """float32 -> bf16 (round to nearest even) -> float64, through torch."""
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).to(torch.float64).numpy()
+
+
+def routed_forward(orc, cfg, w, tokens, cos_t, sin_t, hpT, fk, fv):
+    """float64 restatement of the decode loop on the routed paged path:
+    every token's K/V rows are the given fk / fv [L][T][n_kv*hd] (stored as
+    INT8 codes or bf16), q and everything else computed here.  Once a layer
+    has more than sparse_k pages (inference.c:447) the step routes:
+      q_mean = (sum over heads ascending of q_h) / H in float32 (inference.c:291-295),
+      qh = lsh_hash(q_mean); page j's hash = lsh_hash of its head-0 centroid
+      (sequential float32 sum of the 16 stored rows, x 1/16; paged.c:350-393);
+      candidates = probe qh, then qh with bit 0..15 flipped, each bucket
+      newest page first, no repeats, at most cand_cap (ops_lsh.c:361-418);
+      list = [page 0] + candidates without the first / last page + [last];
+      score = q_head0 . centroid; selection = select_top_k_blocks(list, k)
+      (paged.c:439-495); attention over the selected pages' tokens in
+      selection order with the online softmax (ops_attention.c:330-346).
+    lsh_hash, the score dot and select_top_k_blocks are the oracle's own
+    (each pinned bit-exactly by the reference's golden vectors); their
+    composition is restated here.  Returns per-step logits, the last step's
+    per-layer selections (logical pages) and per-layer rotated queries."""
+    dim, hd, H, KV = cfg["dim"], cfg["hd"], cfg["n_heads"], cfg["n_kv"]
+    G = H // KV
+    fp8 = cfg["wkind"] == 1
+    bf16 = cfg["kv_kind"] == OR_KV_BF16
+    half = hd // 2
+    from oracle_bind import BLOCK_SCORE
+    import ctypes as C
+
+    def deq(q, s):
+        v = _fp8_decode_independent(q) if fp8 else q.astype(np.float64)
+        return v * s.astype(np.float64)[:, None]
+
+    def rope(x, pos, n):
+        x = x.reshape(n, hd).copy()
+        c = cos_t[pos * half:(pos + 1) * half].astype(np.float64)
+        s = sin_t[pos * half:(pos + 1) * half].astype(np.float64)
+        a, b = x[:, :half].copy(), x[:, half:].copy()
+        x[:, :half], x[:, half:] = a * c - b * s, a * s + b * c
+        return x.ravel()
+
+    def norm(x):
+        return x / np.sqrt((x ** 2).mean() + cfg["eps"])
+
+    def store(x):
+        """the stored value of a K or V row [n_kv*hd] (float32 in), per head"""
+        if bf16:
+            return _bf16_round_independent(x).reshape(KV, hd)
+        rows = []
+        for h in range(KV):
+            q, sc = orc.quant_int8(x[h * hd:(h + 1) * hd].astype(np.float32))
+            rows.append(q.astype(np.float64) * np.float64(sc))
+        return np.stack(rows)
+
+    dot = orc.lib.or_dot_f32_f32
+    Ks = [[] for _ in w["layers"]]
+    Vs = [[] for _ in w["layers"]]
+    outs, last_sel, last_q = [], [], []
+    for pos, tok in enumerate(tokens):
+        last_sel, last_q = [], []
+        if fp8:
+            x = _fp8_decode_independent(w["emb"][tok]) * np.float64(w["emb_s"][tok])
+        else:
+            x = w["emb"][tok].astype(np.float64) * np.float64(w["emb_s"][tok])
+        for li, L in enumerate(w["layers"]):
+            xb = norm(x)
+            q = rope(deq(L["wq"], L["sq"]) @ xb, pos, H)
+            last_q.append(q)
+            Ks[li].append(store(fk[li][pos]))
+            Vs[li].append(store(fv[li][pos]))
+            K, V = np.stack(Ks[li]), np.stack(Vs[li])
+            n_tok = pos + 1
+            n_pg = (n_tok + PAGE - 1) // PAGE
+            if n_pg <= cfg["sparse_k"]:
+                order = list(range(n_pg))
+            else:
+                qf = q.astype(np.float32)
+                acc = qf[:hd].copy()
+                for h in range(1, H):
+                    acc = (acc + qf[h * hd:(h + 1) * hd]).astype(np.float32)
+                qm = (acc / np.float32(H)).astype(np.float32)
+                qh = orc.lsh_hash(hpT, qm)
+                cen = []
+                for j in range(n_pg):
+                    c = np.zeros(hd, np.float32)
+                    for t in range(j * PAGE, min((j + 1) * PAGE, n_tok)):
+                        c = (c + K[t, 0].astype(np.float32)).astype(np.float32)
+                    cen.append((c * np.float32(1.0 / PAGE)).astype(np.float32))
+                full = [j for j in range(n_pg) if (j + 1) * PAGE <= n_tok]
+                hashes = {j: orc.lsh_hash(hpT, cen[j]) for j in full}
+                cands = []
+                for p in range(17):
+                    ph = qh if p == 0 else qh ^ (1 << (p - 1))
+                    for j in reversed(full):
+                        if hashes[j] == ph and j not in cands and len(cands) < cfg["cand_cap"]:
+                            cands.append(j)
+                lst = [0] + [j for j in cands if j not in (0, n_pg - 1)] + [n_pg - 1]
+                sc = np.zeros(len(lst), BLOCK_SCORE)
+                q0 = np.ascontiguousarray(qf[:hd])
+                for i, j in enumerate(lst):
+                    sc[i] = (j, j, dot(q0, np.ascontiguousarray(cen[j]), hd))
+                order = [int(j) for j in orc.select_top_k(sc, cfg["sparse_k"])]
+            last_sel.append(order)
+            toks = [t for j in order for t in range(j * PAGE, min((j + 1) * PAGE, n_tok))]
+            att = np.zeros((H, hd))
+            for h in range(H):
+                s = (K[toks, h // G] @ q[h * hd:(h + 1) * hd]) / np.sqrt(hd)
+                m, l, o = -np.inf, 0.0, np.zeros(hd)
+                for i, t in enumerate(toks):
+                    mn = max(m, s[i])
+                    a = float(orc.fast_expf(np.float32(m - mn))[0]) if m > -np.inf else 1.0
+                    p_ = float(orc.fast_expf(np.float32(s[i] - mn))[0])
+                    l, o, m = l * a + p_, o * a + p_ * V[t, h // G], mn
+                att[h] = o / l
+            x = x + deq(L["wo"], L["so"]) @ att.ravel()
+            xb = norm(x)
+            g, u = deq(L["w1"], L["s1"]) @ xb, deq(L["w3"], L["s3"]) @ xb
+            sig = 1.0 / (1.0 + _fexp_vec(-g).astype(np.float64))
+            x = x + deq(L["w2"], L["s2"]) @ (g * sig * u)
+        outs.append(deq(w["out"], w["out_s"]) @ norm(x))
+    return outs, last_sel, last_q
+
+
+@pytest.mark.parametrize("wkind,kv_kind", [(1, OR_KV_BF16), (0, OR_KV_INT8), (1, OR_KV_INT8)])
+def test_routed_decoder_matches_float64_forward(orc, wkind, kv_kind):
+    """The oracle decoder past sparse_k pages (FP8 weights, bf16 or INT8 KV)
+    against routed_forward, with every token's K/V rows forced to the same
+    values in both.  The prefix keys are planted as the configs[3] recipe
+    does: a probe pass finds each layer's q_mean at the last step, and 40% of
+    that layer's middle pages get keys 6 * unit(q_mean) + N(0, 0.05^2) on
+    every KV head, so the route sees full candidate lists and the heap
+    replaces entries (cap 6, k 5).  The last step's selection must equal the
+    restated route page for page, and the logits agree within 2e-3."""
+    rng = np.random.default_rng(33 + wkind + 2 * kv_kind)
+    n_layers, dim, H, KV, hd, hidden, vocab = 2, 64, 4, 2, 16, 96, 300
+    cfg, w = tiny_model(rng, n_layers, dim, H, KV, hd, hidden, vocab)
+    if wkind == 1:
+        for L in w["layers"]:
+            for name in ("wq", "wk", "wv", "wo", "w1", "w2", "w3"):
+                r, c = L[name].shape
+                L[name], L["s" + name[1:]] = orc.quantize_rows(
+                    (rng.standard_normal((r, c)) * 0.05).astype(np.float32), "fp8")
+        w["emb"], w["emb_s"] = orc.quantize_rows((rng.standard_normal((vocab, dim)) * 0.5).astype(np.float32), "fp8")
+        w["out"], w["out_s"] = orc.quantize_rows((rng.standard_normal((vocab, dim)) * 0.05).astype(np.float32), "fp8")
+    else:
+        for L in w["layers"]:
+            for k in ("sq", "sk", "sv", "so", "s1", "s2", "s3"):
+                L[k] = (L[k] * 0.1).astype(np.float32)
+    cfg.update(wkind=wkind, kv_kind=kv_kind, sparse_k=5, cand_cap=6)
+    _, hpT = orc.lsh_init(hd, 42)
+    cos_t, sin_t = orc.rope_table(hd, cfg["max_seq"], cfg["theta"])
+    T = 12 * PAGE + 3                      # 13 pages > sparse_k
+    tokens = rng.integers(0, vocab, T)
+    fk = rng.standard_normal((n_layers, T, KV * hd)).astype(np.float32)
+    fv = rng.standard_normal((n_layers, T, KV * hd)).astype(np.float32)
+    planted = rng.choice(np.arange(1, 11), size=4, replace=False)
+    for li in range(n_layers):
+        # probe: this layer's q at the last step, given the layers planted so far
+        _, _, qs = routed_forward(orc, cfg, w, tokens, cos_t, sin_t, hpT, fk, fv)
+        qm = qs[li].reshape(H, hd).mean(0)
+        u = 6.0 * qm / np.linalg.norm(qm)
+        for pg in planted:
+            for h in range(KV):
+                fk[li, pg * PAGE:(pg + 1) * PAGE, h * hd:(h + 1) * hd] = \
+                    (u + 0.05 * rng.standard_normal((PAGE, hd))).astype(np.float32)
+    want, want_sel, _ = routed_forward(orc, cfg, w, tokens, cos_t, sin_t, hpT, fk, fv)
+    dec = OracleDecoder(orc, cfg, w, hpT)
+    for pos, tok in enumerate(tokens):
+        if pos == T - 1:
+            dec.log_selection()
+        nxt, logits = dec.step(tok, pos, force_k=fk[:, pos], force_v=fv[:, pos])
+        assert nxt == orc.argmax(logits)
+        err = np.max(np.abs(logits - want[pos])) / np.max(np.abs(want[pos]))
+        assert err < 2e-3, (pos, err)
+    for li in range(n_layers):
+        got = dec.last_selection(li)
+        np.testing.assert_array_equal(got, want_sel[li], err_msg=f"layer {li}")
+        # the planted pages fill the candidate list and the heap keeps k - 2 of them
+        assert len(got) == cfg["sparse_k"] and len(set(got) & set(int(p) for p in planted)) >= 3
