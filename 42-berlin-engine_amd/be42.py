@@ -40,6 +40,7 @@ SIGNATURES = {
     "be42_gemv_q8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemv_fp8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemv_prepared_multi": (i32, [vp, i32, vp, i32, i32, i32, vp]),
+    "be42_gemv_noalloc": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, vp]),
     "be42_lsh_attention": (i32, [vp, vp, vp, i32, i32, i32, i32, f32, vp, vp, vp, i32, vp]),
     "be42_gemm_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),

@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 #include "be42_common.h"
@@ -1352,9 +1353,80 @@ static int gemv_launch(float *y, const uint8_t *w, const float *sw, const float 
     return prepared_launch<FP8>(y, w, sw, buf, n, k, batch, s);
 }
 
+// ---- GEMV without allocation ------------------------------------------------------
+// be42_gemv_noalloc keeps its digit planes in a fixed device array instead of
+// the grow-only workspace.  Each GPU holds its own copy for the life of the
+// process; host code reaches it only through the address hipGetSymbolAddress
+// returns for the current device (the array's name is a host-side stand-in).
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_dev[kMaxDevices];
+
+// Look up the scratch address of `device` (which must be current).
+int gemv_scratch_init(int device)
+{
+    BE42_CHECK(device >= 0 && device < kMaxDevices, "gemv scratch: device %d out of range", device);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_dev[device])
+        return BE42_OK;
+    void *p = nullptr;
+    BE42_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    BE42_CHECK(p != nullptr, "gemv scratch: no device address for device %d", device);
+    g_scratch_dev[device] = p;
+    return BE42_OK;
+}
+
+static int gemv_scratch(void **out)
+{
+    int dev = 0;
+    BE42_HIP(hipGetDevice(&dev));
+    const int rc = gemv_scratch_init(dev);
+    if (rc)
+        return rc;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    *out = g_scratch_dev[dev];
+    return BE42_OK;
+}
+
 }  // namespace be42
 
 using namespace be42;
+
+extern "C" int be42_gemv_noalloc(float *y, const void *w, const float *w_scale, const float *x, int n, int k,
+                                 int batch, int fp8, void *stream)
+{
+    BE42_CHECK(y && w && w_scale && x, "be42_gemv_noalloc: null pointer");
+    BE42_CHECK(n >= 0 && k > 0 && batch >= 0, "be42_gemv_noalloc: bad shape n=%d k=%d batch=%d", n, k, batch);
+    if (n == 0 || batch == 0)
+        return BE42_OK;
+    hipStream_t s = as_stream(stream);
+    const uint8_t *wb = (const uint8_t *)w;
+    if (!fast_path(w, k, batch) || !x_aligned(x)) {
+        // the per-row kernel reads x directly and needs no scratch
+        if (fp8)
+            hipLaunchKernelGGL(k_gemv_generic<true>, dim3(n), dim3(256), 0, s, y, wb, w_scale, x, n, k, batch);
+        else
+            hipLaunchKernelGGL(k_gemv_generic<false>, dim3(n), dim3(256), 0, s, y, wb, w_scale, x, n, k, batch);
+        BE42_LAUNCH_CHECK();
+        return BE42_OK;
+    }
+    const size_t need = xdig_bytes(k, batch, fp8 != 0);
+    BE42_CHECK(need <= kNoAllocScratchBytes,
+               "be42_gemv_noalloc: k=%d at batch %d needs %zu bytes of digit planes, more than the %zu-byte scratch "
+               "(use be42_gemv_%s)", k, batch, need, kNoAllocScratchBytes, fp8 ? "fp8" : "q8");
+    void *buf = nullptr;
+    int rc = gemv_scratch(&buf);
+    if (rc)
+        return rc;
+    rc = prepare_launch(buf, x, k, batch, fp8 != 0, s);
+    if (rc)
+        return rc;
+    return fp8 ? prepared_launch<true>(y, wb, w_scale, buf, n, k, batch, s)
+               : prepared_launch<false>(y, wb, w_scale, buf, n, k, batch, s);
+}
 
 extern "C" int be42_gemv_q8(float *y, const int8_t *w, const float *w_scale, const float *x, int n,
                             int k, int batch, void *stream)

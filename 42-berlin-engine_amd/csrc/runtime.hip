@@ -25,6 +25,7 @@ int hip_fail(hipError_t e, const char *what, const char *file, int line)
 }
 
 int upload_fp8_thresholds(int device);
+int gemv_scratch_init(int device);
 
 // Grow-only workspace per device.  Growth synchronises the stream first so
 // that no queued kernel still reads the old buffer when it is freed.
@@ -83,6 +84,9 @@ extern "C" int be42_init(int device)
     }
     BE42_CHECK(device >= 0 && device < n, "be42_init: device %d out of range (%d devices)", device, n);
     BE42_HIP(hipSetDevice(device));
+    const int rc = gemv_scratch_init(device);
+    if (rc)
+        return rc;
     return upload_fp8_thresholds(device);
 }
 

@@ -79,6 +79,18 @@ int be42_gemv_q8_prepared(float *y, const int8_t *w, const float *w_scale, const
                           int n, int k, int batch, void *stream);
 int be42_gemv_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, const void *xdig,
                            int n, int k, int batch, void *stream);
+/* be42_gemv_q8 / be42_gemv_fp8 (fp8 = 0 / 1) without any allocation.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  The digit planes live in a fixed 8 MiB device array per GPU,
+ * held until the process ends, so k * batch is limited to what fits:
+ * be42_gemv_xdig_bytes(k, batch, fp8) <= 8 MiB (k <= 104,448 at batch 16
+ * for FP8, 174,080 for INT8), else BE42_EINVAL.  Same kernels and results as
+ * the allocating entry points.  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (two streams, two threads) race. */
+int be42_gemv_noalloc(float *y, const void *w, const float *w_scale, const float *x, int n, int k, int batch,
+                      int fp8, void *stream);
+
 /* Several weight matrices of one kind and one k that share a prepared input
  * (the q/k/v or gate/up projections of a decode step), streamed in one
  * launch: up to 3 segments, segment i writes y [batch][n]. */
