@@ -57,144 +57,142 @@ __global__ __launch_bounds__(256) void k_embed(float *__restrict__ x, const uint
     x[(size_t)b * dim + i] = v * emb_s[tok];
 }
 
-// block-wide max of non-negative values (blockDim.x a multiple of 64, <= 1024)
-__device__ __forceinline__ float block_max(float v, float *red)
-{
-    v = wave_max(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if (lane == 0)
-        red[wave] = v;
-    __syncthreads();
-    float r = 0.0f;
-    for (int w = 0; w < nw; w++)
-        r = fmaxf(r, red[w]);
-    return r;
-}
+// Row kernels of the decode step (RMSNorm, SiLU*up), written straight as the
+// next GEMV's digit planes.  The digit scale needs the row's max |h|, so a row
+// is spread over workgroups this way: block (c, b) of a row of n elements
+// evaluates the whole row in registers (thread t holds float4 number
+// t + kRowT * j, j < NV) and reduces it itself, then writes only chunk c of the
+// digit planes (elements [kChunk c, kChunk (c + 1)), zero past n; kChunk is
+// the planes' burst, so the chunks tile the padded row).  Every block thus
+// takes the row's few KiB from L2 and does a little redundant arithmetic,
+// instead of one block doing the whole row's digit split.
+constexpr int kRowT = 256;
+constexpr int kChunk = 4 * kRowT;
+constexpr int kRowNV = 16;                       // rows up to 16384 elements
+constexpr int kRowMax = kChunk * kRowNV;
 
-// Row kernels (one block of kRowThreads per batch row) keep the row in
-// registers: thread t owns the float4 number t + kRowThreads * j (j < NV) of
-// the row, and every global load of the row is issued before the first is
-// waited on -- one memory round trip per kernel instead of one per loop trip.
-// NV = ceil(n / 4096) covers rows up to kRowMax elements (n % 16 == 0).
-constexpr int kRowThreads = 1024;
-constexpr int kRowMax = 4 * 4 * kRowThreads;
+__device__ __forceinline__ float f4_absmax(float4 a)
+{
+    return fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
+}
 
 __device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
-// Write row b of the GEMV digit planes from the row's registers (zero past n).
+// block (kRowT threads) reductions; every thread gets the result
+__device__ __forceinline__ float block_sum4(float v, float *red)
+{
+    v = wave_sum_dpp(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float block_max4(float v, float *red)
+{
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+        red[4 + (threadIdx.x >> 6)] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+}
+
+// chunk c of row b's digit planes (and fp32 out) from the row in registers
 template <bool FP8, int NV>
-__device__ __forceinline__ void row_digits_reg(const float4 (&h)[NV], int n, uint8_t *dig, int B, int b, float *red)
+__device__ __forceinline__ void row_chunk_digits(const float4 (&h)[NV], int n, uint8_t *__restrict__ dig,
+                                                 float *__restrict__ out, int B, int b, int c, float *red)
 {
     float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; j++)
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(h[j].x), fabsf(h[j].y)), fmaxf(fabsf(h[j].z), fabsf(h[j].w))));
-    const float amax = block_max(m, red);
-    const float s = digit_scale<FP8>(amax);
+        m = fmaxf(m, f4_absmax(h[j]));
+    const float amax = block_max4(m, red);
+    const float sc = digit_scale<FP8>(amax);
     const int Kp = (int)xdig_kp(n, FP8);
-    if (threadIdx.x == 0)
-        xdig_scales(dig, n, B, FP8)[b] = s;
+    if (c == 0 && threadIdx.x == 0)
+        xdig_scales(dig, n, B, FP8)[b] = sc;
+    const int i = (int)threadIdx.x + kRowT * c, k0 = 4 * i;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int k0 = 4 * ((int)threadIdx.x + kRowThreads * j);
-        if (k0 < Kp) {
-            const float xe[4] = {h[j].x, h[j].y, h[j].z, h[j].w};
-            store_digit_words<FP8>(xe, s, dig, B, Kp, b, k0);
+        if (j == c) {
+            if (k0 < Kp) {
+                const float xe[4] = {h[j].x, h[j].y, h[j].z, h[j].w};
+                store_digit_words<FP8>(xe, sc, dig, B, Kp, b, k0);
+            }
+            if (out && 4 * i < n)
+                ((float4 *)(out + (size_t)b * n))[i] = h[j];
         }
     }
 }
 
-// xn = rmsnorm(x [+ delta]) per row b, written as GEMV digit planes (and, if
-// out != NULL, as fp32); with delta, x is updated in place first (the
-// residual add of inference.c:525/:577 fused with the next norm).  The sum
-// of squares follows compute_rms_f32_avx2: 8 FMA chains (chain l over
-// i = l (mod 8), in order), ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7)), fused
-// scalar remainder; ss / dim; inv = 1 / sqrtf(ss + eps); (x * inv) * w.
-// The chains run on 8 lanes from LDS (xs, dim rounded up to 256 with zeros,
-// whose products add exact zeros), 32 loads ahead of their FMAs.
+// xn = rmsnorm(x [+ delta]) of row b (op_rmsnorm, ops_norm.c:126-138):
+// ss = sum x^2, inv = 1 / sqrtf(ss / dim + eps), h = (x * inv) * w.  With
+// delta the residual add of inference.c:525/:577 comes first and the sum
+// x + delta is written to x_out (chunk c by block c; x_out is not x, so no
+// block reads a value another has already updated).  The sum of squares is
+// a tree (per-thread fused multiply-adds, then DPP and LDS sums), not the
+// reference's 8 sequential lanes: equal to fp32 rounding, far inside the
+// decode tolerance.
 template <bool FP8, int NV>
-__global__ __launch_bounds__(kRowThreads) void k_rmsnorm(float *__restrict__ out, uint8_t *__restrict__ dig,
-                                                        float *__restrict__ x, const float *__restrict__ delta,
-                                                        const uint16_t *__restrict__ w, int dim, int B, float eps)
+__global__ __launch_bounds__(kRowT) void k_rmsnorm(float *__restrict__ out, uint8_t *__restrict__ dig,
+                                                  const float *__restrict__ x, float *__restrict__ x_out,
+                                                  const float *__restrict__ delta, const uint16_t *__restrict__ w,
+                                                  int dim, int B, float eps)
 {
-    extern __shared__ float xs[];
-    __shared__ float inv_s, red[16];
-    const int b = blockIdx.x, n4 = dim >> 2, dimp = (dim + 255) & ~255;
-    float4 *x4 = (float4 *)(x + (size_t)b * dim);
+    __shared__ float red[8];
+    const int b = blockIdx.y, c = blockIdx.x, n4 = dim >> 2;
+    const float4 *x4 = (const float4 *)(x + (size_t)b * dim);
     const float4 *d4 = delta ? (const float4 *)(delta + (size_t)b * dim) : nullptr;
     const uint2 *w4 = (const uint2 *)w;
     float4 v[NV], dv[NV];
     uint2 wv[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = min((int)threadIdx.x + kRowThreads * j, n4 - 1);
+        const int i = min((int)threadIdx.x + kRowT * j, n4 - 1);
         v[j] = x4[i];
         wv[j] = w4[i];
         if (d4)
             dv[j] = d4[i];
     }
+    float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = threadIdx.x + kRowThreads * j;
+        const int i = threadIdx.x + kRowT * j;
         if (d4) {
             v[j] = make_float4(v[j].x + dv[j].x, v[j].y + dv[j].y, v[j].z + dv[j].z, v[j].w + dv[j].w);
-            if (i < n4)
-                x4[i] = v[j];
+            if (j == c && i < n4)
+                ((float4 *)(x_out + (size_t)b * dim))[i] = v[j];
         }
         if (i >= n4)
             v[j] = f4_zero();
-        if (4 * i < dimp)
-            ((float4 *)xs)[i] = v[j];
+        ss = __fmaf_rn(v[j].x, v[j].x, ss);
+        ss = __fmaf_rn(v[j].y, v[j].y, ss);
+        ss = __fmaf_rn(v[j].z, v[j].z, ss);
+        ss = __fmaf_rn(v[j].w, v[j].w, ss);
     }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        float s = 0.0f;
-        if (lane < 8) {
-            for (int c0 = 0; c0 < dimp; c0 += 8 * 32) {
-                float t[32];
-#pragma unroll
-                for (int j = 0; j < 32; j++)
-                    t[j] = xs[c0 + lane + 8 * j];
-#pragma unroll
-                for (int j = 0; j < 32; j++)
-                    s = __fmaf_rn(t[j], t[j], s);
-            }
-        }
-        const float t = s + __shfl_down(s, 4, 8);
-        const float u = t + __shfl_down(t, 1, 8);
-        float ss = u + __shfl_down(u, 2, 8);
-        if (lane == 0) {
-            for (int i = dim & ~7; i < dim; i++)
-                ss = __fmaf_rn(xs[i], xs[i], ss);
-            ss = __fdiv_rn(ss, (float)dim);
-            inv_s = __fdiv_rn(1.0f, __fsqrt_rn(ss + eps));
-        }
-    }
-    __syncthreads();
-    const float inv = inv_s;
+    ss = block_sum4(ss, red);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)dim) + eps));
     float4 h[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = threadIdx.x + kRowThreads * j;
         const uint2 wj = wv[j];
         h[j] = make_float4((v[j].x * inv) * bf16_to_f32((uint16_t)(wj.x & 0xFFFF)),
                            (v[j].y * inv) * bf16_to_f32((uint16_t)(wj.x >> 16)),
                            (v[j].z * inv) * bf16_to_f32((uint16_t)(wj.y & 0xFFFF)),
                            (v[j].w * inv) * bf16_to_f32((uint16_t)(wj.y >> 16)));
-        if (i >= n4)
+        if ((int)threadIdx.x + kRowT * j >= n4)
             h[j] = f4_zero();
-        else if (out)
-            ((float4 *)(out + (size_t)b * dim))[i] = h[j];
     }
-    row_digits_reg<FP8, NV>(h, dim, dig, B, b, red);
+    row_chunk_digits<FP8, NV>(h, dim, dig, out, B, b, c, red);
 }
 
 // h = (g * sigmoid(g)) * u for row b (op_silu_mul_fused_f32): blocks of 8 use
 // the vector Schraudolph exp (clamp, fused multiply-add, round to nearest),
 // the n % 8 remainder the scalar one; written as GEMV digit planes of the
-// down projection (and to out if not NULL).
+// down projection (and to out if not NULL).  Element for element the
+// reference's arithmetic.
 __device__ __forceinline__ float silu_mul1(float gv, float uv, bool vec)
 {
     float e;
@@ -211,32 +209,30 @@ __device__ __forceinline__ float silu_mul1(float gv, float uv, bool vec)
 }
 
 template <bool FP8, int NV>
-__global__ __launch_bounds__(kRowThreads) void k_silu_mul(float *__restrict__ out, uint8_t *__restrict__ dig,
-                                                         const float *__restrict__ g, const float *__restrict__ u,
-                                                         int n, int B)
+__global__ __launch_bounds__(kRowT) void k_silu_mul(float *__restrict__ out, uint8_t *__restrict__ dig,
+                                                   const float *__restrict__ g, const float *__restrict__ u, int n,
+                                                   int B)
 {
-    __shared__ float red[16];
-    const int b = blockIdx.x, n4 = n >> 2, nvec = n & ~7;
+    __shared__ float red[8];
+    const int b = blockIdx.y, c = blockIdx.x, n4 = n >> 2, nvec = n & ~7;
     const float4 *g4 = (const float4 *)(g + (size_t)b * n), *u4 = (const float4 *)(u + (size_t)b * n);
     float4 gv[NV], uv[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = min((int)threadIdx.x + kRowThreads * j, n4 - 1);
+        const int i = min((int)threadIdx.x + kRowT * j, n4 - 1);
         gv[j] = g4[i];
         uv[j] = u4[i];
     }
     float4 h[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = threadIdx.x + kRowThreads * j, e0 = 4 * i;
+        const int i = threadIdx.x + kRowT * j, e0 = 4 * i;
         h[j] = make_float4(silu_mul1(gv[j].x, uv[j].x, e0 < nvec), silu_mul1(gv[j].y, uv[j].y, e0 + 1 < nvec),
                            silu_mul1(gv[j].z, uv[j].z, e0 + 2 < nvec), silu_mul1(gv[j].w, uv[j].w, e0 + 3 < nvec));
         if (i >= n4)
             h[j] = f4_zero();
-        else if (out)
-            ((float4 *)(out + (size_t)b * n))[i] = h[j];
     }
-    row_digits_reg<FP8, NV>(h, n, dig, B, b, red);
+    row_chunk_digits<FP8, NV>(h, n, dig, out, B, b, c, red);
 }
 
 // argmax_simd_f32: the maximum value wins; among equal maxima in the
@@ -570,20 +566,22 @@ static int gemv_multi(be42_decoder *d, std::initializer_list<be42_gemv_seg> segs
     } while (0)
 
 // Calls f(integral_constant FP8, integral_constant NV) for a row of n
-// elements (n <= kRowMax).
+// elements (n <= kRowMax), NV = ceil(n / kChunk).
 template <class F>
 static void launch_rows(bool fp8, int n, F &&f)
 {
     using T = std::true_type;
     using Fa = std::false_type;
-    const int nv = (n + 4095) / 4096;
+    const int nv = (n + kChunk - 1) / kChunk;
     auto pick = [&](auto f8) {
-        switch (nv) {
-        case 1: f(f8, std::integral_constant<int, 1>()); break;
-        case 2: f(f8, std::integral_constant<int, 2>()); break;
-        case 3: f(f8, std::integral_constant<int, 3>()); break;
-        default: f(f8, std::integral_constant<int, 4>()); break;
-        }
+        if (nv <= 1) f(f8, std::integral_constant<int, 1>());
+        else if (nv <= 2) f(f8, std::integral_constant<int, 2>());
+        else if (nv <= 3) f(f8, std::integral_constant<int, 3>());
+        else if (nv <= 4) f(f8, std::integral_constant<int, 4>());
+        else if (nv <= 6) f(f8, std::integral_constant<int, 6>());
+        else if (nv <= 8) f(f8, std::integral_constant<int, 8>());
+        else if (nv <= 12) f(f8, std::integral_constant<int, 12>());
+        else f(f8, std::integral_constant<int, 16>());
     };
     if (fp8)
         pick(T());
@@ -614,14 +612,20 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         hipLaunchKernelGGL(k_embed<false>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, tok,
                            dim);
     BE42_LAUNCH_CHECK();
-    const size_t norm_lds = (size_t)((dim + 255) & ~255) * 4;
     uint8_t *dig = (uint8_t *)d->xdig;
+    // the residual stream alternates between x and xn: a norm with a pending
+    // delta writes x + delta to the other buffer
+    float *xcur = d->x, *xalt = d->xn;
     // RMSNorm (+ residual) straight into the GEMV digit planes
     auto norm = [&](const uint16_t *wn, const float *delta) {
+        float *xo = delta ? xalt : nullptr;
         launch_rows(fp8, dim, [&](auto f8, auto nv) {
-            hipLaunchKernelGGL((k_rmsnorm<decltype(f8)::value, decltype(nv)::value>), dim3(B), dim3(kRowThreads),
-                               norm_lds, st, nullptr, dig, d->x, delta, wn, dim, B, c.norm_eps);
+            hipLaunchKernelGGL((k_rmsnorm<decltype(f8)::value, decltype(nv)::value>),
+                               dim3((dim + kChunk - 1) / kChunk, B), dim3(kRowT), 0, st, nullptr, dig, xcur, xo,
+                               delta, wn, dim, B, c.norm_eps);
         });
+        if (delta)
+            std::swap(xcur, xalt);
         return hipGetLastError();
     };
     const float scale = 1.0f / sqrtf((float)hd);
@@ -679,8 +683,9 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         BE42_HIP(norm(L.ffn_norm, d->xb));                 // x += attention output
         DEC_TRY(gemv_multi(d, {{L.w1, L.s1, d->hb, c.hidden_dim}, {L.w3, L.s3, d->hb2, c.hidden_dim}}, dim, B, st));
         launch_rows(fp8, c.hidden_dim, [&](auto f8, auto nv) {
-            hipLaunchKernelGGL((k_silu_mul<decltype(f8)::value, decltype(nv)::value>), dim3(B), dim3(kRowThreads),
-                               0, st, nullptr, dig, d->hb, d->hb2, c.hidden_dim, B);
+            hipLaunchKernelGGL((k_silu_mul<decltype(f8)::value, decltype(nv)::value>),
+                               dim3((c.hidden_dim + kChunk - 1) / kChunk, B), dim3(kRowT), 0, st, nullptr, dig, d->hb,
+                               d->hb2, c.hidden_dim, B);
         });
         BE42_LAUNCH_CHECK();
         DEC_TRY(gemv(d, d->xb, L.w2, L.s2, dim, c.hidden_dim, B, st));

@@ -14,6 +14,12 @@
 //     position (or the root) takes s.
 // The array order after every push equals the reference's.  Scores must not
 // be NaN.
+//
+// WaveHeapKey runs the same heap on packed integer keys (rank << 8 | entry):
+// when every score to be pushed is known up front, its rank among them (the
+// number of strictly smaller scores, so equal scores share a rank) orders the
+// keys exactly as the scores, ties included, and a sift-up moves one 32-bit
+// key per lane -- one shuffle per push instead of two.
 #pragma once
 
 #include "be42_common.h"
@@ -79,6 +85,79 @@ struct WaveHeap {
                     hs = s;
                     hi = e;
                 }
+            }
+        }
+    }
+};
+
+// Rank of each of n scores held as sc[0..n) (n <= 256): the number of
+// strictly smaller ones.  Lane l returns the ranks of entries l, l+64, ...
+// in r[0..3].
+__device__ __forceinline__ void wave_ranks(const float *sc, int n, int (&r)[4])
+{
+    const int lane = threadIdx.x & 63;
+    float own[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        own[j] = lane + 64 * j < n ? sc[lane + 64 * j] : 0.0f;
+        r[j] = 0;
+    }
+    for (int u0 = 0; u0 < n; u0 += 64) {
+        const float sv = u0 + lane < n ? sc[u0 + lane] : 0.0f;
+        const int c = min(64, n - u0);
+        for (int u = 0; u < c; u++) {
+            const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), u));
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                r[j] += x < own[j] ? 1 : 0;
+        }
+    }
+}
+
+struct WaveHeapKey {
+    int hk = 0;        // key of slot `lane`: rank << 8 | payload
+    int size = 0;      // uniform
+    int cap;           // uniform, <= kHeapMax
+    int lane, par, cl, cr;
+
+    __device__ explicit WaveHeapKey(int capacity) : cap(capacity)
+    {
+        lane = threadIdx.x & 63;
+        par = lane > 0 ? (lane - 1) >> 1 : 0;
+        cl = (2 * lane + 1) & 63;
+        cr = (2 * lane + 2) & 63;
+    }
+
+    __device__ __forceinline__ int payload() const { return hk & 0xFF; }
+
+    // heap_push with the score of rank `rank` (uniform) and payload e < 256
+    __device__ __forceinline__ void push(int rank, int e)
+    {
+        const int k = (rank << 8) | e;
+        const int kr = rank;
+        if (size < cap) {
+            const int pk = __shfl(hk, par, 64);
+            if (heap_on_path(size + 1, lane + 1)) {
+                if (lane > 0 && (pk >> 8) > kr)
+                    hk = pk;
+                else if (lane == size || (hk >> 8) > kr)
+                    hk = k;
+            }
+            size++;
+        } else if (kr > (__builtin_amdgcn_readlane(hk, 0) >> 8)) {
+            const int kl = __shfl(hk, cl, 64), krr = __shfl(hk, cr, 64);
+            const bool hasl = 2 * lane + 1 < size;
+            const bool right = 2 * lane + 2 < size && (krr >> 8) < (kl >> 8);
+            const unsigned long long mh = __ballot(hasl), mr = __ballot(right);
+            int end = 0;
+            while ((mh >> end) & 1ull)
+                end = 2 * end + 1 + (int)((mr >> end) & 1ull);
+            if (heap_on_path(end + 1, lane + 1)) {
+                const int ck = right ? krr : kl;
+                if (hasl && (ck >> 8) < kr)
+                    hk = ck;
+                else if (lane == 0 || (hk >> 8) < kr)
+                    hk = k;
             }
         }
     }

@@ -323,14 +323,20 @@ __device__ __forceinline__ int route_select(int k_sel, int cap, const RouteView 
     int ak = min(k_sel - 2, min(nm, kHeapMax));
     if (k_sel <= 2 || nm == 0)
         ak = 0;
-    WaveHeap heap(ak);
+    // every middle score is known before the first push: the heap runs on
+    // (rank, entry) keys, which order exactly as the scores
+    int rk[4];
+    if (ak > 0)
+        wave_ranks(V.sc, nm, rk);
+    WaveHeapKey heap(ak);
     for (int e0 = 0; e0 < nm && ak > 0; e0 += kWave) {
-        const float sv = e0 + lane < nm ? V.sc[e0 + lane] : 0.0f;
+        const int j = e0 >> 6;
+        const int rv = j == 0 ? rk[0] : (j == 1 ? rk[1] : (j == 2 ? rk[2] : rk[3]));
         const int ecnt = min(kWave, nm - e0);
         for (int u = 0; u < ecnt; u++)
-            heap.push(rlf(sv, u), e0 + u);
+            heap.push(rl(rv, u), e0 + u);
     }
-    const int size = heap.size, hi = heap.hi;
+    const int size = heap.size, hi = heap.payload();
     if (lane < size) {
         if (selb)
             selb[ns + lane] = V.mpt[hi];

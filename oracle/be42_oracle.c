@@ -1080,6 +1080,19 @@ void or_decoder_log_selection(or_decoder *d, int *sel, int *nsel)
     d->nsel_log = nsel;
 }
 
+int or_decoder_route(or_decoder *d, int layer, const float *q, int *sel_logical)
+{
+    const or_decoder_cfg *c = &d->c;
+    int *sel = malloc(sizeof(int) * (size_t)(d->kv.max_logical + 2));
+    int nc = 0;
+    int ns = or_route_pages(sel, &nc, NULL, &d->kv, layer, q, c->n_heads, d->hpT, &d->ix[layer], c->cand_cap,
+                            c->sparse_k);
+    for (int i = 0; i < ns; i++)
+        sel_logical[i] = d->kv.start_pos[sel[i]] / OR_PAGE_TOKENS;
+    free(sel);
+    return ns;
+}
+
 /* paged_kv_append plus the page index: a page that fills is hashed (its
  * centroid under the projection) and inserted as logical page id. */
 int or_decoder_kv_append(or_decoder *d, int layer, const float *k, const float *v, int pos)

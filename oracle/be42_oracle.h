@@ -215,6 +215,10 @@ void or_decoder_force_kv(or_decoder *d, const float *k, const float *v);
  * attended in attention order (sel [n_layers][sparse_k]) and their count
  * (nsel [n_layers]); NULL stops it. */
 void or_decoder_log_selection(or_decoder *d, int *sel, int *nsel);
+/* Test hook: the page selection the decoder's route makes for layer `layer`
+ * and the given rotated query q [n_heads*hd] over its current cache, as
+ * logical page ids in attention order; returns their count. */
+int  or_decoder_route(or_decoder *d, int layer, const float *q, int *sel_logical);
 
 #ifdef __cplusplus
 }

@@ -120,6 +120,14 @@ class OracleDecoder:
     def last_selection(self, layer):
         return self.sel_log[layer, :self.nsel_log[layer]].copy()
 
+    def route(self, layer, q):
+        """The decoder's route for `layer` and rotated query q over its current
+        cache: logical pages in attention order."""
+        out = np.zeros(max(self.cfg.sparse_k, 64) + 2, np.int32)
+        n = self.o.lib.or_decoder_route(self.buf, layer, np.ascontiguousarray(q, np.float32).ctypes.data,
+                                        out.ctypes.data)
+        return out[:n].copy()
+
     def kv_append_n(self, layer, k, v, pos0):
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
@@ -199,6 +207,7 @@ class Oracle:
         _sig(L, "or_decoder_force_kv", None, C.c_void_p, C.c_void_p, C.c_void_p)
         _sig(L, "or_decoder_kv_append_n", C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int)
         _sig(L, "or_decoder_log_selection", None, C.c_void_p, C.c_void_p, C.c_void_p)
+        _sig(L, "or_decoder_route", C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p)
         _sig(L, "or_paged_alloc", C.c_int, C.POINTER(OrPaged))
         _sig(L, "or_paged_release", None, C.POINTER(OrPaged), C.c_int)
         _sig(L, "or_score_blocks", None, C.c_void_p, f32p, C.POINTER(OrPaged), C.c_int, C.c_int)

@@ -10,7 +10,11 @@ steps as the benchmark does), so every layer routes through full candidate
 lists to 64 pages.  The oracle appends the step's K/V rows the GPU computed
 (captured per layer) so both caches hold the same codes; then the greedy
 tokens must be identical and the logits within the north star's 1e-3
-(max|dl| / max|l|), and every layer's selection is the oracle route's."""
+(max|dl| / max|l|).  Every layer's selection is bit-exact (pages and order)
+against the oracle's route given the GPU's query of that layer; against the
+oracle's own run it is the same set of pages (its queries differ from the
+GPU's by fp32 rounding, so two middle pages whose scores are within that
+rounding may take each other's place in the heap order)."""
 import numpy as np
 import pytest
 import torch
@@ -125,12 +129,14 @@ def test_3b_decode_step_at_32k(be, orc):
         on, ol = oracles[b].step(toks[b], T, force_k=hk[:, b], force_v=hv[:, b])
         err = rel_err(lg[b], ol)
         print(f"3b: seq {b} token gpu {int(nxt[b])} oracle {on} logits rel err {err:.2e}", flush=True)
+        qs = cq[:, b].cpu().numpy()
         for l in range(L):
             # physical -> logical through the GPU pool's page table of this slot
             phys = dec.pool.layer_pages(l * B + b)
             logical = {int(p): i for i, p in enumerate(phys)}
             got = [logical[int(p)] for p in sel[l, b, :nsel[l, b]]]
-            np.testing.assert_array_equal(got, oracles[b].last_selection(l), err_msg=f"layer {l} seq {b}")
+            np.testing.assert_array_equal(got, oracles[b].route(l, qs[l]), err_msg=f"layer {l} seq {b}")
+            assert set(got) == set(oracles[b].last_selection(l).tolist()), (l, b)
         assert int(nxt[b]) == on
         assert err <= 1e-3
     dec.close()
