@@ -68,6 +68,11 @@ SIGNATURES = {
     "be42_lsh_route": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp, vp]),
     "be42_attn_workspace_bytes": (sz, [i32, i32, i32, i32, i32]),
     "be42_paged_attention": (i32, [vp, vp, i32, i32, vp, vp, i32, i32, f32, vp, i32, vp, sz, vp]),
+    "be42_kv_linear_append": (i32, [vp, vp, i32, vp, vp, i32, vp]),
+    "be42_linear_attention_workspace_bytes": (sz, [i32, i32, i32, i32]),
+    "be42_linear_attention": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, vp, sz, vp]),
+    "be42_lsh_route_tokens": (i32, [vp, i32, vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]),
+    "be42_kv_linear_evict": (i32, [vp, vp, i32, i32, i32, vp, vp, i32, vp, vp]),
 }
 
 KV_INT8, KV_BF16 = 0, 1
@@ -299,6 +304,44 @@ class Lib:
         self._call("be42_paged_attention", pool.handle, self.p(q), B, H, self.p(sel), self.p(nsel),
                    sel.shape[1], max_sel, float(scale), self.p(out), n_split, ws, wsb, self.stream())
         return out
+
+    # -- linear KV cache [T][n_kv][head_dim] bf16 (kv_cache.c) ------------------
+    def kv_linear_append(self, k_cache, v_cache, pos, k, v, stream=None):
+        """Row `pos` of the bf16 caches from fp32 k, v [n_kv * head_dim]."""
+        row = k.numel()
+        self._call("be42_kv_linear_append", self.p(k_cache), self.p(v_cache), pos, self.p(k), self.p(v), row,
+                   self.stream(stream))
+
+    def linear_attention(self, q, k_cache, v_cache, n_tok, n_heads, scale, idx=None, out=None, stream=None):
+        """Online-softmax attention of q [n_heads * head_dim] over tokens idx
+        (or 0 .. n_tok-1) of the caches [T][n_kv][head_dim]."""
+        t = self.torch
+        n_kv, hd = k_cache.shape[1], k_cache.shape[2]
+        out = out if out is not None else t.empty(n_heads * hd, dtype=t.float32, device=q.device)
+        self._call("be42_linear_attention", self.p(out), self.p(q), self.p(k_cache), self.p(v_cache), self.p(idx),
+                   n_tok, n_heads, n_kv, hd, float(scale), None, 0, self.stream(stream))
+        return out
+
+    def lsh_route_tokens(self, k_cache, kv_len, q, n_heads, hpT, hashes, starts, lens, window, sparse_k,
+                         stream=None):
+        """Token route (window + LSH candidate blocks, top sparse_k by the
+        bf16 dot); returns (positions [sparse_k] device, count)."""
+        t = self.torch
+        n_kv, hd = k_cache.shape[1], k_cache.shape[2]
+        topk = t.full((max(sparse_k, 1),), -1, dtype=t.int32, device=q.device)
+        n = t.zeros(1, dtype=t.int32, device=q.device)
+        self._call("be42_lsh_route_tokens", self.p(k_cache), kv_len, self.p(q), n_heads, n_kv, hd, self.p(hpT),
+                   self.p(hashes), self.p(starts), self.p(lens), 0 if hashes is None else hashes.numel(), window,
+                   sparse_k, self.p(topk), self.p(n), self.stream(stream))
+        return topk, n
+
+    def kv_linear_evict(self, k_cache, v_cache, n, q, w, keep_k, stream=None):
+        """kv_cache_evict in place on the device caches; returns the new length."""
+        heads, dim = k_cache.shape[1], k_cache.shape[2]
+        new_len = C.c_int(n)
+        self._call("be42_kv_linear_evict", self.p(k_cache), self.p(v_cache), n, heads, dim, self.p(q), self.p(w),
+                   keep_k, C.byref(new_len), self.stream(stream))
+        return new_len.value
 
 
 class KVPool:

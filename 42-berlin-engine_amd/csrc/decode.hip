@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kRowT) void k_rmsnorm(float *__restrict__ out, uint
         ss = __fmaf_rn(v[j].w, v[j].w, ss);
     }
     ss = block_sum4(ss, red);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)dim) + eps));
+    const float inv = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(ss, (float)dim) + eps));
     float4 h[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {

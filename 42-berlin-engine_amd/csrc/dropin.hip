@@ -273,6 +273,239 @@ __global__ void k_lightning(float *__restrict__ out, const uint8_t *__restrict__
     }
 }
 
+
+// ---- decode-step adjacents ---------------------------------------------------------
+
+// op_rmsnorm row by row (ops_norm.c:27-138), one wave per row, the
+// reference's arithmetic: 8 FMA chains (chain l over j = l mod 8 below
+// 8 * floor(dim / 8)), ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7)), fused scalar
+// remainder, ss / dim, 1 / sqrtf(ss + eps), out = (x * inv) * w.
+__global__ __launch_bounds__(64) void k_rmsnorm_rows(float *__restrict__ out, const float *__restrict__ x,
+                                                     const uint16_t *__restrict__ w, int dim, float eps)
+{
+    const int lane = threadIdx.x;
+    const float *r = x + (size_t)blockIdx.x * dim;
+    float *o = out + (size_t)blockIdx.x * dim;
+    const int d8 = dim & ~7;
+    float s = 0.0f;
+    if (lane < 8)
+        for (int j = lane; j < d8; j += 8)
+            s = __fmaf_rn(r[j], r[j], s);
+    const float a = s + __shfl_down(s, 4, 8);          // lanes 0-3: s_l + s_(l+4)
+    const float b = a + __shfl_down(a, 1, 8);          // lanes 0, 2: (a0+a1), (a2+a3)
+    float ss = b + __shfl_down(b, 2, 8);               // lane 0
+    ss = __shfl(ss, 0, 64);
+    if (lane == 0)
+        for (int j = d8; j < dim; j++)
+            ss = __fmaf_rn(r[j], r[j], ss);
+    ss = __shfl(ss, 0, 64);
+    ss = __fdiv_rn(ss, (float)dim);
+    const float inv = __fdiv_rn(1.0f, sqrtf(ss + eps));   // sqrtf rounds correctly; __fsqrt_rn is the native one
+    for (int j = lane; j < dim; j += 64)
+        o[j] = (r[j] * inv) * bf16_to_f32(w[j]);
+}
+
+// op_silu_mul_fused_f32 / _bf16 (ops_activation.c:48-105, :143-230): blocks of
+// 8 use the vector Schraudolph exp (round to nearest), the n % 8 remainder
+// the scalar one (truncating); sig = 1 / (1 + e); out = (g * sig) * u; bf16
+// in and out, the result's low 16 bits dropped.
+__device__ __forceinline__ float silu_ref(float g, float u, bool vec)
+{
+    float e;
+    if (vec) {
+        float xv = fminf(fmaxf(0.0f - g, -87.0f), 87.0f);
+        e = __int_as_float(__float2int_rn(__fmaf_rn(xv, 12102203.0f, 1065353216.0f)));
+    } else {
+        e = fast_expf(-g);
+    }
+    const float sig = __fdiv_rn(1.0f, 1.0f + e);
+    return (g * sig) * u;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_silu_mul_ref(void *__restrict__ out, const void *__restrict__ gate,
+                                                      const void *__restrict__ up, size_t n)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    const bool vec = i < (n & ~(size_t)7);
+    if constexpr (BF16) {
+        const float g = bf16_to_f32(((const uint16_t *)gate)[i]), u = bf16_to_f32(((const uint16_t *)up)[i]);
+        ((uint16_t *)out)[i] = (uint16_t)(__float_as_uint(silu_ref(g, u, vec)) >> 16);
+    } else {
+        ((float *)out)[i] = silu_ref(((const float *)gate)[i], ((const float *)up)[i], vec);
+    }
+}
+
+// rope_apply_multihead_cached (ops_rope.c:192-228) as the compiled loop
+// evaluates it: x0' = fma(x0, c, -(x1 * s)), x1' = fma(x0, s, x1 * c).
+__global__ __launch_bounds__(256) void k_rope_heads(float *__restrict__ data, int n_heads, int hd,
+                                                    const float *__restrict__ cos_row,
+                                                    const float *__restrict__ sin_row)
+{
+    const int half = hd / 2;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_heads * half)
+        return;
+    const int h = t / half, i = t % half;
+    float *x = data + (size_t)h * hd;
+    const float c = cos_row[i], s = sin_row[i], x0 = x[i], x1 = x[i + half];
+    x[i] = __fmaf_rn(x0, c, -(x1 * s));
+    x[i + half] = __fmaf_rn(x0, s, x1 * c);
+}
+
+// sample_argmax (sampler.c:42-148) in one block.  F32: argmax_simd_f32 --
+// the maximum wins; equal maxima in the 8-lane part (indices below
+// 8 * floor(n / 8), n >= 8) go to the lowest lane (i % 8), then the first
+// index; tail entries win only with a strictly larger value; n < 8 scans
+// with strict >.  BF16: argmax_loop_bf16 -- the first index with the largest
+// value above -1e9, else 0.
+__device__ __forceinline__ void amax_merge(float &vm, unsigned long long &key, float v2, unsigned long long k2)
+{
+    if (v2 > vm || (v2 == vm && k2 < key)) {
+        vm = v2;
+        key = k2;
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_argmax_ref(int *__restrict__ out, const void *__restrict__ data, int n)
+{
+    __shared__ float rv[4];
+    __shared__ unsigned long long rk[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int main = BF16 ? n : (n < 8 ? 0 : (n & ~7));
+    float vm = -INFINITY;
+    unsigned long long key = ~0ull;
+    for (int i = threadIdx.x; i < main; i += blockDim.x) {
+        const float v = BF16 ? bf16_to_f32(((const uint16_t *)data)[i]) : ((const float *)data)[i];
+        const unsigned long long k = BF16 ? (unsigned)i : (((unsigned long long)(i & 7) << 32) | (unsigned)i);
+        amax_merge(vm, key, v, k);
+    }
+    for (int o = 32; o > 0; o >>= 1)
+        amax_merge(vm, key, __shfl_xor(vm, o), __shfl_xor(key, o));
+    if (lane == 0) {
+        rv[wave] = vm;
+        rk[wave] = key;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0)
+        return;
+    for (int w = 1; w < 4; w++)
+        amax_merge(vm, key, rv[w], rk[w]);
+    if (BF16) {
+        *out = (key != ~0ull && vm > -1e9f) ? (int)(key & 0xFFFFFFFFu) : 0;
+        return;
+    }
+    const float *x = (const float *)data;
+    float tm = -INFINITY;
+    int ti = -1;
+    for (int i = main; i < n; i++)
+        if (ti < 0 || x[i] > tm) {
+            tm = x[i];
+            ti = i;
+        }
+    int res;
+    if (main == 0 || (ti >= 0 && tm > vm))
+        res = ti >= 0 ? ti : 0;
+    else
+        res = key == ~0ull ? 0 : (int)(key & 0xFFFFFFFFu);
+    *out = res;
+}
+
+
+// ---- LSH diagnostics ----------------------------------------------------------------
+
+// bf_compute_topk + hit count of lsh_validate_recall (ops_lsh.c:513-640): one
+// block.  Above 4096 keys every stride-th key is scored (stride = n / 4096);
+// score_i = fused multiply-add chain over d of q[d] * bf16(k_i[d]); the top k
+// by repeated argmax (strict >, first index; chosen entries set to -1e30);
+// hits = how many of lsh[0 .. lsh_k) are among them.
+constexpr int kValMaxKeys = 4096;
+constexpr int kValMaxTopK = 64;
+
+__global__ __launch_bounds__(256) void k_validate_recall(int *__restrict__ hits_out, const float *__restrict__ q,
+                                                         const uint16_t *__restrict__ keys, int actual_n,
+                                                         int stride, int dim, const int *__restrict__ lsh,
+                                                         int lsh_k, int actual_k)
+{
+    __shared__ float sc[kValMaxKeys];
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    __shared__ int top[kValMaxTopK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < actual_n; i += blockDim.x) {
+        const uint16_t *k = keys + (size_t)i * stride * dim;
+        float dot = 0.0f;
+        for (int d = 0; d < dim; d++)
+            dot = __fmaf_rn(q[d], bf16_to_f32(k[d]), dot);
+        sc[i] = dot;
+    }
+    __syncthreads();
+    for (int j = 0; j < actual_k && j < actual_n; j++) {
+        float bv = -1e30f;
+        int bi = 0x7FFFFFFF;
+        for (int i = tid; i < actual_n; i += blockDim.x)
+            if (sc[i] > bv) {
+                bv = sc[i];
+                bi = i;
+            }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float v2 = __shfl_xor(bv, o);
+            const int i2 = __shfl_xor(bi, o);
+            if (v2 > bv || (v2 == bv && i2 < bi)) {
+                bv = v2;
+                bi = i2;
+            }
+        }
+        if (lane == 0) {
+            rv[wave] = bv;
+            ri[wave] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < 4; w++)
+                if (rv[w] > bv || (rv[w] == bv && ri[w] < bi)) {
+                    bv = rv[w];
+                    bi = ri[w];
+                }
+            // nothing above -1e30 left: the reference keeps max_idx = 0
+            if (bi == 0x7FFFFFFF)
+                bi = 0;
+            top[j] = bi * stride;
+            sc[bi] = -1e30f;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        int hits = 0;
+        const int nk = actual_k < actual_n ? actual_k : actual_n;
+        for (int i = 0; i < lsh_k; i++)
+            for (int j = 0; j < nk; j++)
+                if (lsh[i] == top[j]) {
+                    hits++;
+                    break;
+                }
+        *hits_out = hits;
+    }
+}
+
+// adaptive_k_cutoff (ops_lsh.c:645-668): the sequential running sum of the
+// scores until it reaches the threshold; at least 1.
+__global__ void k_adaptive_k(int *__restrict__ out, const float *__restrict__ scores, int n, float threshold)
+{
+    float cum = 0.0f;
+    int k = 0;
+    while (k < n) {
+        cum = cum + scores[k];
+        k++;
+        if (cum >= threshold)
+            break;
+    }
+    *out = k < 1 ? 1 : k;
+}
+
 // ---- host runtime -------------------------------------------------------------
 
 [[noreturn]] void die(const char *what, const char *msg)
@@ -334,6 +567,11 @@ struct Runtime {
         int uploaded = 0;           // block hashes already on the device
     };
     std::unordered_map<const t_lsh_index *, Index> indexes;
+    struct Linear {
+        uint16_t *k = nullptr, *v = nullptr;   // device mirror [max_seq][heads][dim]
+        size_t rows = 0, row = 0;
+    };
+    std::unordered_map<const t_kv_cache *, Linear> linear;
 };
 
 Runtime &rt()
@@ -609,6 +847,107 @@ extern "C" int op_matmul(t_tensor *out, const t_tensor *a, const t_tensor *b)
         return matmul_dense(out, a, b, m, k, n);
     fprintf(stderr, "MatMul unsupported dtypes: A=%d B=%d Out=%d\n", a->dtype, b->dtype, out->dtype);
     return -1;
+}
+
+// ---- decode-step adjacents ------------------------------------------------------------
+
+static int norm_dim(const t_tensor *x)
+{
+    if (x->ndim == 2 && x->shape[1] == 1)
+        return x->shape[0];
+    return x->shape[x->ndim > 0 ? x->ndim - 1 : 0];
+}
+
+extern "C" void op_rmsnorm(t_tensor *out, const t_tensor *x, const t_tensor *w, float epsilon)
+{
+    if (!(x->dtype == DTYPE_F32 && out->dtype == DTYPE_F32 && w->dtype == DTYPE_BF16)) {
+        fprintf(stderr, "RMSNorm unsupported dtypes\n");
+        return;
+    }
+    const int dim = norm_dim(x);
+    if (dim <= 0 || x->size == 0)
+        return;
+    const int rows = (int)(x->size / (size_t)dim);
+    std::lock_guard<std::mutex> g(rt().mu);
+    const size_t bytes = (size_t)rows * dim * 4;
+    const float *dx = (const float *)in_dev(x->data, bytes, kS0);
+    const uint16_t *dw = (const uint16_t *)weight_dev(w->data, (size_t)dim * 2);
+    bool st;
+    float *o = (float *)out_dev(out->data, bytes, kS1, &st);
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(64), 0, nullptr, o, dx, dw, dim, epsilon);
+    hip_ok(hipGetLastError(), "op_rmsnorm");
+    out_done(out->data, o, bytes, st);
+}
+
+extern "C" void op_silu_mul(t_tensor *out, const t_tensor *gate, const t_tensor *val)
+{
+    if (gate->size != out->size || val->size != out->size)
+        return;
+    const bool f32 = out->dtype == DTYPE_F32 && gate->dtype == DTYPE_F32 && val->dtype == DTYPE_F32;
+    const bool bf = out->dtype == DTYPE_BF16 && gate->dtype == DTYPE_BF16 && val->dtype == DTYPE_BF16;
+    if (!f32 && !bf) {
+        fprintf(stderr, "SiLU unsupported dtypes\n");
+        return;
+    }
+    const size_t n = out->size;
+    if (n == 0)
+        return;
+    std::lock_guard<std::mutex> g(rt().mu);
+    const size_t bytes = n * (f32 ? 4 : 2);
+    const void *dg = in_dev(gate->data, bytes, kS0);
+    const void *du = in_dev(val->data, bytes, kS2);
+    bool st;
+    void *o = out_dev(out->data, bytes, kS1, &st);
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (f32)
+        hipLaunchKernelGGL(k_silu_mul_ref<false>, grid, dim3(256), 0, nullptr, o, dg, du, n);
+    else
+        hipLaunchKernelGGL(k_silu_mul_ref<true>, grid, dim3(256), 0, nullptr, o, dg, du, n);
+    hip_ok(hipGetLastError(), "op_silu_mul");
+    out_done(out->data, o, bytes, st);
+}
+
+extern "C" void rope_apply_multihead_cached(float *data, int n_heads, int pos, const t_rope_cache *cache)
+{
+    if (pos >= cache->max_seq_len || n_heads <= 0)
+        return;
+    const int hd = cache->head_dim, half = hd / 2;
+    std::lock_guard<std::mutex> g(rt().mu);
+    // the tables are read-only model state: mirrored once, like weights
+    const size_t tb = (size_t)cache->max_seq_len * half * 4;
+    const float *ct = (const float *)weight_dev(cache->cos_table, tb);
+    const float *sn = (const float *)weight_dev(cache->sin_table, tb);
+    const size_t bytes = (size_t)n_heads * hd * 4;
+    bool st;
+    float *d = (float *)out_dev(data, bytes, kS1, &st);
+    if (st)
+        hip_ok(hipMemcpy(d, data, bytes, hipMemcpyHostToDevice), "rope_apply_multihead_cached");
+    const int n = n_heads * half;
+    hipLaunchKernelGGL(k_rope_heads, dim3((n + 255) / 256), dim3(256), 0, nullptr, d, n_heads, hd,
+                       ct + (size_t)pos * half, sn + (size_t)pos * half);
+    hip_ok(hipGetLastError(), "rope_apply_multihead_cached");
+    out_done(data, d, bytes, st);
+}
+
+extern "C" int sample_argmax(const t_tensor *logits)
+{
+    const bool f32 = logits->dtype == DTYPE_F32;
+    const size_t n = logits->size;
+    if (n == 0)
+        return 0;
+    if (n > (size_t)INT32_MAX)
+        die("sample_argmax", "more than 2^31 logits");
+    std::lock_guard<std::mutex> g(rt().mu);
+    const void *d = in_dev(logits->data, n * (f32 ? 4 : 2), kS0);
+    int *dres = (int *)scratch(kS1, 4);
+    if (f32)
+        hipLaunchKernelGGL(k_argmax_ref<false>, dim3(1), dim3(256), 0, nullptr, dres, d, (int)n);
+    else
+        hipLaunchKernelGGL(k_argmax_ref<true>, dim3(1), dim3(256), 0, nullptr, dres, d, (int)n);
+    hip_ok(hipGetLastError(), "sample_argmax");
+    int res = 0;
+    hip_ok(hipMemcpy(&res, dres, 4, hipMemcpyDeviceToHost), "sample_argmax");
+    return res;
 }
 
 // ---- quant codecs ------------------------------------------------------------------
@@ -1093,6 +1432,285 @@ extern "C" int select_top_k_blocks(int *selected, t_block_score *scores, int n_b
     else
         hip_ok(hipMemcpy(selected, dsel, (size_t)n * 4, hipMemcpyDeviceToHost), "select_top_k_blocks");
     return n;
+}
+
+// ---- LSH diagnostics (ops_lsh.c:447-668) ---------------------------------------------
+
+extern "C" void lsh_stats_reset_atomic(t_lsh_stats_atomic *s)
+{
+    if (!s)
+        return;
+    uint64_t *f[] = {&s->total_queries, &s->validated_queries, &s->topk_hits, &s->topk_total,
+                     &s->recall_scaled, &s->validation_count, &s->total_used_k, &s->k_samples};
+    for (uint64_t *p : f)
+        __atomic_store_n(p, 0, __ATOMIC_SEQ_CST);
+}
+
+extern "C" void lsh_stats_print_atomic(const t_lsh_stats_atomic *s, int sparse_k)
+{
+    if (!s)
+        return;
+    const uint64_t total_q = __atomic_load_n(&s->total_queries, __ATOMIC_SEQ_CST);
+    const uint64_t validated = __atomic_load_n(&s->validated_queries, __ATOMIC_SEQ_CST);
+    const uint64_t hits = __atomic_load_n(&s->topk_hits, __ATOMIC_SEQ_CST);
+    const uint64_t total = __atomic_load_n(&s->topk_total, __ATOMIC_SEQ_CST);
+    const uint64_t used_k = __atomic_load_n(&s->total_used_k, __ATOMIC_SEQ_CST);
+    const uint64_t k_samples = __atomic_load_n(&s->k_samples, __ATOMIC_SEQ_CST);
+    if (validated == 0 || total == 0) {
+        printf("[LSH Stats] No validation data collected.\n");
+        fflush(stdout);
+        return;
+    }
+    const float recall = (float)hits / (float)total;
+    const float avg_k = k_samples > 0 ? (float)used_k / (float)k_samples : 0.0f;
+    const float savings = sparse_k > 0 ? (1.0f - avg_k / (float)sparse_k) * 100.0f : 0.0f;
+    printf("[LSH Stats] Queries: %lu (validated: %lu)\n", (unsigned long)total_q, (unsigned long)validated);
+    printf("[LSH Stats] Recall: %.1f%% (target: >80%%)\n", recall * 100.0f);
+    printf("[LSH Stats] Avg Dynamic K: %.1f (savings: %.1f%%)\n", avg_k, savings);
+    if (recall < 0.8f)
+        printf("[LSH Stats] WARNING: Recall below 80%% - sparse attention degraded!\n");
+    else
+        printf("[LSH Stats] Recall acceptable\n");
+    fflush(stdout);
+}
+
+extern "C" float lsh_validate_recall(const float *query, const uint16_t *keys, int n_keys, int dim,
+                                     const int *lsh_indices, int lsh_k, int actual_k)
+{
+    if (actual_k > n_keys)
+        actual_k = n_keys;
+    if (lsh_k > actual_k)
+        lsh_k = actual_k;
+    if (actual_k > kValMaxTopK)
+        actual_k = kValMaxTopK;
+    if (actual_k <= 0)
+        return NAN;   // the reference divides 0 hits by actual_k = 0
+    const int stride = n_keys > kValMaxKeys ? n_keys / kValMaxKeys : 1;
+    const int actual_n = n_keys > kValMaxKeys ? kValMaxKeys : n_keys;
+    std::lock_guard<std::mutex> g(rt().mu);
+    const float *dq = (const float *)in_dev(query, (size_t)dim * 4, kS0);
+    const uint16_t *dk = (const uint16_t *)in_dev(keys, (size_t)n_keys * dim * 2, kS2);
+    const int nl = lsh_k > 0 ? lsh_k : 0;
+    const int *dl = (const int *)in_dev(lsh_indices, (size_t)nl * 4, kS3);
+    int *dh = (int *)scratch(kS1, 4);
+    hipLaunchKernelGGL(k_validate_recall, dim3(1), dim3(256), 0, nullptr, dh, dq, dk, actual_n, stride, dim,
+                       nl ? dl : nullptr, nl, actual_k);
+    hip_ok(hipGetLastError(), "lsh_validate_recall");
+    int hits = 0;
+    hip_ok(hipMemcpy(&hits, dh, 4, hipMemcpyDeviceToHost), "lsh_validate_recall");
+    return (float)hits / (float)actual_k;
+}
+
+extern "C" int adaptive_k_cutoff(const float *scores, const int *indices, int n_cand, float threshold)
+{
+    (void)indices;
+    if (n_cand <= 0)
+        return 1;
+    std::lock_guard<std::mutex> g(rt().mu);
+    const float *ds = (const float *)in_dev(scores, (size_t)n_cand * 4, kS0);
+    int *dk = (int *)scratch(kS1, 4);
+    hipLaunchKernelGGL(k_adaptive_k, dim3(1), dim3(1), 0, nullptr, dk, ds, n_cand, threshold);
+    hip_ok(hipGetLastError(), "adaptive_k_cutoff");
+    int k = 1;
+    hip_ok(hipMemcpy(&k, dk, 4, hipMemcpyDeviceToHost), "adaptive_k_cutoff");
+    return k;
+}
+
+// ---- linear KV cache and its attention (kv_cache.c, ops_attention.c:41-245) -------------
+
+// arena_alloc_or_die / arena_try_alloc (arena.c:80-115): 64-byte aligned bump
+// allocation, zeroed; fatal when the arena is too small
+static void *arena_take(t_arena *a, size_t size)
+{
+    const size_t padding = (64 - (a->offset % 64)) % 64;
+    if (padding > a->size - a->offset || size > a->size - a->offset - padding) {
+        fprintf(stderr, "Fatal: arena OOM (requested %zu bytes, %zu/%zu used)\n", size, a->offset, a->size);
+        exit(1);
+    }
+    a->offset += padding;
+    void *p = a->base + a->offset;
+    a->offset += size;
+    memset(p, 0, size);
+    return p;
+}
+
+static t_tensor view3(void *data, int d0, int d1, int d2)
+{
+    t_tensor t{};
+    t.data = data;
+    t.ndim = 3;
+    t.shape[0] = d0;
+    t.shape[1] = d1;
+    t.shape[2] = d2;
+    t.shape[3] = 1;
+    t.stride[0] = d1 * d2;
+    t.stride[1] = d2;
+    t.stride[2] = 1;
+    t.size = (size_t)d0 * d1 * d2;
+    t.dtype = DTYPE_BF16;
+    return t;
+}
+
+extern "C" void kv_cache_init(t_kv_cache *c, t_arena *a, t_kv_init_params *p)
+{
+    c->max_seq_len = p->max_seq;
+    c->num_heads = p->num_heads;
+    c->head_dim = p->head_dim;
+    c->current_seq_len = 0;
+    const size_t bytes = (size_t)p->max_seq * p->num_heads * p->head_dim * sizeof(t_bf16);
+    c->k = view3(arena_take(a, bytes), p->max_seq, p->num_heads, p->head_dim);
+    c->v = view3(arena_take(a, bytes), p->max_seq, p->num_heads, p->head_dim);
+    std::lock_guard<std::mutex> g(rt().mu);
+    Runtime::Linear &m = rt().linear[c];
+    if (m.k) {
+        hip_ok(hipDeviceSynchronize(), "kv_cache_init");
+        hip_ok(hipFree(m.k), "kv_cache_init");
+        hip_ok(hipFree(m.v), "kv_cache_init");
+    }
+    m.rows = (size_t)p->max_seq;
+    m.row = (size_t)p->num_heads * p->head_dim;
+    hip_ok(hipMalloc((void **)&m.k, bytes ? bytes : 2), "kv_cache_init");
+    hip_ok(hipMalloc((void **)&m.v, bytes ? bytes : 2), "kv_cache_init");
+}
+
+// the device mirror of a cache: the one kv_cache_init made, or a staged copy
+// of the host rows [0, n) (a cache this library did not create)
+static const Runtime::Linear &linear_dev(const t_kv_cache *c, int n, Runtime::Linear &tmp)
+{
+    auto it = rt().linear.find(c);
+    if (it != rt().linear.end())
+        return it->second;
+    tmp.row = (size_t)c->num_heads * c->head_dim;
+    const size_t bytes = (size_t)n * tmp.row * 2;
+    tmp.k = (uint16_t *)in_dev(c->k.data, bytes, kS6);
+    tmp.v = (uint16_t *)in_dev(c->v.data, bytes, kS7);
+    return tmp;
+}
+
+extern "C" void kv_cache_append(t_kv_cache *c, const t_tensor *k_in, const t_tensor *v_in)
+{
+    if (c->current_seq_len >= c->max_seq_len) {
+        fprintf(stderr, "KV Cache Full!\n");
+        return;
+    }
+    std::lock_guard<std::mutex> g(rt().mu);
+    auto it = rt().linear.find(c);
+    if (it == rt().linear.end())
+        die("kv_cache_append", "cache was not created by kv_cache_init of this library");
+    Runtime::Linear &m = it->second;
+    const int idx = c->current_seq_len;
+    const int row = c->num_heads * c->head_dim;
+    uint16_t *hk = (uint16_t *)c->k.data + (size_t)idx * row, *hv = (uint16_t *)c->v.data + (size_t)idx * row;
+    uint16_t *dk = m.k + (size_t)idx * row, *dv = m.v + (size_t)idx * row;
+    if (k_in->dtype == DTYPE_F32) {
+        const float *fk = (const float *)in_dev(k_in->data, (size_t)row * 4, kS0);
+        const float *fv = (const float *)in_dev(v_in->data, (size_t)row * 4, kS2);
+        ok(be42_kv_linear_append(m.k, m.v, idx, fk, fv, row, nullptr), "kv_cache_append");
+        hip_ok(hipMemcpy(hk, dk, (size_t)row * 2, hipMemcpyDeviceToHost), "kv_cache_append");
+        hip_ok(hipMemcpy(hv, dv, (size_t)row * 2, hipMemcpyDeviceToHost), "kv_cache_append");
+    } else {
+        memcpy(hk, k_in->data, (size_t)row * 2);
+        memcpy(hv, v_in->data, (size_t)row * 2);
+        hip_ok(hipMemcpy(dk, hk, (size_t)row * 2, hipMemcpyHostToDevice), "kv_cache_append");
+        hip_ok(hipMemcpy(dv, hv, (size_t)row * 2, hipMemcpyHostToDevice), "kv_cache_append");
+    }
+    c->current_seq_len++;
+}
+
+extern "C" void kv_cache_evict(t_kv_cache *c, t_evict_params *p)
+{
+    if (p->keep_k <= 0) {
+        fprintf(stderr, "Warning: kv_cache_evict keep_k=%d invalid\n", p->keep_k);
+        return;
+    }
+    int keep_k = p->keep_k;
+    if (keep_k > c->current_seq_len)
+        keep_k = c->current_seq_len;
+    if (keep_k > c->max_seq_len)
+        keep_k = c->max_seq_len;
+    if (c->current_seq_len <= keep_k)
+        return;
+    const int n = c->current_seq_len, heads = c->num_heads, dim = c->head_dim;
+    // the reference takes its sort buffer from the scratch arena (and gives
+    // it back): the same arena must be large enough
+    {
+        const size_t padding = (64 - (p->scratch->offset % 64)) % 64;
+        const size_t need = (size_t)n * 8;
+        if (padding > p->scratch->size - p->scratch->offset || need > p->scratch->size - p->scratch->offset - padding) {
+            fprintf(stderr, "Fatal: arena OOM (requested %zu bytes, %zu/%zu used)\n", need, p->scratch->offset,
+                    p->scratch->size);
+            exit(1);
+        }
+    }
+    std::lock_guard<std::mutex> g(rt().mu);
+    Runtime::Linear tmp;
+    const Runtime::Linear &m = linear_dev(c, n, tmp);
+    const uint16_t *dq = (const uint16_t *)in_dev(p->q->data, (size_t)heads * dim * 2, kS0);
+    const uint16_t *dw = (const uint16_t *)in_dev(p->w->data, (size_t)heads * 2, kS2);
+    int new_len = n;
+    ok(be42_kv_linear_evict(m.k, m.v, n, heads, dim, dq, dw, keep_k, &new_len, nullptr), "kv_cache_evict");
+    const size_t bytes = (size_t)new_len * heads * dim * 2;
+    hip_ok(hipMemcpy(c->k.data, m.k, bytes, hipMemcpyDeviceToHost), "kv_cache_evict");
+    hip_ok(hipMemcpy(c->v.data, m.v, bytes, hipMemcpyDeviceToHost), "kv_cache_evict");
+    c->current_seq_len = new_len;
+}
+
+static void linear_attention(float *out, const float *q, const uint16_t *dk, const uint16_t *dv, const int *idx_host,
+                             int n_tok, int n_heads, int n_kv, int hd, float scale, const char *what)
+{
+    const size_t qb = (size_t)n_heads * hd * 4;
+    const float *dq = (const float *)in_dev(q, qb, kS0);
+    const int *di = idx_host ? (const int *)in_dev(idx_host, (size_t)(n_tok > 0 ? n_tok : 0) * 4, kS3) : nullptr;
+    bool st;
+    float *o = (float *)out_dev(out, qb, kS1, &st);
+    const size_t wsb = be42_linear_attention_workspace_bytes(n_tok, n_heads, n_kv, hd);
+    void *ws = scratch(kS5, wsb ? wsb : 16);
+    ok(be42_linear_attention(o, dq, dk, dv, di, n_tok, n_heads, n_kv, hd, scale, ws, wsb, nullptr), what);
+    out_done(out, o, qb, st);
+}
+
+extern "C" void flash_attention_head(float *out, const float *q, const t_bf16 *k_cache, const t_bf16 *v_cache,
+                                     int seq_len, int head_dim, float scale)
+{
+    std::lock_guard<std::mutex> g(rt().mu);
+    const size_t bytes = (size_t)(seq_len > 0 ? seq_len : 0) * head_dim * 2;
+    const uint16_t *dk = (const uint16_t *)in_dev(k_cache, bytes, kS6);
+    const uint16_t *dv = (const uint16_t *)in_dev(v_cache, bytes, kS7);
+    linear_attention(out, q, dk, dv, nullptr, seq_len, 1, 1, head_dim, scale, "flash_attention_head");
+}
+
+extern "C" void op_attention_dense(t_attention_params *p, int kv_len)
+{
+    std::lock_guard<std::mutex> g(rt().mu);
+    Runtime::Linear tmp;
+    const Runtime::Linear &m = linear_dev(p->kv_cache, kv_len, tmp);
+    linear_attention(p->output, p->q, m.k, m.v, nullptr, kv_len, p->n_heads, p->n_kv_heads, p->head_dim, p->scale,
+                     "op_attention_dense");
+}
+
+extern "C" void op_attention_sparse(t_attention_params *p)
+{
+    std::lock_guard<std::mutex> g(rt().mu);
+    Runtime::Linear tmp;
+    const t_kv_cache *c = p->kv_cache;
+    const Runtime::Linear &m = linear_dev(c, c->current_seq_len, tmp);
+    // positions must name rows the device holds: the whole cache for one that
+    // kv_cache_init made, the first current_seq_len rows of a staged one
+    const int rows = m.rows ? (int)m.rows : c->current_seq_len;
+    for (int i = 0; i < p->attend_k; i++)
+        if (p->topk_idx[i] < 0 || p->topk_idx[i] >= rows)
+            die("op_attention_sparse", "position out of the cache");
+    linear_attention(p->output, p->q, m.k, m.v, p->topk_idx, p->attend_k, p->n_heads, p->n_kv_heads, p->head_dim,
+                     p->scale, "op_attention_sparse");
+}
+
+extern "C" void op_multihead_attention(t_attention_params *p)
+{
+    const int kv_len = p->kv_cache->current_seq_len;
+    if (p->topk_idx != nullptr && p->attend_k > 0 && p->attend_k < kv_len)
+        op_attention_sparse(p);
+    else
+        op_attention_dense(p, kv_len);
 }
 
 // ---- paged attention ------------------------------------------------------------------

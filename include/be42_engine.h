@@ -10,7 +10,8 @@
  * only change is the tensor extension for quantized weights:
  *   t_dtype gains DTYPE_I8 and DTYPE_FP8 (after the reference's two values),
  *   t_tensor gains a trailing `row_scale` (one fp32 scale per row of a
- *   quantized weight; ignored for F32/BF16).
+ *   quantized weight; ignored for F32/BF16), so t_kv_cache, which holds two
+ *   t_tensor by value, grows by two pointers.
  * A build of the reference that links this library compiles its sources
  * against these definitions (the layouts of every other field are unchanged).
  *
@@ -75,6 +76,34 @@ typedef struct s_tensor {
  * (shape mismatch, unsupported dtypes, missing row_scale). */
 int op_matmul(t_tensor *out, const t_tensor *a, const t_tensor *b);
 
+/* ---- decode-step adjacents (src/compute/ops.h:34-41, ops_rope.h:33-81,
+ * sampler.h:19) ---------------------------------------------------------------
+ * op_rmsnorm: out = (x * 1/sqrtf(mean(x^2) + eps)) * w per row of x's last
+ * dimension (a [dim][1] column is one row), F32 x/out with BF16 w, the
+ * reference's summation order; other dtypes print and do nothing.
+ * op_silu_mul: out = (g * sigmoid(g)) * u element-wise, all F32 or all BF16
+ * (the reference's vector/scalar exp split and bf16 truncation); size
+ * mismatch: no-op.
+ * rope_apply_multihead_cached: rotates n_heads contiguous [head_dim] vectors
+ * in place with the cache's tables (host tables, mirrored to HBM once);
+ * positions at or past max_seq_len are left unchanged.
+ * sample_argmax: index of the largest logit (F32: argmax_simd_f32's lane tie
+ * rule; BF16: first maximum above -1e9). */
+typedef struct s_rope_cache {                                      /* ops_rope.h:33-38 */
+    float *cos_table;   /* [max_seq_len][head_dim / 2] */
+    float *sin_table;
+    int head_dim;
+    int max_seq_len;
+} t_rope_cache;
+
+void op_rmsnorm(t_tensor *out, const t_tensor *x, const t_tensor *w,  /* ops.h:34 */
+                float epsilon);
+void op_silu_mul(t_tensor *out, const t_tensor *gate,                /* ops.h:41 */
+                 const t_tensor *val);
+void rope_apply_multihead_cached(float *data, int n_heads, int pos,   /* ops_rope.h:80 */
+                                 const t_rope_cache *cache);
+int sample_argmax(const t_tensor *logits);                         /* sampler.h:19 */
+
 /* ---- quant codecs (src/compute/ops_quant.h:22-117) ------------------------- */
 typedef uint8_t t_fp8_e4m3;
 typedef int8_t t_qint8;
@@ -136,6 +165,30 @@ int lsh_find_candidates(const t_lsh_index *idx, uint16_t query_hash, /* ops_lsh.
                         int *block_ids, int max_blocks);
 int lsh_get_active_block(const t_lsh_index *idx, int *start_pos,  /* ops_lsh.h:115 */
                          int *len);
+/* LSH diagnostics (ops_lsh.h:118-216, ops_lsh.c:447-668).  The reference's
+ * counters are atomic_uint_fast64_t (8 bytes each on the reference's
+ * platform); this library updates them with atomic built-ins. */
+typedef struct s_lsh_stats_atomic {                                /* ops_lsh.h:128-138 */
+    uint64_t total_queries;
+    uint64_t validated_queries;
+    uint64_t topk_hits;
+    uint64_t topk_total;
+    uint64_t recall_scaled;
+    uint64_t validation_count;
+    uint64_t total_used_k;
+    uint64_t k_samples;
+} t_lsh_stats_atomic;
+
+void lsh_stats_reset_atomic(t_lsh_stats_atomic *s);               /* ops_lsh.h:177 */
+void lsh_stats_print_atomic(const t_lsh_stats_atomic *s,          /* ops_lsh.h:178 */
+                            int sparse_k);
+/* fraction of the brute-force top-actual_k keys (q . bf16 key, every
+ * stride-th key above 4096, actual_k capped at 64) found among
+ * lsh_indices[0 .. min(lsh_k, actual_k)) */
+float lsh_validate_recall(const float *query, const uint16_t *keys,  /* ops_lsh.h:195 */
+                          int n_keys, int dim, const int *lsh_indices, int lsh_k, int actual_k);
+int adaptive_k_cutoff(const float *scores, const int *indices,     /* ops_lsh.h:212 */
+                      int n_cand, float threshold);
 /* Release the device copies this library keeps for a context / an index
  * (no counterpart in the reference, whose structs own no device memory). */
 void lsh_ctx_release(const t_lsh_ctx *ctx);
@@ -200,6 +253,73 @@ void score_blocks(t_block_score *scores, const float *q,          /* paged.h:200
                   t_paged_kv_cache *pkv, int n_blocks);
 int select_top_k_blocks(int *selected, t_block_score *scores,     /* paged.h:211 */
                         int n_blocks, int k);
+
+/* ---- linear KV cache (src/memory/kv_cache.h:19-46, arena.h) ---------------
+ * The cache rows live where the reference keeps them -- in the caller's arena
+ * (host memory, [max_seq][num_heads][head_dim] bf16), which inference.c reads
+ * directly -- and in a device mirror this library keeps per t_kv_cache
+ * (created by kv_cache_init, updated by kv_cache_append / kv_cache_evict,
+ * read by the attention functions below).  A cache that did not come from
+ * kv_cache_init is uploaded on each attention call. */
+typedef struct s_arena {                                           /* arena.h:18-23 */
+    char *base;
+    size_t size;
+    size_t offset;
+} t_arena;
+
+typedef struct s_kv_cache {                                        /* kv_cache.h:19-27 */
+    t_tensor k;
+    t_tensor v;
+    int max_seq_len;
+    int num_heads;
+    int head_dim;
+    int current_seq_len;
+} t_kv_cache;
+
+typedef struct s_kv_init_params {                                  /* kv_cache.h:29-34 */
+    int max_seq;
+    int num_heads;
+    int head_dim;
+} t_kv_init_params;
+
+typedef struct s_evict_params {                                    /* kv_cache.h:36-42 */
+    const t_tensor *q;
+    const t_tensor *w;
+    int keep_k;
+    t_arena *scratch;
+} t_evict_params;
+
+/* allocates K and V from the arena (exit(1) when it is too small, as
+ * arena_alloc_or_die) and the device mirror */
+void kv_cache_init(t_kv_cache *c, t_arena *a, t_kv_init_params *p); /* kv_cache.h:44 */
+/* appends one token's rows (F32 rounded to bf16, or BF16 copied); prints
+ * "KV Cache Full!" and does nothing when full */
+void kv_cache_append(t_kv_cache *c, const t_tensor *k,            /* kv_cache.h:45 */
+                     const t_tensor *v);
+/* keeps the keep_k positions with the highest sum_h bf16(w[h]) *
+ * relu(bf16(q[h]) . k[h]) (q->data and w->data read as bf16; ties: lower
+ * position first), compacted to the front in position order */
+void kv_cache_evict(t_kv_cache *c, t_evict_params *p);            /* kv_cache.h:46 */
+
+/* ---- linear-cache attention (src/compute/ops_attention.h:29-68) ------------ */
+typedef struct s_attention_params {                                /* ops_attention.h:29-40 */
+    const float *q;         /* [n_heads * head_dim] */
+    t_kv_cache *kv_cache;
+    float *output;          /* [n_heads * head_dim] */
+    int n_heads;
+    int n_kv_heads;
+    int head_dim;
+    float scale;            /* 1/sqrt(head_dim) */
+    int *topk_idx;          /* optional: positions for sparse attention */
+    int attend_k;
+} t_attention_params;
+
+/* one head over seq_len contiguous [head_dim] bf16 K and V rows */
+void flash_attention_head(float *out, const float *q,              /* ops_attention.h:46 */
+                          const t_bf16 *k_cache, const t_bf16 *v_cache, int seq_len, int head_dim, float scale);
+void op_multihead_attention(t_attention_params *p);                /* ops_attention.h:54 */
+void op_attention_dense(t_attention_params *p, int kv_len);        /* ops_attention.h:59 */
+void op_attention_sparse(t_attention_params *p);                   /* ops_attention.h:64 */
 
 /* ---- paged attention (src/compute/ops_attention.h:75-84) ------------------- */
 void op_paged_attention(float *output, const float *q,            /* ops_attention.h:75 */

@@ -225,6 +225,42 @@ int  be42_lsh_attention(const be42_kv_pool *pool, const float *q, const int *slo
                         int n_heads, int k_sel, int cand_cap, float scale, float *out, int *sel, int *n_sel,
                         int sel_stride, void *stream);
 
+/* ---- linear (non-paged) bf16 KV cache -----------------------------------------------
+ * The cache layout of kv_cache.h:19-27: rows [T][n_kv][head_dim] bf16.
+ *   be42_kv_linear_append: row `pos` of K and V from fp32 [row] (float_to_bf16,
+ *     kv_cache.c:55-80; row = n_kv * head_dim).
+ *   be42_linear_attention: op_attention_sparse / op_attention_dense
+ *     (ops_attention.c:84-245) for one query [n_heads][head_dim]: the online
+ *     softmax over tokens idx[0 .. n_tok) in that order (idx NULL: 0 ..
+ *     n_tok-1), query head h reading KV head h / (n_heads / n_kv); out
+ *     [n_heads][head_dim].  workspace NULL: the library's (grow-only), else
+ *     be42_linear_attention_workspace_bytes() bytes.
+ *   be42_lsh_route_tokens: the token route of transformer_forward
+ *     (inference.c:268-423) for kv_len > sparse_k: the last `window`
+ *     positions, plus every position of the LSH candidate blocks
+ *     (lsh_find_candidates over block_hashes, at most 64 blocks) that end
+ *     before the window, sorted; score = sum over KV heads of
+ *     simd_dot_bf16_f32(K[t][kv], q head kv * G); the reference min-heap keeps
+ *     min(#candidates, sparse_k <= 64) of them.  topk (device, >= sparse_k)
+ *     receives the positions in the heap's array order, *n_topk their count.
+ *     hpT [head_dim][16]; block arrays of the 64-token index (lsh_update).
+ *   be42_kv_linear_evict: kv_cache_evict (kv_cache_evict.c:34-70): keeps the
+ *     keep_k positions with the highest sum_h bf16(w[h]) * relu(q[h] . k[h])
+ *     (ties: lower position first), compacted to the front in position order;
+ *     q [heads][dim] and w [heads] bf16; *new_len (host) gets the length. */
+int    be42_kv_linear_append(uint16_t *k_cache, uint16_t *v_cache, int pos, const float *k, const float *v, int row,
+                             void *stream);
+size_t be42_linear_attention_workspace_bytes(int n_tok, int n_heads, int n_kv, int head_dim);
+int    be42_linear_attention(float *out, const float *q, const uint16_t *k, const uint16_t *v, const int *idx,
+                             int n_tok, int n_heads, int n_kv, int head_dim, float scale, void *workspace,
+                             size_t workspace_bytes, void *stream);
+int    be42_lsh_route_tokens(const uint16_t *k, int kv_len, const float *q, int n_heads, int n_kv, int head_dim,
+                             const float *hpT, const uint16_t *block_hashes, const int *block_starts,
+                             const int *block_lens, int n_blocks, int window, int sparse_k, int *topk, int *n_topk,
+                             void *stream);
+int    be42_kv_linear_evict(uint16_t *k, uint16_t *v, int n, int heads, int dim, const uint16_t *q, const uint16_t *w,
+                            int keep_k, int *new_len, void *stream);
+
 /* ---- decode step ------------------------------------------------------------------
  * transformer_forward (src/inference/inference.c:60-696) on the paged path for a
  * batch of independent sequences at one position: embedding (row-scaled codes),

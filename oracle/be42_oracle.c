@@ -826,6 +826,144 @@ void or_paged_attention_dense(float *out, const float *q, const or_paged *p, int
 }
 
 /* ======================================================================== */
+/* linear KV cache path                                                     */
+/* ======================================================================== */
+
+/* ops_attention.c:84-245: per query head, the online softmax of
+ * flash_attention_head over the listed tokens of its KV head (the token
+ * step of attend_page_bf16), then o *= 1 / l. */
+void or_attention_linear(float *out, const float *q, const uint16_t *k, const uint16_t *v, const int *idx,
+                         int n, int n_heads, int n_kv, int hd, float scale, int n_threads)
+{
+    set_threads(n_threads);
+    const int group = n_heads / n_kv;
+    #pragma omp parallel for schedule(static)
+    for (int h = 0; h < n_heads; h++) {
+        const int kvh = h / group;
+        float *o = out + (size_t)h * hd;
+        const float *qh = q + (size_t)h * hd;
+        float m = -INFINITY, l = 0.0f;
+        for (int d = 0; d < hd; d++)
+            o[d] = 0.0f;
+        for (int i = 0; i < n; i++) {
+            const int t = idx ? idx[i] : i;
+            const size_t row = ((size_t)t * n_kv + kvh) * hd;
+            attend_page_bf16(o, &m, &l, qh, k + row, v + row, 1, hd, scale);
+        }
+        if (l > 0.0f) {
+            float inv = 1.0f / l;
+            for (int d = 0; d < hd; d++)
+                o[d] = o[d] * inv;
+        }
+    }
+}
+
+typedef struct { float val; int idx; } or_score_index;
+
+/* qsort in glibc sorts with a stable merge sort: equal scores keep their
+ * position order */
+static int or_cmp_evict(const void *a, const void *b)
+{
+    const or_score_index *x = a, *y = b;
+    if (x->val != y->val)
+        return x->val < y->val ? 1 : -1;
+    return (x->idx > y->idx) - (x->idx < y->idx);
+}
+
+static int or_cmp_idx(const void *a, const void *b)
+{
+    return ((const or_score_index *)a)->idx - ((const or_score_index *)b)->idx;
+}
+
+int or_kv_evict(uint16_t *k, uint16_t *v, int n, int heads, int dim, const uint16_t *q, const uint16_t *w,
+                int keep_k)
+{
+    if (keep_k <= 0)
+        return n;
+    if (keep_k > n)
+        keep_k = n;
+    if (n <= keep_k)
+        return n;
+    or_score_index *si = malloc(sizeof(or_score_index) * (size_t)n);
+    for (int s = 0; s < n; s++) {
+        float total = 0.0f;
+        for (int h = 0; h < heads; h++) {
+            float dot = 0.0f;
+            const size_t off = ((size_t)s * heads + h) * dim;
+            for (int d = 0; d < dim; d++)
+                dot = fmaf(or_bf16_to_f32(q[h * dim + d]), or_bf16_to_f32(k[off + d]), dot);
+            if (dot < 0)
+                dot = 0.0f;
+            total = fmaf(or_bf16_to_f32(w[h]), dot, total);
+        }
+        si[s].val = total;
+        si[s].idx = s;
+    }
+    qsort(si, (size_t)n, sizeof *si, or_cmp_evict);
+    qsort(si, (size_t)keep_k, sizeof *si, or_cmp_idx);
+    const size_t blk = (size_t)heads * dim;
+    for (int i = 0; i < keep_k; i++)
+        if (si[i].idx != i) {
+            memcpy(k + i * blk, k + (size_t)si[i].idx * blk, blk * 2);
+            memcpy(v + i * blk, v + (size_t)si[i].idx * blk, blk * 2);
+        }
+    free(si);
+    return keep_k;
+}
+
+static int or_cmp_int(const void *a, const void *b)
+{
+    const int x = *(const int *)a, y = *(const int *)b;
+    return (x > y) - (x < y);
+}
+
+int or_route_tokens(int *topk, const uint16_t *k, int kv_len, int n_kv, int hd, const float *q, int n_heads,
+                    const float *hpT, const or_lsh_index *ix, int window, int sparse_k)
+{
+    if (!(sparse_k > 0 && kv_len > sparse_k))
+        return kv_len;
+    int *cand = malloc(sizeof(int) * (size_t)kv_len);
+    int nc = 0;
+    const int ws = kv_len > window ? kv_len - window : 0;
+    for (int t = ws; t < kv_len; t++)
+        cand[nc++] = t;
+    if (ws > 0 && ix && ix->n_blocks > 0) {
+        float *qm = malloc(sizeof(float) * (size_t)hd);
+        or_q_mean(qm, q, n_heads, hd);
+        uint16_t qh = or_lsh_hash(hpT, hd, qm);
+        free(qm);
+        int ids[64];
+        int nb = or_lsh_find_candidates(ix, qh, ids, 64);
+        for (int b = 0; b < nb && nc < kv_len; b++) {
+            int st = ix->start[ids[b]], ln = ix->len[ids[b]];
+            if (st + ln <= ws)
+                for (int p = 0; p < ln && nc < kv_len; p++)
+                    if (st + p < ws)
+                        cand[nc++] = st + p;
+        }
+    }
+    if (nc > 1)
+        qsort(cand, (size_t)nc, sizeof(int), or_cmp_int);
+    const int group = n_heads / n_kv;
+    int size = 0, cap = nc < sparse_k ? nc : sparse_k;
+    float *hs = malloc(sizeof(float) * (size_t)(cap > 0 ? cap : 1));
+    int *hi = malloc(sizeof(int) * (size_t)(cap > 0 ? cap : 1));
+    for (int c = 0; c < nc; c++) {
+        const int t = cand[c];
+        float score = 0.0f;
+        for (int kv = 0; kv < n_kv; kv++)
+            score += or_dot_bf16_f32(k + ((size_t)t * n_kv + kv) * hd, q + (size_t)kv * group * hd, hd);
+        or_heap_push(hs, hi, &size, cap, score, t);
+    }
+    for (int i = 0; i < size; i++)
+        topk[i] = hi[i];
+    free(hs);
+    free(hi);
+    free(cand);
+    return size;
+}
+
+/* ======================================================================== */
 /* routing composition                                                      */
 /* ======================================================================== */
 
@@ -968,6 +1106,47 @@ void or_silu_mul(float *dst, const float *gate, const float *up, int n)
         float sig = 1.0f / (1.0f + or_fast_expf(-g));
         dst[i] = g * sig * up[i];
     }
+}
+
+/* op_silu_mul_fused_bf16, ops_activation.c:143-230: bf16 in (bits << 16),
+ * the f32 arithmetic of the f32 kernel (vector exp for blocks of 8, scalar
+ * exp for the remainder), the result truncated to its high 16 bits. */
+void or_silu_mul_bf16(uint16_t *dst, const uint16_t *gate, const uint16_t *up, int n)
+{
+    int i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) {
+            float g = or_bf16_to_f32(gate[i + l]), u = or_bf16_to_f32(up[i + l]);
+            float sig = 1.0f / (1.0f + fast_expf_vec(0.0f - g));
+            float r = (g * sig) * u;
+            uint32_t b;
+            memcpy(&b, &r, 4);
+            dst[i + l] = (uint16_t)(b >> 16);
+        }
+    for (; i < n; i++) {
+        float g = or_bf16_to_f32(gate[i]), u = or_bf16_to_f32(up[i]);
+        float sig = 1.0f / (1.0f + or_fast_expf(-g));
+        float r = g * sig * u;
+        uint32_t b;
+        memcpy(&b, &r, 4);
+        dst[i] = (uint16_t)(b >> 16);
+    }
+}
+
+/* argmax_loop_bf16, sampler.c:122-140: best starts at -1e9 (index 0), the
+ * first strictly larger value wins. */
+int or_argmax_bf16(const uint16_t *x, int n)
+{
+    int best = 0;
+    float bv = -1e9f;
+    for (int i = 0; i < n; i++) {
+        float v = or_bf16_to_f32(x[i]);
+        if (v > bv) {
+            bv = v;
+            best = i;
+        }
+    }
+    return best;
 }
 
 /* argmax_simd_f32, sampler.c:42-117: 8 lanes keep the first strict maximum
@@ -1189,3 +1368,74 @@ int or_decoder_step(or_decoder *d, int token, int pos, float *logits, int th)
     gemv_kind(logits, c->wkind, d->w.out, d->w.out_s, d->x, c->vocab, dim, th);
     return or_argmax(logits, c->vocab);
 }
+
+/* ======================================================================== */
+/* LSH diagnostics                                                          */
+/* ======================================================================== */
+
+/* bf_compute_topk + lsh_validate_recall, ops_lsh.c:513-640: above 4096 keys
+ * every (n / 4096)-th key is scored; score = fused chain over d of
+ * q[d] * bf16(key[d]); the top k by repeated strict-> argmax from -1e30
+ * (index 0 if nothing is larger), chosen scores set to -1e30; recall =
+ * hits / actual_k, hits = entries of lsh[0 .. min(lsh_k, actual_k)) among
+ * the top k (actual_k clamped to n_keys, then lsh_k to it, then it to 64). */
+float or_lsh_validate_recall(const float *q, const uint16_t *keys, int n_keys, int dim,
+                             const int *lsh, int lsh_k, int actual_k)
+{
+    if (actual_k > n_keys)
+        actual_k = n_keys;
+    if (lsh_k > actual_k)
+        lsh_k = actual_k;
+    if (actual_k > 64)
+        actual_k = 64;
+    int stride = 1, nn = n_keys;
+    if (n_keys > 4096) {
+        stride = n_keys / 4096;
+        nn = 4096;
+    }
+    float *sc = malloc(sizeof(float) * (size_t)(nn > 0 ? nn : 1));
+    int top[64];
+    for (int i = 0; i < nn; i++) {
+        float dot = 0.0f;
+        for (int d = 0; d < dim; d++)
+            dot = fmaf(q[d], or_bf16_to_f32(keys[(size_t)i * stride * dim + d]), dot);
+        sc[i] = dot;
+    }
+    int nk = 0;
+    for (int j = 0; j < actual_k && j < nn; j++) {
+        float mv = -1e30f;
+        int mi = 0;
+        for (int i = 0; i < nn; i++)
+            if (sc[i] > mv) {
+                mv = sc[i];
+                mi = i;
+            }
+        top[j] = mi * stride;
+        sc[mi] = -1e30f;
+        nk++;
+    }
+    int hits = 0;
+    for (int i = 0; i < lsh_k; i++)
+        for (int j = 0; j < actual_k && j < nk; j++)
+            if (lsh[i] == top[j]) {
+                hits++;
+                break;
+            }
+    free(sc);
+    return (float)hits / (float)actual_k;
+}
+
+/* adaptive_k_cutoff, ops_lsh.c:645-668 */
+int or_adaptive_k_cutoff(const float *scores, int n, float threshold)
+{
+    float cum = 0.0f;
+    int k = 0;
+    while (k < n) {
+        cum += scores[k];
+        k++;
+        if (cum >= threshold)
+            break;
+    }
+    return k < 1 ? 1 : k;
+}
+

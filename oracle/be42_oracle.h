@@ -92,6 +92,11 @@ void or_lsh_index_reset(or_lsh_index *ix);                                    /*
 void or_lsh_insert_block(or_lsh_index *ix, uint16_t h, int start, int len);   /* ops_lsh.c:256-272 */
 int  or_lsh_find_candidates(const or_lsh_index *ix, uint16_t qh, int *ids, int max_ids); /* ops_lsh.c:361-418 */
 
+/* ---- LSH diagnostics (ops_lsh.c:513-668) ---------------------------------- */
+float or_lsh_validate_recall(const float *q, const uint16_t *keys, int n_keys, int dim,
+                             const int *lsh, int lsh_k, int actual_k);
+int   or_adaptive_k_cutoff(const float *scores, int n, float threshold);
+
 /* ---- selection ------------------------------------------------------------ */
 typedef struct or_block_score { int block_idx; int phys_idx; float score; } or_block_score; /* paged.h:186-191 */
 /* min-heap push, ops_heap.h:33-100 */
@@ -155,6 +160,27 @@ int or_route_pages(int *selected, int *n_cand_out, int *cand_out,
                    const float *hpT, const or_lsh_index *ix, int cand_cap, int k);
 void or_q_mean(float *qm, const float *q, int n_heads, int hd);
 
+/* ---- linear KV cache path (kv_cache.c, ops_attention.c:41-245, inference.c:268-423) ----
+ * The linear cache is [T][n_kv][hd] bf16 rows (kv_cache.h:19-27). */
+/* attention_head_sparse / attention_head_dense over tokens idx[0..n) of the
+ * cache (idx NULL: 0 .. n-1) in that order, all query heads */
+void or_attention_linear(float *out, const float *q, const uint16_t *k, const uint16_t *v, const int *idx,
+                         int n, int n_heads, int n_kv, int hd, float scale, int n_threads);
+/* kv_cache_evict (kv_cache_evict.c:34-70, kv_cache_score.c): keeps keep_k of
+ * n rows, compacting them to the front in position order; q and w are read
+ * as bf16 ([heads][dim], [heads]); returns the new length */
+int  or_kv_evict(uint16_t *k, uint16_t *v, int n, int heads, int dim, const uint16_t *q, const uint16_t *w,
+                 int keep_k);
+/* the token route of transformer_forward (inference.c:268-423): a window of
+ * the last `window` positions, plus the positions of the LSH candidate
+ * blocks (lsh_find_candidates, max 64) that end before the window, sorted
+ * ascending; score = sum over KV heads of dot_bf16(K[t][kv], q head kv*G);
+ * the min-heap keeps min(#candidates, sparse_k).  Writes the heap's
+ * positions in its array order and returns their count; with kv_len <=
+ * sparse_k returns kv_len and writes nothing (dense). */
+int  or_route_tokens(int *topk, const uint16_t *k, int kv_len, int n_kv, int hd, const float *q, int n_heads,
+                     const float *hpT, const or_lsh_index *ix, int window, int sparse_k);
+
 /* ---- decode-step adjacents (E rows) and the decoder loop ----------------- */
 void or_rmsnorm(float *out, const float *x, const uint16_t *w, int dim, float eps);      /* ops_norm.c:27-138 */
 void or_rope_table(float *cos_t, float *sin_t, int hd, int n_pos, float theta);          /* ops_rope.c:30-95 */
@@ -162,6 +188,8 @@ void or_rope_apply(float *data, int n_heads, int hd, int pos, int n_pos,
                    const float *cos_t, const float *sin_t);                              /* ops_rope.c:192-228 */
 void or_silu_mul(float *dst, const float *gate, const float *up, int n);                 /* ops_activation.c:48-105 */
 int  or_argmax(const float *x, int n);                                                   /* sampler.c:42-117 */
+void or_silu_mul_bf16(uint16_t *dst, const uint16_t *gate, const uint16_t *up, int n);  /* ops_activation.c:143-230 */
+int  or_argmax_bf16(const uint16_t *x, int n);                                          /* sampler.c:122-140 */
 
 typedef struct or_decoder_cfg {
     int n_layers, dim, n_heads, n_kv, hd, hidden, vocab, max_seq;

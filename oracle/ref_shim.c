@@ -17,6 +17,8 @@
 #include "compute/ops_rope.h"
 #include "compute/ops_activation.h"
 #include "compute/sampler.h"
+#include "memory/kv_cache.h"
+#include "memory/arena.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -238,3 +240,112 @@ int ref_argmax(float *x, int n)
     t.dtype = DTYPE_F32;
     return sample_argmax(&t);
 }
+
+void ref_silu_mul_bf16(uint16_t *dst, const uint16_t *gate, const uint16_t *up, int n)
+{
+    op_silu_mul_fused_bf16(dst, gate, up, (size_t)n);
+}
+
+int ref_argmax_bf16(uint16_t *x, int n)
+{
+    int s[1] = {n};
+    t_tensor t = tensor_view(x, s, 1);
+    t.dtype = DTYPE_BF16;
+    return sample_argmax(&t);
+}
+
+float ref_validate_recall(const float *q, const uint16_t *keys, int n_keys, int dim, const int *lsh, int lsh_k,
+                          int actual_k)
+{
+    return lsh_validate_recall(q, keys, n_keys, dim, lsh, lsh_k, actual_k);
+}
+
+int ref_adaptive_k(const float *scores, int n, float threshold)
+{
+    return adaptive_k_cutoff(scores, NULL, n, threshold);
+}
+
+/* linear KV cache path */
+static t_kv_cache ref_linear_cache(const uint16_t *k, const uint16_t *v, int n, int n_kv, int hd)
+{
+    t_kv_cache c;
+    int shape[3] = {n, n_kv, hd};
+    memset(&c, 0, sizeof c);
+    c.k = tensor_view((void *)k, shape, 3);
+    c.v = tensor_view((void *)v, shape, 3);
+    c.k.dtype = DTYPE_BF16;
+    c.v.dtype = DTYPE_BF16;
+    c.max_seq_len = n;
+    c.num_heads = n_kv;
+    c.head_dim = hd;
+    c.current_seq_len = n;
+    return c;
+}
+
+/* idx NULL: op_attention_dense over all n; else op_attention_sparse over
+ * n_idx listed tokens; multi != 0: op_multihead_attention */
+void ref_attention_linear(float *out, const float *q, const uint16_t *k, const uint16_t *v, int n, const int *idx,
+                          int n_idx, int n_heads, int n_kv, int hd, float scale, int multi)
+{
+    t_kv_cache c = ref_linear_cache(k, v, n, n_kv, hd);
+    t_attention_params p;
+    p.q = q;
+    p.kv_cache = &c;
+    p.output = out;
+    p.n_heads = n_heads;
+    p.n_kv_heads = n_kv;
+    p.head_dim = hd;
+    p.scale = scale;
+    p.topk_idx = (int *)idx;
+    p.attend_k = idx ? n_idx : n;
+    if (multi)
+        op_multihead_attention(&p);
+    else if (idx)
+        op_attention_sparse(&p);
+    else
+        op_attention_dense(&p, n);
+}
+
+/* kv_cache_init + kv_cache_append of n_tok f32 rows, bf16 rows copied out */
+void ref_kv_fill(uint16_t *k_out, uint16_t *v_out, const float *kf, const float *vf, int n_tok, int max_seq,
+                 int heads, int dim)
+{
+    t_arena a;
+    t_kv_cache c;
+    t_kv_init_params ip = {max_seq, heads, dim};
+    arena_init(&a, (size_t)max_seq * heads * dim * 4 + 4096);
+    kv_cache_init(&c, &a, &ip);
+    for (int t = 0; t < n_tok; t++) {
+        int shape[1] = {heads * dim};
+        t_tensor tk = tensor_view((void *)(kf + (size_t)t * heads * dim), shape, 1);
+        t_tensor tv = tensor_view((void *)(vf + (size_t)t * heads * dim), shape, 1);
+        tk.dtype = DTYPE_F32;
+        tv.dtype = DTYPE_F32;
+        kv_cache_append(&c, &tk, &tv);
+    }
+    memcpy(k_out, c.k.data, (size_t)c.current_seq_len * heads * dim * 2);
+    memcpy(v_out, c.v.data, (size_t)c.current_seq_len * heads * dim * 2);
+    arena_free(&a);
+}
+
+/* kv_cache_evict over n filled rows (in place); returns the new length */
+int ref_kv_evict(uint16_t *k, uint16_t *v, int n, int heads, int dim, const uint16_t *q, const uint16_t *w,
+                 int keep_k)
+{
+    t_arena scratch;
+    t_kv_cache c = ref_linear_cache(k, v, n, heads, dim);
+    int sq[2] = {heads, dim}, sw[1] = {heads};
+    t_tensor tq = tensor_view((void *)q, sq, 2), tw = tensor_view((void *)w, sw, 1);
+    t_evict_params ep;
+    tq.dtype = DTYPE_BF16;
+    tw.dtype = DTYPE_BF16;
+    arena_init(&scratch, (size_t)n * 8 + 4096);
+    ep.q = &tq;
+    ep.w = &tw;
+    ep.keep_k = keep_k;
+    ep.scratch = &scratch;
+    kv_cache_evict(&c, &ep);
+    arena_free(&scratch);
+    return c.current_seq_len;
+}
+

@@ -48,6 +48,40 @@ class PagedKv(C.Structure):
                 ("n_tokens", C.c_int)]
 
 
+class RopeCache(C.Structure):
+    _fields_ = [("cos_table", C.c_void_p), ("sin_table", C.c_void_p), ("head_dim", C.c_int),
+                ("max_seq_len", C.c_int)]
+
+
+class LshStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("total_queries", "validated_queries", "topk_hits", "topk_total",
+                                          "recall_scaled", "validation_count", "total_used_k", "k_samples")]
+
+
+class Arena(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("size", C.c_size_t), ("offset", C.c_size_t)]
+
+
+class KvCache(C.Structure):
+    _fields_ = [("k", Tensor), ("v", Tensor), ("max_seq_len", C.c_int), ("num_heads", C.c_int),
+                ("head_dim", C.c_int), ("current_seq_len", C.c_int)]
+
+
+class KvInitParams(C.Structure):
+    _fields_ = [("max_seq", C.c_int), ("num_heads", C.c_int), ("head_dim", C.c_int)]
+
+
+class EvictParams(C.Structure):
+    _fields_ = [("q", C.POINTER(Tensor)), ("w", C.POINTER(Tensor)), ("keep_k", C.c_int),
+                ("scratch", C.POINTER(Arena))]
+
+
+class AttentionParams(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("kv_cache", C.POINTER(KvCache)), ("output", C.c_void_p),
+                ("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("scale", C.c_float),
+                ("topk_idx", C.c_void_p), ("attend_k", C.c_int)]
+
+
 class BlockScore(C.Structure):
     _fields_ = [("block_idx", C.c_int), ("phys_idx", C.c_int), ("score", C.c_float)]
 
@@ -88,6 +122,21 @@ def bind(lib):
         "select_top_k_blocks": (i32, [vp, vp, i32, i32]),
         "op_paged_attention": (None, [vp, vp, P(PagedKv), i32, i32, i32, f32]),
         "op_paged_attention_sparse": (None, [vp, vp, P(BlockManager), vp, i32, i32, i32, i32, f32]),
+        "op_rmsnorm": (None, [P(Tensor), P(Tensor), P(Tensor), f32]),
+        "op_silu_mul": (None, [P(Tensor), P(Tensor), P(Tensor)]),
+        "rope_apply_multihead_cached": (None, [vp, i32, i32, P(RopeCache)]),
+        "sample_argmax": (i32, [P(Tensor)]),
+        "lsh_stats_reset_atomic": (None, [P(LshStats)]),
+        "lsh_stats_print_atomic": (None, [P(LshStats), i32]),
+        "lsh_validate_recall": (f32, [vp, vp, i32, i32, vp, i32, i32]),
+        "adaptive_k_cutoff": (i32, [vp, vp, i32, f32]),
+        "kv_cache_init": (None, [P(KvCache), P(Arena), P(KvInitParams)]),
+        "kv_cache_append": (None, [P(KvCache), P(Tensor), P(Tensor)]),
+        "kv_cache_evict": (None, [P(KvCache), P(EvictParams)]),
+        "flash_attention_head": (None, [vp, vp, vp, vp, i32, i32, f32]),
+        "op_multihead_attention": (None, [P(AttentionParams)]),
+        "op_attention_dense": (None, [P(AttentionParams), i32]),
+        "op_attention_sparse": (None, [P(AttentionParams)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -8,6 +8,8 @@
 #include "compute/ops_lsh.h"
 #include "memory/paged.h"
 #include "compute/ops_quant.h"
+#include "memory/kv_cache.h"
+#include "compute/ops_attention.h"
 #else
 #include "be42_engine.h"
 #endif
@@ -25,6 +27,11 @@ int main(void) {
   O(t_block_manager, max_logical); O(t_block_manager, logical_len);
   S(t_paged_kv_cache); O(t_paged_kv_cache, layer_idx); O(t_paged_kv_cache, n_blocks); O(t_paged_kv_cache, n_tokens);
   S(t_block_score); O(t_block_score, phys_idx); O(t_block_score, score);
+  S(t_arena); O(t_arena, size); O(t_arena, offset);
+  O(t_kv_cache, v); O(t_kv_cache, max_seq_len); O(t_kv_cache, num_heads); O(t_kv_cache, head_dim); O(t_kv_cache, current_seq_len);
+  S(t_kv_init_params); S(t_evict_params); O(t_evict_params, w); O(t_evict_params, keep_k); O(t_evict_params, scratch);
+  S(t_attention_params); O(t_attention_params, kv_cache); O(t_attention_params, output); O(t_attention_params, n_heads);
+  O(t_attention_params, scale); O(t_attention_params, topk_idx); O(t_attention_params, attend_k);
   O(t_tensor, shape); O(t_tensor, stride); O(t_tensor, ndim); O(t_tensor, size); O(t_tensor, dtype);
   printf("DTYPE_F32 %d DTYPE_BF16 %d\n", (int)DTYPE_F32, (int)DTYPE_BF16);
   return 0;

@@ -205,6 +205,17 @@ class Oracle:
         _sig(L, "or_decoder_kv_append", C.c_int, C.c_void_p, C.c_int, f32p, f32p, C.c_int)
         _sig(L, "or_decoder_step", C.c_int, C.c_void_p, C.c_int, C.c_int, f32p, C.c_int)
         _sig(L, "or_decoder_force_kv", None, C.c_void_p, C.c_void_p, C.c_void_p)
+        _sig(L, "or_silu_mul_bf16", None, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int)
+        _sig(L, "or_argmax_bf16", C.c_int, C.c_void_p, C.c_int)
+        _sig(L, "or_lsh_validate_recall", C.c_float, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
+             C.c_int)
+        _sig(L, "or_adaptive_k_cutoff", C.c_int, C.c_void_p, C.c_int, C.c_float)
+        _sig(L, "or_attention_linear", None, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+             C.c_int, C.c_int, C.c_int, C.c_float, C.c_int)
+        _sig(L, "or_kv_evict", C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+             C.c_int)
+        _sig(L, "or_route_tokens", C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int,
+             C.c_void_p, C.c_void_p, C.c_int, C.c_int)
         _sig(L, "or_decoder_kv_append_n", C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int)
         _sig(L, "or_decoder_log_selection", None, C.c_void_p, C.c_void_p, C.c_void_p)
         _sig(L, "or_decoder_route", C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p)
@@ -235,6 +246,63 @@ class Oracle:
         out = np.zeros(len(g), np.float32)
         self.lib.or_silu_mul(out, np.ascontiguousarray(g, np.float32), np.ascontiguousarray(u, np.float32), len(g))
         return out
+
+    def silu_mul_bf16(self, g, u):
+        g = np.ascontiguousarray(g, np.uint16)
+        u = np.ascontiguousarray(u, np.uint16)
+        out = np.zeros_like(g)
+        self.lib.or_silu_mul_bf16(out.ctypes.data, g.ctypes.data, u.ctypes.data, len(g))
+        return out
+
+    def argmax_bf16(self, x):
+        x = np.ascontiguousarray(x, np.uint16)
+        return self.lib.or_argmax_bf16(x.ctypes.data, len(x))
+
+    def validate_recall(self, q, keys, lsh, actual_k):
+        q = np.ascontiguousarray(q, np.float32)
+        keys = np.ascontiguousarray(keys, np.uint16)
+        lsh = np.ascontiguousarray(lsh, np.int32)
+        return self.lib.or_lsh_validate_recall(q.ctypes.data, keys.ctypes.data, keys.shape[0], keys.shape[1],
+                                               lsh.ctypes.data, len(lsh), actual_k)
+
+    def adaptive_k(self, scores, threshold):
+        scores = np.ascontiguousarray(scores, np.float32)
+        return self.lib.or_adaptive_k_cutoff(scores.ctypes.data, len(scores), threshold)
+
+    def attention_linear(self, q, k, v, idx, n_heads, scale, threads=0):
+        """or_attention_linear: k, v [T][n_kv][hd] bf16; idx None = dense over T."""
+        T, n_kv, hd = k.shape
+        out = np.zeros(n_heads * hd, np.float32)
+        q = np.ascontiguousarray(q, np.float32)
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        ia = None if idx is None else np.ascontiguousarray(idx, np.int32)
+        self.lib.or_attention_linear(out.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                                     None if ia is None else ia.ctypes.data, T if ia is None else len(ia),
+                                     n_heads, n_kv, hd, scale, threads)
+        return out
+
+    def kv_evict(self, k, v, q, w, keep_k):
+        """or_kv_evict on copies; returns (k, v, new length)."""
+        k = np.ascontiguousarray(k, np.uint16).copy()
+        v = np.ascontiguousarray(v, np.uint16).copy()
+        n, heads, dim = k.shape
+        q = np.ascontiguousarray(q, np.uint16)
+        w = np.ascontiguousarray(w, np.uint16)
+        m = self.lib.or_kv_evict(k.ctypes.data, v.ctypes.data, n, heads, dim, q.ctypes.data, w.ctypes.data, keep_k)
+        return k, v, m
+
+    def route_tokens(self, k, kv_len, q, n_heads, hpT, index, window, sparse_k):
+        """or_route_tokens over the first kv_len rows of k [T][n_kv][hd]."""
+        T, n_kv, hd = k.shape
+        out = np.zeros(max(sparse_k, 1) + 1, np.int32)
+        k = np.ascontiguousarray(k, np.uint16)
+        q = np.ascontiguousarray(q, np.float32)
+        hpT = np.ascontiguousarray(hpT, np.float32)
+        n = self.lib.or_route_tokens(out.ctypes.data, k.ctypes.data, kv_len, n_kv, hd, q.ctypes.data, n_heads,
+                                     hpT.ctypes.data, C.byref(index.ix) if index is not None else None, window,
+                                     sparse_k)
+        return out[:n].copy() if n <= sparse_k and kv_len > sparse_k else None
 
     def argmax(self, x):
         return self.lib.or_argmax(np.ascontiguousarray(x, np.float32), len(x))
@@ -485,6 +553,17 @@ class RefLib:
         _sig(L, "ref_rope_apply", None, f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p, f32p)
         _sig(L, "ref_silu_mul", None, f32p, f32p, f32p, C.c_int)
         _sig(L, "ref_argmax", C.c_int, f32p, C.c_int)
+        _sig(L, "ref_silu_mul_bf16", None, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int)
+        _sig(L, "ref_argmax_bf16", C.c_int, C.c_void_p, C.c_int)
+        _sig(L, "ref_validate_recall", C.c_float, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
+             C.c_int)
+        _sig(L, "ref_adaptive_k", C.c_int, C.c_void_p, C.c_int, C.c_float)
+        _sig(L, "ref_attention_linear", None, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+             C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int)
+        _sig(L, "ref_kv_fill", None, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+             C.c_int)
+        _sig(L, "ref_kv_evict", C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+             C.c_void_p, C.c_int)
         # the reference's block_manager_init prints a banner on stdout; silence nothing,
         # tests capture it.
 

@@ -26,7 +26,8 @@ def test_layouts_match_ctypes_mirror(tmp_path):
     lay, _ = _probe(tmp_path, ["-I", os.path.join(ROOT, "include")])
     mirror = {"t_lsh_ctx": D.LshCtx, "t_block_acc": D.BlockAcc, "t_lsh_index": D.LshIndex, "t_kv_block": D.KvBlock,
               "t_block_manager": D.BlockManager, "t_paged_kv_cache": D.PagedKv, "t_block_score": D.BlockScore,
-              "t_tensor": D.Tensor}
+              "t_tensor": D.Tensor, "t_arena": D.Arena, "t_kv_cache": D.KvCache, "t_kv_init_params": D.KvInitParams,
+              "t_evict_params": D.EvictParams, "t_attention_params": D.AttentionParams}
     for key, val in lay.items():
         if "." in key:
             t, f = key.split(".")
@@ -37,9 +38,18 @@ def test_layouts_match_ctypes_mirror(tmp_path):
 
 @pytest.mark.skipif(not os.path.isdir(REF_SRC), reason="reference sources not present")
 def test_layouts_match_reference_headers(tmp_path):
-    _, mine = _probe(tmp_path, ["-I", os.path.join(ROOT, "include")])
-    _, ref = _probe(tmp_path, ["-DUSE_REF", "-I", REF_SRC])
-    assert mine == ref
+    mine, _ = _probe(tmp_path, ["-I", os.path.join(ROOT, "include")])
+    ref, _ = _probe(tmp_path, ["-DUSE_REF", "-I", REF_SRC])
+    assert mine.keys() == ref.keys()
+    # t_kv_cache holds two t_tensor by value, each one pointer (row_scale)
+    # longer than the reference's; every other layout is identical
+    grow = ctypes.sizeof(ctypes.c_void_p)
+    for key in mine:
+        if key.startswith("t_kv_cache."):
+            n_before = 1 if key == "t_kv_cache.v" else 2
+            assert int(mine[key]) == int(ref[key]) + n_before * grow, key
+        else:
+            assert mine[key] == ref[key], key
 
 
 def test_library_exports_lut_table():

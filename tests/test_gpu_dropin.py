@@ -283,3 +283,81 @@ def test_sparse_attention_skips_unmapped_ids(be, dl, orc):
                                  C.c_float(scale))
     assert not out3.any()
     dl.block_manager_free(C.byref(bm))
+
+
+def test_adjacent_ops(dl, orc):
+    """op_rmsnorm, op_silu_mul (F32 and BF16), rope_apply_multihead_cached and
+    sample_argmax through the drop-in ABI, bit-exact against the oracle (whose
+    functions are pinned to the compiled reference)."""
+    rng = np.random.default_rng(31)
+    # RMSNorm over 3 rows of 3072 and one column vector of 509
+    for rows, dim in ((3, 3072), (1, 509)):
+        x = (rng.standard_normal((rows, dim)) * 2).astype(np.float32)
+        w = orc.f32_to_bf16(rng.uniform(0.5, 1.5, dim).astype(np.float32))
+        out = np.zeros_like(x)
+        tx = D.tensor(x, D.DTYPE_F32, rows, dim) if rows > 1 else D.tensor(x, D.DTYPE_F32, dim, 1)
+        to = D.tensor(out, D.DTYPE_F32, rows, dim) if rows > 1 else D.tensor(out, D.DTYPE_F32, dim, 1)
+        tw = D.tensor(w, D.DTYPE_BF16, 1, dim)
+        dl.op_rmsnorm(C.byref(to), C.byref(tx), C.byref(tw), C.c_float(1e-5))
+        for r in range(rows):
+            np.testing.assert_array_equal(out[r], orc.rmsnorm(x[r], w, 1e-5))
+    # SiLU * up, F32 and BF16 (n not a multiple of 8: the scalar remainder)
+    n = 8195
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    out = np.zeros(n, np.float32)
+    dl.op_silu_mul(C.byref(D.tensor(out, D.DTYPE_F32, 1, n)), C.byref(D.tensor(g, D.DTYPE_F32, 1, n)),
+                   C.byref(D.tensor(u, D.DTYPE_F32, 1, n)))
+    np.testing.assert_array_equal(out, orc.silu_mul(g, u))
+    gb, ub = orc.f32_to_bf16(g), orc.f32_to_bf16(u)
+    ob = np.zeros(n, np.uint16)
+    dl.op_silu_mul(C.byref(D.tensor(ob, D.DTYPE_BF16, 1, n)), C.byref(D.tensor(gb, D.DTYPE_BF16, 1, n)),
+                   C.byref(D.tensor(ub, D.DTYPE_BF16, 1, n)))
+    np.testing.assert_array_equal(ob, orc.silu_mul_bf16(gb, ub))
+    # RoPE over 8 heads of 128 at a position inside and one past the table
+    hd, n_pos = 128, 300
+    cos_t, sin_t = orc.rope_table(hd, n_pos, 1e4)
+    cache = D.RopeCache(cos_t.ctypes.data, sin_t.ctypes.data, hd, n_pos)
+    for pos in (257, 300):
+        q = rng.standard_normal(8 * hd).astype(np.float32)
+        want = orc.rope_apply(q.copy(), 8, hd, pos, cos_t, sin_t)
+        dl.rope_apply_multihead_cached(D.ptr(q), 8, pos, C.byref(cache))
+        np.testing.assert_array_equal(q, want)
+    # argmax: F32 with equal maxima in different lanes and in the tail, BF16
+    x = rng.standard_normal(4099).astype(np.float32)
+    for idx in (17, 9, 4096, 3):
+        x[idx] = 5.0
+    tx = D.tensor(x, D.DTYPE_F32, 1, 4099)
+    assert dl.sample_argmax(C.byref(tx)) == orc.argmax(x) == 9
+    x[8] = 5.0
+    assert dl.sample_argmax(C.byref(tx)) == orc.argmax(x) == 8
+    xb = orc.f32_to_bf16(rng.standard_normal(1000).astype(np.float32))
+    assert dl.sample_argmax(C.byref(D.tensor(xb, D.DTYPE_BF16, 1, 1000))) == orc.argmax_bf16(xb)
+
+
+def test_lsh_diagnostics(dl, orc, capfd):
+    """lsh_validate_recall and adaptive_k_cutoff (ops_lsh.c:513-668) against
+    the oracle (pinned to the compiled reference); the stats counters reset
+    and print as the reference."""
+    rng = np.random.default_rng(44)
+    for n, dim, k in ((300, 128, 32), (9000, 64, 64), (50, 128, 80)):
+        q = rng.standard_normal(dim).astype(np.float32)
+        keys = orc.f32_to_bf16(rng.standard_normal((n, dim)).astype(np.float32))
+        lsh = rng.integers(0, n, 2 * k).astype(np.int32)
+        kf = (keys.astype(np.uint32) << 16).view(np.float32)
+        lsh[: k // 2] = np.argsort(-(kf @ q))[: k // 2]
+        got = dl.lsh_validate_recall(D.ptr(q), D.ptr(keys), n, dim, D.ptr(lsh), len(lsh), k)
+        assert got == orc.validate_recall(q, keys, lsh, k)
+    p = np.sort(rng.random(200).astype(np.float32))[::-1].copy()
+    p /= p.sum()
+    for thr in (0.3, 0.95, 5.0):
+        assert dl.adaptive_k_cutoff(D.ptr(p), None, len(p), C.c_float(thr)) == orc.adaptive_k(p, thr)
+    st = D.LshStats(5, 2, 30, 40, 0, 2, 96, 2)
+    dl.lsh_stats_print_atomic(C.byref(st), 64)
+    out = capfd.readouterr().out
+    assert "Queries: 5 (validated: 2)" in out and "Recall: 75.0%" in out and "Avg Dynamic K: 48.0" in out
+    dl.lsh_stats_reset_atomic(C.byref(st))
+    assert st.total_queries == 0 and st.k_samples == 0
+    dl.lsh_stats_print_atomic(C.byref(st), 64)
+    assert "No validation data" in capfd.readouterr().out
+

@@ -529,3 +529,49 @@ def test_live_reference_paged(orc, ref):
     ref.lib.ref_paged_attention_sparse(r, o2, q, sel, ns, n_heads, scale)
     np.testing.assert_array_equal(bits(pk.attention_pages(q, sel, n_heads, scale)), bits(o2))
     ref.lib.ref_paged_free(r)
+
+
+# --------------------------------------------------------------------------- LSH diagnostics
+def _recall_closed_form(q, keys_f, lsh, actual_k):
+    """Brute force in float64 on untied data: the top actual_k by q . key
+    (every stride-th key past 4096), recall = |lsh[:min(len, k)] & top| / k."""
+    n = keys_f.shape[0]
+    actual_k = min(actual_k, n)
+    lk = min(len(lsh), actual_k)
+    actual_k = min(actual_k, 64)
+    stride = n // 4096 if n > 4096 else 1
+    idx = np.arange(min(n, 4096)) * stride
+    sc = keys_f[idx].astype(np.float64) @ q.astype(np.float64)
+    top = set(idx[np.argsort(-sc, kind="stable")[:actual_k]].tolist())
+    return sum(1 for x in lsh[:lk] if int(x) in top) / actual_k
+
+
+@pytest.mark.parametrize("n,dim,k", [(300, 128, 32), (9000, 64, 64), (50, 128, 80)])
+def test_validate_recall(orc, ref, n, dim, k):
+    rng = np.random.default_rng(n + k)
+    q = rng.standard_normal(dim).astype(np.float32)
+    keys = orc.f32_to_bf16(rng.standard_normal((n, dim)).astype(np.float32))
+    kf = (keys.astype(np.uint32) << 16).view(np.float32)
+    sc = kf @ q
+    stride = n // 4096 if n > 4096 else 1
+    good = np.argsort(-sc[::stride][:4096])[:k] * stride
+    lsh = np.concatenate([good[: k // 2], rng.integers(0, n, k)]).astype(np.int32)
+    got = orc.validate_recall(q, keys, lsh, k)
+    want = ref.lib.ref_validate_recall(q.ctypes.data, keys.ctypes.data, n, dim, lsh.ctypes.data, len(lsh), k)
+    assert got == want
+    assert got == pytest.approx(_recall_closed_form(q, kf, lsh, k), abs=1e-7)
+    assert 0.0 < got <= 1.0
+
+
+def test_adaptive_k(orc, ref):
+    rng = np.random.default_rng(5)
+    p = rng.random(100).astype(np.float32)
+    p /= p.sum()
+    p = np.sort(p)[::-1].copy()
+    for thr in (0.0, 0.5, 0.95, 2.0):
+        got = orc.adaptive_k(p, thr)
+        assert got == ref.lib.ref_adaptive_k(p.ctypes.data, len(p), thr)
+        c = np.cumsum(p.astype(np.float32), dtype=np.float32)
+        want = max(1, int(np.argmax(c >= thr)) + 1) if (c >= thr).any() else len(p)
+        assert got == want
+

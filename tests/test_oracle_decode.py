@@ -84,6 +84,37 @@ def test_argmax(orc, ref):
     assert orc.argmax(x) == ref.lib.ref_argmax(x.copy(), 4099) == 8
 
 
+@pytest.mark.parametrize("n", [4099, 8192, 13])
+def test_silu_mul_bf16(orc, ref, n):
+    """op_silu_mul_fused_bf16: bit-exact against the compiled reference; the
+    result is the f32 SiLU of the bf16 inputs truncated to bf16 (closed form
+    on the inputs, with the f32 oracle giving the unrounded values)."""
+    rng = np.random.default_rng(n + 5)
+    g = _bf16(orc, rng.standard_normal(n) * 3)
+    u = _bf16(orc, rng.standard_normal(n))
+    got = orc.silu_mul_bf16(g, u)
+    want = np.zeros(n, np.uint16)
+    ref.lib.ref_silu_mul_bf16(want.ctypes.data, g.ctypes.data, u.ctypes.data, n)
+    np.testing.assert_array_equal(got, want)
+    f = lambda b: (b.astype(np.uint32) << 16).view(np.float32)
+    full = orc.silu_mul(f(g), f(u))
+    np.testing.assert_array_equal(got, (full.view(np.uint32) >> 16).astype(np.uint16))
+
+
+def test_argmax_bf16(orc, ref):
+    """argmax_loop_bf16: first maximum, strict >, -1e9 floor (all-lower input
+    gives index 0)."""
+    rng = np.random.default_rng(12)
+    x = _bf16(orc, rng.standard_normal(5000))
+    for arr in (x, np.concatenate([x, x]), _bf16(orc, np.full(9, -2e9, np.float32))):
+        a = np.ascontiguousarray(arr)
+        keep = a.copy()
+        want = ref.lib.ref_argmax_bf16(keep.ctypes.data, len(a))
+        assert orc.argmax_bf16(a) == want
+    assert orc.argmax_bf16(x) == int(np.argmax((x.astype(np.uint32) << 16).view(np.float32)))
+    assert orc.argmax_bf16(_bf16(orc, np.full(9, -2e9, np.float32))) == 0
+
+
 def tiny_model(rng, n_layers=2, dim=64, n_heads=4, n_kv=2, hd=16, hidden=96, vocab=300, kind="int8"):
     """Random-init weights in the configs[0] recipe (codes U{-127..127},
     row scales U[0.005, 0.02], norms 1.0)."""
