@@ -1,0 +1,118 @@
+"""The link recipe of INTEGRATION.md, exercised without a GPU: the reference's
+own sources (from /root/reference, compiled into a temporary directory, never
+into the repository) with the documented tensor.h change, the documented
+objects dropped and symbols renamed with objcopy, linked against
+lib42be_hip.so.  The executable must link with no undefined symbol, define
+none of the library's entry points (a definition left in an object would
+silently win over the library), and import the ones the engine calls."""
+import os
+import re
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+
+from test_abi import declared_functions
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REF = "/root/reference"
+LIBDIR = os.path.join(ROOT, "42-berlin-engine_amd")
+DOC = os.path.join(ROOT, "INTEGRATION.md")
+
+pytestmark = pytest.mark.skipif(not os.path.isdir(os.path.join(REF, "src")) or shutil.which("objcopy") is None,
+                                reason="reference sources or binutils not present")
+
+
+def _make_vars(text):
+    """name -> value of `NAME = ...` / `NAME := ...` lines with continuations."""
+    text = text.replace("\\\n", " ")
+    out = {}
+    for m in re.finditer(r"^([A-Z_]+)\s*[:?]?=\s*(.*)$", text, flags=re.M):
+        out[m.group(1)] = m.group(2).strip()
+    return out
+
+
+def _expand(value, env):
+    return re.sub(r"\$\((\w+)\)", lambda m: env.get(m.group(1), ""), value)
+
+
+def _doc_blocks(lang):
+    text = open(DOC).read()
+    return re.findall(r"```" + lang + r"\n(.*?)```", text, flags=re.S)
+
+
+def _patched_tensor_h(src_dir):
+    """Apply the header change INTEGRATION.md shows: its t_dtype and t_tensor
+    replace the reference's."""
+    c = _doc_blocks("c")[0]
+    path = os.path.join(src_dir, "tensor", "tensor.h")
+    h = open(path).read()
+    h2, n1 = re.subn(r"typedef enum e_dtype\s*\{.*?\}\s*t_dtype;", lambda _: re.search(
+        r"typedef enum e_dtype.*?t_dtype;", c, flags=re.S).group(0), h, flags=re.S)
+    h3, n2 = re.subn(r"typedef struct s_tensor\s*\{.*?\}\s*t_tensor;", lambda _: re.search(
+        r"typedef struct s_tensor.*?t_tensor;", c, flags=re.S).group(0), h2, flags=re.S)
+    assert n1 == 1 and n2 == 1
+    with open(path, "w") as f:
+        f.write(h3)
+
+
+def test_reference_links_against_library(tmp_path):
+    lib = os.path.join(LIBDIR, "lib42be_hip.so")
+    assert os.path.exists(lib), "run __graft_entry__.build() first"
+    work = tmp_path / "engine"
+    shutil.copytree(os.path.join(REF, "src"), work / "src")
+    _patched_tensor_h(str(work / "src"))
+
+    mk = _make_vars(open(os.path.join(REF, "Makefile")).read())
+    env = {"SRC_DIR": "src"}
+    srcs = []
+    for var in ("CORE_SRCS", "COMPUTE_SRCS", "MEMORY_SRCS", "NESTED_SRCS", "ENGINE_SRCS", "MAIN_SRC"):
+        srcs += _expand(mk[var], env).split()
+    cflags = ["-O0", "-march=x86-64-v3", "-mavx2", "-mfma", "-fopenmp", "-Isrc"] + _expand(
+        mk["CONFIG_FLAGS"], mk).split()
+
+    def cc(src):
+        obj = src[:-2] + ".o"
+        r = subprocess.run(["gcc"] + cflags + ["-c", src, "-o", obj], cwd=work, capture_output=True, text=True)
+        return src, r.returncode, r.stderr
+
+    with ThreadPoolExecutor(8) as ex:
+        for src, rc, err in ex.map(cc, srcs):
+            assert rc == 0, (src, err[-2000:])
+    objs = [s[:-2] + ".o" for s in srcs]
+
+    # the documented recipe: DROPPED, the *_SYMS variables and the objcopy lines
+    block = [b for b in _doc_blocks("make") if "DROPPED" in b][0]
+    dv = _make_vars(block)
+    dropped = set(_expand(dv["DROPPED"], env).split())
+    assert dropped <= set(objs), dropped - set(objs)
+    renamed = []
+    for m in re.finditer(r"objcopy \$\(foreach s,\$\((\w+)\),--redefine-sym \$\(s\)=cpu_\$\(s\)\) (\S+)", block):
+        syms = dv[m.group(1)].split()
+        obj = _expand(m.group(2), env)
+        args = []
+        for s in syms:
+            args += ["--redefine-sym", f"{s}=cpu_{s}"]
+        subprocess.run(["objcopy"] + args + [obj], cwd=work, check=True)
+        renamed += syms
+    assert renamed
+    keep = [o for o in objs if o not in dropped]
+    r = subprocess.run(["gcc"] + keep + ["-o", "engine", f"-L{LIBDIR}", "-l42be_hip", f"-Wl,-rpath,{LIBDIR}",
+                                         "-Wl,-rpath-link,/opt/rocm/lib", "-lm", "-fopenmp"],
+                       cwd=work, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+
+    def syms(*flags):
+        out = subprocess.run(["nm"] + list(flags) + ["engine"], cwd=work, capture_output=True, text=True,
+                             check=True).stdout
+        return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+    entry = declared_functions()
+    defined = {s for s in syms("--defined-only") if not s.startswith("cpu_")}
+    assert not (defined & entry), sorted(defined & entry)
+    imported = syms("-D", "--undefined-only")
+    for name in ("op_matmul", "paged_kv_append", "op_paged_attention_sparse", "score_blocks",
+                 "select_top_k_blocks", "lsh_update", "op_rmsnorm", "op_silu_mul", "rope_apply_multihead_cached",
+                 "sample_argmax", "kv_cache_append", "op_multihead_attention"):
+        assert name in imported, name
