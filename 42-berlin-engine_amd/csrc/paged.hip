@@ -21,6 +21,7 @@
 // The page allocator (free stack, page table, logical lengths) is host
 // bookkeeping exactly as in the reference; the device copies of the page
 // table and per-layer counts are updated with each append.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -54,6 +55,11 @@ struct PoolImpl {
     std::vector<int> logical_len;  // [n_layers]
     std::vector<int> registered;   // [cap]
     std::vector<int> n_indexed;    // [n_layers]
+    // page lists of a bulk append (device copy, and the host array it is
+    // copied from, which stays untouched until the next bulk append has
+    // waited for the stream)
+    int *d_lists = nullptr;
+    std::vector<int> h_lists;
 };
 
 static PoolImpl *impl(be42_kv_pool *p) { return reinterpret_cast<PoolImpl *>(p); }
@@ -205,6 +211,52 @@ __device__ __forceinline__ void seal_page(const void *__restrict__ kpool, const 
         if (h == 0)
             *hash_out = (uint16_t)(m & 0xFFFFu);
     }
+}
+
+// A bulk append: one wave per (token, kv head) of n_tok consecutive
+// positions, the physical page of each touched logical page read from a list
+// (page_phys[blk - first_blk]); block (0, 0) publishes the new page-table
+// entries.
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_kv_append_bulk(void *__restrict__ kdst, void *__restrict__ vdst,
+                                                       float *__restrict__ kscale, float *__restrict__ vscale,
+                                                       int *__restrict__ ntok, int *__restrict__ page_table,
+                                                       int *__restrict__ n_logical, const int *__restrict__ lists,
+                                                       int pos0, int n_tok, int first_blk, int n_pages, int n_new,
+                                                       int new_first, int layer_base, int layer, int n_log,
+                                                       const float *__restrict__ k, const float *__restrict__ v,
+                                                       int n_kv, int hd)
+{
+    const int tok = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int pos = pos0 + tok, off = pos % kPage;
+    const int phys = lists[pos / kPage - first_blk];
+    if (tok == 0 && h == 0) {
+        for (int i = lane; i < n_new; i += kWave)
+            page_table[layer_base + new_first + i] = lists[n_pages + i];
+        if (lane == 0)
+            n_logical[layer] = n_log;
+    }
+    const size_t slot = ((size_t)phys * n_kv + h) * kPage + off;
+    store_kv_row<BF16>(kdst, vdst, kscale, vscale, slot, k + (size_t)tok * n_kv * hd + (size_t)h * hd,
+                       v + (size_t)tok * n_kv * hd + (size_t)h * hd, hd, lane);
+    if (h == 0 && lane == 0 && (off == kPage - 1 || tok == n_tok - 1))
+        ntok[phys] = off + 1;
+}
+
+// One block per page a bulk append filled: seal list (physical, logical) at
+// lists[0 .. n_seal), lists[n_seal .. 2 n_seal).
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_kv_seal_bulk(const void *__restrict__ kpool, const float *__restrict__ kscale,
+                                                      float *__restrict__ centroid, uint16_t *__restrict__ page_hash,
+                                                      int *__restrict__ n_indexed, const int *__restrict__ lists,
+                                                      int n_seal, int layer_base, int layer, int n_idx,
+                                                      const float *__restrict__ hpT, int n_kv, int hd)
+{
+    __shared__ float c[256];
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        n_indexed[layer] = n_idx;
+    seal_page<BF16>(kpool, kscale, centroid, page_hash + layer_base + lists[n_seal + blockIdx.x],
+                    lists[blockIdx.x], hpT, n_kv, hd, c);
 }
 
 template <bool BF16>
@@ -387,7 +439,10 @@ extern "C" void be42_kv_destroy(be42_kv_pool *pool)
     if (!pool)
         return;
     void *ptrs[] = {pool->k, pool->v, pool->k_scale, pool->v_scale, pool->centroid, pool->ntok,
-                    pool->page_table, pool->n_logical, pool->page_hash, pool->n_indexed, (void *)pool->hpT};
+                    pool->page_table, pool->n_logical, pool->page_hash, pool->n_indexed, (void *)pool->hpT,
+                    impl(pool)->d_lists};
+    if (impl(pool)->d_lists)
+        (void)hipDeviceSynchronize();   // a bulk append may still read its lists
     for (void *q : ptrs)
         if (q)
             (void)hipFree(q);
@@ -476,6 +531,84 @@ static int append_chunk(PoolImpl *p, int layer, const float *k, const float *v, 
     return BE42_OK;
 }
 
+// More than kArgTok tokens: the same bookkeeping for the whole run, its page
+// lists copied to the device, then one append launch and one seal launch.
+static int append_bulk(PoolImpl *p, int layer, const float *k, const float *v, int pos0, int n, hipStream_t s)
+{
+    be42_kv_pool &P = p->pub;
+    const int layer_base = layer * P.max_logical;
+    const int first_blk = pos0 / kPage, last_blk = (pos0 + n - 1) / kPage;
+    const int n_pages = last_blk - first_blk + 1;
+    const int new_first = p->logical_len[layer];
+    // the previous bulk append's lists (host and device) may still be in use
+    BE42_HIP(hipStreamSynchronize(s));
+    if (!p->d_lists) {
+        p->h_lists.assign((size_t)4 * P.max_logical + 4, 0);
+        BE42_HIP(hipMalloc((void **)&p->d_lists, p->h_lists.size() * sizeof(int)));
+    }
+    int *L = p->h_lists.data();
+    std::vector<int> fresh;
+    for (int blk = first_blk; blk <= last_blk; blk++) {
+        if (blk >= p->logical_len[layer]) {
+            if (blk != p->logical_len[layer]) {
+                set_error("be42_kv_append: position %d skips page %d", blk * kPage, p->logical_len[layer]);
+                return BE42_EINVAL;
+            }
+            const int phys = pool_alloc(p);
+            if (phys < 0) {
+                set_error("be42_kv_append: page pool exhausted at pos %d", blk * kPage);
+                return BE42_ENOMEM;
+            }
+            p->page_table[layer_base + blk] = phys;
+            p->logical_len[layer] = blk + 1;
+            fresh.push_back(phys);
+        }
+        L[blk - first_blk] = p->page_table[layer_base + blk];
+    }
+    const int n_new = (int)fresh.size();
+    std::copy(fresh.begin(), fresh.end(), L + n_pages);
+    int *seal = L + n_pages + n_new;
+    std::vector<int> seal_logical;
+    for (int blk = first_blk; blk <= last_blk; blk++) {
+        const int phys = p->page_table[layer_base + blk];
+        const int end = (blk + 1) * kPage - 1;          // the page's last position
+        if (end >= pos0 && end < pos0 + n && !p->registered[phys]) {
+            p->registered[phys] = 1;
+            seal[seal_logical.size()] = phys;
+            seal_logical.push_back(blk);
+            if (blk + 1 > p->n_indexed[layer])
+                p->n_indexed[layer] = blk + 1;
+        }
+    }
+    const int n_seal = (int)seal_logical.size();
+    std::copy(seal_logical.begin(), seal_logical.end(), seal + n_seal);
+    const size_t used = (size_t)n_pages + n_new + 2 * n_seal;
+    BE42_HIP(hipMemcpyAsync(p->d_lists, L, used * sizeof(int), hipMemcpyHostToDevice, s));
+    const dim3 grid(n, P.n_kv);
+    if (P.kind == BE42_KV_BF16)
+        hipLaunchKernelGGL(k_kv_append_bulk<true>, grid, dim3(64), 0, s, P.k, P.v, P.k_scale, P.v_scale, P.ntok,
+                           P.page_table, P.n_logical, p->d_lists, pos0, n, first_blk, n_pages, n_new, new_first,
+                           layer_base, layer, p->logical_len[layer], k, v, P.n_kv, P.head_dim);
+    else
+        hipLaunchKernelGGL(k_kv_append_bulk<false>, grid, dim3(64), 0, s, P.k, P.v, P.k_scale, P.v_scale, P.ntok,
+                           P.page_table, P.n_logical, p->d_lists, pos0, n, first_blk, n_pages, n_new, new_first,
+                           layer_base, layer, p->logical_len[layer], k, v, P.n_kv, P.head_dim);
+    BE42_LAUNCH_CHECK();
+    if (n_seal) {
+        const int *sl = p->d_lists + n_pages + n_new;
+        if (P.kind == BE42_KV_BF16)
+            hipLaunchKernelGGL(k_kv_seal_bulk<true>, dim3(n_seal), dim3(256), 0, s, P.k, P.k_scale, P.centroid,
+                               P.page_hash, P.n_indexed, sl, n_seal, layer_base, layer, p->n_indexed[layer], P.hpT,
+                               P.n_kv, P.head_dim);
+        else
+            hipLaunchKernelGGL(k_kv_seal_bulk<false>, dim3(n_seal), dim3(256), 0, s, P.k, P.k_scale, P.centroid,
+                               P.page_hash, P.n_indexed, sl, n_seal, layer_base, layer, p->n_indexed[layer], P.hpT,
+                               P.n_kv, P.head_dim);
+        BE42_LAUNCH_CHECK();
+    }
+    return BE42_OK;
+}
+
 extern "C" int be42_kv_append(be42_kv_pool *pool, int layer, const float *k, const float *v, int pos0,
                               int n_tokens, void *stream)
 {
@@ -489,6 +622,8 @@ extern "C" int be42_kv_append(be42_kv_pool *pool, int layer, const float *k, con
     BE42_CHECK((pos0 + n_tokens - 1) / kPage < P.max_logical, "be42_kv_append: position %d beyond %d pages",
                pos0 + n_tokens - 1, P.max_logical);
     hipStream_t s = as_stream(stream);
+    if (n_tokens > kArgTok)
+        return append_bulk(p, layer, k, v, pos0, n_tokens, s);
     const size_t row = (size_t)P.n_kv * P.head_dim;
     for (int t = 0; t < n_tokens; t += kArgTok) {
         const int n = n_tokens - t < kArgTok ? n_tokens - t : kArgTok;

@@ -40,6 +40,40 @@ def host_cores():
         return os.cpu_count() or 1
 
 
+def cpu_threads():
+    """Threads for the CPU baselines: every CPU this job is granted.  A GPU
+    box grants each GPU's job a share of the host and states it in
+    OMP_NUM_THREADS (16 per GPU); without it, every CPU the process may run
+    on."""
+    avail = host_cores()
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return min(int(env), avail)
+    return avail
+
+
+def host_info():
+    """The host the CPU baselines ran on: model, sockets, logical CPUs, and
+    the job's CPU grant (cgroup cpu.max, OMP_NUM_THREADS)."""
+    model, sockets = None, set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model is None:
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("physical id"):
+                sockets.add(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    quota = None
+    try:
+        quota = open("/sys/fs/cgroup/cpu.max").read().strip()
+    except OSError:
+        pass
+    return {"cpu_model": model, "sockets": len(sockets) or None, "logical_cpus": os.cpu_count(),
+            "affinity_cpus": host_cores(), "cgroup_cpu_max": quota,
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+
+
 def cpu_baseline(seconds=10.0):
     """The oracle's OpenMP GEMV (a port of the reference GEMV structure with
     the reference dequantisation) on a bounded sample: INT8 14336x4096, B=1."""
@@ -47,7 +81,7 @@ def cpu_baseline(seconds=10.0):
     from oracle_bind import Oracle
 
     orc = Oracle()
-    cores = min(16, host_cores())
+    cores = cpu_threads()
     rng = np.random.default_rng(1)
     n, k = 14336, 4096
     wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
@@ -110,6 +144,7 @@ def plant_keys_gpu(K, q, gen, cfg=LSH):
     rows = (pages[:, None] * P + torch.arange(P, device=K.device)).reshape(-1)
     noise = torch.randn(rows.numel(), KVH, hd, generator=gen, device=K.device) * 0.05
     K.view(T, KVH, hd)[rows] = u + noise
+    return pages
 
 
 def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
@@ -126,15 +161,33 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(4)
     q = rng.standard_normal((BM, H, hd)).astype(np.float32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    P, G, npg = cfg["page"], H // KVH, T // cfg["page"]
+    exact_top, planted, page_mass = [], [], []
     for b in range(BM):
         K = torch.randn(T, KVH * hd, generator=gen, device="cuda")
-        plant_keys_gpu(K, q[b], gen)
+        planted.append(set(plant_keys_gpu(K, q[b], gen).tolist()))
         V = torch.randn(T, KVH * hd, generator=gen, device="cuda")
         pool.append(b, K, V, 0)
-        del K, V
+        # the selection over every page: the anchors (first, last) and the
+        # k-2 best middle pages by q head 0 . head-0 centroid (what
+        # score_blocks + select_top_k_blocks rank, over all pages)
+        cs = K.view(npg, P, KVH, hd)[:, :, 0, :].bfloat16().float().mean(1) @ torch.from_numpy(q[b, 0]).cuda()
+        mid = torch.topk(cs[1:npg - 1], cfg["k_sel"] - 2).indices + 1
+        exact_top.append(set(mid.tolist()) | {0, npg - 1})
+        # dense softmax mass per page, averaged over heads
+        qb = torch.from_numpy(q[b]).cuda().view(KVH, G, hd).transpose(1, 2).contiguous()
+        lg = torch.bmm(K.view(T, KVH, hd).transpose(0, 1).contiguous(), qb) * scale
+        page_mass.append(torch.softmax(lg, dim=1).view(KVH, npg, P, G).sum(2).mean(dim=(0, 2)).cpu().numpy())
+        del K, V, lg
     torch.cuda.synchronize()
+    phys_to_logical = []
+    for b in range(BM):
+        m = {}
+        for j, ph in enumerate(pool.layer_pages(b)):
+            m[int(ph)] = j
+        phys_to_logical.append(m)
     qall = torch.from_numpy(q).cuda()
-    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
     sel_stride = 64
     n_split = 1        # <= 64 pages: the single fused kernel
     rows = []
@@ -190,6 +243,17 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
         assert torch.equal(fsel, sel) and torch.equal(fnsel, nsel), "fused and two-launch selections differ"
         ns = fnsel.cpu().numpy()
         nc = ncand.cpu().numpy()
+        # recall of the LSH route against the same selection over every
+        # page (lsh_validate_recall's hits / k, ops_lsh.c:587, with the
+        # paged path's own ranking), the planted pages it found, and the
+        # share of the dense softmax mass the selected pages hold
+        fs = fsel.cpu().numpy()
+        rec, found, held = [], [], []
+        for b in range(B):
+            got = {phys_to_logical[b][int(x)] for x in fs[b, :ns[b]]}
+            rec.append(len(got & exact_top[b]) / cfg["k_sel"])
+            found.append(len(got & planted[b]) / min(cfg["k_sel"] - 2, len(planted[b])))
+            held.append(float(page_mass[b][sorted(got)].sum()))
         nbytes = sum(lsh_bytes(int(a), int(c)) for a, c in zip(ns, nc))
         kv_bytes = sum(int(a) * cfg["page"] * KVH * hd * 2 * 2 for a in ns)
         rows.append({"batch": B, "us_per_token": round(tot_ms * 1e3 / B, 3), "step_us": round(tot_ms * 1e3, 2),
@@ -198,15 +262,29 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
                      "n_sel_mean": float(ns.mean()), "n_cand_mean": float(nc.mean()),
                      "bytes_per_step": nbytes, "GBps": round(nbytes / (tot_ms * 1e-3) / 1e9, 1),
                      "frac_of_hbm_peak": round(nbytes / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "attention_GBps": round(kv_bytes / (attn_ms * 1e-3) / 1e9, 1)})
+                     "attention_GBps": round(kv_bytes / (attn_ms * 1e-3) / 1e9, 1),
+                     "recall_at_k": round(float(np.mean(rec)), 4), "planted_found": round(float(np.mean(found)), 4),
+                     "attention_mass_held": round(float(np.mean(held)), 4)})
     pool.close()
-    head = max(rows, key=lambda r: r["batch"])
-    return {"workload": f"configs[3]: B sequences x {T}-token bf16 paged KV (page 16), {H} heads / {KVH} KV heads, "
+    head = max(rows, key=lambda r: r["frac_of_hbm_peak"])
+    launch_bytes = head["bytes_per_step"]
+    achieved = launch_bytes / (head["step_us"] * 1e-6) / 1e9
+    roof = {"bound": "hbm", "kernel": "be42::k_attn_fused (route + attention, one launch)",
+            "workload": f"batch {head['batch']}, {T}-token bf16 context",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": lsh_traffic(head["batch"]),
+            "bytes_per_launch": launch_bytes, "launch_us": head["step_us"]}
+    return {"roofline": roof,
+            "recall_definition": "recall_at_k: share of the k pages the same ranking selects over every page "
+                                 "(anchors + best middle pages by q head 0 . head-0 centroid) that the LSH route "
+                                 "selects; planted_found: planted pages selected / min(k-2, planted); "
+                                 "attention_mass_held: dense softmax mass of the selected pages, averaged over heads",
+            "workload": f"configs[3]: B sequences x {T}-token bf16 paged KV (page 16), {H} heads / {KVH} KV heads, "
                         f"head_dim {hd}, top-K {cfg['k_sel']} pages, candidate cap {cfg['cap']}, 5% planted pages; "
                         f"one step = route + sparse attention of one decode token per sequence "
                         f"(be42_lsh_attention: one launch up to 512 query x KV-head pairs, two above; "
                         f"route_us / attention_us time the work as two launches)",
-            "us_per_token": head["us_per_token"], "batch": head["batch"],
+            "us_per_token": head["us_per_token"], "batch": head["batch"], "recall_at_k": head["recall_at_k"],
             "frac_of_hbm_peak": head["frac_of_hbm_peak"], "by_batch": rows}
 
 
@@ -252,7 +330,18 @@ def gemm_bench(lib, steps, warmup):
     tot_ops = sum(2.0 * r["m"] * r["n"] * r["k"] for r in rows)
     tot_s = sum(r["us"] for r in rows) * 1e-6
     best = max(rows, key=lambda r: r["TOPS"])
-    return {"workload": "configs[2]: M in {512,2048,8192} x (N,K) in {4096x4096, 14336x4096, 4096x14336, "
+    traffic = None
+    summ = os.path.join(ROOT, "profiles", "gemm_fp8_8192x4096x14336_and_int8_512x4096x4096_counters.txt")
+    tag = f"traffic_bytes_per_launch[{best['kind']} {best['m']}x{best['n']}x{best['k']}]"
+    if os.path.exists(summ):
+        for line in open(summ):
+            if line.startswith(tag):
+                traffic = int(line.split("=")[1].split()[0])
+    roof = {"bound": "mfma", "kernel": "be42::k_gemm_dma", "workload": f"{best['kind']} M={best['m']} "
+            f"N={best['n']} K={best['k']}", "achieved": best["TOPS"], "peak": MFMA_PEAK_TOPS[best["kind"]],
+            "unit": "TFLOP/s", "frac": best["frac_of_mfma_peak"], "traffic": traffic,
+            "ops_per_launch": 2 * best["m"] * best["n"] * best["k"], "launch_us": best["us"]}
+    return {"roofline": roof, "workload": "configs[2]: M in {512,2048,8192} x (N,K) in {4096x4096, 14336x4096, 4096x14336, "
                         "128256x4096}, INT8xINT8 and FP8xFP8 per-token x per-row scaled",
             "TOPS_aggregate": round(tot_ops / tot_s / 1e12, 1), "best": best, "by_shape": rows}
 
@@ -428,7 +517,7 @@ def decode_cpu_baseline(seconds=10.0):
     import numpy as np
     from oracle_bind import OR_KV_INT8, Oracle, OracleDecoder
     orc = Oracle()
-    cores = min(16, host_cores())
+    cores = cpu_threads()
     rng = np.random.default_rng(31)
     A = TINY
     d, H, KV, hd, F, V = (A[k] for k in ("dim", "n_heads", "n_kv_heads", "head_dim", "hidden_dim", "vocab"))
@@ -475,7 +564,7 @@ def lsh_cpu_baseline(seconds=10.0):
     from oracle_bind import OR_KV_BF16, Oracle, OracleIndex, OraclePaged
     cfg = LSH
     orc = Oracle()
-    cores = min(16, host_cores())
+    cores = cpu_threads()
     H, KVH, hd, T, P = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["ctx"], cfg["page"]
     rng = np.random.default_rng(5)
     _, hpT = orc.lsh_init(hd, 42)
@@ -501,6 +590,177 @@ def lsh_cpu_baseline(seconds=10.0):
     return {"value": round(med * 1e6, 1), "unit": "us/token", "cores": cores, "kind": "port",
             "sample": f"oracle or_route_pages + or_paged_attention_pages (bf16 pages), one {T}-token sequence, "
                       f"OpenMP {cores} threads over heads, median of {len(times)} runs"}
+
+
+def decode_3b_cpu_baseline(seconds=12.0):
+    """The oracle's transformer_forward (OpenMP GEMVs, LSH page route and bf16
+    paged attention) on the configs[4] model dimensions at batch 1 after a
+    32k-token prefix per layer.  A 28-layer step does not fit a bounded
+    sample, so models of 1 and 2 layers of the same dimensions are timed and
+    the step is extrapolated: t28 = t1 + 27 (t2 - t1)."""
+    import numpy as np
+    from oracle_bind import OR_KV_BF16, Oracle, OracleDecoder
+    orc = Oracle()
+    cores = cpu_threads()
+    rng = np.random.default_rng(43)
+    A = B3
+    d, H, KV, hd, F, V = (A[k] for k in ("dim", "n_heads", "n_kv_heads", "head_dim", "hidden_dim", "vocab"))
+    # E4M3 codes without the NaN code (|c| <= 0x7E), tiled from one random block
+    block = (rng.integers(0, 0x7F, 1 << 24, dtype=np.uint8) | (rng.integers(0, 2, 1 << 24, dtype=np.uint8) << 7))
+
+    def fp8(r, c):
+        return np.resize(block, (r, c)), (rng.uniform(0.5, 1.0, r) * (0.02 / 448.0)).astype(np.float32)
+    one = np.full(d, 0x3F80, np.uint16)
+
+    def layer():
+        Lw = {}
+        for name, (r, c) in {"wq": (H * hd, d), "wk": (KV * hd, d), "wv": (KV * hd, d), "wo": (d, H * hd),
+                             "w1": (F, d), "w3": (F, d), "w2": (d, F)}.items():
+            Lw[name], Lw["s" + name[1:]] = fp8(r, c)
+        Lw["attn_norm"], Lw["ffn_norm"] = one, one
+        return Lw
+    layers = [layer(), layer()]
+    emb, emb_s = fp8(V, d)
+    out, out_s = fp8(V, d)
+    _, hpT = orc.lsh_init(hd, 42)
+    T = B3_CTX
+    times = {}
+    for n_layers in (1, 2):
+        w = dict(emb=emb, emb_s=emb_s, final_norm=one, out=out, out_s=out_s, layers=layers[:n_layers])
+        cfg = dict(n_layers=n_layers, dim=d, n_heads=H, n_kv=KV, hd=hd, hidden=F, vocab=V, max_seq=T + 256,
+                   wkind=1, kv_kind=OR_KV_BF16, sparse_k=64, cand_cap=64, theta=1e4, eps=1e-5)
+        dec = OracleDecoder(orc, cfg, w, hpT)
+        for l in range(n_layers):
+            dec.kv_append_n(l, rng.standard_normal((T, KV * hd)).astype(np.float32),
+                            rng.standard_normal((T, KV * hd)).astype(np.float32), 0)
+        tok = 1
+        tok, _ = dec.step(tok, T, threads=cores)            # warm-up
+        ts = []
+        t_end = time.perf_counter() + seconds / 2
+        pos = T + 1
+        while time.perf_counter() < t_end and pos < T + 200:
+            t0 = time.perf_counter()
+            tok, _ = dec.step(tok, pos, threads=cores)
+            ts.append(time.perf_counter() - t0)
+            pos += 1
+        times[n_layers] = (sorted(ts)[len(ts) // 2], len(ts))
+        del dec
+    t1, t2 = times[1][0], times[2][0]
+    t28 = t1 + (A["n_layers"] - 1) * (t2 - t1)
+    return {"value": round(1.0 / t28, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "t_1layer_ms": round(t1 * 1e3, 2), "t_2layer_ms": round(t2 * 1e3, 2), "host": host_info(),
+            "sample": f"oracle or_decoder_step on the configs[4] dimensions (FP8 weights, bf16 pages, LSH route "
+                      f"top-64 pages) at position {T} after a random {T}-token prefix, batch 1, OpenMP {cores} "
+                      f"threads: 1- and 2-layer models timed ({times[1][1]} and {times[2][1]} steps, medians), "
+                      f"28-layer step extrapolated as t1 + 27 (t2 - t1)"}
+
+
+def gemm_cpu_baseline(seconds=10.0):
+    """The oracle's OpenMP GEMM (per-token x per-row scaled FP8, the
+    reference's dequantised dot order) on a bounded sample of configs[2]:
+    FP8 M=512 x 4096x4096."""
+    import numpy as np
+    from oracle_bind import Oracle
+    orc = Oracle()
+    cores = cpu_threads()
+    rng = np.random.default_rng(12)
+    m, n, k = 512, 4096, 4096
+    xq, sx = orc.quantize_rows(rng.standard_normal((m, k)).astype(np.float32), "fp8")
+    wq, sw = orc.quantize_rows((rng.standard_normal((n, k)) * 0.02).astype(np.float32), "fp8")
+    orc.gemm(xq[:16], sx[:16], wq, sw, "fp8", threads=cores)     # warm-up
+    ts = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end and len(ts) < 50:
+        t0 = time.perf_counter()
+        orc.gemm(xq, sx, wq, sw, "fp8", threads=cores)
+        ts.append(time.perf_counter() - t0)
+    med = sorted(ts)[len(ts) // 2]
+    return {"value": round(2.0 * m * n * k / med / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "host": host_info(),
+            "sample": f"oracle or_gemm_fp8 M={m} N={n} K={k}, OpenMP {cores} threads, median of {len(ts)} runs"}
+
+
+LSH_PMC_SUMMARY = os.path.join(ROOT, "profiles", "lsh_attn_fused_32k_pmc.txt")
+
+
+def lsh_traffic(batch):
+    """HBM bytes per launch of the fused route + attention at this batch, from
+    the committed rocprofv3 --pmc summary (scaled like the GEMV's)."""
+    if not os.path.exists(LSH_PMC_SUMMARY):
+        return None
+    for line in open(LSH_PMC_SUMMARY):
+        if line.startswith(f"traffic_bytes_per_launch[b={batch}]"):
+            return int(line.split("=")[-1].split()[0])
+    return None
+
+
+def lsh_probe():
+    """For rocprofv3 runs: the configs[3] pool for 128 sequences (as
+    lsh_bench builds it), then 10 fused route + attention launches at each of
+    batch 1, 64 and 128, then 10 copies of 1 GiB as the counters' byte
+    reference."""
+    import numpy as np
+    import torch
+    import be42
+    lib = be42.load()
+    lib.init(0)
+    cfg = LSH
+    H, KVH, hd, T = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["ctx"]
+    BM = 128
+    _, hpT = lib.lsh_projection(hd, 42)
+    pool = lib.kv_pool(1, BM, KVH, hd, T // cfg["page"] + 1, hpT)
+    rng = np.random.default_rng(4)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    q = rng.standard_normal((BM, H, hd)).astype(np.float32)
+    for b in range(BM):
+        K = torch.randn(T, KVH * hd, generator=gen, device="cuda")
+        plant_keys_gpu(K, q[b], gen)
+        V = torch.randn(T, KVH * hd, generator=gen, device="cuda")
+        pool.append(b, K, V, 0)
+        del K, V
+    torch.cuda.synchronize()
+    print("lsh probe: pool built", flush=True)
+    qall = torch.from_numpy(q).cuda()
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    for B in (1, 64, 128):
+        qd = qall[:B].contiguous()
+        out = torch.empty((B, H, hd), device="cuda")
+        sel = torch.empty((B, 64), dtype=torch.int32, device="cuda")
+        nsel = torch.empty(B, dtype=torch.int32, device="cuda")
+        for _ in range(10):
+            lib._call("be42_lsh_attention", pool.handle, lib.p(qd), None, B, H, cfg["k_sel"], cfg["cap"], scale,
+                      lib.p(out), lib.p(sel), lib.p(nsel), 64, lib.stream())
+        torch.cuda.synchronize()
+        print(f"lsh probe: batch {B} done, n_sel mean {nsel.float().mean().item():.1f}", flush=True)
+    src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    pool.close()
+    print("lsh probe done", flush=True)
+
+
+def gemm_probe():
+    """For rocprofv3 runs: 5 launches each of the prefill GEMM at FP8
+    8192x4096x14336 (the best shape) and INT8 512x4096x4096."""
+    import torch
+    import be42
+    lib = be42.load()
+    lib.init(0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    for kind, m, n, k in (("fp8", 8192, 4096, 14336), ("int8", 512, 4096, 4096)):
+        qf = lib.quant_rows_int8 if kind == "int8" else lib.quant_rows_fp8
+        wq, sw = qf(torch.randn(n, k, generator=g, device="cuda") * 0.02)
+        xq, sx = qf(torch.randn(m, k, generator=g, device="cuda"))
+        y = torch.empty(m, n, device="cuda")
+        for _ in range(5):
+            lib.gemm(xq, sx, wq, sw, kind, out=y)
+        torch.cuda.synchronize()
+        print(f"gemm probe: {kind} {m}x{n}x{k} done", flush=True)
+        del wq, sw, xq, sx, y
 
 
 PMC_CONFIG = ("fp8", 128256, 4096, 16)
@@ -560,9 +820,17 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step leg")
     ap.add_argument("--no-3b", action="store_true", help="skip the 3B-model decode (its setup takes ~1 minute)")
     ap.add_argument("--pmc-probe", action="store_true", help="only run the kernels profiled for HBM traffic")
+    ap.add_argument("--lsh-probe", action="store_true", help="only run the LSH launches profiled for HBM traffic")
+    ap.add_argument("--gemm-probe", action="store_true", help="only run the GEMM launches profiled for counters")
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe()
+        return
+    if args.lsh_probe:
+        lsh_probe()
+        return
+    if args.gemm_probe:
+        gemm_probe()
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -714,10 +982,15 @@ def main():
         out["lsh_attention"] = lsh_bench(lib, max(args.steps, 10), max(args.warmup, 2))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"]["host"] = host_info()
         if not args.no_lsh:
             out["lsh_attention"]["cpu_baseline"] = lsh_cpu_baseline()
+        if not args.no_gemm:
+            out["prefill_gemm"]["cpu_baseline"] = gemm_cpu_baseline()
         if not args.no_decode:
             out["decode"]["tiny"]["cpu_baseline"] = decode_cpu_baseline()
+            if not args.no_3b:
+                out["decode"]["3b"]["cpu_baseline"] = decode_3b_cpu_baseline()
     print(json.dumps(out), flush=True)
 
 
