@@ -209,7 +209,15 @@ __global__ __launch_bounds__(256) void k_attn_apply(const be42_kv_pool P, const 
                 const float wt = wh[i * kPg + tk];
                 const size_t slot = ((size_t)phys * n_kv + kvh) * kPg + tk;
                 float v[D];
-                load_row_f32(v, P.v, slot * HD + dl * D, D, BF16, BF16 ? 1.0f : P.v_scale[slot]);
+                if constexpr (BF16) {
+                    // V pages [kv head][dim][16 tokens]
+                    const uint16_t *vc = (const uint16_t *)P.v + (slot / kPg) * (size_t)HD * kPg + slot % kPg;
+#pragma unroll
+                    for (int j = 0; j < D; j++)
+                        v[j] = bf16_to_f32(vc[(size_t)(dl * D + j) * kPg]);
+                } else {
+                    load_row_f32(v, P.v, slot * HD + dl * D, D, false, P.v_scale[slot]);
+                }
 #pragma unroll
                 for (int j = 0; j < D; j++)
                     o[j] = __fmaf_rn(wt, v[j], o[j]);
@@ -355,9 +363,11 @@ template <int HD, int G, int WAVES>
 struct AttnShared {
     float qs[G][HD];
     float sc[G][kSetMax * 17];
-    float red[WAVES][G][HD];
     float lsh[G];
     int pphys[kSetMax], pnt[kSetMax], order[kFusedMaxPages];
+    // cross-wave reduction of o ([WAVES][G][HD]): a static array of the
+    // kernel, or LDS of a phase that has ended (the router's)
+    float *red;
 };
 
 template <int HD, int G, int WAVES>
@@ -368,12 +378,97 @@ __device__ __forceinline__ void attn_load_q(AttnShared<HD, G, WAVES> &S, const f
         S.qs[i / HD][i % HD] = q[((size_t)b * H + kvh * G + i / HD) * HD + i % HD];
 }
 
+// A on the matrix cores (bf16 pages): S[g][t] = q_g . k_t for the 16 tokens of
+// a page in one v_mfma_f32_16x16x32_bf16 chain.  Each fp32 q_g is written as
+// three bf16 parts hi + mid + lo (exact to 2^-27 |q|; bf16 products are exact
+// in fp32), and A row r = 4 g + part (part 3 and heads past G are zero), so
+// the C value of lane (token t = lane % 16, row group lane / 16 = g) holds the
+// three partial sums of head g: s = ((hi + mid) + lo) * scale, no lane
+// exchange.  The head dimension is permuted the same way in A and B: MFMA j
+// takes dims [32 j, 32 j + 32), lane group gi the 8 at 32 j + 8 gi, so the
+// load of one MFMA's operand reads 64 contiguous bytes of each of 16 rows
+// and two consecutive loads complete the rows' 128-byte lines.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+template <int HD>
+struct QParts {
+    bf16x8_t a[HD / 32];
+};
+
+template <int HD, int G, int WAVES>
+__device__ __forceinline__ QParts<HD> attn_q_parts(const AttnShared<HD, G, WAVES> &S)
+{
+    constexpr int NJ = HD / 32;
+    const int lane = threadIdx.x & 63, r = lane & 15, gi = lane >> 4;
+    const int g = r >> 2, part = r & 3;
+    QParts<HD> Q;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            uint16_t h[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float q = g < G ? S.qs[g < G ? g : 0][32 * j + 8 * gi + i + e] : 0.0f;
+                const uint16_t hi = f32_to_bf16(q);
+                const float r1 = q - bf16_to_f32(hi);
+                const uint16_t mid = f32_to_bf16(r1);
+                const float r2 = r1 - bf16_to_f32(mid);
+                const uint16_t lo = f32_to_bf16(r2);
+                h[e] = part == 0 ? hi : (part == 1 ? mid : (part == 2 ? lo : (uint16_t)0));
+            }
+            w[i / 2] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+        }
+        Q.a[j] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+    return Q;
+}
+
+// scores of the pages at slots [0, ns) of S.pphys, UNR pages per wave step,
+// by waves w0 .. w0+nw-1
+template <int HD, int G, int WAVES, int UNR>
+__device__ __forceinline__ void attn_scores_mfma(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
+                                                 float scale, int w0, int nw)
+{
+    constexpr int NJ = HD / 32;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = lane & 15, gi = lane >> 4;
+    const QParts<HD> Q = attn_q_parts<HD, G, WAVES>(S);
+    const int n_kv = P.n_kv;
+    for (int s0 = (wave - w0) * UNR; s0 < ns; s0 += nw * UNR) {
+        uint4 kb[UNR][NJ];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int sl = min(s0 + u, ns - 1);
+            const uint16_t *row = (const uint16_t *)P.k + (((size_t)S.pphys[sl] * n_kv + kvh) * kPg + t) * HD + 8 * gi;
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                kb[u][j] = *(const uint4 *)(row + 32 * j);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Q.a[j], __builtin_bit_cast(bf16x8_t, kb[u][j]), acc, 0,
+                                                              0, 0);
+            if (gi < G && s0 + u < ns)
+                S.sc[gi < G ? gi : 0][(s0 + u) * 17 + t] = ((acc[0] + acc[1]) + acc[2]) * scale;
+        }
+    }
+}
+
 // A. scores of the ns pages of S.pphys (slot order) for the G heads, by
 // waves w0 .. w0+nw-1.
 template <bool BF16, int HD, int G, int WAVES, int UNR>
 __device__ __forceinline__ void attn_scores(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
                                             float scale, int w0, int nw)
 {
+    if constexpr (BF16 && (HD == 64 || HD == 128)) {
+        attn_scores_mfma<HD, G, WAVES, 4>(P, S, kvh, ns, scale, w0, nw);
+        return;
+    }
     constexpr int RL = HD / 8;                 // lanes per row
     constexpr int RPW = kWave / RL;            // rows per wave per step
     using Raw = typename RawRow<BF16>::T;
@@ -522,15 +617,104 @@ __device__ __forceinline__ void attn_values_load(const be42_kv_pool &P, AttnShar
     }
 }
 
+// out = (sum over the waves' partial o) * (1 / l)
+template <int HD, int G, int WAVES>
+__device__ __forceinline__ void attn_values_finish(const AttnShared<HD, G, WAVES> &S, int b, int kvh, int H,
+                                                   float *__restrict__ out)
+{
+    const int tid = threadIdx.x;
+    for (int i = tid; i < G * HD; i += blockDim.x) {
+        const int g = i / HD, d = i % HD;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; w++)
+            v += S.red[(w * G + g) * HD + d];
+        const float l = S.lsh[g];
+        out[((size_t)b * H + kvh * G + g) * HD + d] = l > 0.0f ? v * (1.0f / l) : v;
+    }
+}
+
+// C on the matrix cores (bf16 pages, V stored [kv head][dim][16 tokens]):
+// o[g][d] = sum_t w[g][t] v[t][d] with one v_mfma_f32_16x16x16bf16_1k per
+// page and 16-dim tile.  A row r = 4 g + part holds the bf16 parts of the
+// weights w[g][t] (zero past the page's token count, for part 3 and for heads
+// past G); B is 4 consecutive tokens of one dim (8 bytes, a tile's 16 dims x
+// 16 tokens = 512 contiguous bytes per load); the C value of lane (dim of the
+// tile, row group g) adds up to the three parts of head g.  Pages go round
+// robin over the waves, UNR in flight per wave.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+
+template <int HD, int G, int WAVES, int UNR>
+__device__ __forceinline__ void attn_values_mfma(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
+                                                 const int *order)
+{
+    constexpr int NT = HD / 16;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = lane & 15, gi = lane >> 4;
+    const int ag = n >> 2, apart = n & 3;
+    v4f acc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++)
+        acc[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p0 = wave * UNR; p0 < ns; p0 += WAVES * UNR) {
+        v2i_t vb[UNR][NT];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int p = min(p0 + u, ns - 1);
+            const int sl = order ? order[p] : p;
+            const uint16_t *vp = (const uint16_t *)P.v + ((size_t)S.pphys[sl] * P.n_kv + kvh) * HD * kPg + 4 * gi;
+#pragma unroll
+            for (int tile = 0; tile < NT; tile++)
+                vb[u][tile] = __builtin_nontemporal_load((const v2i_t *)(vp + (tile * 16 + n) * kPg));
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            if (p0 + u < ns) {
+                const int sl = order ? order[p0 + u] : p0 + u;
+                const int nt = S.pnt[sl];
+                uint16_t h[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = 4 * gi + i;
+                    const float w = ag < G && t < nt ? S.sc[ag < G ? ag : 0][sl * 17 + t] : 0.0f;
+                    const uint16_t hi = f32_to_bf16(w);
+                    const float r1 = w - bf16_to_f32(hi);
+                    const uint16_t mid = f32_to_bf16(r1);
+                    const float r2 = r1 - bf16_to_f32(mid);
+                    const uint16_t lo = f32_to_bf16(r2);
+                    h[i] = apart == 0 ? hi : (apart == 1 ? mid : (apart == 2 ? lo : (uint16_t)0));
+                }
+                const s16x4_t a = {(short)h[0], (short)h[1], (short)h[2], (short)h[3]};
+#pragma unroll
+                for (int tile = 0; tile < NT; tile++)
+                    acc[tile] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                        a, __builtin_bit_cast(s16x4_t, vb[u][tile]), acc[tile], 0, 0, 0);
+            }
+        }
+    }
+    if (gi < G)
+#pragma unroll
+        for (int tile = 0; tile < NT; tile++)
+            S.red[(wave * G + gi) * HD + tile * 16 + n] = (acc[tile][0] + acc[tile][1]) + acc[tile][2];
+}
+
 // C. o = sum_t w_t v_t over the slots (the order of the sum is free), then
 // out = o * (1 / l).
 template <bool BF16, int HD, int G, int WAVES, int UNR>
 __device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int b, int kvh,
                                             int ns, int H, float *__restrict__ out, const int *order)
 {
+    const int tid = threadIdx.x;
+    if constexpr (BF16 && (HD == 64 || HD == 128)) {
+        attn_values_mfma<HD, G, WAVES, 2>(P, S, kvh, ns, order);
+        __syncthreads();
+        attn_values_finish<HD, G, WAVES>(S, b, kvh, H, out);
+        return;
+    }
     constexpr int RL = HD / 8;
     constexpr int RPW = kWave / RL;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wave = tid >> 6, lane = tid & 63;
     const int rsub = lane / RL, rl = lane % RL;
     const int T = ns * kPg;
     constexpr int rows_per_iter = WAVES * RPW;
@@ -578,17 +762,9 @@ __device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD
         for (int g = 0; g < G; g++)
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                S.red[wave][g][rl * 8 + j] = o[g][j];
+                S.red[(wave * G + g) * HD + rl * 8 + j] = o[g][j];
     __syncthreads();
-    for (int i = tid; i < G * HD; i += blockDim.x) {
-        const int g = i / HD, d = i % HD;
-        float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < WAVES; w++)
-            v += S.red[w][g][d];
-        const float l = S.lsh[g];
-        out[((size_t)b * H + kvh * G + g) * HD + d] = l > 0.0f ? v * (1.0f / l) : v;
-    }
+    attn_values_finish<HD, G, WAVES>(S, b, kvh, H, out);
 }
 
 template <bool BF16, int HD, int G, int WAVES, int UNR>
@@ -598,6 +774,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
                                                            float scale, float *__restrict__ out)
 {
     __shared__ AttnShared<HD, G, WAVES> S;
+    __shared__ float red[WAVES * G * HD];
+    S.red = red;
     const int b = blockIdx.x, kvh = blockIdx.y;
     const int ns = min(nsel[b], kFusedMaxPages);
     const int *selb = sel + (size_t)b * sel_stride;
@@ -636,6 +814,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
     __shared__ AttnShared<HD, G, WAVES> S;
     __shared__ int set_n;
     const RouteView V = route_view(smem, route_smem(HD, cap, P.max_logical));
+    S.red = (float *)smem;   // the router's LDS, unused once the weights are computed
     const int b = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int layer = slots ? slots[b] : b;
@@ -753,18 +932,37 @@ static bool launch_fused(const be42_kv_pool &P, const float *q, const int *sel, 
     return false;
 }
 
+// Dynamic LDS of k_lsh_attn: the router's layout, which the cross-wave
+// reduction of o reuses afterwards.
+template <int HD, int G, int WAVES>
+static size_t lsh_attn_lds(const RouteSmem &L)
+{
+    return std::max((size_t)L.bytes, (size_t)WAVES * G * HD * sizeof(float));
+}
+
 template <bool BF16, int HD, int G, bool STAGE>
-static void launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
-                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride, size_t lds,
-                              hipStream_t s)
+static int launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
+                             int cap, float scale, float *out, int *sel, int *nsel, int sel_stride,
+                             const RouteSmem &L, hipStream_t s)
 {
     const dim3 grid(B, P.n_kv);
-    if ((long)B * P.n_kv < 512)
+    if ((long)B * P.n_kv < 512) {
+        const size_t lds = lsh_attn_lds<HD, G, 16>(L);
+        if (lds > 65536)
+            BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_attn<BF16, HD, G, 16, 8, STAGE>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL((k_lsh_attn<BF16, HD, G, 16, 8, STAGE>), grid, dim3(1024), lds, s, P, q, slots, H, k_sel,
                            cap, scale, out, sel, nsel, sel_stride);
-    else
+    } else {
+        const size_t lds = lsh_attn_lds<HD, G, 8>(L);
+        if (lds > 65536)
+            BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_attn<BF16, HD, G, 8, 8, STAGE>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL((k_lsh_attn<BF16, HD, G, 8, 8, STAGE>), grid, dim3(512), lds, s, P, q, slots, H, k_sel,
                            cap, scale, out, sel, nsel, sel_stride);
+    }
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
 }
 
 template <bool BF16, int HD, int G>
@@ -772,22 +970,11 @@ static int launch_lsh_attn_g(const be42_kv_pool &P, const float *q, const int *s
                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride, hipStream_t s)
 {
     const RouteSmem L = route_smem(HD, cap, P.max_logical);
-    if (L.bytes > 65536) {
-        const void *fns[4] = {(const void *)k_lsh_attn<BF16, HD, G, 16, 8, true>,
-                              (const void *)k_lsh_attn<BF16, HD, G, 8, 8, true>,
-                              (const void *)k_lsh_attn<BF16, HD, G, 16, 8, false>,
-                              (const void *)k_lsh_attn<BF16, HD, G, 8, 8, false>};
-        for (const void *f : fns)
-            BE42_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes));
-    }
     if (L.stage)
-        launch_lsh_attn_s<BF16, HD, G, true>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride,
-                                             (size_t)L.bytes, s);
-    else
-        launch_lsh_attn_s<BF16, HD, G, false>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride,
-                                              (size_t)L.bytes, s);
-    BE42_LAUNCH_CHECK();
-    return BE42_OK;
+        return launch_lsh_attn_s<BF16, HD, G, true>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride,
+                                                    L, s);
+    return launch_lsh_attn_s<BF16, HD, G, false>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, L,
+                                                 s);
 }
 
 template <bool BF16, int HD>
@@ -897,6 +1084,7 @@ extern "C" int be42_lsh_attention(const be42_kv_pool *pool, const float *q, cons
     if (n_queries <= 0)
         return BE42_OK;
     hipStream_t s = as_stream(stream);
+    const bool bf16 = P.kind == BE42_KV_BF16;
     if ((long)n_queries * P.n_kv > 1024) {
         // Enough workgroups to fill the chip: the router's latency is better
         // spent once per query in its own launch than once per KV head in
@@ -919,7 +1107,6 @@ extern "C" int be42_lsh_attention(const be42_kv_pool *pool, const float *q, cons
         return be42_paged_attention(pool, q, n_queries, n_heads, ws_sel, ws_n, stride, k_sel, scale, out, 1, nullptr,
                                     0, stream);
     }
-    const bool bf16 = P.kind == BE42_KV_BF16;
     if (P.head_dim == 128)
         return bf16 ? launch_lsh_attn_hd<true, 128>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out,
                                                     sel, n_sel, sel_stride, s)

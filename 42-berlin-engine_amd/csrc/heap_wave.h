@@ -19,7 +19,8 @@
 // when every score to be pushed is known up front, its rank among them (the
 // number of strictly smaller scores, so equal scores share a rank) orders the
 // keys exactly as the scores, ties included, and a sift-up moves one 32-bit
-// key per lane -- one shuffle per push instead of two.
+// key per lane -- one permute per push instead of two, and no branches: each
+// lane knows from a precomputed mask whether it lies on the new slot's path.
 #pragma once
 
 #include "be42_common.h"
@@ -90,42 +91,32 @@ struct WaveHeap {
     }
 };
 
-// Rank of each of n scores held as sc[0..n) (n <= 256): the number of
-// strictly smaller ones.  Lane l returns the ranks of entries l, l+64, ...
-// in r[0..3].
-__device__ __forceinline__ void wave_ranks(const float *sc, int n, int (&r)[4])
-{
-    const int lane = threadIdx.x & 63;
-    float own[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        own[j] = lane + 64 * j < n ? sc[lane + 64 * j] : 0.0f;
-        r[j] = 0;
-    }
-    for (int u0 = 0; u0 < n; u0 += 64) {
-        const float sv = u0 + lane < n ? sc[u0 + lane] : 0.0f;
-        const int c = min(64, n - u0);
-        for (int u = 0; u < c; u++) {
-            const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), u));
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                r[j] += x < own[j] ? 1 : 0;
-        }
-    }
-}
-
 struct WaveHeapKey {
     int hk = 0;        // key of slot `lane`: rank << 8 | payload
     int size = 0;      // uniform
     int cap;           // uniform, <= kHeapMax
-    int lane, par, cl, cr;
+    int lane, par4, cl4, cr4;
+    unsigned long long onpath;   // bit n: slot `lane` lies on the path from the root to slot n
 
     __device__ explicit WaveHeapKey(int capacity) : cap(capacity)
     {
         lane = threadIdx.x & 63;
-        par = lane > 0 ? (lane - 1) >> 1 : 0;
-        cl = (2 * lane + 1) & 63;
-        cr = (2 * lane + 2) & 63;
+        par4 = (lane > 0 ? (lane - 1) >> 1 : 0) * 4;
+        cl4 = ((2 * lane + 1) & 63) * 4;
+        cr4 = ((2 * lane + 2) & 63) * 4;
+        // slots n whose root path passes through `lane`: the subtree of
+        // lane, level j holding 1-based positions [(lane+1) 2^j, (lane+1) 2^j + 2^j)
+        unsigned long long m = 0;
+#pragma unroll
+        for (int j = 0; j < 7; j++) {
+            const int lo = ((lane + 1) << j) - 1;
+            const int hi = min(lo + (1 << j) - 1, 63);
+            if (lo <= 63) {
+                const int len = hi - lo + 1;
+                m |= (len >= 64 ? ~0ull : ((1ull << len) - 1ull)) << lo;
+            }
+        }
+        onpath = m;
     }
 
     __device__ __forceinline__ int payload() const { return hk & 0xFF; }
@@ -134,18 +125,19 @@ struct WaveHeapKey {
     __device__ __forceinline__ void push(int rank, int e)
     {
         const int k = (rank << 8) | e;
-        const int kr = rank;
+        const int kx = (rank << 8) | 0xFF;     // key > kx  <=>  its rank > rank
         if (size < cap) {
-            const int pk = __shfl(hk, par, 64);
-            if (heap_on_path(size + 1, lane + 1)) {
-                if (lane > 0 && (pk >> 8) > kr)
-                    hk = pk;
-                else if (lane == size || (hk >> 8) > kr)
-                    hk = k;
-            }
+            // sift-up from slot `size`, branch-free: a path lane takes its
+            // parent's key if that ranks above k, else k if its own does
+            // (or it is the new slot)
+            const int pk = __builtin_amdgcn_ds_bpermute(par4, hk);
+            const bool on = (onpath >> size) & 1ull;
+            const bool tp = on && lane > 0 && pk > kx;
+            const bool tk = on && !tp && (lane == size || hk > kx);
+            hk = tp ? pk : (tk ? k : hk);
             size++;
-        } else if (kr > (__builtin_amdgcn_readlane(hk, 0) >> 8)) {
-            const int kl = __shfl(hk, cl, 64), krr = __shfl(hk, cr, 64);
+        } else if (rank > (__builtin_amdgcn_readlane(hk, 0) >> 8)) {
+            const int kl = __builtin_amdgcn_ds_bpermute(cl4, hk), krr = __builtin_amdgcn_ds_bpermute(cr4, hk);
             const bool hasl = 2 * lane + 1 < size;
             const bool right = 2 * lane + 2 < size && (krr >> 8) < (kl >> 8);
             const unsigned long long mh = __ballot(hasl), mr = __ballot(right);
@@ -154,9 +146,9 @@ struct WaveHeapKey {
                 end = 2 * end + 1 + (int)((mr >> end) & 1ull);
             if (heap_on_path(end + 1, lane + 1)) {
                 const int ck = right ? krr : kl;
-                if (hasl && (ck >> 8) < kr)
+                if (hasl && (ck >> 8) < rank)
                     hk = ck;
-                else if (lane == 0 || (hk >> 8) < kr)
+                else if (lane == 0 || (hk >> 8) < rank)
                     hk = k;
             }
         }

@@ -42,9 +42,11 @@ __global__ __launch_bounds__(64) void k_linear_gather(uint16_t *__restrict__ kp,
     const int t = idx ? idx[i] : i;
     const size_t src = ((size_t)t * n_kv + h) * hd;
     const size_t dst = (((size_t)(i / kLinPage) * n_kv + h) * kLinPage + i % kLinPage) * hd;
+    // V pages [kv head][dim][16 tokens], as the page pool's bf16 pages
+    const size_t vdst = ((size_t)(i / kLinPage) * n_kv + h) * hd * kLinPage + i % kLinPage;
     for (int d = threadIdx.x; d < hd; d += 64) {
         kp[dst + d] = k[src + d];
-        vp[dst + d] = v[src + d];
+        vp[vdst + (size_t)d * kLinPage] = v[src + d];
     }
     if (h == 0 && threadIdx.x == 0 && i % kLinPage == 0)
         ntok[i / kLinPage] = min(kLinPage, n - i);

@@ -75,10 +75,13 @@ __device__ __forceinline__ void store_kv_row(void *__restrict__ kdst, void *__re
                                              int lane)
 {
     if constexpr (BF16) {
-        uint16_t *kd = (uint16_t *)kdst + slot * hd, *vd = (uint16_t *)vdst + slot * hd;
+        // bf16 V pages are stored [kv head][dim][16 tokens]: the attention's
+        // matrix cores read 4 consecutive tokens of one dim as one operand
+        uint16_t *kd = (uint16_t *)kdst + slot * hd;
+        uint16_t *vd = (uint16_t *)vdst + (slot / kPage) * (size_t)hd * kPage + slot % kPage;
         for (int d = lane; d < hd; d += kWave) {
             kd[d] = f32_to_bf16(ks[d]);
-            vd[d] = f32_to_bf16(vs[d]);
+            vd[(size_t)d * kPage] = f32_to_bf16(vs[d]);
         }
     } else {
         float km = 0.0f, vm = 0.0f;

@@ -18,12 +18,17 @@ constexpr int kMaxCandList = 512;   // be42_lsh_candidates cap
 constexpr int kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
 
 struct RouteSmem {
-    int off_qm, off_q0, off_hp, off_list, off_cnt, off_offs, off_cand, off_mid, off_sc, off_mpt, off_ph, stage, bytes;
+    int off_qm, off_q0, off_hp, off_list, off_cnt, off_offs, off_cand, off_mid, off_sc, off_rk, off_mpt, off_ph,
+        off_pt, stage, bytes;
 };
 
-// LDS layout of the router.  When they fit in the workgroup's LDS, the
-// layer's page hashes are staged there (stage = max_logical), else read from
-// HBM (stage = 0).
+// LDS the router's own layout may take (dynamic shared memory), leaving room
+// for the static LDS of the kernels that embed it.
+constexpr int kRouteLdsBudget = 96 * 1024;
+
+// LDS layout of the router.  When they fit in the budget, the layer's page
+// hashes and page table are staged there (stage = max_logical), else read
+// from HBM (stage = 0).
 __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical)
 {
     RouteSmem r;
@@ -37,8 +42,10 @@ __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical
     r.off_cand = o; o += cap * 4;
     r.off_mid = o;  o += cap * 4;
     r.off_sc = o;   o += cap * 4;
+    r.off_rk = o;   o += 4 * cap * 4;             // partial ranks, [4][cap]
     r.off_mpt = o;  o += cap * 4 + 4 * 4;
-    r.stage = o + max_logical * 2 + 16 <= kLdsBytes ? max_logical : 0;
+    r.stage = o + max_logical * 6 + 32 <= kRouteLdsBudget ? max_logical : 0;
+    r.off_pt = o;   o += (r.stage * 4 + 15) & ~15;
     r.off_ph = o;   o += (r.stage * 2 + 15) & ~15;
     r.bytes = o;
     return r;
@@ -51,7 +58,7 @@ constexpr int kRouteThreads = 256;
 // Pointers into the router's LDS.
 struct RouteView {
     float *qm, *q0, *hp, *sc;
-    int *list, *cnt, *offs, *cand, *mid, *mpt;
+    int *list, *cnt, *offs, *cand, *mid, *mpt, *pt_s, *rk;
     uint16_t *ph_s;
 };
 
@@ -69,6 +76,8 @@ __device__ __forceinline__ RouteView route_view(unsigned char *smem, const Route
     V.sc = (float *)(smem + L.off_sc);
     V.mpt = (int *)(smem + L.off_mpt);   // [cap] physical page of mid[e]; [cap], [cap+1]: first, last page
     V.ph_s = (uint16_t *)(smem + L.off_ph);
+    V.pt_s = (int *)(smem + L.off_pt);
+    V.rk = (int *)(smem + L.off_rk);
     return V;
 }
 
@@ -95,63 +104,68 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
     float *qm = V.qm, *q0 = V.q0, *hp = V.hp, *sc = V.sc;
     int *list = V.list, *cnt = V.cnt, *offs = V.offs, *cand = V.cand, *mid = V.mid, *mpt = V.mpt;
     uint16_t *ph_s = V.ph_s;
-    // 0. loads that do not depend on the query hash, each thread's share
-    //    issued before any is stored: page hashes (staged), projection, the
-    //    first and last page of the table
-    if (STAGE && tid < kRouteThreads) {
-        for (int i0 = 0; i0 < nidx; i0 += 8 * 256) {
-            uint16_t v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + j * 256 + tid;
-                v[j] = i < nidx ? P.page_hash[base + i] : (uint16_t)0;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + j * 256 + tid;
-                if (i < nidx)
-                    ph_s[i] = v[j];
-            }
-        }
-    }
+    // 0./1. loads that do not depend on the query hash, issued before any is
+    //    used: page hashes and page table (staged), projection, the query's
+    //    heads for q_mean; then q_mean (inference.c:291-295: sum in head
+    //    order, then / n_heads)
     const uint16_t *ph = STAGE ? ph_s : P.page_hash + base;
-    for (int i0 = 0; tid < kRouteThreads && i0 < hd * 16; i0 += 8 * 256) {
-        float v[8];
+    const int *ptab = STAGE ? V.pt_s : P.page_table + base;
+    if (tid < kRouteThreads) {
+        // unconditional loads at clamped indices (a conditional load is a
+        // branch, and the compiler then waits for each load on its own);
+        // the values past the ends are never used
+        uint16_t hv[8];
+        int pv[8];
+        float wv[8], qv[32];
+        const int ih = max(nidx - 1, 0), ip = max(n - 1, 0), iw = hd * 16 - 1;
+        const int d = tid, dc = min(d, hd - 1);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int i = i0 + j * 256 + tid;
-            v[j] = i < hd * 16 ? P.hpT[i] : 0.0f;
+            const int i = j * kRouteThreads + tid;
+            if (STAGE) {
+                hv[j] = P.page_hash[base + min(i, ih)];
+                pv[j] = P.page_table[base + min(i, ip)];
+            }
+            wv[j] = P.hpT[min(i, iw)];
         }
 #pragma unroll
+        for (int j = 0; j < 32; j++)
+            qv[j] = qb[min(j, H - 1) * hd + dc];
+#pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int i = i0 + j * 256 + tid;
+            const int i = j * kRouteThreads + tid;
+            if (STAGE && i < nidx)
+                ph_s[i] = hv[j];
+            if (STAGE && i < n)
+                V.pt_s[i] = pv[j];
             if (i < hd * 16)
-                hp[(i & 15) * (hd + 4) + (i >> 4)] = v[j];   // hpT[d][bit] -> hp[bit][d]
+                hp[(i & 15) * (hd + 4) + (i >> 4)] = wv[j];   // hpT[d][bit] -> hp[bit][d]
         }
-    }
-    if (tid == 0) {
-        mpt[cap] = P.page_table[base];
-        mpt[cap + 1] = P.page_table[base + n - 1];
-    }
-
-    // 1. q_mean (inference.c:291-295): sum in head order, then / n_heads;
-    //    32 heads' loads are issued before the sum consumes them
-    for (int d = tid; d < hd; d += kRouteThreads) {
-        float s = 0.0f;
-        for (int h0 = 0; h0 < H; h0 += 32) {
-            float v[32];
+        // the rest (more than 2048 pages, head_dim > 128, more than 32 heads)
+        for (int i = 8 * kRouteThreads + tid; STAGE && i < max(nidx, n); i += kRouteThreads) {
+            if (i < nidx)
+                ph_s[i] = P.page_hash[base + i];
+            if (i < n)
+                V.pt_s[i] = P.page_table[base + i];
+        }
+        for (int i = 8 * kRouteThreads + tid; i < hd * 16; i += kRouteThreads)
+            hp[(i & 15) * (hd + 4) + (i >> 4)] = P.hpT[i];
+        if (d < hd) {
+            float sum = 0.0f;
 #pragma unroll
             for (int j = 0; j < 32; j++)
-                v[j] = h0 + j < H ? qb[(h0 + j) * hd + d] : 0.0f;
-#pragma unroll
-            for (int j = 0; j < 32; j++)
-                if (h0 + j < H)
-                    s = s + v[j];
+                sum = j < H ? sum + qv[j] : sum;
+            for (int h = 32; h < H; h++)
+                sum = sum + qb[h * hd + d];
+            qm[d] = sum / (float)H;
+            q0[d] = qv[0];
         }
-        qm[d] = s / (float)H;
-        q0[d] = qb[d];
     }
     __syncthreads();
+    if (tid == 0) {
+        mpt[cap] = ptab[0];
+        mpt[cap + 1] = ptab[n - 1];
+    }
     if (wave == 0) {
         float s = 0.0f;
         if (lane < 16) {
@@ -184,28 +198,34 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
         const int hi = max(nidx - wave * part, 0), lo = max(nidx - (wave + 1) * part, 0);
         int cntv = 0;    // lane p < 17 holds the hit count of probe p
         int *mylist = list + wave * kProbes * cap;
-        for (int top = hi - 1; top >= lo; top -= kWave) {
-            const int id = top - lane;
-            const bool valid = id >= lo;
-            int p = kProbes;
-            if (valid) {
-                const int dd = (int)ph[id] ^ qh;
-                p = dd == 0 ? 0 : (((dd & (dd - 1)) == 0) ? __ffs(dd) : kProbes);
+        for (int top0 = hi - 1; top0 >= lo; top0 -= 4 * kWave) {
+            // four chunks of 64 ids: their hash reads are issued together
+            int pv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int id = top0 - u * kWave - lane;
+                const int dd = (int)ph[max(id, lo)] ^ qh;
+                pv[u] = id < lo ? kProbes : (dd == 0 ? 0 : (((dd & (dd - 1)) == 0) ? __ffs(dd) : kProbes));
             }
-            unsigned long long hits = __ballot(p < kProbes);
-            while (hits) {
-                const int l0 = __ffsll((long long)hits) - 1;
-                const int pp = rl(p, l0);
-                const unsigned long long m = __ballot(p == pp);
-                const int basec = rl(cntv, pp);
-                if (p == pp) {
-                    const int rank = __popcll(m & ((1ull << lane) - 1ull));
-                    if (basec + rank < cap)
-                        mylist[pp * cap + basec + rank] = id;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int id = top0 - u * kWave - lane;
+                const int p = pv[u];
+                unsigned long long hits = __ballot(p < kProbes);
+                while (hits) {
+                    const int l0 = __ffsll((long long)hits) - 1;
+                    const int pp = rl(p, l0);
+                    const unsigned long long m = __ballot(p == pp);
+                    const int basec = rl(cntv, pp);
+                    if (p == pp) {
+                        const int rank = __popcll(m & ((1ull << lane) - 1ull));
+                        if (basec + rank < cap)
+                            mylist[pp * cap + basec + rank] = id;
+                    }
+                    if (lane == pp)
+                        cntv += __popcll(m);
+                    hits &= ~m;
                 }
-                if (lane == pp)
-                    cntv += __popcll(m);
-                hits &= ~m;
             }
         }
         if (lane < kProbes)
@@ -283,12 +303,37 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
     for (int e0 = 0; tid < kRouteThreads && e0 < nm; e0 += 128) {
         const int e = e0 + (tid >> 1), half = tid & 1;
         const int ee = e < nm ? e : nm - 1;
-        const int phys = P.page_table[base + mid[ee]];
+        const int phys = ptab[mid[ee]];
         const float s = dot_ref8x2(q0, P.centroid + (size_t)phys * hd, hd, half);
         if (half == 0 && e < nm) {
             sc[e] = s;
             mpt[e] = phys;
         }
+    }
+    __syncthreads();
+    // 5a. ranks of the middle scores for the heap's integer keys (the number
+    //     of strictly smaller ones): wave w counts, for entries lane + 64 j,
+    //     the smaller ones among its quarter of the entries (every lane reads
+    //     the same score: an LDS broadcast)
+    if (wave < 4 && nm > 0) {
+        const int q0i = wave * nm / 4, q1i = (wave + 1) * nm / 4;
+        float own[4];
+        int r[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            own[j] = sc[min(lane + 64 * j, nm - 1)];
+            r[j] = 0;
+        }
+        for (int i = q0i; i < q1i; i++) {
+            const float x = sc[i];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                r[j] += x < own[j] ? 1 : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (lane + 64 * j < nm)
+                V.rk[wave * cap + lane + 64 * j] = r[j];
     }
     __syncthreads();
 
@@ -326,8 +371,11 @@ __device__ __forceinline__ int route_select(int k_sel, int cap, const RouteView 
     // every middle score is known before the first push: the heap runs on
     // (rank, entry) keys, which order exactly as the scores
     int rk[4];
-    if (ak > 0)
-        wave_ranks(V.sc, nm, rk);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = min(lane + 64 * j, max(nm - 1, 0));
+        rk[j] = V.rk[e] + V.rk[cap + e] + V.rk[2 * cap + e] + V.rk[3 * cap + e];
+    }
     WaveHeapKey heap(ak);
     for (int e0 = 0; e0 < nm && ak > 0; e0 += kWave) {
         const int j = e0 >> 6;

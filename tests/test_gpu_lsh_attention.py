@@ -117,7 +117,8 @@ def test_kv_append_matches_oracle(be, orc, kind):
         gvs = gp.fetch("v_scale", cap * n_kv * PAGE, np.float32).reshape(cap, n_kv * PAGE)
     else:
         gk = gp.fetch("k", cap * pe, np.uint16).reshape(cap, pe)
-        gv = gp.fetch("v", cap * pe, np.uint16).reshape(cap, pe)
+        # bf16 V pages are stored [kv head][dim][16 tokens]
+        gv = gp.fetch("v", cap * pe, np.uint16).reshape(cap, n_kv, hd, PAGE).transpose(0, 1, 3, 2).reshape(cap, pe)
     gc = gp.fetch("centroid", cap * hd, np.float32).reshape(cap, hd)
     gnt = gp.fetch("ntok", cap, np.int32)
     gh = gp.fetch("page_hash", cap, np.uint16).reshape(n_layers, max_pages)
