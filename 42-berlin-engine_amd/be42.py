@@ -45,6 +45,11 @@ SIGNATURES = {
     "be42_gemm_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_decoder_create": (i32, [vp, vp, vp, vp]),
+    "be42_model_load": (i32, [vp, C.c_char_p, C.c_char_p, vp]),
+    "be42_model_check": (i32, [C.c_char_p, C.c_char_p, i32, vp, vp]),
+    "be42_model_decoder": (vp, [vp]),
+    "be42_model_config": (i32, [vp, vp]),
+    "be42_model_free": (None, [vp]),
     "be42_decoder_destroy": (None, [vp]),
     "be42_decoder_pool": (vp, [vp]),
     "be42_decoder_step": (i32, [vp, vp, i32, i32, vp, vp, vp]),
@@ -87,6 +92,12 @@ class DecoderConfig(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "hidden_dim", "vocab",
                                        "max_seq", "max_batch", "wkind", "kv_kind", "sparse_k", "cand_cap",
                                        "rope_len")] + [("rope_theta", C.c_float), ("norm_eps", C.c_float)]
+
+
+class ModelOptions(C.Structure):
+    """Layout of be42_model_options (include/be42_hip.h)."""
+    _fields_ = [(n, C.c_int) for n in ("max_seq", "max_batch", "kv_kind", "sparse_k", "cand_cap", "rope_len",
+                                       "quant_kind", "lsh_seed")]
 
 
 class DecoderLayer(C.Structure):
@@ -483,6 +494,57 @@ class Decoder:
             self.close()
         except Exception:
             pass
+
+class Model:
+    """A decoder loaded from a safetensors checkpoint (be42_model_load); the
+    library owns its device weights.  step() as Decoder.step()."""
+
+    def __init__(self, lib, model_path, config_path, **opts):
+        self.lib = lib
+        lib.init()
+        o = ModelOptions(**opts)
+        self.handle = C.c_void_p()
+        lib._call("be42_model_load", C.byref(self.handle), os.fsencode(model_path), os.fsencode(config_path),
+                  C.byref(o))
+        self.c = DecoderConfig()
+        lib._call("be42_model_config", self.handle, C.byref(self.c))
+        self.cfg = {n: getattr(self.c, n) for n, _ in DecoderConfig._fields_}
+        self.dec = C.c_void_p(lib.lib.be42_model_decoder(self.handle))
+
+    def step(self, tokens, pos, logits=None, sync=True, batch=None):
+        import numpy as np
+        if tokens is None:
+            t, n = None, batch
+        else:
+            t = np.ascontiguousarray(tokens, np.int32)
+            n = len(t)
+        nxt = np.zeros(n, np.int32)
+        self.lib._call("be42_decoder_step", self.dec, None if t is None else t.ctypes.data, n, int(pos),
+                       nxt.ctypes.data if sync else None, self.lib.p(logits), self.lib.stream())
+        return nxt
+
+    def close(self):
+        if self.handle:
+            self.lib.torch.cuda.synchronize()
+            self.lib.lib.be42_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def model_check(lib, model_path, config_path, quant_kind=1):
+    """Parse, map and validate a checkpoint without device work: (config
+    dict, weight kind) or raises Be42Error with the library's message."""
+    c = DecoderConfig()
+    kind = C.c_int(-1)
+    lib.check(lib.lib.be42_model_check(os.fsencode(model_path), os.fsencode(config_path), quant_kind, C.byref(c),
+                                       C.byref(kind)), "be42_model_check")
+    return {n: getattr(c, n) for n, _ in DecoderConfig._fields_}, kind.value
+
 
 def load():
     """The process-wide library handle (raises if the .so is not built)."""

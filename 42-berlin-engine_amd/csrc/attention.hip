@@ -707,7 +707,7 @@ __device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD
 {
     const int tid = threadIdx.x;
     if constexpr (BF16 && (HD == 64 || HD == 128)) {
-        attn_values_mfma<HD, G, WAVES, 2>(P, S, kvh, ns, order);
+        attn_values_mfma<HD, G, WAVES, 4>(P, S, kvh, ns, order);
         __syncthreads();
         attn_values_finish<HD, G, WAVES>(S, b, kvh, H, out);
         return;

@@ -324,11 +324,16 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
             own[j] = sc[min(lane + 64 * j, nm - 1)];
             r[j] = 0;
         }
-        for (int i = q0i; i < q1i; i++) {
-            const float x = sc[i];
+        for (int i0 = q0i; i0 < q1i; i0 += 8) {
+            float x[8];
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                r[j] += x < own[j] ? 1 : 0;
+            for (int u = 0; u < 8; u++)
+                x[u] = sc[min(i0 + u, q1i - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    r[j] += i0 + u < q1i && x[u] < own[j] ? 1 : 0;
         }
 #pragma unroll
         for (int j = 0; j < 4; j++)

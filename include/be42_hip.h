@@ -332,6 +332,37 @@ int  be42_decoder_capture_kv(be42_decoder *d, float *k_dst, float *v_dst);
  * sel_dst ([n_layers][max_batch][max(sparse_k, 64)], device); NULL stops it. */
 int  be42_decoder_capture_sel(be42_decoder *d, int *sel_dst);
 
+/* ---- checkpoints --------------------------------------------------------------
+ * A decoder from a safetensors checkpoint and an HF config.json: load_config
+ * (src/inference/model.c:32-143), load_model / parse_header (src/loader/loader_io.c:44,
+ * loader_parse.c:28-110) and the weight mapping by name (model.c:180-265, LLaMA and
+ * HF names, output tied to the embedding when absent).  Unlike the reference, which
+ * maps every tensor as BF16 (loader_parse.c:48), the dtype is honoured: I8 and F8_E4M3
+ * weights with a per-row F32 scale tensor "<name>_scale" ([rows] or [rows, 1]) are
+ * streamed as stored; BF16 / F16 / F32 weights are quantized per row on load to
+ * quant_kind (0: INT8, 1: FP8 E4M3); norm weights become bf16.  One model holds one
+ * weight kind.  Errors: BE42_EINVAL with a message naming the tensor. */
+typedef struct be42_model_options {
+    int max_seq;     /* 0: 8192 (seq_len, model.c:140) */
+    int max_batch;   /* 0: 1 */
+    int kv_kind;     /* BE42_KV_INT8 / BE42_KV_BF16 */
+    int sparse_k;    /* 0: 64 (SPARSE_BLOCKS_K) */
+    int cand_cap;    /* 0: 64 */
+    int rope_len;    /* 0: max_seq */
+    int quant_kind;  /* kind BF16 / F16 / F32 weights are quantized to */
+    int lsh_seed;    /* 0: 42 (model.c:620) */
+} be42_model_options;
+typedef struct be42_model be42_model;
+int  be42_model_load(be42_model **out, const char *model_path, const char *config_path,
+                     const be42_model_options *opt);
+/* parse, map and validate only (no device work): the config it would use and
+ * the weight kind */
+int  be42_model_check(const char *model_path, const char *config_path, int quant_kind,
+                      be42_decoder_config *cfg_out, int *wkind_out);
+be42_decoder *be42_model_decoder(be42_model *m);
+int  be42_model_config(const be42_model *m, be42_decoder_config *cfg);
+void be42_model_free(be42_model *m);
+
 #ifdef __cplusplus
 }
 #endif
