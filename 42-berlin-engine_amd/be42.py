@@ -45,6 +45,10 @@ SIGNATURES = {
     "be42_gemm_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_decoder_create": (i32, [vp, vp, vp, vp]),
+    "be42_sample_temperature": (i32, [vp, vp, i32, i32, C.c_float, vp, vp]),
+    "be42_sample_top_p": (i32, [vp, vp, i32, i32, C.c_float, C.c_float, vp, vp]),
+    "be42_sample_temperature_dt": (i32, [vp, vp, i32, i32, i32, C.c_float, vp, vp]),
+    "be42_sample_top_p_dt": (i32, [vp, vp, i32, i32, i32, C.c_float, C.c_float, vp, vp]),
     "be42_model_load": (i32, [vp, C.c_char_p, C.c_char_p, vp]),
     "be42_model_check": (i32, [C.c_char_p, C.c_char_p, i32, vp, vp]),
     "be42_model_decoder": (vp, [vp]),
@@ -275,6 +279,23 @@ class Lib:
         self._call("be42_lsh_candidates", self.p(ids), self.p(n), self.p(hashes), hashes.numel(), self.p(qh),
                    n_q, cap, self.stream())
         return ids, n
+
+    def sample_temperature(self, logits, temp, r):
+        """logits [batch][n] (float32 or bfloat16), r [batch] uniforms -> [batch] int32."""
+        t = self.torch
+        B, n = logits.shape
+        out = t.empty(B, dtype=t.int32, device=logits.device)
+        self._call("be42_sample_temperature_dt", self.p(out), self.p(logits), int(logits.dtype == t.bfloat16), n, B,
+                   float(temp), self.p(r), self.stream())
+        return out
+
+    def sample_top_p(self, logits, temp, top_p, u):
+        t = self.torch
+        B, n = logits.shape
+        out = t.empty(B, dtype=t.int32, device=logits.device)
+        self._call("be42_sample_top_p_dt", self.p(out), self.p(logits), int(logits.dtype == t.bfloat16), n, B,
+                   float(temp), float(top_p), self.p(u), self.stream())
+        return out
 
     def kv_pool(self, kind, n_layers, n_kv, head_dim, max_logical, hpT=None):
         return KVPool(self, kind, n_layers, n_kv, head_dim, max_logical, hpT)

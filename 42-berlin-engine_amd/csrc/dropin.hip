@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <ctime>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
@@ -948,6 +949,59 @@ extern "C" int sample_argmax(const t_tensor *logits)
     int res = 0;
     hip_ok(hipMemcpy(&res, dres, 4, hipMemcpyDeviceToHost), "sample_argmax");
     return res;
+}
+
+// sampler_random_float (sampler.c:33-45): a per-thread LCG seeded from the
+// time and a thread-local address, 15 bits per draw
+static float sampler_draw(void)
+{
+    static thread_local int init = 0;
+    static thread_local unsigned int seed;
+    if (!init) {
+        seed = (unsigned int)time(nullptr) ^ (unsigned int)(size_t)&init;
+        init = 1;
+    }
+    seed = seed * 1103515245u + 12345u;
+    return (float)((seed >> 16) & 0x7FFF) / 32767.0f;
+}
+
+// sample_temperature (sampler_temp.c:96-114) and sample_top_p
+// (sampler_topp.c:113-158) on the GPU; the uniform draws are the reference's
+// (sampler_random_float; rand() / RAND_MAX), made on the host.  The scratch
+// arena is not used (the probabilities live in device memory).
+static int sample_dropin(const t_tensor *logits, float temp, float top_p, bool topp, const char *what)
+{
+    const bool f32 = logits->dtype == DTYPE_F32;
+    const size_t n = logits->size;
+    if (n == 0)
+        return 0;
+    if (n > (size_t)INT32_MAX)
+        die(what, "more than 2^31 logits");
+    const float u = topp ? (float)rand() / (float)RAND_MAX : sampler_draw();
+    std::lock_guard<std::mutex> g(rt().mu);
+    const void *d = in_dev(logits->data, n * (f32 ? 4 : 2), kS0);
+    int *dres = (int *)scratch(kS1, 8);
+    float *du = (float *)(dres + 1);
+    hip_ok(hipMemcpy(du, &u, 4, hipMemcpyHostToDevice), what);
+    const int rc = topp ? be42_sample_top_p_dt(dres, d, f32 ? 0 : 1, (int)n, 1, temp, top_p, du, nullptr)
+                        : be42_sample_temperature_dt(dres, d, f32 ? 0 : 1, (int)n, 1, temp, du, nullptr);
+    if (rc != BE42_OK)
+        die(what, be42_last_error());
+    int res = 0;
+    hip_ok(hipMemcpy(&res, dres, 4, hipMemcpyDeviceToHost), what);
+    return res;
+}
+
+extern "C" int sample_temperature(const t_tensor *logits, float temperature, t_arena *scratch)
+{
+    (void)scratch;
+    return sample_dropin(logits, temperature, 0.0f, false, "sample_temperature");
+}
+
+extern "C" int sample_top_p(const t_tensor *logits, float temperature, float top_p, t_arena *scratch)
+{
+    (void)scratch;
+    return sample_dropin(logits, temperature, top_p, true, "sample_top_p");
 }
 
 // ---- quant codecs ------------------------------------------------------------------

@@ -267,6 +267,21 @@ typedef struct s_arena {                                           /* arena.h:18
     size_t offset;
 } t_arena;
 
+/* sample_temperature: p = expf((x - max) / temperature) / sum (max from -1e9),
+ * the first index whose running sum of p exceeds a draw of the reference's
+ * sampler_random_float LCG (time-seeded per thread).  sample_top_p: the same
+ * probabilities (max from x[0]) sorted descending -- equal probabilities in
+ * ascending index order, which the reference's qsort leaves unspecified -- cut
+ * after the first running sum above top_p, and the first entry whose running
+ * sum exceeds (rand() / RAND_MAX) * that sum.  F32 or BF16 logits; the
+ * scratch arena is not used.  The sums are block scans on the GPU (fp32
+ * rounding apart from the reference's sequential sums); where rounding leaves
+ * no sum above the draw the last index is returned (the reference returns n). */
+int sample_temperature(const t_tensor *logits, float temperature,  /* sampler.h:20 */
+                       t_arena *scratch);
+int sample_top_p(const t_tensor *logits, float temperature,        /* sampler.h:22 */
+                 float top_p, t_arena *scratch);
+
 typedef struct s_kv_cache {                                        /* kv_cache.h:19-27 */
     t_tensor k;
     t_tensor v;

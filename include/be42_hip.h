@@ -332,6 +332,25 @@ int  be42_decoder_capture_kv(be42_decoder *d, float *k_dst, float *v_dst);
  * sel_dst ([n_layers][max_batch][max(sparse_k, 64)], device); NULL stops it. */
 int  be42_decoder_capture_sel(be42_decoder *d, int *sel_dst);
 
+/* ---- sampling ------------------------------------------------------------------
+ * sample_temperature (src/compute/sampler_temp.c:96-114) and sample_top_p
+ * (sampler_topp.c:113-158) for `batch` rows of n device logits [batch][n]:
+ * p = expf((x - max) / temp) / sum; temperature: the first index whose running sum
+ * of p exceeds r[b]; top-p: p sorted descending (stable: equal p in ascending index
+ * order), cut after the first running sum above top_p, then the first sorted entry
+ * whose running sum exceeds u[b] * the cut's sum.  r, u: device [batch] uniforms
+ * (the reference's sampler_random_float and rand() / RAND_MAX draws); out: device
+ * [batch].  The _dt forms take bf16 logits when logits_bf16 != 0.  Both use the
+ * library workspace (one stream at a time). */
+int be42_sample_temperature(int *out, const float *logits, int n, int batch, float temp, const float *r,
+                            void *stream);
+int be42_sample_top_p(int *out, const float *logits, int n, int batch, float temp, float top_p, const float *u,
+                      void *stream);
+int be42_sample_temperature_dt(int *out, const void *logits, int logits_bf16, int n, int batch, float temp,
+                               const float *r, void *stream);
+int be42_sample_top_p_dt(int *out, const void *logits, int logits_bf16, int n, int batch, float temp, float top_p,
+                         const float *u, void *stream);
+
 /* ---- checkpoints --------------------------------------------------------------
  * A decoder from a safetensors checkpoint and an HF config.json: load_config
  * (src/inference/model.c:32-143), load_model / parse_header (src/loader/loader_io.c:44,

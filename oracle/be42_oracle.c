@@ -1133,6 +1133,98 @@ void or_silu_mul_bf16(uint16_t *dst, const uint16_t *gate, const uint16_t *up, i
     }
 }
 
+/* sample_temperature, sampler_temp.c:17-114, with the uniform draw r given
+ * (the reference draws it from sampler_random_float): max from -1e9 (strict
+ * >), p_i = expf((x_i - max) / temp) summed in index order, p_i /= sum, the
+ * first index whose running sum exceeds r -- n when none does, as the
+ * reference. */
+int or_sample_temperature(const float *x, int n, float temp, float r)
+{
+    float m = -1e9f;
+    for (int i = 0; i < n; i++)
+        if (x[i] > m)
+            m = x[i];
+    float *p = (float *)malloc((size_t)n * sizeof(float));
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        p[i] = expf((x[i] - m) / temp);
+        sum += p[i];
+    }
+    for (int i = 0; i < n; i++)
+        p[i] /= sum;
+    float cum = 0.0f;
+    int idx = 0;
+    while (idx < n) {
+        cum += p[idx];
+        if (r < cum)
+            break;
+        idx++;
+    }
+    free(p);
+    return idx;
+}
+
+typedef struct {
+    float prob;
+    int idx;
+} or_prob_idx;
+
+/* probability descending; equal probabilities by ascending index (the
+ * reference's qsort comparator returns 0 for them: unspecified order) */
+static int or_cmp_prob(const void *a, const void *b)
+{
+    const or_prob_idx *pa = (const or_prob_idx *)a, *pb = (const or_prob_idx *)b;
+    if (pa->prob > pb->prob)
+        return -1;
+    if (pa->prob < pb->prob)
+        return 1;
+    return (pa->idx > pb->idx) - (pa->idx < pb->idx);
+}
+
+/* sample_top_p, sampler_topp.c:17-158, with u = rand() / RAND_MAX given: max
+ * from x[0], p_i = expf((x_i - max) / temp) / sum, sorted as above, cut after
+ * the first running sum above top_p (that entry included), r = u * that sum,
+ * the first entry whose running sum exceeds r, else the last of the cut. */
+int or_sample_top_p(const float *x, int n, float temp, float top_p, float u)
+{
+    float m = x[0];
+    for (int i = 1; i < n; i++)
+        if (x[i] > m)
+            m = x[i];
+    or_prob_idx *pi = (or_prob_idx *)malloc((size_t)n * sizeof(or_prob_idx));
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        pi[i].prob = expf((x[i] - m) / temp);
+        pi[i].idx = i;
+        sum += pi[i].prob;
+    }
+    for (int i = 0; i < n; i++)
+        pi[i].prob /= sum;
+    qsort(pi, (size_t)n, sizeof(or_prob_idx), or_cmp_prob);
+    float cum = 0.0f;
+    int i = 0;
+    while (i < n) {
+        cum += pi[i].prob;
+        if (cum > top_p) {
+            i++;
+            break;
+        }
+        i++;
+    }
+    const float r = u * cum;
+    float running = 0.0f;
+    int res = pi[i - 1].idx;
+    for (int j = 0; j < i; j++) {
+        running += pi[j].prob;
+        if (running > r) {
+            res = pi[j].idx;
+            break;
+        }
+    }
+    free(pi);
+    return res;
+}
+
 /* argmax_loop_bf16, sampler.c:122-140: best starts at -1e9 (index 0), the
  * first strictly larger value wins. */
 int or_argmax_bf16(const uint16_t *x, int n)

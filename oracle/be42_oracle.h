@@ -188,6 +188,8 @@ void or_rope_apply(float *data, int n_heads, int hd, int pos, int n_pos,
                    const float *cos_t, const float *sin_t);                              /* ops_rope.c:192-228 */
 void or_silu_mul(float *dst, const float *gate, const float *up, int n);                 /* ops_activation.c:48-105 */
 int  or_argmax(const float *x, int n);                                                   /* sampler.c:42-117 */
+int  or_sample_temperature(const float *x, int n, float temp, float r);                         /* sampler_temp.c:96-114 */
+int  or_sample_top_p(const float *x, int n, float temp, float top_p, float u);                  /* sampler_topp.c:113-158 */
 void or_silu_mul_bf16(uint16_t *dst, const uint16_t *gate, const uint16_t *up, int n);  /* ops_activation.c:143-230 */
 int  or_argmax_bf16(const uint16_t *x, int n);                                          /* sampler.c:122-140 */
 

@@ -241,6 +241,33 @@ int ref_argmax(float *x, int n)
     return sample_argmax(&t);
 }
 
+/* sample_top_p after srand(seed): its draw is the first rand() of that seed */
+int ref_sample_top_p(float *x, int n, float temp, float top_p, unsigned int seed)
+{
+    int s[1] = {n};
+    t_tensor t = tensor_view(x, s, 1);
+    t.dtype = DTYPE_F32;
+    t_arena a;
+    arena_init(&a, (size_t)n * 8 + 4096);
+    srand(seed);
+    const int r = sample_top_p(&t, temp, top_p, &a);
+    arena_free(&a);
+    return r;
+}
+
+/* sample_temperature (its draw comes from the reference's own time-seeded LCG) */
+int ref_sample_temperature(float *x, int n, float temp)
+{
+    int s[1] = {n};
+    t_tensor t = tensor_view(x, s, 1);
+    t.dtype = DTYPE_F32;
+    t_arena a;
+    arena_init(&a, (size_t)n * 4 + 4096);
+    const int r = sample_temperature(&t, temp, &a);
+    arena_free(&a);
+    return r;
+}
+
 void ref_silu_mul_bf16(uint16_t *dst, const uint16_t *gate, const uint16_t *up, int n)
 {
     op_silu_mul_fused_bf16(dst, gate, up, (size_t)n);

@@ -126,6 +126,8 @@ def bind(lib):
         "op_silu_mul": (None, [P(Tensor), P(Tensor), P(Tensor)]),
         "rope_apply_multihead_cached": (None, [vp, i32, i32, P(RopeCache)]),
         "sample_argmax": (i32, [P(Tensor)]),
+        "sample_temperature": (i32, [P(Tensor), f32, P(Arena)]),
+        "sample_top_p": (i32, [P(Tensor), f32, f32, P(Arena)]),
         "lsh_stats_reset_atomic": (None, [P(LshStats)]),
         "lsh_stats_print_atomic": (None, [P(LshStats), i32]),
         "lsh_validate_recall": (f32, [vp, vp, i32, i32, vp, i32, i32]),

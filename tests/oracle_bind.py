@@ -200,6 +200,8 @@ class Oracle:
         _sig(L, "or_rope_apply", None, f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p, f32p)
         _sig(L, "or_silu_mul", None, f32p, f32p, f32p, C.c_int)
         _sig(L, "or_argmax", C.c_int, f32p, C.c_int)
+        _sig(L, "or_sample_temperature", C.c_int, f32p, C.c_int, C.c_float, C.c_float)
+        _sig(L, "or_sample_top_p", C.c_int, f32p, C.c_int, C.c_float, C.c_float, C.c_float)
         _sig(L, "or_decoder_init", C.c_int, C.c_void_p, C.POINTER(OrDecoderCfg), C.POINTER(OrModelW), f32p)
         _sig(L, "or_decoder_free", None, C.c_void_p)
         _sig(L, "or_decoder_kv_append", C.c_int, C.c_void_p, C.c_int, f32p, f32p, C.c_int)
@@ -306,6 +308,12 @@ class Oracle:
 
     def argmax(self, x):
         return self.lib.or_argmax(np.ascontiguousarray(x, np.float32), len(x))
+
+    def sample_temperature(self, x, temp, r):
+        return self.lib.or_sample_temperature(np.ascontiguousarray(x, np.float32), len(x), temp, r)
+
+    def sample_top_p(self, x, temp, top_p, u):
+        return self.lib.or_sample_top_p(np.ascontiguousarray(x, np.float32), len(x), temp, top_p, u)
 
     def gemv_bf16(self, wb, x, threads=0):
         n, k = wb.shape
@@ -553,6 +561,8 @@ class RefLib:
         _sig(L, "ref_rope_apply", None, f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p, f32p)
         _sig(L, "ref_silu_mul", None, f32p, f32p, f32p, C.c_int)
         _sig(L, "ref_argmax", C.c_int, f32p, C.c_int)
+        _sig(L, "ref_sample_top_p", C.c_int, f32p, C.c_int, C.c_float, C.c_float, C.c_uint)
+        _sig(L, "ref_sample_temperature", C.c_int, f32p, C.c_int, C.c_float)
         _sig(L, "ref_silu_mul_bf16", None, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int)
         _sig(L, "ref_argmax_bf16", C.c_int, C.c_void_p, C.c_int)
         _sig(L, "ref_validate_recall", C.c_float, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
