@@ -43,6 +43,10 @@ SIGNATURES = {
     "be42_gemv_noalloc": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, vp]),
     "be42_lsh_attention": (i32, [vp, vp, vp, i32, i32, i32, i32, f32, vp, vp, vp, i32, vp]),
     "be42_gemm_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+    "be42_gemm_xdig_bytes": (C.c_size_t, [i32, i32, i32]),
+    "be42_gemm_prepare": (i32, [vp, vp, i32, i32, i32, vp]),
+    "be42_gemm_q8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "be42_gemm_fp8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_decoder_create": (i32, [vp, vp, vp, vp]),
     "be42_sample_temperature": (i32, [vp, vp, i32, i32, C.c_float, vp, vp]),
@@ -57,6 +61,7 @@ SIGNATURES = {
     "be42_decoder_destroy": (None, [vp]),
     "be42_decoder_pool": (vp, [vp]),
     "be42_decoder_step": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "be42_decoder_prefill": (i32, [vp, i32, vp, i32, i32, vp, vp, vp]),
     "be42_decoder_next_tokens": (i32, [vp, vp]),
     "be42_decoder_capture": (i32, [vp, vp, vp]),
     "be42_decoder_capture_kv": (i32, [vp, vp, vp]),
@@ -254,6 +259,20 @@ class Lib:
         y = out if out is not None else t.empty((m, n), dtype=t.float32, device=xq.device)
         name = "be42_gemm_i8" if kind == "int8" else "be42_gemm_fp8"
         self._call(name, self.p(y), self.p(xq), self.p(sx), self.p(wq), self.p(sw), m, n, k, self.stream(stream))
+        return y
+
+    def gemm_f32(self, x, w, sw, kind, out=None, stream=None):
+        """Y [M][N] = sw[n] * w [N][K] . x [M][K] for fp32 x, through the
+        GEMV's digit planes (be42_gemm_prepare + be42_gemm_*_prepared)."""
+        t = self.torch
+        m, k = x.shape
+        n = w.shape[0]
+        fp8 = 0 if kind == "int8" else 1
+        buf = t.empty(self.lib.be42_gemm_xdig_bytes(k, m, fp8), dtype=t.uint8, device=x.device)
+        self._call("be42_gemm_prepare", self.p(buf), self.p(x), k, m, fp8, self.stream(stream))
+        y = out if out is not None else t.empty((m, n), dtype=t.float32, device=x.device)
+        name = "be42_gemm_q8_prepared" if kind == "int8" else "be42_gemm_fp8_prepared"
+        self._call(name, self.p(y), self.p(w), self.p(sw), self.p(buf), n, k, m, self.stream(stream))
         return y
 
     # -- LSH / paged KV / attention --------------------------------------------
@@ -493,6 +512,16 @@ class Decoder:
         self.lib._call("be42_decoder_step", self.handle, None if t is None else t.ctypes.data, n, int(pos),
                        nxt.ctypes.data if sync else None, self.lib.p(logits), self.lib.stream())
         return nxt
+
+    def prefill(self, tokens, pos0=0, seq=0, logits=None):
+        """The prompt tokens of sequence seq at positions pos0.. in batched
+        passes; returns the argmax after the last one."""
+        import numpy as np
+        t = np.ascontiguousarray(tokens, np.int32)
+        nxt = np.zeros(1, np.int32)
+        self.lib._call("be42_decoder_prefill", self.handle, int(seq), t.ctypes.data, len(t), int(pos0),
+                       nxt.ctypes.data, self.lib.p(logits), self.lib.stream())
+        return int(nxt[0])
 
     def capture(self, q=None, nsel=None):
         self.lib._call("be42_decoder_capture", self.handle, self.lib.p(q), self.lib.p(nsel))

@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "be42_common.h"
+#include "paged_step.h"
 #include "route.h"
 
 namespace be42 {
@@ -803,10 +804,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
 // weights and V then follow the heap's order through S.order.  With more
 // candidates the scores wait for the heap.  The workgroup of KV head 0
 // writes the selection to sel / nsel (when given).
+// With lim, query b sees only the first lim[b] positions of its slot: the
+// pages, the LSH index and the last page's token count it would have seen
+// when position lim[b] - 1 was the newest (a prefill runs the queries of many
+// positions after appending all of their K/V).
 template <bool BF16, int HD, int G, int WAVES, int UNR, bool STAGE>
 __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, const float *__restrict__ q,
-                                                         const int *__restrict__ slots, int H, int k_sel, int cap,
-                                                         float scale, float *__restrict__ out, int *__restrict__ sel,
+                                                         const int *__restrict__ slots, const int *__restrict__ lim,
+                                                         int H, int k_sel, int cap, float scale,
+                                                         float *__restrict__ out, int *__restrict__ sel,
                                                          int *__restrict__ nsel, int sel_stride)
 {
     static_assert(WAVES * 64 >= kRouteThreads, "the router needs 4 waves");
@@ -819,7 +825,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int layer = slots ? slots[b] : b;
     const int base = layer * P.max_logical;
-    const int n = P.n_logical[layer];
+    const int lim_b = lim ? lim[b] : 0;
+    const int n = lim ? (lim_b + kPg - 1) / kPg : P.n_logical[layer];
+    // tokens of a page: the view's last page holds lim - 16 (n - 1)
+    const int last_ph = lim && n > 0 ? P.page_table[base + n - 1] : -1;
+    const int last_nt = lim_b - kPg * (n - 1);
+    auto page_nt = [&](int ph) { return ph == last_ph ? last_nt : P.ntok[ph]; };
     int *selb = sel && kvh == 0 ? sel + (size_t)b * sel_stride : nullptr;
     attn_load_q(S, q, b, kvh, H);
 
@@ -829,7 +840,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
         for (int i = tid; i < ns; i += blockDim.x) {
             const int ph = P.page_table[base + i];
             S.pphys[i] = ph;
-            S.pnt[i] = P.ntok[ph];
+            S.pnt[i] = page_nt(ph);
             if (selb)
                 selb[i] = ph;
         }
@@ -848,7 +859,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
         attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out, nullptr);
         return;
     }
-    const int nidx = min(P.n_indexed[layer], P.max_logical);
+    const int nidx = min(lim ? min(P.n_indexed[layer], lim_b / kPg) : P.n_indexed[layer], P.max_logical);
     route_prepare<STAGE>(P, q + (size_t)b * H * HD, base, n, nidx, H, cap, V, nullptr, nullptr, nullptr);
     const int nm = route_middles(V);
     const int ns0 = V.mpt[cap + 1] != V.mpt[cap] ? 2 : 1;
@@ -858,7 +869,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
         for (int i = tid; i < nset; i += blockDim.x) {
             const int ph = i == 0 ? V.mpt[cap] : (i < ns0 ? V.mpt[cap + 1] : V.mpt[i - ns0]);
             S.pphys[i] = ph;
-            S.pnt[i] = P.ntok[ph];
+            S.pnt[i] = page_nt(ph);
         }
     }
     __syncthreads();
@@ -880,7 +891,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
             const int slot = S.order[i];
             const int ph = slot == 0 ? V.mpt[cap] : (slot < ns0 ? V.mpt[cap + 1] : V.mpt[slot - ns0]);
             S.pphys[i] = ph;
-            S.pnt[i] = P.ntok[ph];
+            S.pnt[i] = page_nt(ph);
         }
         __syncthreads();
         attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns, scale, 0, WAVES);
@@ -940,26 +951,34 @@ static size_t lsh_attn_lds(const RouteSmem &L)
     return std::max((size_t)L.bytes, (size_t)WAVES * G * HD * sizeof(float));
 }
 
+// lim: per-query visible positions (NULL: the slot's whole cache).  The
+// grid shape picks 16 or 8 waves; wide16 keeps 16 for any grid, so that a
+// query is computed exactly as it is in a small (decode-sized) launch.
+struct LshAttnOpt {
+    const int *lim = nullptr;
+    bool wide16 = false;
+};
+
 template <bool BF16, int HD, int G, bool STAGE>
 static int launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride,
-                             const RouteSmem &L, hipStream_t s)
+                             const RouteSmem &L, const LshAttnOpt &o, hipStream_t s)
 {
     const dim3 grid(B, P.n_kv);
-    if ((long)B * P.n_kv < 512) {
+    if ((long)B * P.n_kv < 512 || o.wide16) {
         const size_t lds = lsh_attn_lds<HD, G, 16>(L);
         if (lds > 65536)
             BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_attn<BF16, HD, G, 16, 8, STAGE>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL((k_lsh_attn<BF16, HD, G, 16, 8, STAGE>), grid, dim3(1024), lds, s, P, q, slots, H, k_sel,
-                           cap, scale, out, sel, nsel, sel_stride);
+        hipLaunchKernelGGL((k_lsh_attn<BF16, HD, G, 16, 8, STAGE>), grid, dim3(1024), lds, s, P, q, slots, o.lim, H,
+                           k_sel, cap, scale, out, sel, nsel, sel_stride);
     } else {
         const size_t lds = lsh_attn_lds<HD, G, 8>(L);
         if (lds > 65536)
             BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_attn<BF16, HD, G, 8, 8, STAGE>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL((k_lsh_attn<BF16, HD, G, 8, 8, STAGE>), grid, dim3(512), lds, s, P, q, slots, H, k_sel,
-                           cap, scale, out, sel, nsel, sel_stride);
+        hipLaunchKernelGGL((k_lsh_attn<BF16, HD, G, 8, 8, STAGE>), grid, dim3(512), lds, s, P, q, slots, o.lim, H,
+                           k_sel, cap, scale, out, sel, nsel, sel_stride);
     }
     BE42_LAUNCH_CHECK();
     return BE42_OK;
@@ -967,26 +986,43 @@ static int launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *s
 
 template <bool BF16, int HD, int G>
 static int launch_lsh_attn_g(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
-                             int cap, float scale, float *out, int *sel, int *nsel, int sel_stride, hipStream_t s)
+                             int cap, float scale, float *out, int *sel, int *nsel, int sel_stride,
+                             const LshAttnOpt &o, hipStream_t s)
 {
     const RouteSmem L = route_smem(HD, cap, P.max_logical);
     if (L.stage)
         return launch_lsh_attn_s<BF16, HD, G, true>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride,
-                                                    L, s);
+                                                    L, o, s);
     return launch_lsh_attn_s<BF16, HD, G, false>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, L,
-                                                 s);
+                                                 o, s);
 }
 
 template <bool BF16, int HD>
 static int launch_lsh_attn_hd(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
-                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride, hipStream_t s)
+                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride,
+                              const LshAttnOpt &o, hipStream_t s)
 {
     switch (H / P.n_kv) {
-    case 1: return launch_lsh_attn_g<BF16, HD, 1>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, s);
-    case 2: return launch_lsh_attn_g<BF16, HD, 2>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, s);
-    case 3: return launch_lsh_attn_g<BF16, HD, 3>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, s);
-    default: return launch_lsh_attn_g<BF16, HD, 4>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, s);
+    case 1: return launch_lsh_attn_g<BF16, HD, 1>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, o, s);
+    case 2: return launch_lsh_attn_g<BF16, HD, 2>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, o, s);
+    case 3: return launch_lsh_attn_g<BF16, HD, 3>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, o, s);
+    default: return launch_lsh_attn_g<BF16, HD, 4>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, o, s);
     }
+}
+
+static int launch_lsh_attn(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel, int cap,
+                           float scale, float *out, int *sel, int *nsel, int sel_stride, const LshAttnOpt &o,
+                           hipStream_t s)
+{
+    const bool bf16 = P.kind == BE42_KV_BF16;
+    if (P.head_dim == 128)
+        return bf16 ? launch_lsh_attn_hd<true, 128>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride,
+                                                    o, s)
+                    : launch_lsh_attn_hd<false, 128>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel,
+                                                     sel_stride, o, s);
+    return bf16 ? launch_lsh_attn_hd<true, 64>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, o, s)
+                : launch_lsh_attn_hd<false, 64>(P, q, slots, B, H, k_sel, cap, scale, out, sel, nsel, sel_stride, o,
+                                                s);
 }
 
 }  // namespace be42
@@ -1084,7 +1120,6 @@ extern "C" int be42_lsh_attention(const be42_kv_pool *pool, const float *q, cons
     if (n_queries <= 0)
         return BE42_OK;
     hipStream_t s = as_stream(stream);
-    const bool bf16 = P.kind == BE42_KV_BF16;
     if ((long)n_queries * P.n_kv > 1024) {
         // Enough workgroups to fill the chip: the router's latency is better
         // spent once per query in its own launch than once per KV head in
@@ -1107,13 +1142,25 @@ extern "C" int be42_lsh_attention(const be42_kv_pool *pool, const float *q, cons
         return be42_paged_attention(pool, q, n_queries, n_heads, ws_sel, ws_n, stride, k_sel, scale, out, 1, nullptr,
                                     0, stream);
     }
-    if (P.head_dim == 128)
-        return bf16 ? launch_lsh_attn_hd<true, 128>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out,
-                                                    sel, n_sel, sel_stride, s)
-                    : launch_lsh_attn_hd<false, 128>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out,
-                                                     sel, n_sel, sel_stride, s);
-    return bf16 ? launch_lsh_attn_hd<true, 64>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, sel,
-                                               n_sel, sel_stride, s)
-                : launch_lsh_attn_hd<false, 64>(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, sel,
-                                                n_sel, sel_stride, s);
+    return launch_lsh_attn(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, sel, n_sel, sel_stride,
+                           LshAttnOpt(), s);
 }
+
+namespace be42 {
+
+// Prefill attention: query b of slot slots[b] sees the first lim[b]
+// positions, computed exactly as a one-query decode launch computes it.
+int lsh_attention_prefix(const be42_kv_pool &P, const float *q, const int *slots, const int *lim, int n_queries,
+                         int n_heads, int k_sel, int cand_cap, float scale, float *out, hipStream_t s)
+{
+    BE42_CHECK(k_sel > 0 && k_sel <= kFusedMaxPages && cand_cap > 0 && cand_cap <= kMaxCand &&
+                   n_heads % P.n_kv == 0 && n_heads / P.n_kv <= 4 && (P.head_dim == 64 || P.head_dim == 128),
+               "prefill attention: unsupported shape (k %d, cap %d, %d heads / %d kv, head_dim %d)", k_sel, cand_cap,
+               n_heads, P.n_kv, P.head_dim);
+    LshAttnOpt o;
+    o.lim = lim;
+    o.wide16 = true;
+    return launch_lsh_attn(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, nullptr, nullptr, 0, o, s);
+}
+
+}  // namespace be42

@@ -340,6 +340,30 @@ __global__ __launch_bounds__(256) void k_argmax(int *__restrict__ out, const flo
     }
 }
 
+// RoPE of a prefill chunk in place: token t (position p0 + t), KV head h:
+// q heads of h's group and k head h, with the arithmetic of the decode
+// step's rotation (k_rope_append_dev): y0 = fma(x0, c, -(x1 s)),
+// y1 = fma(x0, s, x1 c); positions at or past rope_len are not rotated.
+__global__ __launch_bounds__(256) void k_rope_rows(float *__restrict__ q, float *__restrict__ k,
+                                                   const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                                                   int p0, int rope_len, int H, int KV, int hd)
+{
+    const int t = blockIdx.x, h = blockIdx.y, half = hd / 2, G = H / KV, pos = p0 + t;
+    if (pos >= rope_len)
+        return;
+    for (int i = threadIdx.x; i < (G + 1) * half; i += blockDim.x) {
+        const int j = i / half, pr = i % half;
+        float *base = j < G ? q + ((size_t)t * H + h * G + j) * hd : k + ((size_t)t * KV + h) * hd;
+        const float cs = cos_t[(size_t)pos * half + pr], sn = sin_t[(size_t)pos * half + pr];
+        const float x0 = base[pr], x1 = base[pr + half];
+        base[pr] = __fmaf_rn(x0, cs, -(x1 * sn));
+        base[pr + half] = __fmaf_rn(x0, sn, x1 * cs);
+    }
+}
+
+// Tokens of one prefill pass (positions p0 .. p0 + T - 1 of one sequence).
+constexpr int kPrefillChunk = 256;
+
 }  // namespace be42
 
 using namespace be42;
@@ -388,6 +412,14 @@ struct be42_decoder {
     } key[2];
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     bool use_graph = true;
+    // prefill activations [kPrefillChunk][...], digit planes, and the chunk's
+    // metadata (tokens [T], visible lengths [T], slots [n_layers][T]) with
+    // its pinned host copy; allocated by the first prefill
+    float *px = nullptr, *pxn = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *patt = nullptr,
+          *pxb = nullptr, *phb = nullptr, *phb2 = nullptr;
+    void *pdig = nullptr;
+    int *pmeta = nullptr, *pmeta_host = nullptr;
+    size_t pmeta_bytes = 0;
 };
 
 static int dec_fail(be42_decoder *d, int rc)
@@ -533,8 +565,11 @@ extern "C" void be42_decoder_destroy(be42_decoder *d)
         (void)hipStreamDestroy(d->gstream);
     if (d->pool)
         be42_kv_destroy(d->pool);
+    if (d->pmeta_host)
+        (void)hipHostFree(d->pmeta_host);
     void *ptrs[] = {d->cos_t, d->sin_t, d->x, d->xb, d->xn, d->q, d->k, d->v, d->att, d->hb, d->hb2, d->logits, d->sel,
-                    d->nsel, d->slots, d->next, d->cand, d->ncand, d->xdig, d->attn_ws, d->arg_parts, d->arg_cnt};
+                    d->nsel, d->slots, d->next, d->cand, d->ncand, d->xdig, d->attn_ws, d->arg_parts, d->arg_cnt,
+                    d->px, d->pxn, d->pq, d->pk, d->pv, d->patt, d->pxb, d->phb, d->phb2, d->pdig, d->pmeta};
     for (void *p : ptrs)
         if (p)
             (void)hipFree(p);
@@ -847,5 +882,203 @@ extern "C" int be42_decoder_capture_sel(be42_decoder *d, int *sel_dst)
 {
     BE42_CHECK(d, "be42_decoder_capture_sel: null decoder");
     d->capture_sel = sel_dst;
+    return BE42_OK;
+}
+
+// ---- prefill ------------------------------------------------------------------
+// A prompt of n tokens of one sequence in passes of up to kPrefillChunk
+// tokens, each pass layer by layer over all of its tokens: the projections
+// are GEMMs over the activation digit planes (every weight tile read once
+// per pass, and each output equal to the decode GEMV's), RMSNorm, RoPE and
+// SiLU*up are the decode step's row kernels, the pass's K/V rows are
+// appended (pages sealed as they fill), and each token's attention sees the
+// cache as the decode step at its position saw it.  The argmax (and the
+// logits) of the prompt's last token follow through the final norm, the
+// lm_head GEMV and the argmax of the decode step.  For INT8 weights the
+// result is bit-identical to n single-sequence decode steps (the KV pages,
+// LSH index and logits); for FP8 it differs only by the order of the fp32
+// accumulations inside the matrix cores.
+// This is the fixed layout of forward_prefill_batch
+// (src/inference/inference.c:718-1112), whose activations are token-major
+// but described to op_matmul as [dim][batch] (:812-843).
+
+static int prefill_alloc(be42_decoder *d)
+{
+    if (d->px)
+        return BE42_OK;
+    const be42_decoder_config &c = d->c;
+    const size_t T = kPrefillChunk;
+    const int qd = c.n_heads * c.head_dim, kd = c.n_kv_heads * c.head_dim;
+    const int wide = std::max(std::max(c.dim, qd), c.hidden_dim);
+    hipError_t e = hipSuccess;
+    auto alloc = [&](void **p, size_t bytes) {
+        if (e == hipSuccess)
+            e = hipMalloc(p, bytes);
+    };
+    alloc((void **)&d->px, T * c.dim * 4);
+    alloc((void **)&d->pxn, T * c.dim * 4);
+    alloc((void **)&d->pq, T * qd * 4);
+    alloc((void **)&d->pk, T * kd * 4);
+    alloc((void **)&d->pv, T * kd * 4);
+    alloc((void **)&d->patt, T * qd * 4);
+    alloc((void **)&d->pxb, T * c.dim * 4);
+    alloc((void **)&d->phb, T * c.hidden_dim * 4);
+    alloc((void **)&d->phb2, T * c.hidden_dim * 4);
+    alloc(&d->pdig, be42_gemm_xdig_bytes(wide, (int)T, c.wkind));
+    d->pmeta_bytes = (2 + (size_t)c.n_layers) * T * sizeof(int);
+    alloc((void **)&d->pmeta, d->pmeta_bytes);
+    if (e == hipSuccess)
+        e = hipHostMalloc((void **)&d->pmeta_host, d->pmeta_bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        void **ptrs[] = {(void **)&d->px, (void **)&d->pxn, (void **)&d->pq, (void **)&d->pk, (void **)&d->pv,
+                         (void **)&d->patt, (void **)&d->pxb, (void **)&d->phb, (void **)&d->phb2, &d->pdig,
+                         (void **)&d->pmeta};
+        for (void **p : ptrs)
+            if (*p) {
+                (void)hipFree(*p);
+                *p = nullptr;
+            }
+        if (d->pmeta_host) {
+            (void)hipHostFree(d->pmeta_host);
+            d->pmeta_host = nullptr;
+        }
+        return hip_fail(e, "be42_decoder_prefill", __FILE__, __LINE__);
+    }
+    return BE42_OK;
+}
+
+static int pgemm(be42_decoder *d, float *y, const void *w, const float *s, int n, int k, int T, hipStream_t st)
+{
+    return d->c.wkind == 0 ? be42_gemm_q8_prepared(y, (const int8_t *)w, s, d->pdig, n, k, T, st)
+                           : be42_gemm_fp8_prepared(y, (const uint8_t *)w, s, d->pdig, n, k, T, st);
+}
+
+// One pass: tokens at d->pmeta (device), positions p0 .. p0 + T - 1 of
+// sequence seq.  Leaves the residual stream's last row and its pending delta
+// in *x_last / *delta_last.
+static int prefill_pass(be42_decoder *d, int seq, int T, int p0, const float **x_last, const float **delta_last,
+                        float **x_alt_last, hipStream_t st)
+{
+    const be42_decoder_config &c = d->c;
+    const int dim = c.dim, hd = c.head_dim, H = c.n_heads, KV = c.n_kv_heads;
+    const int qd = H * hd, kd = KV * hd, fp8 = c.wkind;
+    const int *tok = d->pmeta, *lim = d->pmeta + T;
+    const dim3 eg((dim + 255) / 256, T);
+    if (fp8)
+        hipLaunchKernelGGL(k_embed<true>, eg, dim3(256), 0, st, d->px, (const uint8_t *)d->w.emb, d->w.emb_s, tok,
+                           dim);
+    else
+        hipLaunchKernelGGL(k_embed<false>, eg, dim3(256), 0, st, d->px, (const uint8_t *)d->w.emb, d->w.emb_s, tok,
+                           dim);
+    BE42_LAUNCH_CHECK();
+    uint8_t *dig = (uint8_t *)d->pdig;
+    float *xcur = d->px, *xalt = d->pxn;
+    auto norm = [&](const uint16_t *wn, const float *delta) {
+        float *xo = delta ? xalt : nullptr;
+        launch_rows(fp8, dim, [&](auto f8, auto nv) {
+            hipLaunchKernelGGL((k_rmsnorm<decltype(f8)::value, decltype(nv)::value>),
+                               dim3((dim + kChunk - 1) / kChunk, T), dim3(kRowT), 0, st, nullptr, dig, xcur, xo,
+                               delta, wn, dim, T, c.norm_eps);
+        });
+        if (delta)
+            std::swap(xcur, xalt);
+        return hipGetLastError();
+    };
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int rope_len = c.rope_len > 0 ? c.rope_len : c.max_seq;
+    const float *pending = nullptr;
+    for (int l = 0; l < c.n_layers; l++) {
+        const be42_decoder_layer &L = d->w.layers[l];
+        const int slot = l * c.max_batch + seq;
+        BE42_HIP(norm(L.attn_norm, pending));
+        DEC_TRY(pgemm(d, d->pq, L.wq, L.sq, qd, dim, T, st));
+        DEC_TRY(pgemm(d, d->pk, L.wk, L.sk, kd, dim, T, st));
+        DEC_TRY(pgemm(d, d->pv, L.wv, L.sv, kd, dim, T, st));
+        hipLaunchKernelGGL(k_rope_rows, dim3(T, KV), dim3(256), 0, st, d->pq, d->pk, d->cos_t, d->sin_t, p0,
+                           rope_len, H, KV, hd);
+        BE42_LAUNCH_CHECK();
+        // the pass's K/V rows, in appends of at most 64 tokens (one launch
+        // each, plus one for the pages they fill)
+        for (int t = 0; t < T; t += 64)
+            DEC_TRY(be42_kv_append(d->pool, slot, d->pk + (size_t)t * kd, d->pv + (size_t)t * kd, p0 + t,
+                                   std::min(64, T - t), st));
+        DEC_TRY(lsh_attention_prefix(*d->pool, d->pq, d->pmeta + (size_t)(2 + l) * T, lim, T, H, c.sparse_k,
+                                     c.cand_cap, scale, d->patt, st));
+        DEC_TRY(xdig_prepare(d->pdig, d->patt, qd, T, fp8 != 0, st));
+        DEC_TRY(pgemm(d, d->pxb, L.wo, L.so, dim, qd, T, st));
+        BE42_HIP(norm(L.ffn_norm, d->pxb));                 // x += attention output
+        DEC_TRY(pgemm(d, d->phb, L.w1, L.s1, c.hidden_dim, dim, T, st));
+        DEC_TRY(pgemm(d, d->phb2, L.w3, L.s3, c.hidden_dim, dim, T, st));
+        launch_rows(fp8, c.hidden_dim, [&](auto f8, auto nv) {
+            hipLaunchKernelGGL((k_silu_mul<decltype(f8)::value, decltype(nv)::value>),
+                               dim3((c.hidden_dim + kChunk - 1) / kChunk, T), dim3(kRowT), 0, st, nullptr, dig,
+                               d->phb, d->phb2, c.hidden_dim, T);
+        });
+        BE42_LAUNCH_CHECK();
+        DEC_TRY(pgemm(d, d->pxb, L.w2, L.s2, dim, c.hidden_dim, T, st));
+        pending = d->pxb;
+    }
+    *x_last = xcur + (size_t)(T - 1) * dim;
+    *delta_last = pending + (size_t)(T - 1) * dim;
+    *x_alt_last = xalt + (size_t)(T - 1) * dim;
+    return BE42_OK;
+}
+
+extern "C" int be42_decoder_prefill(be42_decoder *d, int seq, const int *tokens, int n, int pos0, int *next_token,
+                                    float *logits_out, void *stream)
+{
+    BE42_CHECK(d && tokens, "be42_decoder_prefill: null pointer");
+    const be42_decoder_config &c = d->c;
+    BE42_CHECK(seq >= 0 && seq < c.max_batch, "be42_decoder_prefill: sequence %d (max_batch %d)", seq, c.max_batch);
+    BE42_CHECK(n > 0 && pos0 >= 0 && pos0 + n <= c.max_seq, "be42_decoder_prefill: positions %d .. %d (max_seq %d)",
+               pos0, pos0 + n - 1, c.max_seq);
+    BE42_CHECK(c.sparse_k <= 64 && c.cand_cap <= 256 && c.n_heads / c.n_kv_heads <= 4 &&
+                   (c.head_dim == 64 || c.head_dim == 128),
+               "be42_decoder_prefill: needs sparse_k <= 64, cand_cap <= 256, <= 4 heads per KV head and head_dim "
+               "64 or 128 (the decode step serves the others token by token)");
+    for (int i = 0; i < n; i++)
+        BE42_CHECK(tokens[i] >= 0 && tokens[i] < c.vocab, "be42_decoder_prefill: token %d out of range", tokens[i]);
+    DEC_TRY(prefill_alloc(d));
+    hipStream_t caller = as_stream(stream), st = d->gstream;
+    BE42_HIP(hipEventRecord(d->ev_in, caller));
+    BE42_HIP(hipStreamWaitEvent(st, d->ev_in, 0));
+    const float *x_last = nullptr, *delta_last = nullptr;
+    float *xo_last = nullptr;
+    for (int c0 = 0; c0 < n; c0 += kPrefillChunk) {
+        const int T = std::min(kPrefillChunk, n - c0), p0 = pos0 + c0;
+        // the previous pass has copied the metadata before it is rewritten
+        BE42_HIP(hipStreamSynchronize(st));
+        int *mh = d->pmeta_host;
+        for (int t = 0; t < T; t++) {
+            mh[t] = tokens[c0 + t];
+            mh[T + t] = p0 + t + 1;
+        }
+        for (int l = 0; l < c.n_layers; l++)
+            for (int t = 0; t < T; t++)
+                mh[(size_t)(2 + l) * T + t] = l * c.max_batch + seq;
+        BE42_HIP(hipMemcpyAsync(d->pmeta, mh, (2 + (size_t)c.n_layers) * T * sizeof(int), hipMemcpyHostToDevice, st));
+        DEC_TRY(prefill_pass(d, seq, T, p0, &x_last, &delta_last, &xo_last, st));
+    }
+    // the last token: final residual + norm (one row, into the decode GEMV's
+    // digit planes), lm_head, argmax into the sequence's feedback slot
+    const int dim = c.dim;
+    launch_rows(c.wkind, dim, [&](auto f8, auto nv) {
+        hipLaunchKernelGGL((k_rmsnorm<decltype(f8)::value, decltype(nv)::value>), dim3((dim + kChunk - 1) / kChunk, 1),
+                           dim3(kRowT), 0, st, nullptr, (uint8_t *)d->xdig, x_last, xo_last, delta_last,
+                           d->w.final_norm, dim, 1, c.norm_eps);
+    });
+    BE42_LAUNCH_CHECK();
+    float *lg = logits_out ? logits_out : d->logits + (size_t)seq * c.vocab;
+    DEC_TRY(gemv(d, lg, d->w.out, d->w.out_s, c.vocab, dim, 1, st));
+    hipLaunchKernelGGL(k_argmax, dim3(kArgChunks, 1), dim3(256), 0, st, d->next + seq, lg, c.vocab,
+                       d->arg_parts + (size_t)seq * kArgChunks, d->arg_cnt + seq);
+    BE42_LAUNCH_CHECK();
+    BE42_HIP(hipMemcpyAsync(d->next_host, d->next + seq, sizeof(int), hipMemcpyDeviceToHost, st));
+    BE42_HIP(hipEventRecord(d->ev_out, st));
+    BE42_HIP(hipStreamWaitEvent(caller, d->ev_out, 0));
+    if (next_token) {
+        BE42_HIP(hipEventSynchronize(d->ev_out));
+        *next_token = d->next_host[0];
+    }
     return BE42_OK;
 }

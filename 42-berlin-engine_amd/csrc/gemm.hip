@@ -32,8 +32,10 @@
 // k.  The accumulator of a 16x16 tile holds, in lane l, rows 4*(l/16)+j
 // (j = 0..3) of column l%16.
 #include <cstdlib>
+#include <type_traits>
 
 #include "be42_common.h"
+#include "xdigits.h"
 
 namespace be42 {
 
@@ -469,6 +471,177 @@ static void gemm_dispatch(float *Y, const uint8_t *X, const float *sx, const uin
         launch_gemm<FP8, 64, 128, 2, 2>(Y, X, sx, W, sw, M, N, K, s);
 }
 
+// Prefill GEMM with fp32 activations: the decode GEMV's arithmetic for many
+// tokens at once.  X arrives as the GEMV's digit planes (xdigits.h, one batch
+// row per token, dig[d][m][Kp]), so each weight tile is read once for all
+// the tokens of a workgroup instead of once per token, and every output is
+// formed exactly as the GEMV forms it: INT8 digit sums are exact int32,
+// combined in int64 and scaled once in fp64, y = tot * ((sx * 254^-2) * sw),
+// so the result is bit-identical to the GEMV's for the same row; FP8 digit
+// sums are fp32 matrix-core accumulations combined in fp64 (equal to the
+// GEMV's to fp32 accumulation order).
+// A workgroup of WGM x WGN waves owns BT = 16 WGM tokens x BN = 16 TN WGN
+// features; wave (wm, wn) holds, for its 16 tokens, one 16x16 accumulator
+// per digit plane and feature tile, so the epilogue combines a token's
+// digits in registers.  LDS rows of a stage: digit d of token row t at
+// d * BT + t, then the BN weight rows; stages of 128 k-bytes go global ->
+// registers -> LDS (rows padded to 144 bytes), double buffered with one
+// barrier per stage, as in k_gemm.  Chunks past K read as zero.
+template <bool FP8, int WGM, int WGN, int TN>
+__global__ __launch_bounds__(WGM *WGN * 64) void k_gemm_dig(float *__restrict__ Y, const uint8_t *__restrict__ dig,
+                                                            const float *__restrict__ sx,
+                                                            const uint8_t *__restrict__ W,
+                                                            const float *__restrict__ sw, int M, int N, int K,
+                                                            int Kp, int tiles_m)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr int NT = WGM * WGN * 64;
+    constexpr int BT = 16 * WGM, BN = 16 * TN * WGN, XR = ND * BT;
+    constexpr int CHUNKS = (XR + BN) * (kGemmBK / 16);
+    constexpr int CPT = (CHUNKS + NT - 1) / NT;
+    constexpr int KI = FP8 ? 128 : 64;
+    constexpr int LB = KI / 4;
+    __shared__ __align__(16) uint8_t lds[2][(XR + BN) * kGemmLd];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int bm = blockIdx.x % tiles_m, bn = blockIdx.x / tiles_m;
+    const int m0 = bm * BT, n0 = bn * BN;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    const uint8_t *src[CPT];
+    int dst[CPT];
+    bool live[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+        const int c = min(tid + i * NT, CHUNKS - 1);
+        live[i] = tid + i * NT < CHUNKS;
+        const int row = c >> 3, col = (c & 7) * 16;
+        if (row < XR) {
+            const int d = row / BT, t = min(m0 + row % BT, M - 1);
+            src[i] = dig + ((size_t)d * M + t) * Kp + col;
+        } else {
+            src[i] = W + (size_t)min(n0 + row - XR, N - 1) * K + col;
+        }
+        dst[i] = row * kGemmLd + col;
+    }
+    const int nk = (K + kGemmBK - 1) / kGemmBK;
+    v4i stage[CPT];
+    auto gload = [&](int ks) {
+        const int kb = ks * kGemmBK;
+#pragma unroll
+        for (int i = 0; i < CPT; i++) {
+            const int col = (min(tid + i * NT, CHUNKS - 1) & 7) * 16;
+            stage[i] = kb + col < K ? *(const v4i *)(src[i] + kb) : v4i{0, 0, 0, 0};
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CPT; i++)
+            if (live[i])
+                *(v4i *)(&lds[buf][dst[i]]) = stage[i];
+    };
+
+    using Acc = typename std::conditional<FP8, v4f, v4i>::type;
+    Acc acc[ND][TN];
+#pragma unroll
+    for (int i = 0; i < ND; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            acc[i][j] = Acc{0, 0, 0, 0};
+
+    const int r = lane & 15, g = lane >> 4;
+    const int arow0 = wm * 16 + r;                   // + d * BT
+    const int brow0 = XR + wn * (TN * 16) + r;       // + j * 16
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int ks = 0; ks < nk; ks++) {
+        const int cur = ks & 1;
+        if (ks + 1 < nk)
+            gload(ks + 1);
+        const uint8_t *L = lds[cur];
+#pragma unroll
+        for (int kk = 0; kk < kGemmBK / KI; kk++) {
+            const int kof = kk * KI + g * LB;
+            if constexpr (FP8) {
+                v8i a[ND], b[TN];
+#pragma unroll
+                for (int i = 0; i < ND; i++) {
+                    const v4i lo = *(const v4i *)(L + (arow0 + i * BT) * kGemmLd + kof);
+                    const v4i hi = *(const v4i *)(L + (arow0 + i * BT) * kGemmLd + kof + 16);
+                    a[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const v4i lo = *(const v4i *)(L + (brow0 + j * 16) * kGemmLd + kof);
+                    const v4i hi = *(const v4i *)(L + (brow0 + j * 16) * kGemmLd + kof + 16);
+                    b[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+#pragma unroll
+                for (int i = 0; i < ND; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[i], b[j], acc[i][j], 0, 0,
+                                                                                     0, 127, 0, 127);
+            } else {
+                v4i a[ND], b[TN];
+#pragma unroll
+                for (int i = 0; i < ND; i++)
+                    a[i] = *(const v4i *)(L + (arow0 + i * BT) * kGemmLd + kof);
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    b[j] = *(const v4i *)(L + (brow0 + j * 16) * kGemmLd + kof);
+#pragma unroll
+                for (int i = 0; i < ND; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if (ks + 1 < nk)
+            sstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // lane l holds tokens 4*(l/16)+e of feature column l%16 of every tile
+    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = n0 + wn * (TN * 16) + j * 16 + r;
+        if (n >= N)
+            continue;
+        const double swn = (double)sw[n];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = m0 + wm * 16 + 4 * g + e;
+            if (m >= M)
+                continue;
+            double tot;
+            if constexpr (FP8) {
+                tot = 0.0;
+#pragma unroll
+                for (int d = 0; d < ND; d++)
+                    tot += (double)acc[d][j][e] * kF8DigitW[d];
+            } else {
+                const long long it = (long long)acc[0][j][e] * ((long long)kI8Base * kI8Base) +
+                                     (long long)acc[1][j][e] * kI8Base + (long long)acc[2][j][e];
+                tot = (double)it;
+            }
+            Y[(size_t)m * N + n] = (float)(tot * ((double)sx[m] * sxw * swn));
+        }
+    }
+}
+
+template <bool FP8, int WGM, int WGN, int TN>
+static void launch_gemm_dig(float *Y, const uint8_t *dig, const float *sx, const uint8_t *W, const float *sw, int M,
+                            int N, int K, hipStream_t s)
+{
+    const int tm = (M + 16 * WGM - 1) / (16 * WGM), tn = (N + 16 * TN * WGN - 1) / (16 * TN * WGN);
+    hipLaunchKernelGGL((k_gemm_dig<FP8, WGM, WGN, TN>), dim3(tm * tn), dim3(WGM * WGN * 64), 0, s, Y, dig, sx, W, sw,
+                       M, N, K, (int)xdig_kp(K, FP8), tm);
+}
+
 }  // namespace be42
 
 using namespace be42;
@@ -502,4 +675,53 @@ extern "C" int be42_gemm_fp8(float *y, const uint8_t *xq, const float *sx, const
                              int m, int n, int k, void *stream)
 {
     return gemm_entry(true, y, xq, sx, wq, sw, m, n, k, stream);
+}
+
+// ---- prefill GEMM over activation digit planes ------------------------------
+
+extern "C" size_t be42_gemm_xdig_bytes(int k, int m, int fp8)
+{
+    if (k <= 0 || m <= 0)
+        return 0;
+    return xdig_bytes(k, m, fp8 != 0);
+}
+
+extern "C" int be42_gemm_prepare(void *xdig, const float *x, int k, int m, int fp8, void *stream)
+{
+    BE42_CHECK(xdig && x, "be42_gemm_prepare: null pointer");
+    BE42_CHECK(k > 0 && k % 16 == 0 && m > 0 && m <= 65535 && ((uintptr_t)x & 15) == 0,
+               "be42_gemm_prepare: needs k %% 16 == 0, 1 <= m <= 65535 and 16-byte aligned x (k=%d m=%d)", k, m);
+    return xdig_prepare(xdig, x, k, m, fp8 != 0, as_stream(stream));
+}
+
+static int gemm_dig_entry(bool fp8, float *y, const void *w, const float *sw, const void *xdig, int n, int k, int m,
+                          void *stream)
+{
+    const char *name = fp8 ? "be42_gemm_fp8_prepared" : "be42_gemm_q8_prepared";
+    BE42_CHECK(y && w && sw && xdig, "%s: null pointer", name);
+    BE42_CHECK(n > 0 && k > 0 && k % 16 == 0 && m > 0 && m <= 65535,
+               "%s: bad shape n=%d k=%d m=%d (k %% 16 == 0, m <= 65535)", name, n, k, m);
+    BE42_CHECK(((uintptr_t)w & 15) == 0, "%s: weights must be 16-byte aligned", name);
+    BE42_CHECK(fp8 || k < 133144, "%s: k=%d would overflow the int32 accumulator", name, k);
+    const uint8_t *dig = (const uint8_t *)xdig;
+    const float *sx = xdig_scales((void *)xdig, k, m, fp8);
+    hipStream_t s = as_stream(stream);
+    if (fp8)
+        launch_gemm_dig<true, 4, 2, 4>(y, dig, sx, (const uint8_t *)w, sw, m, n, k, s);
+    else
+        launch_gemm_dig<false, 4, 2, 4>(y, dig, sx, (const uint8_t *)w, sw, m, n, k, s);
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
+extern "C" int be42_gemm_q8_prepared(float *y, const int8_t *w, const float *w_scale, const void *xdig, int n, int k,
+                                     int m, void *stream)
+{
+    return gemm_dig_entry(false, y, w, w_scale, xdig, n, k, m, stream);
+}
+
+extern "C" int be42_gemm_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, const void *xdig, int n,
+                                      int k, int m, void *stream)
+{
+    return gemm_dig_entry(true, y, w, w_scale, xdig, n, k, m, stream);
 }

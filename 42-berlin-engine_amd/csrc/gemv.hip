@@ -523,11 +523,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dma(const GemvSegs S, const
     }
 }
 
-// Partial sums of split-K slab launches, [ks][b][row] floats, added up by a
-// second launch (k_gemv_part_sum).  Shared by every launch on the device, so
-// split-K GEMVs on one device must not run concurrently (one stream).
-constexpr size_t kGemvPartFloats = (size_t)1 << 20;   // 4 MiB
-__device__ float g_gemv_part[kGemvPartFloats];
+// Partial sums of split-K launches, [ks][b][row]: the digit-combined sum of
+// each K range before any scale (exact integers for INT8), added up in K
+// order and scaled by a second launch (k_gemv_part_sum), so that a split
+// GEMV rounds once, like an unsplit one.  Shared by every launch on the
+// device, so split-K GEMVs on one device must not run concurrently (one
+// stream).
+constexpr size_t kGemvPartFloats = (size_t)1 << 20;   // entries (8 MiB)
+__device__ double g_gemv_part[kGemvPartFloats];
 
 // Streaming GEMV for many rows (the lm_head) with the digit planes resident in
 // LDS one K-slice at a time.
@@ -758,28 +761,31 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_slab(const GemvSegs S, cons
                     it += (long long)acc[t][d][j] * (long long)kI8W[d];
                 tot = (double)it;
             }
-            const float v = (float)(tot * ((double)e_sx[j] * sxw * (double)e_sw[t]));
             if (ksplit == 1)
-                st_global(e_y[t] + (size_t)b * e_n[t], v);
+                st_global(e_y[t] + (size_t)b * e_n[t], (float)(tot * ((double)e_sx[j] * sxw * (double)e_sw[t])));
             else
-                g_gemv_part[((size_t)ks * B + b) * S.total + row0 + t * 16 + r] = v;
+                g_gemv_part[((size_t)ks * B + b) * S.total + row0 + t * 16 + r] = tot;
         }
     }
 }
 
-// y[b][row] = sum over the K ranges of a split slab launch, in K order.
-__global__ __launch_bounds__(256) void k_gemv_part_sum(const GemvSegs S, int B, int ksplit)
+// y[b][row] = (sum over the K ranges of a split launch, in K order) times the
+// scales, as the unsplit epilogue forms it (sxw: 254^-2 for INT8, 1 for FP8).
+__global__ __launch_bounds__(256) void k_gemv_part_sum(const GemvSegs S, const float *__restrict__ sx, double sxw,
+                                                       int B, int ksplit)
 {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= B * S.total)
         return;
     const int b = i / S.total, row = i % S.total;
-    float v = 0.0f;
+    double tot = 0.0;
     for (int q = 0; q < ksplit; q++)
-        v += g_gemv_part[((size_t)q * B + b) * S.total + row];
+        tot += g_gemv_part[((size_t)q * B + b) * S.total + row];
     int local;
     const int sg = seg_of(S, row, &local);
-    st_global(seg_pick(S.y, sg) + (size_t)b * seg_pick(S.n, sg) + local, v);
+    const float sw = seg_pick(S.sw, sg)[local];
+    st_global(seg_pick(S.y, sg) + (size_t)b * seg_pick(S.n, sg) + local,
+              (float)(tot * ((double)sx[b] * sxw * (double)sw)));
 }
 
 // Block-cooperative streaming GEMV for many rows.
@@ -891,6 +897,7 @@ __global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S,
     const int o_src = (32 * wave + lane) >> 2, o_j = lane & 3;
     const int o_r = o_src & 15, o_b = 4 * (o_src >> 4) + o_j;
     double o_sx = (double)ld_global(sx + min(o_b, B - 1)) * (FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base));
+    // (every GEMV epilogue forms y = tot * ((sx * sxw) * sw) in fp64 and rounds once)
     // weight scales of the block's rows, staged in LDS before the loop: a
     // plain load inside it would make the compiler wait for every load in
     // flight (it cannot count plain loads apart from the ones into LDS);
@@ -927,9 +934,11 @@ __global__ __launch_bounds__(kCoopWaves * 64) void k_gemv_coop(const GemvSegs S,
                 // y[b][local] of the row's segment, or the partial [ks][b][row]
                 int local;
                 const int sg = seg_of(S, row, &local);
-                float *dst = ksplit == 1 ? seg_pick(S.y, sg) + (size_t)o_b * seg_pick(S.n, sg) + local
-                                         : g_gemv_part + ((size_t)ks * B + o_b) * S.total + row;
-                st_global(dst, (float)((double)tot * o_sx * (double)lsw[t * 16 + o_r]));
+                if (ksplit == 1)
+                    st_global(seg_pick(S.y, sg) + (size_t)o_b * seg_pick(S.n, sg) + local,
+                              (float)((double)tot * (o_sx * (double)lsw[t * 16 + o_r])));
+                else
+                    g_gemv_part[((size_t)ks * B + o_b) * S.total + row] = (double)tot;
             }
         }
     };
@@ -1006,7 +1015,8 @@ static void launch_coop(const GemvSegs &S, const uint8_t *dig, const float *sx, 
     hipLaunchKernelGGL((k_gemv_coop<FP8, SPW, D>), dim3(blocks, ksplit), dim3(kCoopWaves * 64), 0, s, S, dig, sx, k,
                        Kp, batch, tpb);
     if (ksplit > 1)
-        hipLaunchKernelGGL(k_gemv_part_sum, dim3((batch * S.total + 255) / 256), dim3(256), 0, s, S, batch, ksplit);
+        hipLaunchKernelGGL(k_gemv_part_sum, dim3((batch * S.total + 255) / 256), dim3(256), 0, s, S, sx,
+                           FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base), batch, ksplit);
 }
 
 template <bool FP8, int RT, int SB, int KSL, int D, int WAVES>
@@ -1017,7 +1027,8 @@ static void launch_slab(const GemvSegs &S, const uint8_t *dig, const float *sx, 
     hipLaunchKernelGGL((k_gemv_slab<FP8, RT, SB, KSL, D, WAVES>), dim3(blocks, ksplit), dim3(WAVES * 64), 0, s, S,
                        dig, sx, k, Kp, batch, Kp / KSL / ksplit);
     if (ksplit > 1)
-        hipLaunchKernelGGL(k_gemv_part_sum, dim3((batch * S.total + 255) / 256), dim3(256), 0, s, S, batch, ksplit);
+        hipLaunchKernelGGL(k_gemv_part_sum, dim3((batch * S.total + 255) / 256), dim3(256), 0, s, S, sx,
+                           FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base), batch, ksplit);
 }
 
 template <bool FP8, int RT, int NC, int P, int WAVES>
@@ -1066,7 +1077,7 @@ __global__ __launch_bounds__(256) void k_gemv_generic(float *y, const uint8_t *W
     }
 }
 
-static int prepare_launch(void *buf, const float *x, int k, int batch, bool fp8, hipStream_t s)
+int xdig_prepare(void *buf, const float *x, int k, int batch, bool fp8, hipStream_t s)
 {
     const int Kp = (int)xdig_kp(k, fp8);
     uint8_t *dig = (uint8_t *)buf;
@@ -1347,7 +1358,7 @@ static int gemv_launch(float *y, const uint8_t *w, const float *sw, const float 
     void *buf = workspace(xdig_bytes(k, batch, FP8), s);
     if (!buf)
         return BE42_ENOMEM;
-    int rc = prepare_launch(buf, x, k, batch, FP8, s);
+    int rc = xdig_prepare(buf, x, k, batch, FP8, s);
     if (rc)
         return rc;
     return prepared_launch<FP8>(y, w, sw, buf, n, k, batch, s);
@@ -1421,7 +1432,7 @@ extern "C" int be42_gemv_noalloc(float *y, const void *w, const float *w_scale, 
     int rc = gemv_scratch(&buf);
     if (rc)
         return rc;
-    rc = prepare_launch(buf, x, k, batch, fp8 != 0, s);
+    rc = xdig_prepare(buf, x, k, batch, fp8 != 0, s);
     if (rc)
         return rc;
     return fp8 ? prepared_launch<true>(y, wb, w_scale, buf, n, k, batch, s)
@@ -1453,7 +1464,7 @@ extern "C" int be42_gemv_prepare(void *xdig, const float *x, int k, int batch, i
     BE42_CHECK(k > 0 && k % 16 == 0 && batch > 0 && batch <= 16 && x_aligned(x),
                "be42_gemv_prepare: needs k %% 16 == 0, 1 <= batch <= 16 and 16-byte aligned x (k=%d batch=%d)",
                k, batch);
-    return prepare_launch(xdig, x, k, batch, fp8 != 0, as_stream(stream));
+    return xdig_prepare(xdig, x, k, batch, fp8 != 0, as_stream(stream));
 }
 
 extern "C" int be42_gemv_q8_prepared(float *y, const int8_t *w, const float *w_scale, const void *xdig,

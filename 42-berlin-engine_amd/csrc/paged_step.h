@@ -1,5 +1,6 @@
 // paged_step.h -- the per-step KV append of a decode batch, shared by the page
-// pool (paged.hip) and the decode step (decode.hip).
+// pool (paged.hip) and the decode step (decode.hip), and the prefill's view of
+// the paged attention (attention.hip).
 #pragma once
 
 #include <vector>
@@ -45,5 +46,13 @@ void undo_append_plans(be42_kv_pool *pool, const PlanUndo &undo);
 int launch_rope_append_step_dev(const be42_kv_pool &P, const AppendStepArgs *a_dev, int n, float *q, float *k,
                                 const float *v, const float *cos_t, const float *sin_t, const int *pos_p,
                                 int rope_len, int n_heads, hipStream_t st);
+
+// device: paged attention of n_queries queries of the slots slots[b] (device
+// array), query b seeing only the first lim[b] positions of its slot (its
+// pages, LSH index and last page as they were when position lim[b] - 1 was
+// the newest), each computed exactly as a one-query decode launch computes it
+// (attention.hip); needs k_sel <= 64, groups of <= 4 heads, head_dim 64/128
+int lsh_attention_prefix(const be42_kv_pool &P, const float *q, const int *slots, const int *lim, int n_queries,
+                         int n_heads, int k_sel, int cand_cap, float scale, float *out, hipStream_t s);
 
 }  // namespace be42

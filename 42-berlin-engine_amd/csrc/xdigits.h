@@ -8,8 +8,10 @@
 //   FP8:  5 integer digits in [-15, 15] stored as exact E4M3 codes, R = 30,
 //         s_b = max|x_b| / 15
 // (to ~2^-24 relative to max|x_b|).  Buffer layout: digit planes
-// dig[d][b][0..Kp) bytes (zero past K), then, on a 256-byte boundary, 16
-// floats s_b.  Kp is K rounded up to the largest burst a GEMV tile uses.
+// dig[d][b][0..Kp) bytes (zero past K), then, on a 256-byte boundary, the
+// floats s_b (room for max(16, batch)).  Kp is K rounded up to the largest
+// burst a GEMV tile uses.  The prefill GEMM reads the same layout with one
+// "batch row" per token.
 #pragma once
 
 #include "be42_common.h"
@@ -20,6 +22,8 @@ constexpr int kI8Digits = 3;
 constexpr int kI8Base = 254;
 constexpr int kF8Digits = 5;
 constexpr int kF8Base = 30;
+// weight of FP8 digit d in the recombination, 30^-d
+__device__ constexpr double kF8DigitW[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 27000, 1.0 / 810000};
 
 // integer in [-15, 15] -> exact E4M3 code
 __device__ __forceinline__ uint8_t small_int_to_e4m3(int n)
@@ -81,16 +85,20 @@ __host__ __device__ inline size_t xdig_kp(int k, bool fp8)
     const XDigits L = xdig_layout(fp8);
     return ((size_t)(k + L.burst - 1) / L.burst) * L.burst;
 }
-// digits first, then 16 float scales on a 256-byte boundary
+// digits first, then the float scales on a 256-byte boundary
 __host__ __device__ inline size_t xdig_bytes(int k, int batch, bool fp8)
 {
     const size_t dig = (size_t)xdig_layout(fp8).nd * batch * xdig_kp(k, fp8);
-    return ((dig + 255) & ~(size_t)255) + 16 * sizeof(float);
+    return ((dig + 255) & ~(size_t)255) + (size_t)(batch > 16 ? batch : 16) * sizeof(float);
 }
 __host__ __device__ inline float *xdig_scales(void *buf, int k, int batch, bool fp8)
 {
     const size_t dig = (size_t)xdig_layout(fp8).nd * batch * xdig_kp(k, fp8);
     return (float *)((uint8_t *)buf + ((dig + 255) & ~(size_t)255));
 }
+
+// host: the digit planes (and scales) of x [batch][k] into buf (gemv.hip);
+// any batch, k % 16 == 0
+int xdig_prepare(void *buf, const float *x, int k, int batch, bool fp8, hipStream_t s);
 
 }  // namespace be42

@@ -118,6 +118,20 @@ int be42_gemm_i8(float *y, const int8_t *xq, const float *sx, const int8_t *wq, 
                  int m, int n, int k, void *stream);
 int be42_gemm_fp8(float *y, const uint8_t *xq, const float *sx, const uint8_t *wq, const float *sw,
                   int m, int n, int k, void *stream);
+/* The same GEMM for fp32 activations, as the decode GEMV computes them: x
+ * [m][k] is split once into the GEMV's digit planes (be42_gemm_prepare, one
+ * "batch row" per token, m <= 65535, buffer of be42_gemm_xdig_bytes), then
+ * Y[m][n] = sw[n] * sum_k w[n][k] * x[m][k] through the matrix cores.  INT8:
+ * bit-identical to be42_gemv_q8_prepared on each row; FP8: equal to
+ * be42_gemv_fp8_prepared up to the order of the fp32 accumulations.  This is
+ * the projection step of the batched prefill (op_matmul with n > 1,
+ * src/inference/inference.c:841-843, :1033-1036, :1087). */
+size_t be42_gemm_xdig_bytes(int k, int m, int fp8);
+int    be42_gemm_prepare(void *xdig, const float *x, int k, int m, int fp8, void *stream);
+int    be42_gemm_q8_prepared(float *y, const int8_t *w, const float *w_scale, const void *xdig, int n, int k,
+                             int m, void *stream);
+int    be42_gemm_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, const void *xdig, int n, int k,
+                              int m, void *stream);
 
 /* ---- paged KV cache in HBM ------------------------------------------------------
  * Mirrors t_block_manager / t_paged_kv_cache (src/memory/paged.h:53-99): pages
@@ -318,6 +332,21 @@ be42_kv_pool *be42_decoder_pool(be42_decoder *d);
 int  be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
                        float *logits_out, void *stream);
 int  be42_decoder_next_tokens(be42_decoder *d, const int **dev_ptr);
+/* Batched prefill (forward_prefill_batch, src/inference/inference.c:718-1112,
+ * with its token-major / feature-major layout fixed): the n prompt tokens of
+ * sequence seq at positions pos0 .. pos0+n-1, in passes of up to 256 tokens
+ * whose projections are GEMMs (be42_gemm_*_prepared) and whose attention lets
+ * each token see the cache as of its own position.  The argmax of the last
+ * token goes to *next_token (host, may be NULL) and to the sequence's device
+ * feedback slot (a following be42_decoder_step with tokens == NULL continues
+ * from it); logits_out (device [vocab], may be NULL) takes its logits.  INT8
+ * weights: bit-identical to n one-sequence decode steps (KV pages, LSH index,
+ * logits); FP8: equal up to fp32 accumulation order.  Needs sparse_k <= 64,
+ * cand_cap <= 256, <= 4 heads per KV head, head_dim 64 or 128.  Ordered on
+ * `stream` like be42_decoder_step; on error the sequence's cache may hold
+ * part of the prompt (reset its slots with be42_kv_reset). */
+int  be42_decoder_prefill(be42_decoder *d, int seq, const int *tokens, int n, int pos0, int *next_token,
+                          float *logits_out, void *stream);
 /* Inspection: each step copies every layer's rotated queries into q_dst
  * ([n_layers][max_batch][n_heads * head_dim], device) and the number of pages
  * each layer attended into nsel_dst ([n_layers][max_batch], device); NULL

@@ -152,3 +152,56 @@ def test_gemm_every_tile(be, orc, kind, tile, monkeypatch):
     else:
         assert rel_err(y, want) <= TOL
         assert rel_err(y.astype(np.float64), _exact_fp8(orc, xq, sx, wq, sw)) <= 2e-4
+
+
+# ---- fp32 activations through the digit planes (the prefill projections) ----
+
+def _weights(rng, n, k, kind, be):
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wt = torch.from_numpy(w).cuda()
+    return be.quant_rows_int8(wt) if kind == "int8" else be.quant_rows_fp8(wt)
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("m,n,k", [(1, 64, 512), (17, 1000, 1424), (64, 3072, 512), (200, 1408, 4096),
+                                   (300, 96, 8192)])
+def test_gemm_f32_equals_gemv_rows(be, kind, m, n, k):
+    """Every row of the digit-plane GEMM against the decode GEMV of the same
+    row (batches of up to 16 rows, and single rows): INT8 bit-identical
+    (exact int32 digit sums, one fp64 scaling), FP8 to fp32 accumulation
+    order; within the GEMV tests' bounds of the float64 product of the
+    codes: 1e-5 (INT8: digits to 2^-24 of max|x|) and 1e-4 (FP8: the matrix
+    core's own fp32 reduction of each block of digit products)."""
+    rng = np.random.default_rng(m * 7 + n + k)
+    wq, sw = _weights(rng, n, k, kind, be)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random((m, k)) < 0.01] *= 50.0
+    xt = torch.from_numpy(x).cuda()
+    y = be.gemm_f32(xt, wq, sw, kind)
+    ref = torch.empty_like(y)
+    for r0 in range(0, m, 16):
+        r1 = min(m, r0 + 16)
+        ref[r0:r1] = be.gemv(wq, sw, xt[r0:r1].contiguous(), kind)
+    single = [0, m - 1, m // 2]
+    for r in single:
+        ref1 = be.gemv(wq, sw, xt[r:r + 1].contiguous(), kind)
+        if kind == "int8":
+            assert torch.equal(ref1[0], ref[r]), r
+    yh, rh = y.cpu().numpy(), ref.cpu().numpy()
+    if kind == "int8":
+        np.testing.assert_array_equal(yh, rh)
+        wd = wq.cpu().numpy().astype(np.float64)
+    else:
+        from oracle_bind import Oracle
+        wd = Oracle().fp8_lut()[wq.cpu().numpy()].astype(np.float64)
+        assert rel_err(yh, rh) <= 1e-4
+    exact = (x.astype(np.float64) @ wd.T) * sw.cpu().numpy().astype(np.float64)
+    assert rel_err(yh, exact) <= (1e-5 if kind == "int8" else 1e-4)
+
+
+def test_gemm_f32_rejects_bad_shapes(be):
+    import be42
+    w = torch.zeros((16, 24), dtype=torch.int8, device="cuda")
+    s = torch.ones(16, device="cuda")
+    with pytest.raises(be42.Be42Error, match="k % 16 == 0"):
+        be.gemm_f32(torch.zeros((4, 24), device="cuda"), w, s, "int8")
