@@ -47,6 +47,7 @@ SIGNATURES = {
     "be42_gemm_prepare": (i32, [vp, vp, i32, i32, i32, vp]),
     "be42_gemm_q8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8_prepared": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "be42_gemm_prepared_multi": (i32, [vp, i32, vp, i32, i32, i32, vp]),
     "be42_gemm_fp8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
     "be42_decoder_create": (i32, [vp, vp, vp, vp]),
     "be42_sample_temperature": (i32, [vp, vp, i32, i32, C.c_float, vp, vp]),
@@ -274,6 +275,23 @@ class Lib:
         name = "be42_gemm_q8_prepared" if kind == "int8" else "be42_gemm_fp8_prepared"
         self._call(name, self.p(y), self.p(w), self.p(sw), self.p(buf), n, k, m, self.stream(stream))
         return y
+
+    def gemm_f32_multi(self, x, segs, kind, stream=None):
+        """segs: [(w [n][k], w_scale [n])], up to 3, sharing x [M][K]: one
+        launch (be42_gemm_prepared_multi); returns the outputs [M][n]."""
+        t = self.torch
+        m, k = x.shape
+        fp8 = 0 if kind == "int8" else 1
+        buf = t.empty(self.lib.be42_gemm_xdig_bytes(k, m, fp8), dtype=t.uint8, device=x.device)
+        self._call("be42_gemm_prepare", self.p(buf), self.p(x), k, m, fp8, self.stream(stream))
+        outs = [t.empty((m, w.shape[0]), dtype=t.float32, device=x.device) for w, _ in segs]
+        arr = (GemvSeg * len(segs))()
+        for i, ((w, sw), y) in enumerate(zip(segs, outs)):
+            assert w.shape[1] == k
+            arr[i] = GemvSeg(self.p(w), self.p(sw), self.p(y), w.shape[0])
+        self._call("be42_gemm_prepared_multi", C.addressof(arr), len(segs), self.p(buf), k, m, fp8,
+                   self.stream(stream))
+        return outs
 
     # -- LSH / paged KV / attention --------------------------------------------
     def lsh_projection(self, dim, seed):

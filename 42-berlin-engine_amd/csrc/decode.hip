@@ -99,7 +99,8 @@ __device__ __forceinline__ float block_max4(float v, float *red)
     return fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
 }
 
-// chunk c of row b's digit planes (and fp32 out) from the row in registers
+// chunk c of row b's digit planes (and fp32 out) from the row in registers;
+// c < 0: every chunk (one block per row, for many rows)
 template <bool FP8, int NV>
 __device__ __forceinline__ void row_chunk_digits(const float4 (&h)[NV], int n, uint8_t *__restrict__ dig,
                                                  float *__restrict__ out, int B, int b, int c, float *red)
@@ -111,12 +112,12 @@ __device__ __forceinline__ void row_chunk_digits(const float4 (&h)[NV], int n, u
     const float amax = block_max4(m, red);
     const float sc = digit_scale<FP8>(amax);
     const int Kp = (int)xdig_kp(n, FP8);
-    if (c == 0 && threadIdx.x == 0)
+    if (c <= 0 && threadIdx.x == 0)
         xdig_scales(dig, n, B, FP8)[b] = sc;
-    const int i = (int)threadIdx.x + kRowT * c, k0 = 4 * i;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        if (j == c) {
+        if (j == c || c < 0) {
+            const int i = (int)threadIdx.x + kRowT * j, k0 = 4 * i;
             if (k0 < Kp) {
                 const float xe[4] = {h[j].x, h[j].y, h[j].z, h[j].w};
                 store_digit_words<FP8>(xe, sc, dig, B, Kp, b, k0);
@@ -139,10 +140,10 @@ template <bool FP8, int NV>
 __global__ __launch_bounds__(kRowT) void k_rmsnorm(float *__restrict__ out, uint8_t *__restrict__ dig,
                                                   const float *__restrict__ x, float *__restrict__ x_out,
                                                   const float *__restrict__ delta, const uint16_t *__restrict__ w,
-                                                  int dim, int B, float eps)
+                                                  int dim, int B, float eps, bool all_chunks)
 {
     __shared__ float red[8];
-    const int b = blockIdx.y, c = blockIdx.x, n4 = dim >> 2;
+    const int b = blockIdx.y, c = all_chunks ? -1 : (int)blockIdx.x, n4 = dim >> 2;
     const float4 *x4 = (const float4 *)(x + (size_t)b * dim);
     const float4 *d4 = delta ? (const float4 *)(delta + (size_t)b * dim) : nullptr;
     const uint2 *w4 = (const uint2 *)w;
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(kRowT) void k_rmsnorm(float *__restrict__ out, uint
         const int i = threadIdx.x + kRowT * j;
         if (d4) {
             v[j] = make_float4(v[j].x + dv[j].x, v[j].y + dv[j].y, v[j].z + dv[j].z, v[j].w + dv[j].w);
-            if (j == c && i < n4)
+            if ((j == c || c < 0) && i < n4)
                 ((float4 *)(x_out + (size_t)b * dim))[i] = v[j];
         }
         if (i >= n4)
@@ -211,10 +212,10 @@ __device__ __forceinline__ float silu_mul1(float gv, float uv, bool vec)
 template <bool FP8, int NV>
 __global__ __launch_bounds__(kRowT) void k_silu_mul(float *__restrict__ out, uint8_t *__restrict__ dig,
                                                    const float *__restrict__ g, const float *__restrict__ u, int n,
-                                                   int B)
+                                                   int B, bool all_chunks)
 {
     __shared__ float red[8];
-    const int b = blockIdx.y, c = blockIdx.x, n4 = n >> 2, nvec = n & ~7;
+    const int b = blockIdx.y, c = all_chunks ? -1 : (int)blockIdx.x, n4 = n >> 2, nvec = n & ~7;
     const float4 *g4 = (const float4 *)(g + (size_t)b * n), *u4 = (const float4 *)(u + (size_t)b * n);
     float4 gv[NV], uv[NV];
 #pragma unroll
@@ -362,7 +363,7 @@ __global__ __launch_bounds__(256) void k_rope_rows(float *__restrict__ q, float 
 }
 
 // Tokens of one prefill pass (positions p0 .. p0 + T - 1 of one sequence).
-constexpr int kPrefillChunk = 256;
+constexpr int kPrefillChunk = 1024;
 
 }  // namespace be42
 
@@ -657,7 +658,7 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         launch_rows(fp8, dim, [&](auto f8, auto nv) {
             hipLaunchKernelGGL((k_rmsnorm<decltype(f8)::value, decltype(nv)::value>),
                                dim3((dim + kChunk - 1) / kChunk, B), dim3(kRowT), 0, st, nullptr, dig, xcur, xo,
-                               delta, wn, dim, B, c.norm_eps);
+                               delta, wn, dim, B, c.norm_eps, false);
         });
         if (delta)
             std::swap(xcur, xalt);
@@ -720,7 +721,7 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         launch_rows(fp8, c.hidden_dim, [&](auto f8, auto nv) {
             hipLaunchKernelGGL((k_silu_mul<decltype(f8)::value, decltype(nv)::value>),
                                dim3((c.hidden_dim + kChunk - 1) / kChunk, B), dim3(kRowT), 0, st, nullptr, dig, d->hb,
-                               d->hb2, c.hidden_dim, B);
+                               d->hb2, c.hidden_dim, B, false);
         });
         BE42_LAUNCH_CHECK();
         DEC_TRY(gemv(d, d->xb, L.w2, L.s2, dim, c.hidden_dim, B, st));
@@ -925,7 +926,7 @@ static int prefill_alloc(be42_decoder *d)
     alloc((void **)&d->phb, T * c.hidden_dim * 4);
     alloc((void **)&d->phb2, T * c.hidden_dim * 4);
     alloc(&d->pdig, be42_gemm_xdig_bytes(wide, (int)T, c.wkind));
-    d->pmeta_bytes = (2 + (size_t)c.n_layers) * T * sizeof(int);
+    d->pmeta_bytes = ((2 + (size_t)c.n_layers) * T + (size_t)c.n_layers * append_run_list_cap((int)T)) * sizeof(int);
     alloc((void **)&d->pmeta, d->pmeta_bytes);
     if (e == hipSuccess)
         e = hipHostMalloc((void **)&d->pmeta_host, d->pmeta_bytes, hipHostMallocDefault);
@@ -953,11 +954,17 @@ static int pgemm(be42_decoder *d, float *y, const void *w, const float *s, int n
                            : be42_gemm_fp8_prepared(y, (const uint8_t *)w, s, d->pdig, n, k, T, st);
 }
 
-// One pass: tokens at d->pmeta (device), positions p0 .. p0 + T - 1 of
-// sequence seq.  Leaves the residual stream's last row and its pending delta
-// in *x_last / *delta_last.
-static int prefill_pass(be42_decoder *d, int seq, int T, int p0, const float **x_last, const float **delta_last,
-                        float **x_alt_last, hipStream_t st)
+static int pgemm_multi(be42_decoder *d, std::initializer_list<be42_gemv_seg> segs, int k, int T, hipStream_t st)
+{
+    return be42_gemm_prepared_multi(segs.begin(), (int)segs.size(), d->pdig, k, T, d->c.wkind, st);
+}
+
+// One pass: tokens, visible lengths, slots and each layer's page lists
+// (runs[l], lists at the metadata's offset list_off[l]) at d->pmeta (device),
+// positions p0 .. p0 + T - 1 of sequence seq.  Leaves the residual stream's
+// last row and its pending delta in *x_last / *delta_last.
+static int prefill_pass(be42_decoder *d, int seq, int T, int p0, const AppendRun *runs, const size_t *list_off,
+                        const float **x_last, const float **delta_last, float **x_alt_last, hipStream_t st)
 {
     const be42_decoder_config &c = d->c;
     const int dim = c.dim, hd = c.head_dim, H = c.n_heads, KV = c.n_kv_heads;
@@ -977,8 +984,8 @@ static int prefill_pass(be42_decoder *d, int seq, int T, int p0, const float **x
         float *xo = delta ? xalt : nullptr;
         launch_rows(fp8, dim, [&](auto f8, auto nv) {
             hipLaunchKernelGGL((k_rmsnorm<decltype(f8)::value, decltype(nv)::value>),
-                               dim3((dim + kChunk - 1) / kChunk, T), dim3(kRowT), 0, st, nullptr, dig, xcur, xo,
-                               delta, wn, dim, T, c.norm_eps);
+                               dim3(1, T), dim3(kRowT), 0, st, nullptr, dig, xcur, xo, delta, wn, dim, T,
+                               c.norm_eps, true);
         });
         if (delta)
             std::swap(xcur, xalt);
@@ -989,30 +996,25 @@ static int prefill_pass(be42_decoder *d, int seq, int T, int p0, const float **x
     const float *pending = nullptr;
     for (int l = 0; l < c.n_layers; l++) {
         const be42_decoder_layer &L = d->w.layers[l];
-        const int slot = l * c.max_batch + seq;
         BE42_HIP(norm(L.attn_norm, pending));
-        DEC_TRY(pgemm(d, d->pq, L.wq, L.sq, qd, dim, T, st));
-        DEC_TRY(pgemm(d, d->pk, L.wk, L.sk, kd, dim, T, st));
-        DEC_TRY(pgemm(d, d->pv, L.wv, L.sv, kd, dim, T, st));
+        DEC_TRY(pgemm_multi(d, {{L.wq, L.sq, d->pq, qd}, {L.wk, L.sk, d->pk, kd}, {L.wv, L.sv, d->pv, kd}}, dim, T,
+                            st));
         hipLaunchKernelGGL(k_rope_rows, dim3(T, KV), dim3(256), 0, st, d->pq, d->pk, d->cos_t, d->sin_t, p0,
                            rope_len, H, KV, hd);
         BE42_LAUNCH_CHECK();
-        // the pass's K/V rows, in appends of at most 64 tokens (one launch
-        // each, plus one for the pages they fill)
-        for (int t = 0; t < T; t += 64)
-            DEC_TRY(be42_kv_append(d->pool, slot, d->pk + (size_t)t * kd, d->pv + (size_t)t * kd, p0 + t,
-                                   std::min(64, T - t), st));
+        // the pass's K/V rows and the pages they fill: one launch each
+        DEC_TRY(launch_append_run(*d->pool, runs[l], d->pmeta + list_off[l], d->pk, d->pv, st));
         DEC_TRY(lsh_attention_prefix(*d->pool, d->pq, d->pmeta + (size_t)(2 + l) * T, lim, T, H, c.sparse_k,
                                      c.cand_cap, scale, d->patt, st));
         DEC_TRY(xdig_prepare(d->pdig, d->patt, qd, T, fp8 != 0, st));
         DEC_TRY(pgemm(d, d->pxb, L.wo, L.so, dim, qd, T, st));
         BE42_HIP(norm(L.ffn_norm, d->pxb));                 // x += attention output
-        DEC_TRY(pgemm(d, d->phb, L.w1, L.s1, c.hidden_dim, dim, T, st));
-        DEC_TRY(pgemm(d, d->phb2, L.w3, L.s3, c.hidden_dim, dim, T, st));
+        DEC_TRY(pgemm_multi(d, {{L.w1, L.s1, d->phb, c.hidden_dim}, {L.w3, L.s3, d->phb2, c.hidden_dim}}, dim, T,
+                            st));
         launch_rows(fp8, c.hidden_dim, [&](auto f8, auto nv) {
             hipLaunchKernelGGL((k_silu_mul<decltype(f8)::value, decltype(nv)::value>),
-                               dim3((c.hidden_dim + kChunk - 1) / kChunk, T), dim3(kRowT), 0, st, nullptr, dig,
-                               d->phb, d->phb2, c.hidden_dim, T);
+                               dim3(1, T), dim3(kRowT), 0, st, nullptr, dig, d->phb, d->phb2, c.hidden_dim, T,
+                               true);
         });
         BE42_LAUNCH_CHECK();
         DEC_TRY(pgemm(d, d->pxb, L.w2, L.s2, dim, c.hidden_dim, T, st));
@@ -1056,8 +1058,17 @@ extern "C" int be42_decoder_prefill(be42_decoder *d, int seq, const int *tokens,
         for (int l = 0; l < c.n_layers; l++)
             for (int t = 0; t < T; t++)
                 mh[(size_t)(2 + l) * T + t] = l * c.max_batch + seq;
-        BE42_HIP(hipMemcpyAsync(d->pmeta, mh, (2 + (size_t)c.n_layers) * T * sizeof(int), hipMemcpyHostToDevice, st));
-        DEC_TRY(prefill_pass(d, seq, T, p0, &x_last, &delta_last, &xo_last, st));
+        // every layer's pages for the pass, allocated before anything is queued
+        std::vector<AppendRun> runs(c.n_layers);
+        std::vector<size_t> off(c.n_layers);
+        size_t o = (2 + (size_t)c.n_layers) * T;
+        for (int l = 0; l < c.n_layers; l++) {
+            off[l] = o;
+            DEC_TRY(plan_append_run(d->pool, l * c.max_batch + seq, p0, T, mh + o, &runs[l]));
+            o += runs[l].list_len;
+        }
+        BE42_HIP(hipMemcpyAsync(d->pmeta, mh, o * sizeof(int), hipMemcpyHostToDevice, st));
+        DEC_TRY(prefill_pass(d, seq, T, p0, runs.data(), off.data(), &x_last, &delta_last, &xo_last, st));
     }
     // the last token: final residual + norm (one row, into the decode GEMV's
     // digit planes), lm_head, argmax into the sequence's feedback slot
@@ -1065,7 +1076,7 @@ extern "C" int be42_decoder_prefill(be42_decoder *d, int seq, const int *tokens,
     launch_rows(c.wkind, dim, [&](auto f8, auto nv) {
         hipLaunchKernelGGL((k_rmsnorm<decltype(f8)::value, decltype(nv)::value>), dim3((dim + kChunk - 1) / kChunk, 1),
                            dim3(kRowT), 0, st, nullptr, (uint8_t *)d->xdig, x_last, xo_last, delta_last,
-                           d->w.final_norm, dim, 1, c.norm_eps);
+                           d->w.final_norm, dim, 1, c.norm_eps, false);
     });
     BE42_LAUNCH_CHECK();
     float *lg = logits_out ? logits_out : d->logits + (size_t)seq * c.vocab;

@@ -31,6 +31,7 @@
 // A and B fragments use the same k assignment, so every product pairs equal
 // k.  The accumulator of a 16x16 tile holds, in lane l, rows 4*(l/16)+j
 // (j = 0..3) of column l%16.
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -642,6 +643,216 @@ static void launch_gemm_dig(float *Y, const uint8_t *dig, const float *sx, const
                        M, N, K, (int)xdig_kp(K, FP8), tm);
 }
 
+// The digit-plane GEMM on the direct-to-LDS stages and 32x32 matrix-core
+// steps of k_gemm_dma (K a multiple of 128).  A workgroup of WGM x WGN waves
+// owns BT = 32 WGM tokens x BN = 32 TN WGN features; wave (wm, wn) holds,
+// for its 32 tokens, one 32x32 accumulator per digit plane and feature tile.
+// A stage's LDS rows: digit d of token row t at d * BT + t, then the BN
+// weight rows, 128 bytes each with chunks placed by dma_slot.  The epilogue
+// is k_gemm_dig's: digits combined in registers, one fp64 scaling.
+// Up to three weight matrices that share the activations (q/k/v, gate/up):
+// feature tiles are numbered through the segments one after another
+// (segment s owns tiles [tn_end[s-1], tn_end[s])), so one launch covers them.
+constexpr int kDigSegs = 3;
+struct DigSegs {
+    const uint8_t *w[kDigSegs];
+    const float *sw[kDigSegs];
+    float *y[kDigSegs];
+    int n[kDigSegs], tn_end[kDigSegs];
+    int nseg;
+};
+
+template <bool FP8, int WGM, int WGN, int TN, int NS>
+__global__ __launch_bounds__(WGM *WGN * 64) void k_gemm_dig_dma(const DigSegs S, const uint8_t *__restrict__ dig,
+                                                                const float *__restrict__ sx, int M, int K, int Kp,
+                                                                int tiles_m, int tiles)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr int NW = WGM * WGN;
+    constexpr int BT = 32 * WGM, BN = 32 * TN * WGN, XR = ND * BT, R = XR + BN;
+    constexpr int SBYTES = R * 128;
+    constexpr int DPW = R / 8 / NW;
+    static_assert(R % (8 * NW) == 0, "stage loads must divide over the waves");
+    static_assert(XR % 8 == 0, "a load instruction stays within the digit rows or the weight rows");
+    using AccT = typename std::conditional<FP8, v16f, v16i>::type;
+    extern __shared__ __align__(1024) uint8_t lds_dyn[];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int per = nb / 8, rem = nb % 8, x = b % 8, i8 = b / 8;
+    const int tile = (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + i8;
+    if (tile >= tiles)
+        return;
+    // token tiles innermost: the workgroups of one XCD share a weight slab
+    const int bm = tile % tiles_m, bng = tile / tiles_m;
+    const int sg = (S.nseg > 1 && bng >= S.tn_end[0]) + (S.nseg > 2 && bng >= S.tn_end[1]);
+    const int bn = bng - (sg == 0 ? 0 : S.tn_end[sg - 1]);
+    const uint8_t *__restrict__ W = S.w[sg];
+    const float *__restrict__ sw = S.sw[sg];
+    float *__restrict__ Y = S.y[sg];
+    const int N = S.n[sg];
+    const int m0 = bm * BT, n0 = bn * BN;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    // byte offset of this lane's 16-byte chunk (digit planes or weights)
+    uint32_t src[DPW];
+#pragma unroll
+    for (int j = 0; j < DPW; j++) {
+        const int row = (wave * DPW + j) * 8 + (lane >> 3);
+        const uint32_t off = dma_slot(row, lane & 7) * 16;
+        if (row < XR) {
+            const int d = row / BT, t = min(m0 + row % BT, M - 1);
+            src[j] = ((uint32_t)d * (uint32_t)M + (uint32_t)t) * (uint32_t)Kp + off;
+        } else {
+            src[j] = (uint32_t)min(n0 + row - XR, N - 1) * (uint32_t)K + off;
+        }
+    }
+    auto issue = [&](int st) {
+        uint8_t *base = lds_dyn + (st % NS) * SBYTES + wave * DPW * 1024;
+#pragma unroll
+        for (int j = 0; j < DPW; j++) {
+            const uint8_t *g = (wave * DPW + j) * 8 < XR ? dig : W;
+            __builtin_amdgcn_global_load_lds((const void *)(g + src[j] + (size_t)st * 128),
+                                             (lds_void *)(base + j * 1024), 16, 0, 0);
+        }
+        asm volatile("" ::: "memory");
+    };
+
+    AccT acc[ND][TN];
+#pragma unroll
+    for (int i = 0; i < ND; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            acc[i][j] = AccT{};
+
+    const int r = lane & 31, h = lane >> 5;
+    const int arow = (wm * 32 + r) * 128, brow = (XR + wn * TN * 32 + r) * 128;
+    struct Frags {
+        v8i a[ND], b[TN];
+    };
+    const int c0 = FP8 ? 2 * h : h, c1 = FP8 ? 2 * h + 1 : 2 + h;
+    auto load = [&](int buf, int u, Frags &f) {
+        const uint8_t *L = lds_dyn + buf * SBYTES;
+        auto rd = [&](int rowoff, int c) -> v4i { return *(const v4i *)(L + rowoff + dma_slot(r, c) * 16); };
+#pragma unroll
+        for (int i = 0; i < ND + TN; i++) {
+            const int ro = i < ND ? arow + i * BT * 128 : brow + (i - ND) * 32 * 128;
+            const v4i lo = rd(ro, 4 * u + c0), hi = rd(ro, 4 * u + c1);
+            const v8i v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if (i < ND)
+                f.a[i] = v;
+            else
+                f.b[i - ND] = v;
+        }
+    };
+    auto mfma = [&](const Frags &f) {
+#pragma unroll
+        for (int i = 0; i < ND; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                if constexpr (FP8) {
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0, 0,
+                                                                                127, 0, 127);
+                } else {
+                    const v4i alo = {f.a[i][0], f.a[i][1], f.a[i][2], f.a[i][3]};
+                    const v4i ahi = {f.a[i][4], f.a[i][5], f.a[i][6], f.a[i][7]};
+                    const v4i blo = {f.b[j][0], f.b[j][1], f.b[j][2], f.b[j][3]};
+                    const v4i bhi = {f.b[j][4], f.b[j][5], f.b[j][6], f.b[j][7]};
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(alo, blo, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ahi, bhi, acc[i][j], 0, 0, 0);
+                }
+            }
+    };
+    auto interleave = [&]() {
+        if constexpr (FP8)
+            sched_interleave<ND * TN, (ND + TN) * 2>();
+    };
+
+    const int nk = K / 128;
+#pragma unroll
+    for (int st = 0; st < NS; st++)
+        if (st < nk)
+            issue(st);
+    if (nk >= NS)
+        wait_vmcnt<(NS - 1) * DPW>();
+    else
+        wait_vmcnt<0>();
+    __syncthreads();
+    Frags F[2];
+    load(0, 0, F[0]);
+    for (int st = 0; st < nk; st++) {
+        const int buf = st % NS, nbuf = (st + 1) % NS;
+        __builtin_amdgcn_sched_barrier(0);
+        load(buf, 1, F[1]);
+        mfma(F[0]);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + 1 < nk) {
+            if (st + NS - 1 < nk)
+                wait_vmcnt<(NS - 2) * DPW>();
+            else
+                wait_vmcnt<0>();
+            __syncthreads();
+            if (st + NS < nk)
+                issue(st + NS);
+        }
+        load(nbuf, 0, F[0]);
+        mfma(F[1]);
+        interleave();
+    }
+
+    // lane l holds tokens 8*(e/4) + 4*(l/32) + e%4 of feature column l%32
+    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = n0 + wn * (TN * 32) + j * 32 + r;
+        if (n >= N)
+            continue;
+        const double swn = (double)sw[n];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int m = m0 + wm * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (m >= M)
+                continue;
+            double tot;
+            if constexpr (FP8) {
+                tot = 0.0;
+#pragma unroll
+                for (int d = 0; d < ND; d++)
+                    tot += (double)acc[d][j][e] * kF8DigitW[d];
+            } else {
+                const long long it = (long long)acc[0][j][e] * ((long long)kI8Base * kI8Base) +
+                                     (long long)acc[1][j][e] * kI8Base + (long long)acc[2][j][e];
+                tot = (double)it;
+            }
+            Y[(size_t)m * N + n] = (float)(tot * ((double)sx[m] * sxw * swn));
+        }
+    }
+}
+
+template <bool FP8, int WGM, int WGN, int TN, int NS>
+static void launch_gemm_dig_dma(DigSegs S, const uint8_t *dig, const float *sx, int M, int K, hipStream_t s)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr int BT = 32 * WGM, BN = 32 * TN * WGN;
+    constexpr size_t lds = (size_t)NS * (ND * BT + BN) * 128;
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    const int tm = (M + BT - 1) / BT;
+    int tn = 0;
+    for (int i = 0; i < S.nseg; i++) {
+        tn += (S.n[i] + BN - 1) / BN;
+        S.tn_end[i] = tn;
+    }
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void *)k_gemm_dig_dma<FP8, WGM, WGN, TN, NS>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_gemm_dig_dma<FP8, WGM, WGN, TN, NS>), dim3(tm * tn), dim3(WGM * WGN * 64), lds, s, S, dig,
+                       sx, M, K, (int)xdig_kp(K, FP8), tm, tm * tn);
+}
+
 }  // namespace be42
 
 using namespace be42;
@@ -694,24 +905,74 @@ extern "C" int be42_gemm_prepare(void *xdig, const float *x, int k, int m, int f
     return xdig_prepare(xdig, x, k, m, fp8 != 0, as_stream(stream));
 }
 
+static int gemm_dig_run(bool fp8, const be42_gemv_seg *segs, int nseg, const void *xdig, int k, int m,
+                        void *stream, const char *name)
+{
+    BE42_CHECK(segs && xdig && nseg >= 1 && nseg <= kDigSegs, "%s: null pointer or %d segments (1..%d)", name, nseg,
+               kDigSegs);
+    BE42_CHECK(k > 0 && k % 16 == 0 && m > 0 && m <= 65535, "%s: bad shape k=%d m=%d (k %% 16 == 0, m <= 65535)",
+               name, k, m);
+    BE42_CHECK(fp8 || k < 133144, "%s: k=%d would overflow the int32 accumulator", name, k);
+    DigSegs S{};
+    S.nseg = nseg;
+    size_t nmax = 0;
+    for (int i = 0; i < nseg; i++) {
+        BE42_CHECK(segs[i].w && segs[i].w_scale && segs[i].y && segs[i].n > 0, "%s: segment %d: null pointer or n %d",
+                   name, i, segs[i].n);
+        BE42_CHECK(((uintptr_t)segs[i].w & 15) == 0, "%s: weights must be 16-byte aligned", name);
+        S.w[i] = (const uint8_t *)segs[i].w;
+        S.sw[i] = segs[i].w_scale;
+        S.y[i] = segs[i].y;
+        S.n[i] = segs[i].n;
+        nmax = std::max(nmax, (size_t)segs[i].n);
+    }
+    const uint8_t *dig = (const uint8_t *)xdig;
+    const float *sx = xdig_scales((void *)xdig, k, m, fp8);
+    hipStream_t s = as_stream(stream);
+    // K a multiple of 128 and 32-bit offsets: the direct-to-LDS kernel, all
+    // segments in one launch; else the register-staged one per segment
+    const int nd = xdig_layout(fp8).nd;
+    const bool dma = k % 128 == 0 && (size_t)nd * m * xdig_kp(k, fp8) < (1ull << 32) && nmax * k < (1ull << 32);
+    const char *e = getenv("BE42_GEMM_DIG");
+    const int force = e ? atoi(e) : 0;
+    if (dma && force != 1) {
+        if (fp8) {
+            if (force == 3)
+                launch_gemm_dig_dma<true, 2, 2, 2, 2>(S, dig, sx, m, k, s);
+            else
+                launch_gemm_dig_dma<true, 2, 4, 1, 2>(S, dig, sx, m, k, s);
+        } else {
+            if (force == 3)
+                launch_gemm_dig_dma<false, 2, 2, 2, 3>(S, dig, sx, m, k, s);
+            else
+                launch_gemm_dig_dma<false, 2, 4, 2, 2>(S, dig, sx, m, k, s);
+        }
+    } else {
+        for (int i = 0; i < nseg; i++) {
+            if (fp8)
+                launch_gemm_dig<true, 4, 2, 4>(S.y[i], dig, sx, S.w[i], S.sw[i], m, S.n[i], k, s);
+            else
+                launch_gemm_dig<false, 4, 2, 4>(S.y[i], dig, sx, S.w[i], S.sw[i], m, S.n[i], k, s);
+        }
+    }
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
 static int gemm_dig_entry(bool fp8, float *y, const void *w, const float *sw, const void *xdig, int n, int k, int m,
                           void *stream)
 {
     const char *name = fp8 ? "be42_gemm_fp8_prepared" : "be42_gemm_q8_prepared";
     BE42_CHECK(y && w && sw && xdig, "%s: null pointer", name);
-    BE42_CHECK(n > 0 && k > 0 && k % 16 == 0 && m > 0 && m <= 65535,
-               "%s: bad shape n=%d k=%d m=%d (k %% 16 == 0, m <= 65535)", name, n, k, m);
-    BE42_CHECK(((uintptr_t)w & 15) == 0, "%s: weights must be 16-byte aligned", name);
-    BE42_CHECK(fp8 || k < 133144, "%s: k=%d would overflow the int32 accumulator", name, k);
-    const uint8_t *dig = (const uint8_t *)xdig;
-    const float *sx = xdig_scales((void *)xdig, k, m, fp8);
-    hipStream_t s = as_stream(stream);
-    if (fp8)
-        launch_gemm_dig<true, 4, 2, 4>(y, dig, sx, (const uint8_t *)w, sw, m, n, k, s);
-    else
-        launch_gemm_dig<false, 4, 2, 4>(y, dig, sx, (const uint8_t *)w, sw, m, n, k, s);
-    BE42_LAUNCH_CHECK();
-    return BE42_OK;
+    BE42_CHECK(n > 0, "%s: bad shape n=%d", name, n);
+    const be42_gemv_seg seg = {w, sw, y, n};
+    return gemm_dig_run(fp8, &seg, 1, xdig, k, m, stream, name);
+}
+
+extern "C" int be42_gemm_prepared_multi(const be42_gemv_seg *segs, int nseg, const void *xdig, int k, int m, int fp8,
+                                        void *stream)
+{
+    return gemm_dig_run(fp8 != 0, segs, nseg, xdig, k, m, stream, "be42_gemm_prepared_multi");
 }
 
 extern "C" int be42_gemm_q8_prepared(float *y, const int8_t *w, const float *w_scale, const void *xdig, int n, int k,

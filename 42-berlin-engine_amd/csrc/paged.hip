@@ -534,25 +534,31 @@ static int append_chunk(PoolImpl *p, int layer, const float *k, const float *v, 
     return BE42_OK;
 }
 
-// More than kArgTok tokens: the same bookkeeping for the whole run, its page
-// lists copied to the device, then one append launch and one seal launch.
-static int append_bulk(PoolImpl *p, int layer, const float *k, const float *v, int pos0, int n, hipStream_t s)
+namespace be42 {
+
+// Host bookkeeping of a run of n consecutive positions of one layer slot
+// (paged.c:195-272 for each): pages allocated in logical order, and the page
+// lists of the run written to L: the physical page of each logical page the
+// run touches [n_pages], the new ones [n_new], then the pages it fills
+// (physical [n_seal], logical [n_seal]).  L holds 4 * (n / 16 + 2) ints.
+int plan_append_run(be42_kv_pool *pool, int layer, int pos0, int n, int *L, AppendRun *out)
 {
+    PoolImpl *p = impl(pool);
     be42_kv_pool &P = p->pub;
-    const int layer_base = layer * P.max_logical;
-    const int first_blk = pos0 / kPage, last_blk = (pos0 + n - 1) / kPage;
-    const int n_pages = last_blk - first_blk + 1;
-    const int new_first = p->logical_len[layer];
-    // the previous bulk append's lists (host and device) may still be in use
-    BE42_HIP(hipStreamSynchronize(s));
-    if (!p->d_lists) {
-        p->h_lists.assign((size_t)4 * P.max_logical + 4, 0);
-        BE42_HIP(hipMalloc((void **)&p->d_lists, p->h_lists.size() * sizeof(int)));
-    }
-    int *L = p->h_lists.data();
-    std::vector<int> fresh;
-    for (int blk = first_blk; blk <= last_blk; blk++) {
+    AppendRun &r = *out;
+    r.layer = layer;
+    r.layer_base = layer * P.max_logical;
+    r.pos0 = pos0;
+    r.n = n;
+    r.first_blk = pos0 / kPage;
+    const int last_blk = (pos0 + n - 1) / kPage;
+    r.n_pages = last_blk - r.first_blk + 1;
+    r.new_first = p->logical_len[layer];
+    int *fresh = L + r.n_pages;
+    r.n_new = 0;
+    for (int blk = r.first_blk; blk <= last_blk; blk++) {
         if (blk >= p->logical_len[layer]) {
+            // pages are appended in order: a gap would leave unmapped pages
             if (blk != p->logical_len[layer]) {
                 set_error("be42_kv_append: position %d skips page %d", blk * kPage, p->logical_len[layer]);
                 return BE42_EINVAL;
@@ -562,54 +568,85 @@ static int append_bulk(PoolImpl *p, int layer, const float *k, const float *v, i
                 set_error("be42_kv_append: page pool exhausted at pos %d", blk * kPage);
                 return BE42_ENOMEM;
             }
-            p->page_table[layer_base + blk] = phys;
+            p->page_table[r.layer_base + blk] = phys;
             p->logical_len[layer] = blk + 1;
-            fresh.push_back(phys);
+            fresh[r.n_new++] = phys;
         }
-        L[blk - first_blk] = p->page_table[layer_base + blk];
+        L[blk - r.first_blk] = p->page_table[r.layer_base + blk];
     }
-    const int n_new = (int)fresh.size();
-    std::copy(fresh.begin(), fresh.end(), L + n_pages);
-    int *seal = L + n_pages + n_new;
-    std::vector<int> seal_logical;
-    for (int blk = first_blk; blk <= last_blk; blk++) {
-        const int phys = p->page_table[layer_base + blk];
+    int *seal = L + r.n_pages + r.n_new;
+    int ns = 0;
+    for (int blk = r.first_blk; blk <= last_blk; blk++) {
+        const int phys = p->page_table[r.layer_base + blk];
         const int end = (blk + 1) * kPage - 1;          // the page's last position
         if (end >= pos0 && end < pos0 + n && !p->registered[phys]) {
             p->registered[phys] = 1;
-            seal[seal_logical.size()] = phys;
-            seal_logical.push_back(blk);
+            seal[ns++] = phys;
             if (blk + 1 > p->n_indexed[layer])
                 p->n_indexed[layer] = blk + 1;
         }
     }
-    const int n_seal = (int)seal_logical.size();
-    std::copy(seal_logical.begin(), seal_logical.end(), seal + n_seal);
-    const size_t used = (size_t)n_pages + n_new + 2 * n_seal;
-    BE42_HIP(hipMemcpyAsync(p->d_lists, L, used * sizeof(int), hipMemcpyHostToDevice, s));
-    const dim3 grid(n, P.n_kv);
+    // logical ids of the sealed pages, after the physical ones
+    int ls = 0;
+    for (int blk = r.first_blk; blk <= last_blk && ls < ns; blk++)
+        if (p->page_table[r.layer_base + blk] == seal[ls])
+            seal[ns + ls++] = blk;
+    r.n_seal = ns;
+    r.n_log = p->logical_len[layer];
+    r.n_idx = p->n_indexed[layer];
+    r.list_len = r.n_pages + r.n_new + 2 * ns;
+    return BE42_OK;
+}
+
+// The run's store and seal launches, with its lists at d_lists (device).
+int launch_append_run(const be42_kv_pool &P, const AppendRun &r, const int *d_lists, const float *k, const float *v,
+                      hipStream_t s)
+{
+    const dim3 grid(r.n, P.n_kv);
     if (P.kind == BE42_KV_BF16)
         hipLaunchKernelGGL(k_kv_append_bulk<true>, grid, dim3(64), 0, s, P.k, P.v, P.k_scale, P.v_scale, P.ntok,
-                           P.page_table, P.n_logical, p->d_lists, pos0, n, first_blk, n_pages, n_new, new_first,
-                           layer_base, layer, p->logical_len[layer], k, v, P.n_kv, P.head_dim);
+                           P.page_table, P.n_logical, d_lists, r.pos0, r.n, r.first_blk, r.n_pages, r.n_new,
+                           r.new_first, r.layer_base, r.layer, r.n_log, k, v, P.n_kv, P.head_dim);
     else
         hipLaunchKernelGGL(k_kv_append_bulk<false>, grid, dim3(64), 0, s, P.k, P.v, P.k_scale, P.v_scale, P.ntok,
-                           P.page_table, P.n_logical, p->d_lists, pos0, n, first_blk, n_pages, n_new, new_first,
-                           layer_base, layer, p->logical_len[layer], k, v, P.n_kv, P.head_dim);
+                           P.page_table, P.n_logical, d_lists, r.pos0, r.n, r.first_blk, r.n_pages, r.n_new,
+                           r.new_first, r.layer_base, r.layer, r.n_log, k, v, P.n_kv, P.head_dim);
     BE42_LAUNCH_CHECK();
-    if (n_seal) {
-        const int *sl = p->d_lists + n_pages + n_new;
+    if (r.n_seal) {
+        const int *sl = d_lists + r.n_pages + r.n_new;
         if (P.kind == BE42_KV_BF16)
-            hipLaunchKernelGGL(k_kv_seal_bulk<true>, dim3(n_seal), dim3(256), 0, s, P.k, P.k_scale, P.centroid,
-                               P.page_hash, P.n_indexed, sl, n_seal, layer_base, layer, p->n_indexed[layer], P.hpT,
-                               P.n_kv, P.head_dim);
+            hipLaunchKernelGGL(k_kv_seal_bulk<true>, dim3(r.n_seal), dim3(256), 0, s, P.k, P.k_scale, P.centroid,
+                               P.page_hash, P.n_indexed, sl, r.n_seal, r.layer_base, r.layer, r.n_idx, P.hpT, P.n_kv,
+                               P.head_dim);
         else
-            hipLaunchKernelGGL(k_kv_seal_bulk<false>, dim3(n_seal), dim3(256), 0, s, P.k, P.k_scale, P.centroid,
-                               P.page_hash, P.n_indexed, sl, n_seal, layer_base, layer, p->n_indexed[layer], P.hpT,
-                               P.n_kv, P.head_dim);
+            hipLaunchKernelGGL(k_kv_seal_bulk<false>, dim3(r.n_seal), dim3(256), 0, s, P.k, P.k_scale, P.centroid,
+                               P.page_hash, P.n_indexed, sl, r.n_seal, r.layer_base, r.layer, r.n_idx, P.hpT, P.n_kv,
+                               P.head_dim);
         BE42_LAUNCH_CHECK();
     }
     return BE42_OK;
+}
+
+}  // namespace be42
+
+// More than kArgTok tokens: the bookkeeping of the whole run, its page lists
+// copied to the device, then one append launch and one seal launch.
+static int append_bulk(PoolImpl *p, int layer, const float *k, const float *v, int pos0, int n, hipStream_t s)
+{
+    be42_kv_pool &P = p->pub;
+    // the previous bulk append's lists (host and device) may still be in use
+    BE42_HIP(hipStreamSynchronize(s));
+    if (!p->d_lists) {
+        p->h_lists.assign((size_t)4 * P.max_logical + 8, 0);
+        BE42_HIP(hipMalloc((void **)&p->d_lists, p->h_lists.size() * sizeof(int)));
+    }
+    AppendRun r;
+    const int rc = plan_append_run(&p->pub, layer, pos0, n, p->h_lists.data(), &r);
+    if (rc)
+        return rc;
+    BE42_HIP(hipMemcpyAsync(p->d_lists, p->h_lists.data(), (size_t)r.list_len * sizeof(int), hipMemcpyHostToDevice,
+                            s));
+    return launch_append_run(P, r, p->d_lists, k, v, s);
 }
 
 extern "C" int be42_kv_append(be42_kv_pool *pool, int layer, const float *k, const float *v, int pos0,

@@ -47,6 +47,20 @@ int launch_rope_append_step_dev(const be42_kv_pool &P, const AppendStepArgs *a_d
                                 const float *v, const float *cos_t, const float *sin_t, const int *pos_p,
                                 int rope_len, int n_heads, hipStream_t st);
 
+// A run of n consecutive positions of one layer slot, appended with one
+// store launch and one seal launch from page lists in device memory.
+struct AppendRun {
+    int layer, layer_base, pos0, n, first_blk, n_pages, n_new, new_first, n_seal, n_log, n_idx, list_len;
+};
+// ints of page lists a run of n positions needs
+inline int append_run_list_cap(int n) { return 4 * (n / 16 + 2); }
+// host: allocate the run's pages and write its lists to L (host memory of
+// append_run_list_cap(n) ints)
+int plan_append_run(be42_kv_pool *pool, int layer, int pos0, int n, int *L, AppendRun *out);
+// device: the run's store and seal, its lists (as planned) at d_lists
+int launch_append_run(const be42_kv_pool &P, const AppendRun &r, const int *d_lists, const float *k, const float *v,
+                      hipStream_t s);
+
 // device: paged attention of n_queries queries of the slots slots[b] (device
 // array), query b seeing only the first lim[b] positions of its slot (its
 // pages, LSH index and last page as they were when position lim[b] - 1 was

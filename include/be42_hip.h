@@ -132,6 +132,10 @@ int    be42_gemm_q8_prepared(float *y, const int8_t *w, const float *w_scale, co
                              int m, void *stream);
 int    be42_gemm_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, const void *xdig, int n, int k,
                               int m, void *stream);
+/* Up to three weight matrices that share the activations (q/k/v, gate/up) in
+ * one launch; y of each segment is [m][n]. */
+int    be42_gemm_prepared_multi(const be42_gemv_seg *segs, int nseg, const void *xdig, int k, int m, int fp8,
+                                void *stream);
 
 /* ---- paged KV cache in HBM ------------------------------------------------------
  * Mirrors t_block_manager / t_paged_kv_cache (src/memory/paged.h:53-99): pages

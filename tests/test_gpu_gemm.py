@@ -162,16 +162,20 @@ def _weights(rng, n, k, kind, be):
     return be.quant_rows_int8(wt) if kind == "int8" else be.quant_rows_fp8(wt)
 
 
+@pytest.mark.parametrize("variant", ["0", "1", "3"])
 @pytest.mark.parametrize("kind", ["int8", "fp8"])
 @pytest.mark.parametrize("m,n,k", [(1, 64, 512), (17, 1000, 1424), (64, 3072, 512), (200, 1408, 4096),
                                    (300, 96, 8192)])
-def test_gemm_f32_equals_gemv_rows(be, kind, m, n, k):
+def test_gemm_f32_equals_gemv_rows(be, kind, m, n, k, variant, monkeypatch):
     """Every row of the digit-plane GEMM against the decode GEMV of the same
     row (batches of up to 16 rows, and single rows): INT8 bit-identical
     (exact int32 digit sums, one fp64 scaling), FP8 to fp32 accumulation
     order; within the GEMV tests' bounds of the float64 product of the
     codes: 1e-5 (INT8: digits to 2^-24 of max|x|) and 1e-4 (FP8: the matrix
-    core's own fp32 reduction of each block of digit products)."""
+    core's own fp32 reduction of each block of digit products).  Kernels:
+    the direct-to-LDS one at its two tile shapes (BE42_GEMM_DIG 0, 3; K a
+    multiple of 128) and the register-staged one (1, any K)."""
+    monkeypatch.setenv("BE42_GEMM_DIG", variant)
     rng = np.random.default_rng(m * 7 + n + k)
     wq, sw = _weights(rng, n, k, kind, be)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -197,6 +201,21 @@ def test_gemm_f32_equals_gemv_rows(be, kind, m, n, k):
         assert rel_err(yh, rh) <= 1e-4
     exact = (x.astype(np.float64) @ wd.T) * sw.cpu().numpy().astype(np.float64)
     assert rel_err(yh, exact) <= (1e-5 if kind == "int8" else 1e-4)
+
+
+@pytest.mark.parametrize("variant", ["0", "1", "3"])
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+def test_gemm_f32_segments_equal_single(be, kind, variant, monkeypatch):
+    """q/k/v-shaped segments (3072, 1024, 1000 rows) in one launch equal
+    three single-matrix launches bit for bit."""
+    monkeypatch.setenv("BE42_GEMM_DIG", variant)
+    rng = np.random.default_rng(11)
+    k, m = 1024, 333
+    segs = [_weights(rng, n, k, kind, be) for n in (3072, 1024, 1000)]
+    xt = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).cuda()
+    outs = be.gemm_f32_multi(xt, segs, kind)
+    for (w, sw), y in zip(segs, outs):
+        assert torch.equal(y, be.gemm_f32(xt, w, sw, kind))
 
 
 def test_gemm_f32_rejects_bad_shapes(be):
