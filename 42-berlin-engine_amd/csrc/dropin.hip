@@ -729,16 +729,26 @@ int matmul_quant(t_tensor *out, const t_tensor *a, const t_tensor *b, int m, int
         out_done(out->data, y, (size_t)m * 4, st);
         return 0;
     }
-    // b [k][n] -> x [n][k]; y [n][m] in chunks of 16 tokens; out = y^T [m][n]
+    // b [k][n] -> x [n][k]; y [n][m]: up to 16 tokens as one GEMV, more as
+    // the prefill GEMM over the same digit planes (INT8: identical values);
+    // out = y^T [m][n]
     const float *bd = (const float *)in_dev(b->data, (size_t)k * n * 4, kS0);
     float *x = (float *)scratch(kS2, (size_t)n * k * 4);
     float *y = (float *)scratch(kS3, (size_t)n * m * 4);
     hipLaunchKernelGGL(k_transpose, dim3((n + 31) / 32, (k + 31) / 32), dim3(256), 0, nullptr, x, bd, k, n);
     hip_ok(hipGetLastError(), "op_matmul transpose");
-    for (int c0 = 0; c0 < n; c0 += kGemvBatch) {
-        const int bc = n - c0 < kGemvBatch ? n - c0 : kGemvBatch;
-        ok(fp8 ? be42_gemv_fp8(y + (size_t)c0 * m, (const uint8_t *)w, ws, x + (size_t)c0 * k, m, k, bc, nullptr)
-               : be42_gemv_q8(y + (size_t)c0 * m, (const int8_t *)w, ws, x + (size_t)c0 * k, m, k, bc, nullptr),
+    if (n <= kGemvBatch || k % 16 != 0 || n > 65535) {
+        for (int c0 = 0; c0 < n; c0 += kGemvBatch) {
+            const int bc = n - c0 < kGemvBatch ? n - c0 : kGemvBatch;
+            ok(fp8 ? be42_gemv_fp8(y + (size_t)c0 * m, (const uint8_t *)w, ws, x + (size_t)c0 * k, m, k, bc, nullptr)
+                   : be42_gemv_q8(y + (size_t)c0 * m, (const int8_t *)w, ws, x + (size_t)c0 * k, m, k, bc, nullptr),
+               "op_matmul");
+        }
+    } else {
+        void *dig = scratch(kS4, be42_gemm_xdig_bytes(k, n, fp8));
+        ok(be42_gemm_prepare(dig, x, k, n, fp8, nullptr), "op_matmul");
+        ok(fp8 ? be42_gemm_fp8_prepared(y, (const uint8_t *)w, ws, dig, m, k, n, nullptr)
+               : be42_gemm_q8_prepared(y, (const int8_t *)w, ws, dig, m, k, n, nullptr),
            "op_matmul");
     }
     bool st;

@@ -343,7 +343,61 @@ def gemm_bench(lib, steps, warmup):
             "ops_per_launch": 2 * best["m"] * best["n"] * best["k"], "launch_us": best["us"]}
     return {"roofline": roof, "workload": "configs[2]: M in {512,2048,8192} x (N,K) in {4096x4096, 14336x4096, 4096x14336, "
                         "128256x4096}, INT8xINT8 and FP8xFP8 per-token x per-row scaled",
-            "TOPS_aggregate": round(tot_ops / tot_s / 1e12, 1), "best": best, "by_shape": rows}
+            "TOPS_aggregate": round(tot_ops / tot_s / 1e12, 1), "best": best, "by_shape": rows,
+            "digit_gemm": digit_gemm_bench(lib, steps, warmup)}
+
+
+def digit_gemm_bench(lib, steps, warmup):
+    """The prefill's projections: fp32 activations (N(0,1)) as digit planes
+    against per-row INT8 / FP8 weights, at the 3B model's layer shapes for a
+    1024-token pass (q/k/v and gate/up as one multi-segment launch).  The
+    matrix cores run nd = 3 (INT8) or 5 (FP8) digit products per logical
+    multiply-add: 'TOPS' counts 2 M N K nd, 'logical_TOPS' 2 M N K."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(12)
+    m = 1024
+    d, F, kvd = B3["dim"], B3["hidden_dim"], B3["n_kv_heads"] * B3["head_dim"]
+    shapes = [("qkv", [d, kvd, kvd], d), ("o", [d], d), ("gate_up", [F, F], d), ("down", [d], F)]
+    rows = []
+    for kind in KINDS:
+        nd = 3 if kind == "int8" else 5
+        qf = lib.quant_rows_int8 if kind == "int8" else lib.quant_rows_fp8
+        for name, ns, k in shapes:
+            segs = [qf(torch.randn(n, k, generator=g, device="cuda") * 0.02) for n in ns]
+            x = torch.randn(m, k, generator=g, device="cuda")
+            for _ in range(warmup):
+                lib.gemm_f32_multi(x, segs, kind)
+            torch.cuda.synchronize()
+            # the digit split once, then the timed GEMM launches
+            fp8 = 0 if kind == "int8" else 1
+            buf = torch.empty(lib.lib.be42_gemm_xdig_bytes(k, m, fp8), dtype=torch.uint8, device="cuda")
+            lib._call("be42_gemm_prepare", lib.p(buf), lib.p(x), k, m, fp8, lib.stream())
+            import ctypes as C
+            import be42
+            outs = [torch.empty((m, w.shape[0]), device="cuda") for w, _ in segs]
+            arr = (be42.GemvSeg * len(segs))()
+            for i, ((w, sw), y) in enumerate(zip(segs, outs)):
+                arr[i] = be42.GemvSeg(lib.p(w), lib.p(sw), lib.p(y), w.shape[0])
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                lib._call("be42_gemm_prepared_multi", C.addressof(arr), len(segs), lib.p(buf), k, m, fp8,
+                          lib.stream())
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            n = sum(ns)
+            ops = 2.0 * m * n * k
+            rows.append({"kind": kind, "proj": name, "m": m, "n": n, "k": k, "us": round(ms * 1e3, 1),
+                         "TOPS": round(ops * nd / (ms * 1e-3) / 1e12, 1),
+                         "logical_TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+                         "frac_of_mfma_peak": round(ops * nd / (ms * 1e-3) / 1e12 / MFMA_PEAK_TOPS[kind], 4)})
+            del segs, x, buf, outs
+            torch.cuda.empty_cache()
+    return {"workload": "prefill projections of configs[4] for a 1024-token pass: fp32 activations as digit planes "
+                        "(INT8 3, FP8 5) x per-row INT8/FP8 weights, be42_gemm_prepared_multi",
+            "by_shape": rows}
 
 
 # ---- decode step (BASELINE.json configs[0] and configs[4]) -----------------------
@@ -410,25 +464,34 @@ def decode_tiny_bench(lib, n_gen=64, reps=3):
     _, hpT = lib.lsh_projection(TINY["head_dim"], 42)
     dec = be42.Decoder(lib, decoder_cfg(TINY, 256, 1, 0, be42.KV_INT8), w, hpT)
     prompt = np.random.default_rng(3).integers(0, TINY["vocab"], 128)
-    best = None
+    best = best_pf = None
     for _ in range(reps):
-        for pos in range(128):
-            dec.step([int(prompt[pos])], pos, sync=False)
+        for l in range(TINY["n_layers"]):
+            dec.pool.reset(l)
         torch.cuda.synchronize()
+        # the prompt in one batched prefill call, then the greedy steps fed
+        # from the device argmax the prefill left
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        p0.record()
+        dec.prefill(prompt)
+        p1.record()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for pos in range(128, 128 + n_gen):
             dec.step(None, pos, sync=False, batch=1)
         e1.record()
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1)
+        ms, pf = e0.elapsed_time(e1), p0.elapsed_time(p1)
         best = ms if best is None else min(best, ms)
+        best_pf = pf if best_pf is None else min(best_pf, pf)
     dec.close()
     wb = weight_bytes(TINY)
     return {"workload": "configs[0]: tiny Llama (4 layers, d 512, 8/8 heads, FFN 1408, vocab 4096), INT8 row-scaled "
-                        "weights, 128-token prompt, 64 greedy tokens, dense paged INT8 attention, batch 1",
+                        "weights, 128-token prompt (one be42_decoder_prefill call), 64 greedy tokens, dense paged "
+                        "INT8 attention, batch 1",
             "tokens_per_s": round(n_gen / (best * 1e-3), 1), "ms_per_token": round(best / n_gen, 4),
-            "weight_bytes_per_token": wb, "weight_GBps": round(wb * n_gen / (best * 1e-3) / 1e9, 1)}
+            "weight_bytes_per_token": wb, "weight_GBps": round(wb * n_gen / (best * 1e-3) / 1e9, 1),
+            "prefill_ms": round(best_pf, 3), "prefill_tokens_per_s": round(128 / (best_pf * 1e-3), 1)}
 
 
 def decode_3b_bench(lib, batches=(1, 8), steps=10):
@@ -504,11 +567,33 @@ def decode_3b_bench(lib, batches=(1, 8), steps=10):
                      "step_bytes": wb + kv_bytes, "GBps": round((wb + kv_bytes) / (ms * 1e-3) / 1e9, 1),
                      "frac_of_hbm_peak": round((wb + kv_bytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
     dec.capture(None, None)
+    # batched prefill of a fresh 4096-token prompt into sequence 0 (its
+    # slots reset first): 4 passes of 1024 tokens, dense attention up to 64
+    # pages and LSH-routed after
+    n_pf = 4096
+    prompt = np.random.default_rng(6).integers(0, A["vocab"], n_pf)
+    pf_ms = []
+    for _ in range(3):
+        for l in range(L):
+            dec.pool.reset(l * BM)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dec.prefill(prompt)
+        e1.record()
+        torch.cuda.synchronize()
+        pf_ms.append(e0.elapsed_time(e1))
     dec.close()
+    pf = min(pf_ms)
     return {"workload": "configs[4]: 3B-class Llama (28 layers, d 3072, 24/8 heads, hd 128, FFN 8192, vocab "
                         "128256), FP8 E4M3 per-row weights, 32k-token bf16 paged KV prefix per sequence with "
                         "configs[3] planting, LSH sparse attention top-K 64 pages / candidate cap 64",
-            "by_batch": rows}
+            "by_batch": rows,
+            "prefill": {"tokens": n_pf, "ms": round(pf, 2), "tokens_per_s": round(n_pf / (pf * 1e-3), 1),
+                        "us_per_token": round(pf * 1e3 / n_pf, 2),
+                        "note": "be42_decoder_prefill: digit-plane MFMA GEMMs over 1024-token passes, each "
+                                "token attending to the cache as of its position (bit-identical to token-by-"
+                                "token decode for INT8 weights)"}}
 
 
 def decode_cpu_baseline(seconds=10.0):

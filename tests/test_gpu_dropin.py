@@ -61,7 +61,8 @@ def test_op_matmul_errors(dl, capfd):
 
 
 @pytest.mark.parametrize("kind", ["int8", "fp8"])
-@pytest.mark.parametrize("m,k,n", [(64, 512, 1), (300, 1024, 1), (96, 256, 5), (40, 512, 37)])
+@pytest.mark.parametrize("m,k,n", [(64, 512, 1), (300, 1024, 1), (96, 256, 5), (40, 512, 37), (300, 1024, 200),
+                                   (64, 1424, 70)])
 def test_op_matmul_quantized(dl, orc, kind, m, k, n):
     rng = np.random.default_rng(m + k + n)
     w = (rng.standard_normal((m, k)) * 0.02).astype(np.float32)
