@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "be42_common.h"
+#include "paged_dev.h"
 #include "paged_step.h"
 #include "xdigits.h"
 
@@ -362,6 +363,549 @@ __global__ __launch_bounds__(256) void k_rope_rows(float *__restrict__ q, float 
     }
 }
 
+// ---- the fused layer of a one-sequence decode step ------------------------------
+// At batch 1 every operation of a layer but the attention is a few
+// microseconds of dependent memory round trips on a few CUs, and a launch of
+// its own costs about as much again.  One launch per layer runs, after the
+// layer's attention: the o projection, the residual add and RMSNorm, gate/up
+// with SiLU*up, the down projection, then the next layer's residual add,
+// RMSNorm, q/k/v and its RoPE + K/V append + seal -- with a grid barrier
+// between dependent phases.  Every block is resident (one per CU), keeps its
+// own copy of the phase's activation digit planes in LDS (it computes them
+// from the fp32 vector itself), and streams its row tiles of the phase's
+// weights straight from HBM into MFMA operand registers; the loads of the
+// next phase's weights are issued before waiting at the barrier, so the HBM
+// stream runs on across the phases.
+//
+// Coherence: the activations one block writes and another reads go through
+// device-scope (agent) atomic stores and loads, which act at the device's
+// coherence point, so the barrier needs no L2 write-back or invalidate: a
+// block waits for its own stores (vmcnt), publishes an arrival flag, block 0
+// gathers every flag and publishes a release flag.  Flags hold increasing
+// barrier numbers (a per-decoder launch counter times kFBars plus the
+// barrier index), so graph replays need no reset.  Every wait is bounded: a
+// barrier that does not complete within ~kFSpinMax polls sets an error flag
+// the host reports, and the launch runs on (its results are then invalid).
+//
+// Arithmetic: the row kernels' (RMSNorm sums of squares in the same thread
+// layout and tree, the same digit split and SiLU), and the GEMV's single
+// rounding of exact INT8 digit sums -- so with INT8 weights a fused step
+// equals the step of separate launches bit for bit; FP8 digit sums are fp32
+// matrix-core accumulations in another order.
+constexpr int kFT = 512;                  // threads per block
+constexpr int kFW = kFT / kWave;          // waves per block
+constexpr int kFMaxU = 12;                // MFMA steps (128 k-bytes) one wave holds in registers
+constexpr int kFMaxTiles = 8;             // 16-row tiles of one block in one phase
+constexpr int kFDigBytes = 84 * 1024;     // LDS digit planes; also keeps one block per CU
+constexpr int kFBars = 8;                 // barrier numbers per launch
+constexpr unsigned kFSpinMax = 1u << 16;  // polls (about 1 us each) before a wait gives up
+
+__device__ __forceinline__ float ld_dev(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Device-scope (sc1) direct-to-LDS loads of a vector other blocks wrote:
+// lane l of wave w moves floats 4 (64 w + l + 256 q) .. + 3 for q = 0, 1, ...
+// (threads < kRowT, n floats, n a multiple of 4) into dst at the same float
+// index.  The caller waits (vmcnt) before reading dst.
+__device__ __forceinline__ void vec_to_lds(const float *src, float *dst, int n)
+{
+    const int tid = threadIdx.x, wave = tid >> 6;
+    if (tid >= kRowT)
+        return;
+    for (int q = 0; (wave * 64 + q * kRowT) * 4 < n; q++) {
+        const int i4 = tid + q * kRowT;
+        if (4 * i4 < n)
+            __builtin_amdgcn_global_load_lds((const void *)(src + 4 * i4),
+                                             (lds_void *)(dst + 4 * (wave * 64 + q * kRowT)), 16, 0, 16);
+    }
+}
+
+// One projection phase: up to three weight matrices over the same input
+// (q/k/v), or gate/up pairs (silu: tile pair p = gate tile p, up tile p, and
+// y[0] takes silu(gate) * up).  units: tiles, or pairs.
+struct FPhase {
+    const uint8_t *w[3];
+    const float *sw[3];
+    float *y[3];
+    int n[3], tend[3];
+    int nseg, K, steps, units, silu;
+};
+
+struct FusedArgs {
+    FPhase o, gu, down, qkv;      // qkv.nseg == 0: the last layer
+    const float *att;
+    float *X, *Hb, *XB, *H2, *q, *k, *v;
+    const uint16_t *ffn_norm, *attn_norm;   // this layer's FFN norm, the next layer's attention norm
+    be42_kv_pool P;
+    const AppendStepArgs *app;              // the next layer's append
+    const float *cos_t, *sin_t;
+    const int *pos_p;
+    int rope_len, dim, hidden, qd, kd, H, KV;
+    float eps;
+    unsigned *flags, *gen;
+    int *err;
+};
+
+struct GridBar {
+    unsigned *flags;
+    unsigned base;
+    int nb;
+    int *err;
+};
+
+__device__ __forceinline__ bool flag_before(unsigned v, unsigned target) { return (int)(v - target) < 0; }
+
+// Arrive, run `during` (loads of the next phase's weights), then wait for
+// every block.  After a timed-out wait (error flag set) later barriers do not
+// wait again; whether to wait is decided once per block.
+template <class F>
+__device__ __forceinline__ void grid_barrier(const GridBar &gb, unsigned idx, F &&during)
+{
+    __shared__ int failed;
+    const unsigned target = gb.base + idx;
+    wait_vmcnt<0>();              // this thread's stores have completed
+    if (threadIdx.x == 0)
+        failed = __hip_atomic_load(gb.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_store(gb.flags + blockIdx.x * 32, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    during();
+    asm volatile("" ::: "memory");
+    const bool skip = failed;
+    if (blockIdx.x == 0 && !skip) {
+        for (int i = threadIdx.x; i < gb.nb; i += blockDim.x) {
+            unsigned spins = 0;
+            while (flag_before(__hip_atomic_load(gb.flags + i * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                               target))
+                if (++spins > kFSpinMax) {
+                    atomicExch(gb.err, 1);
+                    break;
+                }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(gb.flags + gb.nb * 32, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x == 0 && !skip) {
+        unsigned spins = 0;
+        while (flag_before(__hip_atomic_load(gb.flags + gb.nb * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                           target))
+            if (++spins > kFSpinMax) {
+                atomicExch(gb.err, 2);
+                break;
+            }
+    }
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__device__ __forceinline__ int ph_count(const FPhase &ph, int b, int nb)
+{
+    const int c = ph.units > b ? (ph.units - 1 - b) / nb + 1 : 0;
+    return ph.silu ? 2 * c : c;
+}
+
+// tile slot j of block b -> (segment, tile within the segment)
+__device__ __forceinline__ void ph_slot(const FPhase &ph, int b, int nb, int j, int &seg, int &lt)
+{
+    if (ph.silu) {
+        seg = j & 1;
+        lt = b + (j >> 1) * nb;
+        return;
+    }
+    const int T = b + j * nb;
+    seg = (int)(ph.nseg > 1 && T >= ph.tend[0]) + (int)(ph.nseg > 2 && T >= ph.tend[1]);
+    lt = T - (seg == 0 ? 0 : (seg == 1 ? ph.tend[0] : ph.tend[1]));
+}
+
+template <class T>
+__device__ __forceinline__ T seg_sel(const T (&a)[3], int seg)
+{
+    return seg == 0 ? a[0] : (seg == 1 ? a[1] : a[2]);
+}
+
+// wave -> (tile slot, step range): the tiles rounded up to a power of two
+// share the 8 waves, each tile's waves splitting its K steps
+struct FWave {
+    int j, s0, s1, wpt;
+    bool on;
+};
+__device__ __forceinline__ FWave ph_wave(int nt, int steps, int wave)
+{
+    const int np = nt <= 1 ? 1 : (nt <= 2 ? 2 : (nt <= 4 ? 4 : 8));
+    FWave w;
+    w.wpt = kFW / np;
+    w.j = wave / w.wpt;
+    const int gw = wave % w.wpt;
+    w.on = w.j < nt;
+    w.s0 = gw * steps / w.wpt;
+    w.s1 = (gw + 1) * steps / w.wpt;
+    return w;
+}
+
+// this wave's weight fragments of the phase (waves lo .. hi-1 only): lane
+// (r, g) holds row r of its tile, k bytes 128 s + 16 g .. + 15 and
+// 128 s + 64 + 16 g .. + 15 of each of its steps s (so each load instruction
+// reads 64 contiguous bytes of each of 16 rows; the digit fragments use the
+// same k positions)
+__device__ __forceinline__ void ph_prefetch(const FPhase &ph, int b, int nb, v8i (&fr)[kFMaxU], int lo, int hi)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+    if (wave < lo || wave >= hi)
+        return;
+    const FWave fw = ph_wave(ph_count(ph, b, nb), ph.steps, wave);
+    if (!fw.on)
+        return;
+    int seg, lt;
+    ph_slot(ph, b, nb, fw.j, seg, lt);
+    const int row = min(lt * 16 + r, seg_sel(ph.n, seg) - 1);
+    const uint8_t *wr = seg_sel(ph.w, seg) + (size_t)row * ph.K + 16 * g;
+#pragma unroll
+    for (int u = 0; u < kFMaxU; u++) {
+        const int s = fw.s0 + u;
+        if (s < fw.s1) {
+            const v4i lo = *(const v4i *)(wr + (size_t)s * 128), hi = *(const v4i *)(wr + (size_t)s * 128 + 64);
+            fr[u] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+    }
+}
+
+// The phase's MFMAs against the digit planes in LDS (dig[d][Kp]), the
+// cross-wave sum of each tile's partials, and the outputs (device-scope
+// stores).  sx: the digit scale of the input.
+template <bool FP8>
+__device__ __forceinline__ void ph_compute(const FPhase &ph, int b, int nb, const v8i (&fr)[kFMaxU],
+                                           const uint8_t *dig, int Kp, float sx, long long (*part)[16], float *ybuf)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c = lane & 15, g = lane >> 4;
+    const int nt = ph_count(ph, b, nb);
+    const FWave fw = ph_wave(nt, ph.steps, wave);
+    using Acc = typename std::conditional<FP8, v4f, v4i>::type;
+    Acc acc = Acc{0, 0, 0, 0};
+    if (fw.on) {
+#pragma unroll
+        for (int u = 0; u < kFMaxU; u++) {
+            const int s = fw.s0 + u;
+            if (s < fw.s1) {
+                v8i bf = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                if (c < ND) {
+                    const uint8_t *dp = dig + (size_t)c * Kp + (size_t)s * 128 + 16 * g;
+                    const v4i lo = *(const v4i *)dp, hi = *(const v4i *)(dp + 64);
+                    bf = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+                if constexpr (FP8) {
+                    acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fr[u], bf, acc, 0, 0, 0, 127, 0, 127);
+                } else {
+                    const v4i alo = {fr[u][0], fr[u][1], fr[u][2], fr[u][3]}, ahi = {fr[u][4], fr[u][5], fr[u][6], fr[u][7]};
+                    const v4i blo = {bf[0], bf[1], bf[2], bf[3]}, bhi = {bf[4], bf[5], bf[6], bf[7]};
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, blo, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, bhi, acc, 0, 0, 0);
+                }
+            }
+        }
+    }
+    // lane l holds rows 4 (l / 16) + e of digit column l % 16: combine the
+    // digit columns of each row (exact int64 / fp64) into part[wave][row]
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        if constexpr (FP8) {
+            double t = 0.0;
+#pragma unroll
+            for (int d = 0; d < ND; d++)
+                t += (double)__shfl(acc[e], (lane & 48) + d, kWave) * kF8DigitW[d];
+            if (c == 0)
+                part[wave][4 * g + e] = __double_as_longlong(t);
+        } else {
+            long long t = 0;
+#pragma unroll
+            for (int d = 0; d < ND; d++)
+                t += (long long)__shfl(acc[e], (lane & 48) + d, kWave) *
+                     (d == 0 ? (long long)kI8Base * kI8Base : (d == 1 ? (long long)kI8Base : 1ll));
+            if (c == 0)
+                part[wave][4 * g + e] = t;
+        }
+    }
+    __syncthreads();
+    const double sxw = FP8 ? 1.0 : 1.0 / (double)(kI8Base * kI8Base);
+    const int i = threadIdx.x;
+    if (i < nt * 16) {
+        const int j = i >> 4, r = i & 15;
+        const int w0 = j * fw.wpt;   // the tile's waves (wpt is the same for every wave)
+        double tot;
+        if constexpr (FP8) {
+            tot = 0.0;
+            for (int w = 0; w < fw.wpt; w++)
+                tot += __longlong_as_double(part[w0 + w][r]);
+        } else {
+            long long it = 0;
+            for (int w = 0; w < fw.wpt; w++)
+                it += part[w0 + w][r];
+            tot = (double)it;
+        }
+        int seg, lt;
+        ph_slot(ph, b, nb, j, seg, lt);
+        const int row = lt * 16 + r, n = seg_sel(ph.n, seg);
+        const float y = row < n ? (float)(tot * ((double)sx * sxw * (double)seg_sel(ph.sw, seg)[row])) : 0.0f;
+        if (ph.silu)
+            ybuf[i] = y;
+        else if (row < n)
+            st_dev(seg_sel(ph.y, seg) + row, y);
+    }
+    if (ph.silu) {
+        __syncthreads();
+        if (i < (nt / 2) * 16) {
+            const int p = i >> 4, r = i & 15;
+            int seg, lt;
+            ph_slot(ph, b, nb, 2 * p, seg, lt);
+            const int row = lt * 16 + r;
+            if (row < ph.n[0])
+                st_dev(ph.y[0] + row, silu_mul1(ybuf[2 * p * 16 + r], ybuf[(2 * p + 1) * 16 + r],
+                                                row < (ph.n[0] & ~7)));
+        }
+    }
+}
+
+// block-wide max of non-negative values (every thread gets it)
+__device__ __forceinline__ float fblock_max(float v, float *red)
+{
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < kFW; w++)
+        m = fmaxf(m, red[w]);
+    return m;
+}
+
+// fp32 staging of a phase's input vector in LDS, after its digit planes
+__device__ __forceinline__ float *dig_stage(uint8_t *dig, int nd, int K)
+{
+    return (float *)(dig + (((size_t)nd * K + 15) & ~(size_t)15));
+}
+
+// digit planes of the staged vector (scale sc), by all threads
+template <bool FP8>
+__device__ __forceinline__ void stage_digits(const float *stage, int K, float sc, uint8_t *dig)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    for (int i4 = threadIdx.x; 4 * i4 < K; i4 += kFT) {
+        const float4 x4 = *(const float4 *)(stage + 4 * i4);
+        const float xe[4] = {x4.x, x4.y, x4.z, x4.w};
+        uint32_t word[ND];
+        digit_words<FP8>(xe, sc, word);
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+            *(uint32_t *)(dig + (size_t)d * K + 4 * i4) = word[d];
+    }
+    __syncthreads();
+}
+
+// Digit planes of a vector written by other blocks (K a multiple of 128,
+// at most kRowT * 4 * kFVecG).  Threads < kRowT stage it in LDS with
+// device-scope loads and wait for them, then `mid` runs (their weight loads
+// of the phase), then every thread takes part in the scale and the digits.
+constexpr int kFVecG = 8;
+template <bool FP8, class Mid>
+__device__ __forceinline__ float vec_digits(const float *x, int K, uint8_t *dig, float *red, Mid &&mid)
+{
+    const int tid = threadIdx.x;
+    float *stage = dig_stage(dig, FP8 ? kF8Digits : kI8Digits, K);
+    vec_to_lds(x, stage, K);
+    asm volatile("" ::: "memory");
+    __syncthreads();              // the vector's loads leave before any weight load of the block
+    if (tid < kRowT)
+        wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    mid();
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    float m = 0.0f;
+    for (int i4 = tid; 4 * i4 < K; i4 += kFT)
+        m = fmaxf(m, f4_absmax(*(const float4 *)(stage + 4 * i4)));
+    const float sc = digit_scale<FP8>(fblock_max(m, red));
+    stage_digits<FP8>(stage, K, sc, dig);
+    return sc;
+}
+
+// x + delta (both written by other blocks), RMSNorm with w, into digit
+// planes; block b writes its share of x + delta to x_out.  Threads < kRowT
+// hold the row exactly as k_rmsnorm's threads do (same sum of squares).
+template <bool FP8, int NV, class Mid>
+__device__ __forceinline__ float norm_digits(const float *x, const float *delta, const uint16_t *w, float *x_out,
+                                             int dim, float eps, uint8_t *dig, float *red, int b, int nb, Mid &&mid)
+{
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    const int tid = threadIdx.x, n4 = dim >> 2;
+    float4 v[NV], h[NV];
+    uint2 wv[NV];
+    float ss = 0.0f;
+    // x and delta staged in LDS (device-scope loads), then read in the
+    // thread layout of k_rmsnorm
+    float *sx_ = dig_stage(dig, ND, dim), *sd_ = sx_ + dim;
+    vec_to_lds(x, sx_, dim);
+    vec_to_lds(delta, sd_, dim);
+    asm volatile("" ::: "memory");
+    __syncthreads();              // the vector's loads leave before any weight load of the block
+    if (tid < kRowT)
+        wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    mid();
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    if (tid < kRowT) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int i = min(tid + kRowT * j, n4 - 1);
+            const float4 xv = *(const float4 *)(sx_ + 4 * i), dv = *(const float4 *)(sd_ + 4 * i);
+            v[j] = make_float4(xv.x + dv.x, xv.y + dv.y, xv.z + dv.z, xv.w + dv.w);
+            wv[j] = ((const uint2 *)w)[i];
+        }
+    }
+    if (tid < kRowT) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int i = tid + kRowT * j;
+            if (i < n4 && i % nb == b) {
+                float *o = x_out + 4 * i;
+                st_dev(o, v[j].x);
+                st_dev(o + 1, v[j].y);
+                st_dev(o + 2, v[j].z);
+                st_dev(o + 3, v[j].w);
+            }
+            if (i >= n4)
+                v[j] = f4_zero();
+            ss = __fmaf_rn(v[j].x, v[j].x, ss);
+            ss = __fmaf_rn(v[j].y, v[j].y, ss);
+            ss = __fmaf_rn(v[j].z, v[j].z, ss);
+            ss = __fmaf_rn(v[j].w, v[j].w, ss);
+        }
+    }
+    ss = wave_sum_dpp(ss);
+    __syncthreads();
+    if ((tid & 63) == 0)
+        red[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(tot, (float)dim) + eps));
+    float m = 0.0f;
+    if (tid < kRowT) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const uint2 wj = wv[j];
+            h[j] = make_float4((v[j].x * inv) * bf16_to_f32((uint16_t)(wj.x & 0xFFFF)),
+                               (v[j].y * inv) * bf16_to_f32((uint16_t)(wj.x >> 16)),
+                               (v[j].z * inv) * bf16_to_f32((uint16_t)(wj.y & 0xFFFF)),
+                               (v[j].w * inv) * bf16_to_f32((uint16_t)(wj.y >> 16)));
+            if (tid + kRowT * j >= n4)
+                h[j] = f4_zero();
+            m = fmaxf(m, f4_absmax(h[j]));
+        }
+    }
+    // h into the staging area (every read of x there happened before the
+    // sum-of-squares barriers)
+    if (tid < kRowT) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int i = tid + kRowT * j;
+            if (i < n4)
+                *(float4 *)(sx_ + 4 * i) = h[j];
+        }
+    }
+    const float sc = digit_scale<FP8>(fblock_max(m, red + 8));
+    stage_digits<FP8>(sx_, dim, sc, dig);
+    return sc;
+}
+
+template <bool FP8, bool BF16KV, int NV>
+__global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
+{
+    __shared__ __align__(16) uint8_t dig[kFDigBytes];
+    __shared__ long long part[kFW][16];
+    __shared__ float ybuf[kFMaxTiles * 16];
+    __shared__ float red[16];
+    const int b = blockIdx.x, nb = gridDim.x;
+    GridBar gb{A.flags, __hip_atomic_load(A.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kFBars, nb, A.err};
+    v8i fr[kFMaxU];
+#pragma unroll
+    for (int u = 0; u < kFMaxU; u++)
+        fr[u] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    // A phase's input vector is loaded first (waves 0-3), then every wave
+    // loads its weight fragments: vector loads queued behind the whole
+    // phase's weight stream would hold up its digit planes.  Waves 0-3 issue
+    // theirs once the vector has landed.
+    auto early = [&](const FPhase &ph) {};
+    auto late = [&](const FPhase &ph) {
+        const FPhase *pp = &ph;
+        return [pp, b, nb, &fr] { ph_prefetch(*pp, b, nb, fr, 0, kFW); };
+    };
+    // o projection of the attention output
+    early(A.o);
+    float sx = vec_digits<FP8>(A.att, A.qd, dig, red, late(A.o));
+    ph_compute<FP8>(A.o, b, nb, fr, dig, A.qd, sx, part, ybuf);
+    grid_barrier(gb, 1, [&] { early(A.gu); });
+    // h = x + o, RMSNorm, gate/up, SiLU * up
+    sx = norm_digits<FP8, NV>(A.X, A.XB, A.ffn_norm, A.Hb, A.dim, A.eps, dig, red, b, nb, late(A.gu));
+    ph_compute<FP8>(A.gu, b, nb, fr, dig, A.dim, sx, part, ybuf);
+    grid_barrier(gb, 2, [&] { early(A.down); });
+    // down projection
+    sx = vec_digits<FP8>(A.H2, A.hidden, dig, red, late(A.down));
+    ph_compute<FP8>(A.down, b, nb, fr, dig, A.hidden, sx, part, ybuf);
+    if (A.qkv.nseg == 0) {
+        // last layer: h and the down output stay for the final norm
+        if (b == 0 && threadIdx.x == 0)
+            __hip_atomic_store(A.gen, gb.base / kFBars + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    grid_barrier(gb, 3, [&] { early(A.qkv); });
+    // next layer: x = h + down, RMSNorm, q/k/v
+    sx = norm_digits<FP8, NV>(A.Hb, A.XB, A.attn_norm, A.X, A.dim, A.eps, dig, red, b, nb, late(A.qkv));
+    ph_compute<FP8>(A.qkv, b, nb, fr, dig, A.dim, sx, part, ybuf);
+    grid_barrier(gb, 4, [] {});
+    if (b == 0 && threadIdx.x == 0)
+        __hip_atomic_store(A.gen, gb.base / kFBars + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (b >= A.KV)
+        return;
+    // RoPE of the q heads of KV head b and of k head b, K/V append and seal
+    const int hd = A.P.head_dim, half = hd / 2, G = A.H / A.KV, tid = threadIdx.x;
+    float *qs = (float *)dig, *ks = qs + G * hd, *vs = ks + hd, *cs = vs + hd;
+    float *qrow = A.q + (size_t)b * G * hd, *krow = A.k + (size_t)b * hd;
+    for (int i = tid; i < G * hd; i += kFT)
+        qs[i] = ld_dev(qrow + i);
+    for (int i = tid; i < hd; i += kFT) {
+        ks[i] = ld_dev(krow + i);
+        vs[i] = ld_dev(A.v + (size_t)b * hd + i);
+    }
+    __syncthreads();
+    const int pos = *A.pos_p;
+    if (pos < A.rope_len) {
+        for (int i = tid; i < (G + 1) * half; i += kFT) {
+            const int j = i / half, pr = i % half;
+            float *base = j < G ? qs + j * hd : ks;
+            const float c = A.cos_t[(size_t)pos * half + pr], sn = A.sin_t[(size_t)pos * half + pr];
+            const float x0 = base[pr], x1 = base[pr + half];
+            base[pr] = __fmaf_rn(x0, c, -(x1 * sn));
+            base[pr + half] = __fmaf_rn(x0, sn, x1 * c);
+        }
+    }
+    __syncthreads();
+    // the rotated rows for the attention launch that follows (and captures)
+    for (int i = tid; i < G * hd; i += kFT)
+        qrow[i] = qs[i];
+    for (int i = tid; i < hd; i += kFT)
+        krow[i] = ks[i];
+    if (A.app->n > 0)
+        append_seal_tail<BF16KV>(A.P, *A.app, 0, b, ks, vs, cs);
+}
+
 // Tokens of one prefill pass (positions p0 .. p0 + T - 1 of one sequence).
 constexpr int kPrefillChunk = 1024;
 
@@ -397,7 +941,7 @@ struct be42_decoder {
     void *params_host[2] = {nullptr, nullptr}, *params_dev[2] = {nullptr, nullptr};
     hipEvent_t params_free[2] = {nullptr, nullptr};
     int parity = 0;
-    int *next_host = nullptr;     // pinned copy of the argmax
+    int *next_host = nullptr;     // pinned copy of the argmax [kMaxBatch], then the fused layer's error flag
     hipStream_t gstream = nullptr;
     hipEvent_t ev_in = nullptr, ev_out = nullptr;
     struct Key {
@@ -413,6 +957,11 @@ struct be42_decoder {
     } key[2];
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     bool use_graph = true;
+    // the fused layer of one-sequence steps: grid = the CU count; barrier
+    // flags [(nb + 1) * 32], launch counter, error flag (device, zeroed at create)
+    bool fused = false;
+    int fnb = 0;
+    unsigned *fflags = nullptr;
     // prefill activations [kPrefillChunk][...], digit planes, and the chunk's
     // metadata (tokens [T], visible lengths [T], slots [n_layers][T]) with
     // its pinned host copy; allocated by the first prefill
@@ -422,6 +971,37 @@ struct be42_decoder {
     int *pmeta = nullptr, *pmeta_host = nullptr;
     size_t pmeta_bytes = 0;
 };
+
+// Whether the fused layer kernel serves this shape at batch 1 (sets d->fnb).
+static bool fused_layer_fits(const be42_decoder_config &c, be42_decoder *d)
+{
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return false;
+    const int qd = c.n_heads * c.head_dim, kd = c.n_kv_heads * c.head_dim, nd = c.wkind ? kF8Digits : kI8Digits;
+    if (c.dim % 128 || c.hidden_dim % 128 || qd % 128 || kd % 16 || c.dim > 4096 ||
+        c.hidden_dim > kRowT * 4 * kFVecG || qd > kRowT * 4 * kFVecG ||
+        (size_t)(nd + 4) * std::max(c.hidden_dim, qd) + 16 > (size_t)kFDigBytes ||
+        (size_t)(nd + 8) * c.dim + 16 > (size_t)kFDigBytes ||
+        (size_t)(c.n_heads / c.n_kv_heads + 2) * c.head_dim * 4 + 1024 > (size_t)kFDigBytes || c.n_kv_heads > cus)
+        return false;
+    // every block's tiles (rounded up to a power of two) share its 8 waves,
+    // and a wave's K steps must fit its registers
+    auto ok = [&](int units, bool pairs, int K) {
+        const int cnt = (units + cus - 1) / cus * (pairs ? 2 : 1);
+        if (cnt > kFMaxTiles)
+            return false;
+        const int np = cnt <= 1 ? 1 : (cnt <= 2 ? 2 : (cnt <= 4 ? 4 : 8));
+        const int wpt = kFW / np, steps = K / 128;
+        return (steps + wpt - 1) / wpt <= kFMaxU;
+    };
+    if (!ok((c.dim + 15) / 16, false, qd) || !ok((c.hidden_dim + 15) / 16, true, c.dim) ||
+        !ok((c.dim + 15) / 16, false, c.hidden_dim) || !ok((qd + 2 * kd + 15) / 16 + 2, false, c.dim))
+        return false;
+    d->fnb = cus;
+    return true;
+}
 
 static int dec_fail(be42_decoder *d, int rc)
 {
@@ -517,7 +1097,7 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
             e = hipEventCreateWithFlags(&d->params_free[i], hipEventDisableTiming);
     }
     if (e == hipSuccess)
-        e = hipHostMalloc((void **)&d->next_host, kMaxBatch * sizeof(int), hipHostMallocDefault);
+        e = hipHostMalloc((void **)&d->next_host, (kMaxBatch + 1) * sizeof(int), hipHostMallocDefault);
     if (e == hipSuccess)
         e = hipStreamCreateWithFlags(&d->gstream, hipStreamNonBlocking);
     if (e == hipSuccess)
@@ -532,6 +1112,18 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
         const char *ng = getenv("BE42_DECODE_NO_GRAPH");
         d->use_graph = !(ng && ng[0] == '1');
     }
+    if (e == hipSuccess && fused_layer_fits(c, d)) {
+        const char *fz = getenv("BE42_DECODE_FUSED");
+        if (!(fz && fz[0] == '0')) {
+            const size_t fbytes = ((size_t)d->fnb + 1) * 128 + 256;
+            e = hipMalloc((void **)&d->fflags, fbytes);
+            if (e == hipSuccess)
+                e = hipMemset(d->fflags, 0, fbytes);
+            d->fused = e == hipSuccess;
+        }
+    }
+    if (e == hipSuccess)
+        d->next_host[kMaxBatch] = 0;
     if (e != hipSuccess) {
         be42_decoder_destroy(d);
         return hip_fail(e, "be42_decoder_create", __FILE__, __LINE__);
@@ -569,7 +1161,7 @@ extern "C" void be42_decoder_destroy(be42_decoder *d)
     if (d->pmeta_host)
         (void)hipHostFree(d->pmeta_host);
     void *ptrs[] = {d->cos_t, d->sin_t, d->x, d->xb, d->xn, d->q, d->k, d->v, d->att, d->hb, d->hb2, d->logits, d->sel,
-                    d->nsel, d->slots, d->next, d->cand, d->ncand, d->xdig, d->attn_ws, d->arg_parts, d->arg_cnt,
+                    d->nsel, d->slots, d->next, d->cand, d->ncand, d->xdig, d->attn_ws, d->arg_parts, d->arg_cnt, d->fflags,
                     d->px, d->pxn, d->pq, d->pk, d->pv, d->patt, d->pxb, d->phb, d->phb2, d->pdig, d->pmeta};
     for (void *p : ptrs)
         if (p)
@@ -625,6 +1217,104 @@ static void launch_rows(bool fp8, int n, F &&f)
         pick(Fa());
 }
 
+// The fused layer launch after layer l's attention (batch 1).
+static FPhase one_phase(const void *w, const float *sw, float *y, int n, int K)
+{
+    FPhase p{};
+    p.w[0] = (const uint8_t *)w;
+    p.sw[0] = sw;
+    p.y[0] = y;
+    p.n[0] = n;
+    p.nseg = 1;
+    p.K = K;
+    p.steps = K / 128;
+    p.units = (n + 15) / 16;
+    p.tend[0] = p.units;
+    return p;
+}
+
+static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app, const int *pos_p, int rope_len,
+                              hipStream_t st)
+{
+    const be42_decoder_config &c = d->c;
+    const be42_decoder_layer &L = d->w.layers[l];
+    const int dim = c.dim, hidden = c.hidden_dim, qd = c.n_heads * c.head_dim, kd = c.n_kv_heads * c.head_dim;
+    FusedArgs A{};
+    A.o = one_phase(L.wo, L.so, d->xb, dim, qd);
+    A.gu = one_phase(L.w1, L.s1, d->hb, hidden, dim);
+    A.gu.w[1] = (const uint8_t *)L.w3;
+    A.gu.sw[1] = L.s3;
+    A.gu.n[1] = hidden;
+    A.gu.nseg = 2;
+    A.gu.silu = 1;
+    A.down = one_phase(L.w2, L.s2, d->xb, dim, hidden);
+    if (l + 1 < c.n_layers) {
+        const be42_decoder_layer &N = d->w.layers[l + 1];
+        A.qkv = one_phase(N.wq, N.sq, d->q, qd, dim);
+        A.qkv.w[1] = (const uint8_t *)N.wk;
+        A.qkv.w[2] = (const uint8_t *)N.wv;
+        A.qkv.sw[1] = N.sk;
+        A.qkv.sw[2] = N.sv;
+        A.qkv.y[1] = d->k;
+        A.qkv.y[2] = d->v;
+        A.qkv.n[1] = A.qkv.n[2] = kd;
+        A.qkv.nseg = 3;
+        A.qkv.tend[0] = qd / 16;
+        A.qkv.tend[1] = qd / 16 + kd / 16;
+        A.qkv.tend[2] = qd / 16 + 2 * (kd / 16);
+        A.qkv.units = A.qkv.tend[2];
+        A.attn_norm = N.attn_norm;
+        A.app = app + l + 1;
+    } else {
+        A.qkv.nseg = 0;
+        A.app = app + l;
+    }
+    A.att = d->att;
+    A.X = d->x;
+    A.Hb = d->xn;
+    A.XB = d->xb;
+    A.H2 = d->hb;
+    A.q = d->q;
+    A.k = d->k;
+    A.v = d->v;
+    A.ffn_norm = L.ffn_norm;
+    A.P = *d->pool;
+    A.cos_t = d->cos_t;
+    A.sin_t = d->sin_t;
+    A.pos_p = pos_p;
+    A.rope_len = rope_len;
+    A.dim = dim;
+    A.hidden = hidden;
+    A.qd = qd;
+    A.kd = kd;
+    A.H = c.n_heads;
+    A.KV = c.n_kv_heads;
+    A.eps = c.norm_eps;
+    A.flags = d->fflags;
+    A.gen = d->fflags + ((size_t)d->fnb + 1) * 32;
+    A.err = (int *)(A.gen + 1);
+    const int nv = (dim + kChunk - 1) / kChunk;
+    const bool fp8 = c.wkind != 0, bf16 = c.kv_kind == BE42_KV_BF16;
+    auto go = [&](auto f8, auto kb, auto nvc) {
+        hipLaunchKernelGGL((k_fused_layer<decltype(f8)::value, decltype(kb)::value, decltype(nvc)::value>),
+                           dim3(d->fnb), dim3(kFT), 0, st, A);
+    };
+    auto pick_nv = [&](auto f8, auto kb) {
+        switch (nv) {
+        case 1: go(f8, kb, std::integral_constant<int, 1>()); break;
+        case 2: go(f8, kb, std::integral_constant<int, 2>()); break;
+        case 3: go(f8, kb, std::integral_constant<int, 3>()); break;
+        default: go(f8, kb, std::integral_constant<int, 4>()); break;
+        }
+    };
+    if (fp8)
+        bf16 ? pick_nv(std::true_type(), std::true_type()) : pick_nv(std::true_type(), std::false_type());
+    else
+        bf16 ? pick_nv(std::false_type(), std::true_type()) : pick_nv(std::false_type(), std::false_type());
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
 // The launches of one step.  Everything that changes from step to step (the
 // position, the tokens, the page bookkeeping of the appends) is read from
 // device memory at params_dev, so this sequence depends only on the key
@@ -672,13 +1362,19 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     const int dense_max = std::min(c.sparse_k, P.max_logical);
     const float *pending = nullptr;   // residual delta not yet added to x
     const bool fused_route = c.sparse_k <= 64 && c.cand_cap <= 256 && H / KV <= 4 && (hd == 64 || hd == 128);
+    // one sequence: everything of a layer after its attention (and the next
+    // layer's q/k/v and append) in one fused launch
+    const bool fz = d->fused && B == 1;
     for (int l = 0; l < c.n_layers; l++) {
         const be42_decoder_layer &L = d->w.layers[l];
-        BE42_HIP(norm(L.attn_norm, pending));
-        DEC_TRY(gemv_multi(d, {{L.wq, L.sq, d->q, qd}, {L.wk, L.sk, d->k, kd}, {L.wv, L.sv, d->v, kd}}, dim, B, st));
-        // RoPE of q and k, the K/V append and the seal of filled pages: one launch
-        DEC_TRY(launch_rope_append_step_dev(P, app + l, B, d->q, d->k, d->v, d->cos_t, d->sin_t, &head->pos, rope_len,
-                                            H, st));
+        if (!fz || l == 0) {
+            BE42_HIP(norm(L.attn_norm, pending));
+            DEC_TRY(gemv_multi(d, {{L.wq, L.sq, d->q, qd}, {L.wk, L.sk, d->k, kd}, {L.wv, L.sv, d->v, kd}}, dim, B,
+                               st));
+            // RoPE of q and k, the K/V append and the seal of filled pages: one launch
+            DEC_TRY(launch_rope_append_step_dev(P, app + l, B, d->q, d->k, d->v, d->cos_t, d->sin_t, &head->pos,
+                                                rope_len, H, st));
+        }
         if (d->capture_q)
             BE42_HIP(hipMemcpyAsync(d->capture_q + (size_t)l * c.max_batch * qd, d->q, (size_t)B * qd * 4,
                                     hipMemcpyDeviceToDevice, st));
@@ -714,6 +1410,10 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
             BE42_HIP(hipMemcpyAsync(d->capture_nsel + (size_t)l * c.max_batch, src, (size_t)B * 4,
                                     hipMemcpyDeviceToDevice, st));
         }
+        if (fz) {
+            DEC_TRY(launch_fused_layer(d, l, app, &head->pos, rope_len, st));
+            continue;
+        }
         DEC_TRY(be42_gemv_prepare(d->xdig, d->att, qd, B, fp8, st));
         DEC_TRY(gemv(d, d->xb, L.wo, L.so, dim, qd, B, st));
         BE42_HIP(norm(L.ffn_norm, d->xb));                 // x += attention output
@@ -728,6 +1428,12 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         pending = d->xb;
     }
     // final residual + norm, lm_head, argmax
+    if (fz) {
+        // the fused launches leave h in xn and the last down output in xb
+        xcur = d->xn;
+        xalt = d->x;
+        pending = d->xb;
+    }
     BE42_HIP(norm(d->w.final_norm, pending));
     float *lg = logits_out ? logits_out : d->logits;
     DEC_TRY(gemv(d, lg, d->w.out, d->w.out_s, c.vocab, dim, B, st));
@@ -735,6 +1441,9 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
                        d->arg_cnt);
     BE42_LAUNCH_CHECK();
     BE42_HIP(hipMemcpyAsync(d->next_host, d->next, (size_t)B * 4, hipMemcpyDeviceToHost, st));
+    if (fz)
+        BE42_HIP(hipMemcpyAsync(d->next_host + kMaxBatch, d->fflags + ((size_t)d->fnb + 1) * 32 + 1, 4,
+                                hipMemcpyDeviceToHost, st));
     return BE42_OK;
 }
 
@@ -784,6 +1493,9 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
     }
     if (next_tokens) {
         BE42_HIP(hipEventSynchronize(d->ev_out));
+        BE42_CHECK(d->next_host[kMaxBatch] == 0,
+                   "be42_decoder_step: a grid barrier of the fused layer timed out (code %d); the step's results "
+                   "are invalid", d->next_host[kMaxBatch]);
         memcpy(next_tokens, d->next_host, (size_t)B * sizeof(int));
     }
     return BE42_OK;

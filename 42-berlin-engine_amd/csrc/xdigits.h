@@ -25,22 +25,48 @@ constexpr int kF8Base = 30;
 // weight of FP8 digit d in the recombination, 30^-d
 __device__ constexpr double kF8DigitW[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 27000, 1.0 / 810000};
 
-// integer in [-15, 15] -> exact E4M3 code
-__device__ __forceinline__ uint8_t small_int_to_e4m3(int n)
-{
-    const uint32_t s = n < 0 ? 0x80u : 0u;
-    int a = n < 0 ? -n : n;
-    if (a == 0)
-        return 0;
-    int e = 31 - __clz(a);               // floor(log2 a), 0..3
-    int m = (a << (3 - e)) & 7;          // 3 mantissa bits below the leading one
-    return (uint8_t)(s | ((uint32_t)(e + 7) << 3) | (uint32_t)m);
-}
-
 template <bool FP8>
 __device__ __forceinline__ float digit_scale(float amax)
 {
     return amax > 0.0f ? amax / (FP8 ? 15.0f : 127.0f) : 1.0f;
+}
+
+// digits of four consecutive elements xe at scale s, one 32-bit word (four
+// digit bytes) per plane.  FP8 digits (integers in [-15, 15], exact in E4M3)
+// are encoded by the hardware conversion, two per instruction; + 0.0f turns
+// a -0 digit into +0, so the code of 0 is 0x00 (the conversion gives -0 the
+// code 0x80).
+template <bool FP8>
+__device__ __forceinline__ void digit_words(const float xe[4], float s, uint32_t (&word)[FP8 ? kF8Digits : kI8Digits])
+{
+    constexpr int R0 = FP8 ? 15 : 127;
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
+    constexpr float BASE = FP8 ? (float)kF8Base : (float)kI8Base;
+    const float rs = 1.0f / s;
+    float dv[4][ND];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float v = xe[e] * rs;
+#pragma unroll
+        for (int d = 0; d < ND; d++) {
+            float t = rintf(v);
+            t = fminf(fmaxf(t, -(float)R0), (float)R0);
+            v = (v - t) * BASE;
+            dv[e][d] = t + 0.0f;
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < ND; d++) {
+        if constexpr (FP8) {
+            int w = __builtin_amdgcn_cvt_pk_fp8_f32(dv[0][d], dv[1][d], 0, false);
+            w = __builtin_amdgcn_cvt_pk_fp8_f32(dv[2][d], dv[3][d], w, true);
+            word[d] = (uint32_t)w;
+        } else {
+            word[d] = (uint32_t)(uint8_t)(int8_t)(int)dv[0][d] | ((uint32_t)(uint8_t)(int8_t)(int)dv[1][d] << 8) |
+                      ((uint32_t)(uint8_t)(int8_t)(int)dv[2][d] << 16) |
+                      ((uint32_t)(uint8_t)(int8_t)(int)dv[3][d] << 24);
+        }
+    }
 }
 
 // digits of x[b][k0 .. k0+4) (xe), one 32-bit word per plane
@@ -48,26 +74,9 @@ template <bool FP8>
 __device__ __forceinline__ void store_digit_words(const float xe[4], float s, uint8_t *__restrict__ dig, int B,
                                                   int Kp, int b, int k0)
 {
-    constexpr int R0 = FP8 ? 15 : 127;
     constexpr int ND = FP8 ? kF8Digits : kI8Digits;
-    constexpr float BASE = FP8 ? (float)kF8Base : (float)kI8Base;
     uint32_t word[ND];
-#pragma unroll
-    for (int d = 0; d < ND; d++)
-        word[d] = 0;
-    const float rs = 1.0f / s;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        float v = xe[e] * rs;
-#pragma unroll
-        for (int d = 0; d < ND; d++) {
-            float dv = rintf(v);
-            dv = fminf(fmaxf(dv, -(float)R0), (float)R0);
-            v = (v - dv) * BASE;
-            const uint32_t code = FP8 ? small_int_to_e4m3((int)dv) : (uint32_t)(uint8_t)(int8_t)(int)dv;
-            word[d] |= code << (8 * e);
-        }
-    }
+    digit_words<FP8>(xe, s, word);
 #pragma unroll
     for (int d = 0; d < ND; d++)
         *(uint32_t *)(dig + ((size_t)d * B + b) * Kp + k0) = word[d];

@@ -247,3 +247,45 @@ def test_graph_replay_matches_eager(be, orc, monkeypatch):
     assert np.array_equal(na, nb) and torch.equal(la, lc)
     eager.close()
     graph.close()
+
+
+@pytest.mark.parametrize("kind,kv_kind", [("int8", OR_KV_INT8), ("int8", OR_KV_BF16), ("fp8", OR_KV_BF16)])
+def test_fused_layer_matches_separate_launches(be, orc, monkeypatch, kind, kv_kind):
+    """The one-sequence fused layer launch (o, norm, gate/up + SiLU, down and
+    the next layer's norm, q/k/v, RoPE and append in one launch with grid
+    barriers) against the same steps with separate launches
+    (BE42_DECODE_FUSED=0): 4 layers, d 512, sparse_k 8 so that every position
+    past 128 routes; 200 prompt tokens, then 20 greedy steps.  INT8 weights:
+    the logits of every step bit-identical (same arithmetic, exact digit
+    sums); FP8: the matrix cores' fp32 digit sums run in another order, so
+    logits agree to ~1e-6 until a K/V element rounds to another code (bounds
+    as in the free-running decode tests)."""
+    rng = np.random.default_rng(77)
+    w = make_model(rng, 4, 512, 8, 8, 64, 1408, 4096, kind)
+    oc, gc = configs(4, 512, 8, 8, 64, 1408, 4096, 512, 1, kind, kv_kind, 8, 64)
+    _, hpT = orc.lsh_init(64, 42)
+    wd = to_device(w)
+    prompt = rng.integers(0, 4096, 200)
+
+    def run():
+        dec = be42.Decoder(be, gc, wd, hpT)
+        lg = torch.empty((1, 4096), device="cuda")
+        outs, toks = [], []
+        for pos in range(220):
+            t = int(prompt[pos]) if pos < 200 else toks[-1]
+            toks.append(int(dec.step([t], pos, logits=lg)[0]))
+            outs.append(lg[0].cpu().numpy().copy())
+        dec.close()
+        return np.array(outs), toks
+
+    monkeypatch.setenv("BE42_DECODE_FUSED", "0")
+    l0, t0 = run()
+    monkeypatch.delenv("BE42_DECODE_FUSED")
+    l1, t1 = run()
+    if kind == "int8":
+        np.testing.assert_array_equal(l0, l1)
+        assert t0 == t1
+    else:
+        errs = np.abs(l0 - l1).max(axis=1) / np.abs(l0).max(axis=1)
+        assert errs[0] <= 1e-5 and np.median(errs) <= 1e-4 and errs.max() <= 2e-2, (errs[0], np.median(errs),
+                                                                                    errs.max())
