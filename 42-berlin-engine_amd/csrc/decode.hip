@@ -671,97 +671,123 @@ __device__ __forceinline__ void ph_compute(const FPhase &ph, int b, int nb, cons
     }
 }
 
-// block-wide max of non-negative values (every thread gets it)
-__device__ __forceinline__ float fblock_max(float v, float *red)
-{
-    v = wave_max(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = red[0];
-#pragma unroll
-    for (int w = 1; w < kFW; w++)
-        m = fmaxf(m, red[w]);
-    return m;
-}
-
 // fp32 staging of a phase's input vector in LDS, after its digit planes
 __device__ __forceinline__ float *dig_stage(uint8_t *dig, int nd, int K)
 {
     return (float *)(dig + (((size_t)nd * K + 15) & ~(size_t)15));
 }
 
-// digit planes of the staged vector (scale sc), by all threads
-template <bool FP8>
-__device__ __forceinline__ void stage_digits(const float *stage, int K, float sc, uint8_t *dig)
+// Waves 0-3 of a block wait for each other through an LDS counter (waves
+// 4-7 take no part: they may be stalled issuing weight loads, and a block
+// barrier would hold waves 0-3 behind them).  Every call adds 4 to the
+// target; the wait is bounded like the grid barrier's.
+struct QuadSync {
+    int *cnt;     // LDS, 0 at kernel start
+    int target;
+    int *err;     // the launch's error flag
+};
+__device__ __forceinline__ void quad_sync(QuadSync &q)
 {
-    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
-    for (int i4 = threadIdx.x; 4 * i4 < K; i4 += kFT) {
-        const float4 x4 = *(const float4 *)(stage + 4 * i4);
-        const float xe[4] = {x4.x, x4.y, x4.z, x4.w};
-        uint32_t word[ND];
-        digit_words<FP8>(xe, sc, word);
-#pragma unroll
-        for (int d = 0; d < ND; d++)
-            *(uint32_t *)(dig + (size_t)d * K + 4 * i4) = word[d];
+    q.target += 4;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if ((threadIdx.x & 63) == 0)
+        __hip_atomic_fetch_add(q.cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    unsigned spins = 0;
+    while (__hip_atomic_load(q.cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < q.target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > kFSpinMax * 16) {
+            if ((threadIdx.x & 63) == 0)
+                atomicExch(q.err, 3);
+            break;
+        }
     }
-    __syncthreads();
+    asm volatile("" ::: "memory");
+}
+
+// max over waves 0-3 of a per-lane value (red: 4 floats of LDS)
+__device__ __forceinline__ float quad_max(float v, float *red, QuadSync &q)
+{
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    quad_sync(q);
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
 // Digit planes of a vector written by other blocks (K a multiple of 128,
-// at most kRowT * 4 * kFVecG).  Threads < kRowT stage it in LDS with
-// device-scope loads and wait for them, then `mid` runs (their weight loads
-// of the phase), then every thread takes part in the scale and the digits.
+// at most kRowT * 4 * kFVecG).  Waves 0-3 stage it in LDS with device-scope
+// loads; once those have left, waves 4-7 issue their weight loads of the
+// phase (`mid`) while waves 0-3 wait for the vector, compute the scale and
+// the digit planes, and only then issue theirs.  Returns the scale (in every
+// thread).
 constexpr int kFVecG = 8;
 template <bool FP8, class Mid>
-__device__ __forceinline__ float vec_digits(const float *x, int K, uint8_t *dig, float *red, Mid &&mid)
+__device__ __forceinline__ float vec_digits(const float *x, int K, uint8_t *dig, float *red, QuadSync &q, Mid &&mid)
 {
+    constexpr int ND = FP8 ? kF8Digits : kI8Digits;
     const int tid = threadIdx.x;
-    float *stage = dig_stage(dig, FP8 ? kF8Digits : kI8Digits, K);
+    float *stage = dig_stage(dig, ND, K);
     vec_to_lds(x, stage, K);
     asm volatile("" ::: "memory");
     __syncthreads();              // the vector's loads leave before any weight load of the block
-    if (tid < kRowT)
+    if (tid >= kRowT) {
+        mid();
+    } else {
         wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    mid();
-    asm volatile("" ::: "memory");
+        quad_sync(q);
+        float m = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kFVecG; g++) {
+            const int i4 = tid + g * kRowT;
+            if (4 * i4 < K)
+                m = fmaxf(m, f4_absmax(*(const float4 *)(stage + 4 * i4)));
+        }
+        const float sc = digit_scale<FP8>(quad_max(m, red + 8, q));
+#pragma unroll
+        for (int g = 0; g < kFVecG; g++) {
+            const int i4 = tid + g * kRowT;
+            if (4 * i4 < K) {
+                const float4 x4 = *(const float4 *)(stage + 4 * i4);
+                const float xe[4] = {x4.x, x4.y, x4.z, x4.w};
+                uint32_t word[ND];
+                digit_words<FP8>(xe, sc, word);
+#pragma unroll
+                for (int d = 0; d < ND; d++)
+                    *(uint32_t *)(dig + (size_t)d * K + 4 * i4) = word[d];
+            }
+        }
+        if (tid == 0)
+            red[12] = sc;
+        asm volatile("" ::: "memory");
+        mid();
+    }
     __syncthreads();
-    float m = 0.0f;
-    for (int i4 = tid; 4 * i4 < K; i4 += kFT)
-        m = fmaxf(m, f4_absmax(*(const float4 *)(stage + 4 * i4)));
-    const float sc = digit_scale<FP8>(fblock_max(m, red));
-    stage_digits<FP8>(stage, K, sc, dig);
-    return sc;
+    return red[12];
 }
 
 // x + delta (both written by other blocks), RMSNorm with w, into digit
-// planes; block b writes its share of x + delta to x_out.  Threads < kRowT
-// hold the row exactly as k_rmsnorm's threads do (same sum of squares).
+// planes, with the work split as in vec_digits; block b writes its share of
+// x + delta to x_out.  Threads < kRowT (waves 0-3) hold the row exactly as
+// k_rmsnorm's threads do (same sum of squares, same reduction tree).
 template <bool FP8, int NV, class Mid>
 __device__ __forceinline__ float norm_digits(const float *x, const float *delta, const uint16_t *w, float *x_out,
-                                             int dim, float eps, uint8_t *dig, float *red, int b, int nb, Mid &&mid)
+                                             int dim, float eps, uint8_t *dig, float *red, int b, int nb,
+                                             QuadSync &q, Mid &&mid)
 {
     constexpr int ND = FP8 ? kF8Digits : kI8Digits;
     const int tid = threadIdx.x, n4 = dim >> 2;
-    float4 v[NV], h[NV];
-    uint2 wv[NV];
-    float ss = 0.0f;
-    // x and delta staged in LDS (device-scope loads), then read in the
-    // thread layout of k_rmsnorm
     float *sx_ = dig_stage(dig, ND, dim), *sd_ = sx_ + dim;
     vec_to_lds(x, sx_, dim);
     vec_to_lds(delta, sd_, dim);
     asm volatile("" ::: "memory");
-    __syncthreads();              // the vector's loads leave before any weight load of the block
-    if (tid < kRowT)
+    __syncthreads();              // the vectors' loads leave before any weight load of the block
+    if (tid >= kRowT) {
+        mid();
+    } else {
+        float4 v[NV], h[NV];
+        uint2 wv[NV];
         wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    mid();
-    asm volatile("" ::: "memory");
-    __syncthreads();
-    if (tid < kRowT) {
+        quad_sync(q);
 #pragma unroll
         for (int j = 0; j < NV; j++) {
             const int i = min(tid + kRowT * j, n4 - 1);
@@ -769,8 +795,7 @@ __device__ __forceinline__ float norm_digits(const float *x, const float *delta,
             v[j] = make_float4(xv.x + dv.x, xv.y + dv.y, xv.z + dv.z, xv.w + dv.w);
             wv[j] = ((const uint2 *)w)[i];
         }
-    }
-    if (tid < kRowT) {
+        float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < NV; j++) {
             const int i = tid + kRowT * j;
@@ -788,16 +813,13 @@ __device__ __forceinline__ float norm_digits(const float *x, const float *delta,
             ss = __fmaf_rn(v[j].z, v[j].z, ss);
             ss = __fmaf_rn(v[j].w, v[j].w, ss);
         }
-    }
-    ss = wave_sum_dpp(ss);
-    __syncthreads();
-    if ((tid & 63) == 0)
-        red[tid >> 6] = ss;
-    __syncthreads();
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(tot, (float)dim) + eps));
-    float m = 0.0f;
-    if (tid < kRowT) {
+        ss = wave_sum_dpp(ss);
+        if ((tid & 63) == 0)
+            red[tid >> 6] = ss;
+        quad_sync(q);
+        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(tot, (float)dim) + eps));
+        float m = 0.0f;
 #pragma unroll
         for (int j = 0; j < NV; j++) {
             const uint2 wj = wv[j];
@@ -809,20 +831,26 @@ __device__ __forceinline__ float norm_digits(const float *x, const float *delta,
                 h[j] = f4_zero();
             m = fmaxf(m, f4_absmax(h[j]));
         }
-    }
-    // h into the staging area (every read of x there happened before the
-    // sum-of-squares barriers)
-    if (tid < kRowT) {
+        const float sc = digit_scale<FP8>(quad_max(m, red + 8, q));
 #pragma unroll
         for (int j = 0; j < NV; j++) {
             const int i = tid + kRowT * j;
-            if (i < n4)
-                *(float4 *)(sx_ + 4 * i) = h[j];
+            if (i < n4) {
+                const float xe[4] = {h[j].x, h[j].y, h[j].z, h[j].w};
+                uint32_t word[ND];
+                digit_words<FP8>(xe, sc, word);
+#pragma unroll
+                for (int d = 0; d < ND; d++)
+                    *(uint32_t *)(dig + (size_t)d * dim + 4 * i) = word[d];
+            }
         }
+        if (tid == 0)
+            red[12] = sc;
+        asm volatile("" ::: "memory");
+        mid();
     }
-    const float sc = digit_scale<FP8>(fblock_max(m, red + 8));
-    stage_digits<FP8>(sx_, dim, sc, dig);
-    return sc;
+    __syncthreads();
+    return red[12];
 }
 
 template <bool FP8, bool BF16KV, int NV>
@@ -832,32 +860,35 @@ __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
     __shared__ long long part[kFW][16];
     __shared__ float ybuf[kFMaxTiles * 16];
     __shared__ float red[16];
+    __shared__ int qcnt;
     const int b = blockIdx.x, nb = gridDim.x;
+    if (threadIdx.x == 0)
+        qcnt = 0;
+    __syncthreads();
+    QuadSync quad{&qcnt, 0, A.err};
     GridBar gb{A.flags, __hip_atomic_load(A.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kFBars, nb, A.err};
     v8i fr[kFMaxU];
 #pragma unroll
     for (int u = 0; u < kFMaxU; u++)
         fr[u] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-    // A phase's input vector is loaded first (waves 0-3), then every wave
-    // loads its weight fragments: vector loads queued behind the whole
-    // phase's weight stream would hold up its digit planes.  Waves 0-3 issue
-    // theirs once the vector has landed.
-    auto early = [&](const FPhase &ph) {};
-    auto late = [&](const FPhase &ph) {
+    // A phase's input vector is loaded first (waves 0-3); then waves 4-7
+    // issue their weight loads of the phase while waves 0-3 compute the
+    // digit planes, and waves 0-3 issue theirs after (a vector load queued
+    // behind the phase's weight stream would hold up the digits).
+    auto wload = [&](const FPhase &ph) {
         const FPhase *pp = &ph;
         return [pp, b, nb, &fr] { ph_prefetch(*pp, b, nb, fr, 0, kFW); };
     };
     // o projection of the attention output
-    early(A.o);
-    float sx = vec_digits<FP8>(A.att, A.qd, dig, red, late(A.o));
+    float sx = vec_digits<FP8>(A.att, A.qd, dig, red, quad, wload(A.o));
     ph_compute<FP8>(A.o, b, nb, fr, dig, A.qd, sx, part, ybuf);
-    grid_barrier(gb, 1, [&] { early(A.gu); });
+    grid_barrier(gb, 1, [] {});
     // h = x + o, RMSNorm, gate/up, SiLU * up
-    sx = norm_digits<FP8, NV>(A.X, A.XB, A.ffn_norm, A.Hb, A.dim, A.eps, dig, red, b, nb, late(A.gu));
+    sx = norm_digits<FP8, NV>(A.X, A.XB, A.ffn_norm, A.Hb, A.dim, A.eps, dig, red, b, nb, quad, wload(A.gu));
     ph_compute<FP8>(A.gu, b, nb, fr, dig, A.dim, sx, part, ybuf);
-    grid_barrier(gb, 2, [&] { early(A.down); });
+    grid_barrier(gb, 2, [] {});
     // down projection
-    sx = vec_digits<FP8>(A.H2, A.hidden, dig, red, late(A.down));
+    sx = vec_digits<FP8>(A.H2, A.hidden, dig, red, quad, wload(A.down));
     ph_compute<FP8>(A.down, b, nb, fr, dig, A.hidden, sx, part, ybuf);
     if (A.qkv.nseg == 0) {
         // last layer: h and the down output stay for the final norm
@@ -865,9 +896,9 @@ __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
             __hip_atomic_store(A.gen, gb.base / kFBars + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    grid_barrier(gb, 3, [&] { early(A.qkv); });
+    grid_barrier(gb, 3, [] {});
     // next layer: x = h + down, RMSNorm, q/k/v
-    sx = norm_digits<FP8, NV>(A.Hb, A.XB, A.attn_norm, A.X, A.dim, A.eps, dig, red, b, nb, late(A.qkv));
+    sx = norm_digits<FP8, NV>(A.Hb, A.XB, A.attn_norm, A.X, A.dim, A.eps, dig, red, b, nb, quad, wload(A.qkv));
     ph_compute<FP8>(A.qkv, b, nb, fr, dig, A.dim, sx, part, ybuf);
     grid_barrier(gb, 4, [] {});
     if (b == 0 && threadIdx.x == 0)
