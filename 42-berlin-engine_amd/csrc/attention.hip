@@ -640,7 +640,8 @@ __device__ __forceinline__ void attn_values_finish(const AttnShared<HD, G, WAVES
 // page and 16-dim tile.  A row r = 4 g + part holds the bf16 parts of the
 // weights w[g][t] (zero past the page's token count, for part 3 and for heads
 // past G); B is 4 consecutive tokens of one dim (8 bytes, a tile's 16 dims x
-// 16 tokens = 512 contiguous bytes per load); the C value of lane (dim of the
+// 16 tokens = 512 contiguous bytes per load; zero past the page's token
+// count); the C value of lane (dim of the
 // tile, row group g) adds up to the three parts of head g.  Pages go round
 // robin over the waves, UNR in flight per wave.
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
@@ -687,10 +688,16 @@ __device__ __forceinline__ void attn_values_mfma(const be42_kv_pool &P, AttnShar
                     h[i] = apart == 0 ? hi : (apart == 1 ? mid : (apart == 2 ? lo : (uint16_t)0));
                 }
                 const s16x4_t a = {(short)h[0], (short)h[1], (short)h[2], (short)h[3]};
+                // token slots past the count hold whatever the page held
+                // before: zero them (a zero weight times a NaN or infinite
+                // bf16 pattern would still be NaN)
+                const int t0 = 4 * gi;
+                const v2i_t keep = {(int)((t0 < nt ? 0xFFFFu : 0u) | (t0 + 1 < nt ? 0xFFFF0000u : 0u)),
+                                    (int)((t0 + 2 < nt ? 0xFFFFu : 0u) | (t0 + 3 < nt ? 0xFFFF0000u : 0u))};
 #pragma unroll
                 for (int tile = 0; tile < NT; tile++)
                     acc[tile] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                        a, __builtin_bit_cast(s16x4_t, vb[u][tile]), acc[tile], 0, 0, 0);
+                        a, __builtin_bit_cast(s16x4_t, vb[u][tile] & keep), acc[tile], 0, 0, 0);
             }
         }
     }

@@ -70,10 +70,21 @@ def test_lsh_candidates_gpu(be):
 
 
 def _build(be, orc, kind, n_layers, n_kv, hd, max_pages, lens, rng, hpT, planted=None, chunks=(1, 7, 64, 100),
-           kgen=None):
+           kgen=None, poison=False):
     """The same appends on the GPU pool and the oracle; returns both plus the
-    per-layer oracle LSH indexes (page hashes inserted as pages fill)."""
+    per-layer oracle LSH indexes (page hashes inserted as pages fill).
+    poison: fill the pool's K/V rows and scales with 0xFF bytes first (NaN
+    bf16 and fp32 patterns), so token slots past a page's count hold NaNs."""
     gp = be.kv_pool(be42_kind(kind), n_layers, n_kv, hd, max_pages, hpT)
+    if poison:
+        cap = gp.s.capacity
+        row = 2 if kind == OR_KV_BF16 else 1
+        for field, nbytes in (("k", cap * n_kv * PAGE * hd * row), ("v", cap * n_kv * PAGE * hd * row),
+                              ("k_scale", cap * n_kv * PAGE * 4), ("v_scale", cap * n_kv * PAGE * 4)):
+            ptr = getattr(gp.s, field)
+            if ptr:
+                be._call("be42_memset", ptr, 0xFF, nbytes, be.stream())
+        torch.cuda.synchronize()
     op = OraclePaged(orc, n_layers, n_kv, hd, max_pages, kind)
     idx = [OracleIndex(orc, max_pages) for _ in range(n_layers)]
     for layer, T in enumerate(lens):
@@ -271,6 +282,43 @@ def test_attention_fused_group_shapes(be, orc, kind, n_kv, H, hd):
     for layer in range(3):
         want = op.attention_pages(q[layer], sl[layer], H, scale)
         assert rel_err(out[layer].ravel(), want) <= 2e-5, layer
+    gp.close()
+
+
+@pytest.mark.parametrize("kind", [OR_KV_INT8, OR_KV_BF16])
+def test_attention_ignores_unwritten_token_slots(be, orc, kind):
+    """Pages whose last token slots were never written (a partial last page)
+    hold whatever the memory held: here NaN patterns.  The dense, split and
+    routed attention read those slots (whole 16-token tiles on the matrix
+    cores) and must give them no weight and no value."""
+    rng = np.random.default_rng(1200 + kind)
+    n_kv, hd, H = 2, 128, 6
+    lens = (20 * PAGE + 5, 70 * PAGE + 3)
+    _, hpT = orc.lsh_init(hd, 42)
+    q = rng.standard_normal((2, H, hd)).astype(np.float32)
+    gp, op, idx = _build(be, orc, kind, 2, n_kv, hd, 72, lens, rng, hpT,
+                         planted=_planter(orc, hpT, hd, H, q, 0.1, rng), chunks=(64, 3), poison=True)
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    qd = torch.from_numpy(q).cuda()
+    sl = [[op.phys(layer, i) for i in range(op.n_blocks(layer))][:64] for layer in range(2)]
+    sl[1][-1] = op.phys(1, op.n_blocks(1) - 1)      # the partial last page of layer 1
+    sel = np.full((2, 64), -1, np.int32)
+    nsel = np.array([len(x) for x in sl], np.int32)
+    for i, x in enumerate(sl):
+        sel[i, :len(x)] = x
+    for n_split in (1, 3):
+        out = be.paged_attention(gp, qd, torch.from_numpy(sel).cuda(), torch.from_numpy(nsel).cuda(), 64, scale,
+                                 n_split=n_split).cpu().numpy()
+        for layer in range(2):
+            assert np.isfinite(out[layer]).all(), (n_split, layer)
+            assert rel_err(out[layer].ravel(), op.attention_pages(q[layer], sl[layer], H, scale)) <= 2e-5
+    fo, fsel, fn = be.lsh_attention(gp, qd, 64, 64, scale)
+    fo, fsel, fn = fo.cpu().numpy(), fsel.cpu().numpy(), fn.cpu().numpy()
+    for layer in range(2):
+        want_sel, _ = op.route(layer, q[layer], H, hpT, idx[layer], 64, 64) if layer == 1 else (sl[0], None)
+        np.testing.assert_array_equal(fsel[layer, :fn[layer]], want_sel)
+        assert np.isfinite(fo[layer]).all(), layer
+        assert rel_err(fo[layer].ravel(), op.attention_pages(q[layer], list(want_sel), H, scale)) <= 2e-5
     gp.close()
 
 
