@@ -21,6 +21,13 @@
 // keys exactly as the scores, ties included, and a sift-up moves one 32-bit
 // key per lane -- one permute per push instead of two, and no branches: each
 // lane knows from a precomputed mask whether it lies on the new slot's path.
+// WaveHeapKey::fill runs the pushes that do not replace the root (the first
+// `cap`) on the scalar unit: the keys are uniform and, with the pushes
+// unrolled, every slot index is a compile-time constant, so the heap lives
+// in scalar registers; and since a root path is sorted, the sift-up from
+// slot n sets each path slot i (bottom up) to max(key[parent], min(key[i],
+// new)) and the root to min(key[0], new) -- two scalar operations per level.
+// A push of INT_MAX changes nothing, so pushes past the count need no branch.
 #pragma once
 
 #include "be42_common.h"
@@ -120,6 +127,31 @@ struct WaveHeapKey {
     }
 
     __device__ __forceinline__ int payload() const { return hk & 0xFF; }
+
+    // The first m <= cap pushes, of entries e = 0 .. m-1 whose ranks are in
+    // lane e % 64 of rk[e / 64] (uniform m); the heap must be empty.
+    __device__ __forceinline__ void fill(int m, const int (&rk)[4])
+    {
+        int h[kHeapMax];
+#pragma unroll
+        for (int n = 0; n < kHeapMax; n++)
+            h[n] = 0x7FFFFFFF;
+#pragma unroll
+        for (int n = 0; n < kHeapMax; n++) {
+            const int r = __builtin_amdgcn_readlane(rk[n >> 6], n & 63);
+            const int key = n < m ? (r << 8) | n : 0x7FFFFFFF;
+#pragma unroll
+            for (int i = n; i > 0; i = (i - 1) >> 1)
+                h[i] = max(h[(i - 1) >> 1], min(h[i], key));
+            h[0] = min(h[0], key);
+        }
+        int v = 0;
+#pragma unroll
+        for (int n = 0; n < kHeapMax; n++)
+            v = lane == n ? h[n] : v;
+        hk = v;
+        size = m;
+    }
 
     // heap_push with the score of rank `rank` (uniform) and payload e < 256
     __device__ __forceinline__ void push(int rank, int e)

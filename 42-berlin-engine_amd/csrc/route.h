@@ -382,11 +382,14 @@ __device__ __forceinline__ int route_select(int k_sel, int cap, const RouteView 
         rk[j] = V.rk[e] + V.rk[cap + e] + V.rk[2 * cap + e] + V.rk[3 * cap + e];
     }
     WaveHeapKey heap(ak);
-    for (int e0 = 0; e0 < nm && ak > 0; e0 += kWave) {
+    // the pushes that fill the heap on the scalar unit, then the ones that
+    // may replace its root
+    heap.fill(ak, rk);
+    for (int e0 = ak & ~(kWave - 1); e0 < nm && ak > 0; e0 += kWave) {
         const int j = e0 >> 6;
         const int rv = j == 0 ? rk[0] : (j == 1 ? rk[1] : (j == 2 ? rk[2] : rk[3]));
         const int ecnt = min(kWave, nm - e0);
-        for (int u = 0; u < ecnt; u++)
+        for (int u = max(ak - e0, 0); u < ecnt; u++)
             heap.push(rl(rv, u), e0 + u);
     }
     const int size = heap.size, hi = heap.payload();
