@@ -426,18 +426,18 @@ __device__ __forceinline__ QParts<HD> attn_q_parts(const AttnShared<HD, G, WAVES
     return Q;
 }
 
-// scores of the pages at slots [0, ns) of S.pphys, UNR pages per wave step,
+// scores of the pages at slots [lo, ns) of S.pphys, UNR pages per wave step,
 // by waves w0 .. w0+nw-1
 template <int HD, int G, int WAVES, int UNR>
 __device__ __forceinline__ void attn_scores_mfma(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
-                                                 float scale, int w0, int nw)
+                                                 float scale, int w0, int nw, int lo = 0)
 {
     constexpr int NJ = HD / 32;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = lane & 15, gi = lane >> 4;
     const QParts<HD> Q = attn_q_parts<HD, G, WAVES>(S);
     const int n_kv = P.n_kv;
-    for (int s0 = (wave - w0) * UNR; s0 < ns; s0 += nw * UNR) {
+    for (int s0 = lo + (wave - w0) * UNR; s0 < ns; s0 += nw * UNR) {
         uint4 kb[UNR][NJ];
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
@@ -647,12 +647,15 @@ __device__ __forceinline__ void attn_values_finish(const AttnShared<HD, G, WAVES
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef int v2i_t __attribute__((ext_vector_type(2)));
 
-template <int HD, int G, int WAVES, int UNR>
-__device__ __forceinline__ void attn_values_mfma(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
-                                                 const int *order)
+// The pages of wave `wave` of a WAVES-wave layout (positions wave * UNR +
+// WAVES * UNR * i + u) into put(index, value), index = g * HD + dim: the
+// partial o of that wave.
+template <int HD, int G, int WAVES, int UNR, class Put>
+__device__ __forceinline__ void attn_values_mfma_wave(const be42_kv_pool &P, const AttnShared<HD, G, WAVES> &S,
+                                                      int kvh, int ns, const int *order, int wave, Put &&put)
 {
     constexpr int NT = HD / 16;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63;
     const int n = lane & 15, gi = lane >> 4;
     const int ag = n >> 2, apart = n & 3;
     v4f acc[NT];
@@ -704,7 +707,16 @@ __device__ __forceinline__ void attn_values_mfma(const be42_kv_pool &P, AttnShar
     if (gi < G)
 #pragma unroll
         for (int tile = 0; tile < NT; tile++)
-            S.red[(wave * G + gi) * HD + tile * 16 + n] = (acc[tile][0] + acc[tile][1]) + acc[tile][2];
+            put(gi * HD + tile * 16 + n, (acc[tile][0] + acc[tile][1]) + acc[tile][2]);
+}
+
+template <int HD, int G, int WAVES, int UNR>
+__device__ __forceinline__ void attn_values_mfma(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
+                                                 const int *order)
+{
+    const int wave = threadIdx.x >> 6;
+    float *red = S.red + wave * G * HD;
+    attn_values_mfma_wave<HD, G, WAVES, UNR>(P, S, kvh, ns, order, wave, [red](int i, float v) { red[i] = v; });
 }
 
 // C. o = sum_t w_t v_t over the slots (the order of the sum is free), then
@@ -816,7 +828,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
 // when position lim[b] - 1 was the newest (a prefill runs the queries of many
 // positions after appending all of their K/V).
 template <bool BF16, int HD, int G, int WAVES, int UNR, bool STAGE>
-__global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, const float *__restrict__ q,
+__global__ __launch_bounds__(WAVES * 64, 4) void k_lsh_attn(const be42_kv_pool P, const float *__restrict__ q,
                                                          const int *__restrict__ slots, const int *__restrict__ lim,
                                                          int H, int k_sel, int cap, float scale,
                                                          float *__restrict__ out, int *__restrict__ sel,
@@ -909,6 +921,221 @@ __global__ __launch_bounds__(WAVES * 64) void k_lsh_attn(const be42_kv_pool P, c
     attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out, early ? S.order : nullptr);
 }
 
+// Route + attention of few queries over more CUs: the NS workgroups
+// (blockIdx.z) of a (query, KV head) pair each run the router and the heap
+// (as k_lsh_attn does), score 1/NS of the pages, exchange the scores, compute
+// every weight, and take 16/NS of the 16 value waves of k_lsh_attn's 16-wave
+// layout; the last workgroup to finish adds the 16 wave partials in wave
+// order.  Every page's scores, every weight and every wave partial are
+// computed exactly as in that layout, so the output is the same to the bit.
+// The exchange goes through device-scope loads and stores; the NS workgroups
+// meet at one counter barrier (the last to arrive resets the count and flips
+// a flag the others wait on, so nothing is reset between launches).  A wait
+// that does not end within ~kSplitSpinMax polls (workgroups of a pair not
+// resident together) gives up and scores every page itself, so the result
+// never depends on the others.
+constexpr int kSplitMaxPairs = 128;           // (query, KV head) pairs of a split launch
+constexpr int kSplitWaves = 16;                // the value layout a split launch reproduces
+constexpr unsigned kSplitSpinMax = 1u << 14;
+struct SplitSync {
+    unsigned arrive, flag, done, pad[13];      // one 64-byte line per pair
+};
+__device__ SplitSync g_split_sync[kSplitMaxPairs];
+__device__ float g_split_sc[kSplitMaxPairs][4][kSetMax * 17];          // scores, AttnShared::sc layout
+__device__ float g_split_o[kSplitMaxPairs][kSplitWaves][4 * 128];       // wave partials [g][dim]
+
+__device__ __forceinline__ unsigned ld_dev_u(const unsigned *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u(unsigned *p, unsigned v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev_f(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_f(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int HD, int G, bool STAGE>
+__global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_kv_pool P, const float *__restrict__ q,
+                                                                    const int *__restrict__ slots,
+                                                                    const int *__restrict__ lim, int H, int k_sel,
+                                                                    int cap, float scale, float *__restrict__ out,
+                                                                    int *__restrict__ sel, int *__restrict__ nsel,
+                                                                    int sel_stride)
+{
+    constexpr int WAVES = kSplitWaves;
+    static_assert(G <= 4 && HD <= 128, "exchange buffers");
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ AttnShared<HD, G, WAVES> S;
+    __shared__ int set_n, last, alone;
+    __shared__ unsigned sense;
+    const RouteView V = route_view(smem, route_smem(HD, cap, P.max_logical));
+    S.red = (float *)smem;
+    const int b = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z, NS = gridDim.z;
+    const int pair = b * gridDim.y + kvh;
+    SplitSync *sy = &g_split_sync[pair];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the flag flips only once every workgroup of the pair has arrived, so
+    // each reads it before that
+    if (tid == 0)
+        sense = ld_dev_u(&sy->flag);
+    const int layer = slots ? slots[b] : b;
+    const int base = layer * P.max_logical;
+    const int lim_b = lim ? lim[b] : 0;
+    const int n = lim ? (lim_b + kPg - 1) / kPg : P.n_logical[layer];
+    const int last_ph = lim && n > 0 ? P.page_table[base + n - 1] : -1;
+    const int last_nt = lim_b - kPg * (n - 1);
+    auto page_nt = [&](int ph) { return ph == last_ph ? last_nt : P.ntok[ph]; };
+    int *selb = sel && kvh == 0 && z == 0 ? sel + (size_t)b * sel_stride : nullptr;
+    if (n <= k_sel) {
+        // dense: the first workgroup of the pair alone, as k_lsh_attn
+        if (z != 0)
+            return;
+        attn_load_q(S, q, b, kvh, H);
+        const int ns = n > 0 ? n : 0;
+        for (int i = tid; i < ns; i += blockDim.x) {
+            const int ph = P.page_table[base + i];
+            S.pphys[i] = ph;
+            S.pnt[i] = page_nt(ph);
+            if (selb)
+                selb[i] = ph;
+        }
+        if (tid == 0 && selb)
+            nsel[b] = ns;
+        __syncthreads();
+        if (ns == 0) {
+            for (int i = tid; i < G * HD; i += blockDim.x)
+                out[((size_t)b * H + kvh * G) * HD + i] = 0.0f;
+            return;
+        }
+        attn_scores<true, HD, G, WAVES, 8>(P, S, kvh, ns, scale, 0, WAVES);
+        __syncthreads();
+        attn_weights(S, ns, nullptr);
+        __syncthreads();
+        attn_values<true, HD, G, WAVES, 8>(P, S, b, kvh, ns, H, out, nullptr);
+        return;
+    }
+    attn_load_q(S, q, b, kvh, H);
+    const int nidx = min(lim ? min(P.n_indexed[layer], lim_b / kPg) : P.n_indexed[layer], P.max_logical);
+    route_prepare<STAGE>(P, q + (size_t)b * H * HD, base, n, nidx, H, cap, V, nullptr, nullptr, nullptr);
+    const int nm = route_middles(V);
+    const int ns0 = V.mpt[cap + 1] != V.mpt[cap] ? 2 : 1;
+    const int nset = ns0 + nm;
+    const bool early = nset <= kSetMax;
+    if (early) {
+        for (int i = tid; i < nset; i += blockDim.x) {
+            const int ph = i == 0 ? V.mpt[cap] : (i < ns0 ? V.mpt[cap + 1] : V.mpt[i - ns0]);
+            S.pphys[i] = ph;
+            S.pnt[i] = page_nt(ph);
+        }
+    }
+    __syncthreads();
+    // this workgroup's share of the scored slots: [lo, hi) of the set slots
+    // (early) or of the selection (after the heap)
+    int lo = z * nset / NS, hi = (z + 1) * nset / NS;
+    if (wave == 0) {
+        const int ns = route_select(k_sel, cap, V, selb, S.order);
+        if (lane == 0) {
+            set_n = ns;
+            if (selb)
+                nsel[b] = ns;
+        }
+    } else if (early) {
+        attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, hi, scale, 1, WAVES - 1, lo);
+    }
+    __syncthreads();
+    const int ns = set_n;
+    const int E = early ? nset : ns;
+    if (!early) {
+        for (int i = tid; i < ns; i += blockDim.x) {
+            const int slot = S.order[i];
+            const int ph = slot == 0 ? V.mpt[cap] : (slot < ns0 ? V.mpt[cap + 1] : V.mpt[slot - ns0]);
+            S.pphys[i] = ph;
+            S.pnt[i] = page_nt(ph);
+        }
+        __syncthreads();
+        lo = z * ns / NS;
+        hi = (z + 1) * ns / NS;
+        attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, hi, scale, 0, WAVES, lo);
+        __syncthreads();
+    }
+    // publish this share, then meet the pair's other workgroups
+    float *xs = &g_split_sc[pair][0][0];
+    const int nsh = (hi - lo) * kPg;
+    for (int i = tid; i < G * nsh; i += blockDim.x) {
+        const int g = i / nsh, r = lo * kPg + i % nsh;
+        const int at = (r / kPg) * 17 + r % kPg;
+        st_dev_f(xs + g * (kSetMax * 17) + at, S.sc[g][at]);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned s0 = sense;
+        int gave_up = 0;
+        if (__hip_atomic_fetch_add(&sy->arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)NS - 1) {
+            st_dev_u(&sy->arrive, 0u);
+            st_dev_u(&sy->flag, s0 ^ 1u);
+        } else {
+            unsigned spins = 0;
+            while (ld_dev_u(&sy->flag) == s0) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > kSplitSpinMax) {
+                    gave_up = 1;
+                    break;
+                }
+            }
+        }
+        alone = gave_up;
+    }
+    __syncthreads();
+    if (alone) {
+        attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, E, scale, 0, WAVES, 0);
+    } else {
+        for (int i = tid; i < G * E * kPg; i += blockDim.x) {
+            const int g = i / (E * kPg), r = i % (E * kPg), sl = r / kPg;
+            const int at = sl * 17 + r % kPg;
+            if (sl < lo || sl >= hi)
+                S.sc[g][at] = ld_dev_f(xs + g * (kSetMax * 17) + at);
+        }
+    }
+    __syncthreads();
+    attn_weights(S, ns, early ? S.order : nullptr);
+    __syncthreads();
+    // value waves z * per .. z * per + per - 1 of the 16-wave layout
+    const int per = WAVES / NS;
+    if (wave < per) {
+        float *dst = &g_split_o[pair][z * per + wave][0];
+        attn_values_mfma_wave<HD, G, WAVES, 4>(P, S, kvh, ns, early ? S.order : nullptr, z * per + wave,
+                                               [dst](int i, float v) { st_dev_f(dst + i, v); });
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = __hip_atomic_fetch_add(&sy->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == (unsigned)NS - 1;
+        if (last)
+            st_dev_u(&sy->done, 0u);
+    }
+    __syncthreads();
+    if (!last)
+        return;
+    // out = (sum of the 16 wave partials in wave order) * (1 / l)
+    for (int i = tid; i < G * HD; i += blockDim.x) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; w++)
+            v += ld_dev_f(&g_split_o[pair][w][i]);
+        const float l = S.lsh[i / HD];
+        out[((size_t)b * H + kvh * G) * HD + i] = l > 0.0f ? v * (1.0f / l) : v;
+    }
+}
+
 // 16 waves when the grid is small (more loads in flight per workgroup), 8
 // waves once there are enough workgroups to fill the chip.
 template <bool BF16, int HD, int G>
@@ -966,11 +1193,39 @@ struct LshAttnOpt {
     bool wide16 = false;
 };
 
+// BE42_ATTN_SPLIT=0 keeps every launch at one workgroup per (query, KV head)
+static bool split_enabled()
+{
+    static const bool on = [] {
+        const char *e = getenv("BE42_ATTN_SPLIT");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 template <bool BF16, int HD, int G, bool STAGE>
 static int launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride,
                              const RouteSmem &L, const LshAttnOpt &o, hipStream_t s)
 {
+    if constexpr (BF16 && (HD == 64 || HD == 128)) {
+        // few pairs: NS workgroups per pair, NS * pairs <= 256 (one per CU);
+        // at 2 per pair the exchange costs more than it saves (measured)
+        const long pairs = (long)B * P.n_kv;
+        if (pairs <= 64 && split_enabled()) {
+            int ns = kSplitWaves;
+            while (ns > 4 && pairs * ns > 256)
+                ns >>= 1;
+            const size_t lds = lsh_attn_lds<HD, G, kSplitWaves>(L);
+            if (lds > 65536)
+                BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_attn_split<HD, G, STAGE>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            hipLaunchKernelGGL((k_lsh_attn_split<HD, G, STAGE>), dim3(B, P.n_kv, ns), dim3(kSplitWaves * 64), lds, s,
+                               P, q, slots, o.lim, H, k_sel, cap, scale, out, sel, nsel, sel_stride);
+            BE42_LAUNCH_CHECK();
+            return BE42_OK;
+        }
+    }
     const dim3 grid(B, P.n_kv);
     if ((long)B * P.n_kv < 512 || o.wide16) {
         const size_t lds = lsh_attn_lds<HD, G, 16>(L);

@@ -386,6 +386,42 @@ def test_lsh_attention_fused_matches_oracle(be, orc, kind, cap, k_sel, n_kv, H, 
     gp.close()
 
 
+@pytest.mark.parametrize("k_sel,cap,frac", [(64, 64, 0.1), (40, 128, 0.7)])
+def test_lsh_attention_split_bit_identical(be, orc, k_sel, cap, frac):
+    """A launch of at most 128 (query, KV head) pairs splits each pair over
+    2-16 workgroups (bf16 pages): every score, weight and 16-wave partial is
+    computed as in one workgroup, so 1, 8 and 16 queries give the bits of
+    the same queries inside a 24-query launch (192 pairs, one workgroup
+    each).  frac 0.7 plants ~90 pages, more candidates than the slots
+    scored while the heap runs (the scores then follow the heap) and more
+    than the heap holds (root replacements)."""
+    rng = np.random.default_rng(1300 + cap)
+    n_kv, hd, H = 8, 128, 24
+    lens = (70 * PAGE + 5, 130 * PAGE + 9, 3 * PAGE + 2, 90 * PAGE)
+    _, hpT = orc.lsh_init(hd, 42)
+    q4 = rng.standard_normal((4, H, hd)).astype(np.float32)
+    gp, op, idx = _build(be, orc, OR_KV_BF16, 4, n_kv, hd, 140, lens, rng, hpT,
+                         planted=_planter(orc, hpT, hd, H, q4, frac, rng), chunks=(64,))
+    B = 24
+    slots_np = np.array([b % 4 for b in range(B)], np.int32)
+    qn = q4[slots_np] + 0.01 * rng.standard_normal((B, H, hd)).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    full, fsel, fn = be.lsh_attention(gp, torch.from_numpy(qn).cuda(), k_sel, cap, scale,
+                                      slots=torch.from_numpy(slots_np).cuda())
+    full, fsel, fn = full.cpu().numpy(), fsel.cpu().numpy(), fn.cpu().numpy()
+    for b in range(4):
+        want_sel, _ = op.route(b, qn[b], H, hpT, idx[b], cap, k_sel)
+        np.testing.assert_array_equal(fsel[b, :fn[b]], want_sel)
+        assert rel_err(full[b].ravel(), op.attention_pages(qn[b], list(want_sel), H, scale)) <= 2e-5
+    for lo, hi in ((5, 6), (8, 16), (0, 16), (1, 3)):
+        o, s_, n_ = be.lsh_attention(gp, torch.from_numpy(qn[lo:hi]).cuda(), k_sel, cap, scale,
+                                     slots=torch.from_numpy(slots_np[lo:hi]).cuda())
+        np.testing.assert_array_equal(n_.cpu().numpy(), fn[lo:hi])
+        np.testing.assert_array_equal(s_.cpu().numpy(), fsel[lo:hi])
+        np.testing.assert_array_equal(bits(o.cpu().numpy()), bits(full[lo:hi]), err_msg=f"queries {lo}:{hi}")
+    gp.close()
+
+
 def test_lsh_attention_many_queries(be, orc):
     """65 queries x 8 KV heads (> 512 pairs): be42_lsh_attention runs the
     router and the attention as two launches; the result equals those two
