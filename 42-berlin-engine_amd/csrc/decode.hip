@@ -373,9 +373,12 @@ __global__ __launch_bounds__(256) void k_rope_rows(float *__restrict__ q, float 
 // between dependent phases.  Every block is resident (one per CU), keeps its
 // own copy of the phase's activation digit planes in LDS (it computes them
 // from the fp32 vector itself), and streams its row tiles of the phase's
-// weights straight from HBM into MFMA operand registers; the loads of the
-// next phase's weights are issued before waiting at the barrier, so the HBM
-// stream runs on across the phases.
+// weights straight from HBM into MFMA operand registers.  A phase's input
+// vector is loaded first; half of the block's weight loads leave while the
+// other half of its waves compute the digit planes.  (Weight loads issued
+// before a barrier were measured to slow the barrier itself more than they
+// gained, and so was a barrier in which every block reads a packed array of
+// all the arrival flags.)
 //
 // Coherence: the activations one block writes and another reads go through
 // device-scope (agent) atomic stores and loads, which act at the device's
