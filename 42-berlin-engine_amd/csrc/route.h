@@ -16,9 +16,13 @@ constexpr int kMaxCand = 256;       // router candidate cap
 constexpr int kMaxCandList = 512;   // be42_lsh_candidates cap
 
 constexpr int kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
+// Waves the candidate scan can use (a block's waves, at most 16); the
+// router's counters after them: query hash, candidates, middle entries.
+constexpr int kScanWaves = 16;
+constexpr int kCntHash = kScanWaves * kProbes, kCntTotal = kCntHash + 1, kCntMid = kCntHash + 2;
 
 struct RouteSmem {
-    int off_qm, off_q0, off_hp, off_list, off_cnt, off_offs, off_cand, off_mid, off_sc, off_rk, off_mpt, off_ph,
+    int off_qm, off_q0, off_hp, off_cnt, off_offs, off_cand, off_mid, off_sc, off_rk, off_mpt, off_ph,
         off_pt, stage, bytes;
 };
 
@@ -36,9 +40,8 @@ __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical
     r.off_qm = o;   o += 256 * 4;
     r.off_q0 = o;   o += 256 * 4;
     r.off_hp = o;   o += 16 * (hd + 4) * 4;   // projection, bit-major, rows padded by 16 bytes
-    r.off_list = o; o += 4 * kProbes * cap * 4;
-    r.off_cnt = o;  o += 4 * kProbes * 4 + 4 * 4;
-    r.off_offs = o; o += 4 * kProbes * 4 + 4 * 4;
+    r.off_cnt = o;  o += kScanWaves * kProbes * 4 + 4 * 4;
+    r.off_offs = o; o += kScanWaves * kProbes * 4 + 4 * 4;
     r.off_cand = o; o += cap * 4;
     r.off_mid = o;  o += cap * 4;
     r.off_sc = o;   o += cap * 4;
@@ -58,7 +61,7 @@ constexpr int kRouteThreads = 256;
 // Pointers into the router's LDS.
 struct RouteView {
     float *qm, *q0, *hp, *sc;
-    int *list, *cnt, *offs, *cand, *mid, *mpt, *pt_s, *rk;
+    int *cnt, *offs, *cand, *mid, *mpt, *pt_s, *rk;
     uint16_t *ph_s;
 };
 
@@ -68,7 +71,6 @@ __device__ __forceinline__ RouteView route_view(unsigned char *smem, const Route
     V.qm = (float *)(smem + L.off_qm);
     V.q0 = (float *)(smem + L.off_q0);
     V.hp = (float *)(smem + L.off_hp);
-    V.list = (int *)(smem + L.off_list);
     V.cnt = (int *)(smem + L.off_cnt);
     V.offs = (int *)(smem + L.off_offs);
     V.cand = (int *)(smem + L.off_cand);
@@ -91,7 +93,7 @@ __device__ __forceinline__ float rlf(float v, int lane)
 // `base`): staging, q_mean and its hash, the candidate scan, concatenation
 // and middle entries, and the middle entries' scores.  Called by every thread
 // of the block (>= kRouteThreads threads).  Leaves in LDS: mid[e] (logical
-// page), mpt[e] (physical page), sc[e] for e < cnt[4 * kProbes + 2], and the
+// page), mpt[e] (physical page), sc[e] for e < cnt[kCntMid], and the
 // first and last physical page in mpt[cap], mpt[cap + 1]; qhash_b, cand_b
 // and ncand_b (optional) receive the query hash and the candidate list.
 template <bool STAGE>
@@ -102,7 +104,7 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
     const int hd = P.head_dim;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     float *qm = V.qm, *q0 = V.q0, *hp = V.hp, *sc = V.sc;
-    int *list = V.list, *cnt = V.cnt, *offs = V.offs, *cand = V.cand, *mid = V.mid, *mpt = V.mpt;
+    int *cnt = V.cnt, *offs = V.offs, *cand = V.cand, *mid = V.mid, *mpt = V.mpt;
     uint16_t *ph_s = V.ph_s;
     // 0./1. loads that do not depend on the query hash, issued before any is
     //    used: page hashes and page table (staged), projection, the query's
@@ -185,27 +187,32 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
         }
         const unsigned long long m = __ballot(lane < 16 && s > 0.0f);
         if (lane == 0)
-            cnt[4 * kProbes] = (int)(m & 0xFFFFu);
+            cnt[kCntHash] = (int)(m & 0xFFFFu);
     }
     __syncthreads();
-    const int qh = cnt[4 * kProbes];
+    const int qh = cnt[kCntHash];
     if (tid == 0 && qhash_b)
         *qhash_b = (uint16_t)qh;
 
-    // 2. candidate scan: wave w < 4 owns ids [lo, hi), scanned from hi-1 down
-    if (wave < 4) {
-        const int part = (nidx + 3) / 4;
-        const int hi = max(nidx - wave * part, 0), lo = max(nidx - (wave + 1) * part, 0);
-        int cntv = 0;    // lane p < 17 holds the hit count of probe p
-        int *mylist = list + wave * kProbes * cap;
-        for (int top0 = hi - 1; top0 >= lo; top0 -= 4 * kWave) {
+    // 2. candidate scan in two passes over the ids, wave w of the nw waves
+    //    owning ids [lo, hi) scanned from hi-1 down (wave 0 the highest):
+    //    (a) every wave counts its hits per probe; (b) the counts give each
+    //    (probe, wave) run its place in the concatenation (probe order, then
+    //    descending id), and the second pass writes the hits there, up to
+    //    cap.  Lane p < 17 keeps the running count of probe p.
+    const int nw = min((int)(blockDim.x >> 6), kScanWaves);
+    const int part = (nidx + nw - 1) / nw;
+    const int shi = max(nidx - wave * part, 0), slo = max(nidx - (wave + 1) * part, 0);
+    auto scan = [&](auto &&hit) {
+        int cntv = 0;
+        for (int top0 = shi - 1; top0 >= slo; top0 -= 4 * kWave) {
             // four chunks of 64 ids: their hash reads are issued together
             int pv[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int id = top0 - u * kWave - lane;
-                const int dd = (int)ph[max(id, lo)] ^ qh;
-                pv[u] = id < lo ? kProbes : (dd == 0 ? 0 : (((dd & (dd - 1)) == 0) ? __ffs(dd) : kProbes));
+                const int dd = (int)ph[max(id, slo)] ^ qh;
+                pv[u] = id < slo ? kProbes : (dd == 0 ? 0 : (((dd & (dd - 1)) == 0) ? __ffs(dd) : kProbes));
             }
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -217,65 +224,61 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
                     const int pp = rl(p, l0);
                     const unsigned long long m = __ballot(p == pp);
                     const int basec = rl(cntv, pp);
-                    if (p == pp) {
-                        const int rank = __popcll(m & ((1ull << lane) - 1ull));
-                        if (basec + rank < cap)
-                            mylist[pp * cap + basec + rank] = id;
-                    }
+                    if (p == pp)
+                        hit(pp, basec + __popcll(m & ((1ull << lane) - 1ull)), id);
                     if (lane == pp)
                         cntv += __popcll(m);
                     hits &= ~m;
                 }
             }
         }
+        return cntv;
+    };
+    if (wave < nw) {
+        const int c = scan([](int, int, int) {});
         if (lane < kProbes)
-            cnt[wave * kProbes + lane] = cntv;
+            cnt[wave * kProbes + lane] = c;
     }
     __syncthreads();
-
-    // 3. concatenation: list j = 4 * probe + wave (probe order, then
-    //    descending id) starts at offs[j]; lane l of wave 0 owns lists 2l, 2l+1
+    // run j = probe * nw + w starts at offs[j]; lane l of wave 0 owns runs
+    // 5l .. 5l + 4 (at most 16 * 17 = 272 runs)
     if (wave == 0) {
-        int c0 = 0, c1 = 0;
-        if (lane < 2 * kProbes) {
-            const int j0 = 2 * lane, j1 = j0 + 1;
-            c0 = min(cnt[(j0 & 3) * kProbes + (j0 >> 2)], cap);
-            c1 = min(cnt[(j1 & 3) * kProbes + (j1 >> 2)], cap);
+        constexpr int RPL = (kScanWaves * kProbes + kWave - 1) / kWave;
+        const int nj = nw * kProbes;
+        int c[RPL], sum = 0;
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            const int j = lane * RPL + i;
+            c[i] = j < nj ? cnt[(j % nw) * kProbes + j / nw] : 0;
+            sum += c[i];
         }
-        int inc = c0 + c1;
+        int inc = sum;
 #pragma unroll
         for (int o = 1; o < kWave; o <<= 1) {
             const int v = __shfl_up(inc, o, kWave);
             if (lane >= o)
                 inc += v;
         }
-        if (lane < 2 * kProbes) {
-            offs[2 * lane] = inc - c0 - c1;
-            offs[2 * lane + 1] = inc - c1;
+        int run = inc - sum;
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            const int j = lane * RPL + i;
+            if (j < nj)
+                offs[j] = run;
+            run += c[i];
         }
         if (lane == kWave - 1)
-            cnt[4 * kProbes + 1] = min(inc, cap);
+            cnt[kCntTotal] = min(inc, cap);
     }
     __syncthreads();
-    // candidate i belongs to the last list j with offs[j] <= i (lists are
-    // concatenated, empty ones share the next list's offset)
-    {
-        const int tot = cnt[4 * kProbes + 1];
-        for (int i = tid; i < tot; i += blockDim.x) {
-            int lo = 0, hi = 4 * kProbes - 1;
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (offs[mid] <= i)
-                    lo = mid;
-                else
-                    hi = mid - 1;
-            }
-            const int j = lo;
-            cand[i] = list[((j & 3) * kProbes + (j >> 2)) * cap + (i - offs[j])];
-        }
-    }
+    if (wave < nw)
+        scan([&](int pp, int rank, int id) {
+            const int at = offs[pp * nw + wave] + rank;
+            if (at < cap)
+                cand[at] = id;
+        });
     __syncthreads();
-    const int total = cnt[4 * kProbes + 1];
+    const int total = cnt[kCntTotal];
     if (cand_b)
         for (int i = tid; i < total; i += kRouteThreads)
             cand_b[i] = cand[i];
@@ -294,10 +297,10 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
             nm += __popcll(m);
         }
         if (lane == 0)
-            cnt[4 * kProbes + 2] = nm;
+            cnt[kCntMid] = nm;
     }
     __syncthreads();
-    const int nm = cnt[4 * kProbes + 2];
+    const int nm = cnt[kCntMid];
 
     // 4. scores of the middle entries (score_blocks semantics), a lane pair each
     for (int e0 = 0; tid < kRouteThreads && e0 < nm; e0 += 128) {
@@ -344,7 +347,7 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
 
 }
 
-__device__ __forceinline__ int route_middles(const RouteView &V) { return V.cnt[4 * kProbes + 2]; }
+__device__ __forceinline__ int route_middles(const RouteView &V) { return V.cnt[kCntMid]; }
 
 // Phase 5 on wave 0: selection = [first page, last page] + the reference
 // min-heap over the middle entries (capacity min(k-2, #middle, 62), strict
