@@ -28,6 +28,7 @@
 //   k_attn_apply    partial o = sum_t w_t v_t over the split's pages;
 //   k_attn_combine  out = (sum over splits) * (1 / l).
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "be42_common.h"
@@ -967,7 +968,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
                                                                     const int *__restrict__ lim, int H, int k_sel,
                                                                     int cap, float scale, float *__restrict__ out,
                                                                     int *__restrict__ sel, int *__restrict__ nsel,
-                                                                    int sel_stride)
+                                                                    int sel_stride, unsigned spin_max)
 {
     constexpr int WAVES = kSplitWaves;
     static_assert(G <= 4 && HD <= 128, "exchange buffers");
@@ -1085,7 +1086,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
             unsigned spins = 0;
             while (ld_dev_u(&sy->flag) == s0) {
                 __builtin_amdgcn_s_sleep(1);
-                if (++spins > kSplitSpinMax) {
+                if (++spins > spin_max) {
                     gave_up = 1;
                     break;
                 }
@@ -1203,6 +1204,15 @@ static bool split_enabled()
     return on;
 }
 
+// polls before a workgroup of a split pair stops waiting for the others and
+// scores every page itself; BE42_ATTN_SPLIT_SPIN overrides it (read at every
+// launch: the tests set 0 to run that path)
+static unsigned split_spin_max()
+{
+    const char *e = getenv("BE42_ATTN_SPLIT_SPIN");
+    return e ? (unsigned)strtoul(e, nullptr, 10) : kSplitSpinMax;
+}
+
 template <bool BF16, int HD, int G, bool STAGE>
 static int launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *slots, int B, int H, int k_sel,
                              int cap, float scale, float *out, int *sel, int *nsel, int sel_stride,
@@ -1221,7 +1231,7 @@ static int launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *s
                 BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_attn_split<HD, G, STAGE>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
             hipLaunchKernelGGL((k_lsh_attn_split<HD, G, STAGE>), dim3(B, P.n_kv, ns), dim3(kSplitWaves * 64), lds, s,
-                               P, q, slots, o.lim, H, k_sel, cap, scale, out, sel, nsel, sel_stride);
+                               P, q, slots, o.lim, H, k_sel, cap, scale, out, sel, nsel, sel_stride, split_spin_max());
             BE42_LAUNCH_CHECK();
             return BE42_OK;
         }

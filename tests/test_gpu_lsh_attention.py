@@ -422,6 +422,31 @@ def test_lsh_attention_split_bit_identical(be, orc, k_sel, cap, frac):
     gp.close()
 
 
+def test_lsh_attention_split_without_waiting(be, orc, monkeypatch):
+    """BE42_ATTN_SPLIT_SPIN=0: a workgroup of a split pair that finds the
+    others not yet arrived stops waiting at once and scores every page
+    itself (the path taken when a pair's workgroups are not resident
+    together); the output keeps the same bits."""
+    rng = np.random.default_rng(1400)
+    n_kv, hd, H = 8, 128, 24
+    lens = (130 * PAGE + 9, 70 * PAGE + 5)
+    _, hpT = orc.lsh_init(hd, 42)
+    q2 = rng.standard_normal((2, H, hd)).astype(np.float32)
+    gp, op, idx = _build(be, orc, OR_KV_BF16, 2, n_kv, hd, 140, lens, rng, hpT,
+                         planted=_planter(orc, hpT, hd, H, q2, 0.1, rng), chunks=(64,))
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    for B in (1, 8):
+        slots = torch.tensor([b % 2 for b in range(B)], dtype=torch.int32, device="cuda")
+        q = torch.from_numpy(q2[[b % 2 for b in range(B)]] + 0.01 * rng.standard_normal((B, H, hd)).astype(np.float32)).cuda()
+        o1, s1, n1 = be.lsh_attention(gp, q, 64, 64, scale, slots=slots)
+        monkeypatch.setenv("BE42_ATTN_SPLIT_SPIN", "0")
+        o2, s2, n2 = be.lsh_attention(gp, q, 64, 64, scale, slots=slots)
+        monkeypatch.delenv("BE42_ATTN_SPLIT_SPIN")
+        assert torch.equal(n1, n2) and torch.equal(s1, s2)
+        np.testing.assert_array_equal(bits(o1.cpu().numpy()), bits(o2.cpu().numpy()), err_msg=f"batch {B}")
+    gp.close()
+
+
 def test_lsh_attention_many_queries(be, orc):
     """65 queries x 8 KV heads (> 512 pairs): be42_lsh_attention runs the
     router and the attention as two launches; the result equals those two
