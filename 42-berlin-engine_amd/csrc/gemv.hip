@@ -1143,10 +1143,15 @@ static TileCfg pick_tile(bool fp8, int nc, int n, int k, int batch)
     // contiguous bytes; long rows, or FP8 at 4096 .. 14336 rows: split K,
     // partials added by a second launch
     // the block-cooperative kernel when k splits into 8 wave ranges of at
-    // most 4 steps (k <= 4096): many rows (the lm_head) at any batch, and
-    // 8193 .. 32768 rows at 1-2 column groups (measured: 14336 x 4096 FP8
-    // batch 1 -6%, INT8 batch 4 -16%; at 3+ groups the split slab is faster)
-    if (n > 32768 || (n > 8192 && nc < 3)) {
+    // most 4 steps (k <= 4096): many rows (the lm_head) at any batch,
+    // 8193 .. 32768 rows at one column group (measured: 14336 x 4096 FP8
+    // batch 1 -6%, INT8 batch 4 -16%), and past 4096 rows at 2-4 column
+    // groups (measured against the other kernels at batch 4-16: the 3B
+    // model's q/k/v (5120 x 3072) FP8 batch 4 15.7 -> 9.4 us, INT8 batch 16
+    // 19.2 -> 10.6 us; gate/up (16384 x 3072) FP8 batch 8 17.8 -> 15.7 us;
+    // 14336 x 4096 INT8 batch 16 19.6 -> 17.5 us).  At 5 groups (FP8 batch
+    // >= 13) the split slab kernel is as fast or faster.
+    if (n > 32768 || (n > 8192 && nc < 3) || (n > 4096 && nc >= 2 && nc <= 4)) {
         const int steps = (int)(xdig_kp(k, fp8) / 128);
         if (steps % kCoopWaves == 0 && steps / kCoopWaves <= 4)
             return TileCfg{0, 6, 0, kCoopWaves, 0, 4, 1};
