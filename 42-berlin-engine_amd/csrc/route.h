@@ -315,10 +315,12 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
     }
     __syncthreads();
     // 5a. ranks of the middle scores for the heap's integer keys (the number
-    //     of strictly smaller ones): wave w counts, for entries lane + 64 j,
-    //     the smaller ones among its quarter of the entries (every lane reads
-    //     the same score: an LDS broadcast)
-    if (wave < 4 && nm > 0) {
+    //     of strictly smaller ones), for more than 64 entries: wave w counts,
+    //     for entries lane + 64 j, the smaller ones among its quarter of the
+    //     entries (every lane reads the same score: an LDS broadcast).  Up to
+    //     64 entries route_select ranks them itself on wave 0, so the other
+    //     waves go on to the attention's scores without this phase.
+    if (wave < 4 && nm > kWave) {
         const int q0i = wave * nm / 4, q1i = (wave + 1) * nm / 4;
         float own[4];
         int r[4];
@@ -379,10 +381,20 @@ __device__ __forceinline__ int route_select(int k_sel, int cap, const RouteView 
     // every middle score is known before the first push: the heap runs on
     // (rank, entry) keys, which order exactly as the scores
     int rk[4];
+    if (nm <= kWave) {
+        // entry lane's rank: a broadcast of every entry's score in turn
+        const float own = V.sc[min(lane, max(nm - 1, 0))];
+        int r = 0;
+        for (int j = 0; j < nm; j++)
+            r += rlf(own, j) < own ? 1 : 0;
+        rk[0] = r;
+        rk[1] = rk[2] = rk[3] = 0;
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int e = min(lane + 64 * j, max(nm - 1, 0));
-        rk[j] = V.rk[e] + V.rk[cap + e] + V.rk[2 * cap + e] + V.rk[3 * cap + e];
+        for (int j = 0; j < 4; j++) {
+            const int e = min(lane + 64 * j, max(nm - 1, 0));
+            rk[j] = V.rk[e] + V.rk[cap + e] + V.rk[2 * cap + e] + V.rk[3 * cap + e];
+        }
     }
     WaveHeapKey heap(ak);
     // the pushes that fill the heap on the scalar unit, then the ones that
