@@ -974,7 +974,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
     static_assert(G <= 4 && HD <= 128, "exchange buffers");
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ AttnShared<HD, G, WAVES> S;
-    __shared__ int set_n, last, alone;
+    __shared__ int set_n, last, alone, xcnt;
     __shared__ unsigned sense;
     const RouteView V = route_view(smem, route_smem(HD, cap, P.max_logical));
     S.red = (float *)smem;
@@ -984,8 +984,10 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // the flag flips only once every workgroup of the pair has arrived, so
     // each reads it before that
-    if (tid == 0)
+    if (tid == 0) {
         sense = ld_dev_u(&sy->flag);
+        xcnt = 0;
+    }
     const int layer = slots ? slots[b] : b;
     const int base = layer * P.max_logical;
     const int lim_b = lim ? lim[b] : 0;
@@ -1040,6 +1042,51 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
     // this workgroup's share of the scored slots: [lo, hi) of the set slots
     // (early) or of the selection (after the heap)
     int lo = z * nset / NS, hi = (z + 1) * nset / NS;
+    float *xs = &g_split_sc[pair][0][0];
+    // Publish the scores of [lo, hi), meet the pair's other workgroups and
+    // take their scores of [0, E) (or, after a wait that did not end, score
+    // every page here): run by waves w0 .. WAVES-1, which sync() joins.
+    auto exchange = [&](int w0, int E, auto &&sync) {
+        const int t = tid - w0 * kWave, nt = (WAVES - w0) * kWave;
+        const int nsh = (hi - lo) * kPg;
+        for (int i = t; i < G * nsh; i += nt) {
+            const int g = i / nsh, r = lo * kPg + i % nsh;
+            const int at = (r / kPg) * 17 + r % kPg;
+            st_dev_f(xs + g * (kSetMax * 17) + at, S.sc[g][at]);
+        }
+        wait_vmcnt<0>();
+        sync();
+        if (t == 0) {
+            const unsigned s0 = sense;
+            int gave_up = 0;
+            if (__hip_atomic_fetch_add(&sy->arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                (unsigned)NS - 1) {
+                st_dev_u(&sy->arrive, 0u);
+                st_dev_u(&sy->flag, s0 ^ 1u);
+            } else {
+                unsigned spins = 0;
+                while (ld_dev_u(&sy->flag) == s0) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins > spin_max) {
+                        gave_up = 1;
+                        break;
+                    }
+                }
+            }
+            alone = gave_up;
+        }
+        sync();
+        if (alone) {
+            attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, E, scale, w0, WAVES - w0, 0);
+        } else {
+            for (int i = t; i < G * E * kPg; i += nt) {
+                const int g = i / (E * kPg), r = i % (E * kPg), sl = r / kPg;
+                const int at = sl * 17 + r % kPg;
+                if (sl < lo || sl >= hi)
+                    S.sc[g][at] = ld_dev_f(xs + g * (kSetMax * 17) + at);
+            }
+        }
+    };
     if (wave == 0) {
         const int ns = route_select(k_sel, cap, V, selb, S.order);
         if (lane == 0) {
@@ -1048,11 +1095,29 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
                 nsel[b] = ns;
         }
     } else if (early) {
+        // the set's scores do not depend on the heap: waves 1.. score this
+        // share, exchange it and take the others' while wave 0 runs the heap,
+        // joined by a counter in LDS (a block barrier would wait for wave 0)
+        int target = 0;
+        auto sync15 = [&] {
+            target += WAVES - 1;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0)
+                __hip_atomic_fetch_add(&xcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            unsigned spins = 0;
+            while (__hip_atomic_load(&xcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > (1u << 22))
+                    break;
+            }
+            asm volatile("" ::: "memory");
+        };
         attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, hi, scale, 1, WAVES - 1, lo);
+        sync15();      // every wave's scores are in LDS before any is published
+        exchange(1, nset, sync15);
     }
     __syncthreads();
     const int ns = set_n;
-    const int E = early ? nset : ns;
     if (!early) {
         for (int i = tid; i < ns; i += blockDim.x) {
             const int slot = S.order[i];
@@ -1065,47 +1130,9 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
         hi = (z + 1) * ns / NS;
         attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, hi, scale, 0, WAVES, lo);
         __syncthreads();
+        exchange(0, ns, [] { __syncthreads(); });
+        __syncthreads();
     }
-    // publish this share, then meet the pair's other workgroups
-    float *xs = &g_split_sc[pair][0][0];
-    const int nsh = (hi - lo) * kPg;
-    for (int i = tid; i < G * nsh; i += blockDim.x) {
-        const int g = i / nsh, r = lo * kPg + i % nsh;
-        const int at = (r / kPg) * 17 + r % kPg;
-        st_dev_f(xs + g * (kSetMax * 17) + at, S.sc[g][at]);
-    }
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned s0 = sense;
-        int gave_up = 0;
-        if (__hip_atomic_fetch_add(&sy->arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)NS - 1) {
-            st_dev_u(&sy->arrive, 0u);
-            st_dev_u(&sy->flag, s0 ^ 1u);
-        } else {
-            unsigned spins = 0;
-            while (ld_dev_u(&sy->flag) == s0) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++spins > spin_max) {
-                    gave_up = 1;
-                    break;
-                }
-            }
-        }
-        alone = gave_up;
-    }
-    __syncthreads();
-    if (alone) {
-        attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, E, scale, 0, WAVES, 0);
-    } else {
-        for (int i = tid; i < G * E * kPg; i += blockDim.x) {
-            const int g = i / (E * kPg), r = i % (E * kPg), sl = r / kPg;
-            const int at = sl * 17 + r % kPg;
-            if (sl < lo || sl >= hi)
-                S.sc[g][at] = ld_dev_f(xs + g * (kSetMax * 17) + at);
-        }
-    }
-    __syncthreads();
     attn_weights(S, ns, early ? S.order : nullptr);
     __syncthreads();
     // value waves z * per .. z * per + per - 1 of the 16-wave layout
