@@ -7,11 +7,14 @@
  * the default stream) and returns without synchronising.  Return value:
  * BE42_OK or a negative BE42_E* code; be42_last_error() then holds a message.
  *
- * One stream at a time per device: the library keeps one grow-only workspace
- * and one split-K partial-sum buffer per process (used by the GEMVs, by
- * be42_paged_attention / be42_lsh_attention without a caller workspace, and
- * by the decoder's fallback paths), so calls that use them must not run
- * concurrently on two streams.  Calls on one stream are always safe.
+ * One stream at a time per device: the library keeps one grow-only workspace,
+ * one split-K partial-sum buffer and the exchange buffers of the split route +
+ * attention per process (used by the GEMVs, by be42_paged_attention /
+ * be42_lsh_attention without a caller workspace, by be42_lsh_attention and the
+ * decoder when at most 64 (query, KV head) pairs are split over several
+ * workgroups each, and by the decoder's fallback paths), so calls that use
+ * them must not run concurrently on two streams.  Calls on one stream are
+ * always safe.
  *
  * The reference-signature entry points built on top of these (op_matmul,
  * paged_kv_append, lsh_hash, op_paged_attention_sparse, ...) are declared in
