@@ -34,6 +34,7 @@
 #include "be42_common.h"
 #include "paged_step.h"
 #include "route.h"
+#include "xdigits.h"
 
 namespace be42 {
 
@@ -944,6 +945,7 @@ struct SplitSync {
 __device__ SplitSync g_split_sync[kSplitMaxPairs];
 __device__ float g_split_sc[kSplitMaxPairs][4][kSetMax * 17];          // scores, AttnShared::sc layout
 __device__ float g_split_o[kSplitMaxPairs][kSplitWaves][4 * 128];       // wave partials [g][dim]
+__device__ unsigned g_split_seq[kSplitMaxPairs];                         // pairs of a query done (digit output)
 
 __device__ __forceinline__ unsigned ld_dev_u(const unsigned *p)
 {
@@ -968,7 +970,8 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
                                                                     const int *__restrict__ lim, int H, int k_sel,
                                                                     int cap, float scale, float *__restrict__ out,
                                                                     int *__restrict__ sel, int *__restrict__ nsel,
-                                                                    int sel_stride, unsigned spin_max)
+                                                                    int sel_stride, unsigned spin_max,
+                                                                    uint8_t *__restrict__ dig, int Kp, int dig_fp8)
 {
     constexpr int WAVES = kSplitWaves;
     static_assert(G <= 4 && HD <= 128, "exchange buffers");
@@ -1160,8 +1163,62 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
         for (int w = 0; w < WAVES; w++)
             v += ld_dev_f(&g_split_o[pair][w][i]);
         const float l = S.lsh[i / HD];
-        out[((size_t)b * H + kvh * G) * HD + i] = l > 0.0f ? v * (1.0f / l) : v;
+        const float o = l > 0.0f ? v * (1.0f / l) : v;
+        if (dig)
+            st_dev_f(out + ((size_t)b * H + kvh * G) * HD + i, o);
+        else
+            out[((size_t)b * H + kvh * G) * HD + i] = o;
     }
+    if (!dig)
+        return;
+    // the last of the query's KV-head pairs to finish writes the query's
+    // output row as the next GEMV's digit planes, as xdig_prepare does
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = __hip_atomic_fetch_add(&g_split_seq[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == (unsigned)gridDim.y - 1;
+        if (last)
+            __hip_atomic_store(&g_split_seq[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last)
+        return;
+    const int K = H * HD, B = gridDim.x;
+    const float *row = out + (size_t)b * K;
+    float m = 0.0f;
+    for (int i4 = tid; 4 * i4 < K; i4 += blockDim.x)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            m = fmaxf(m, fabsf(ld_dev_f(row + 4 * i4 + e)));
+    m = wave_max(m);
+    __syncthreads();
+    if (lane == 0)
+        S.red[wave] = m;
+    __syncthreads();
+    float amax = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; w++)
+        amax = fmaxf(amax, S.red[w]);
+    auto put = [&](auto f8) {
+        constexpr bool F8 = decltype(f8)::value;
+        const float sc = digit_scale<F8>(amax);
+        if (tid == 0)
+            xdig_scales(dig, K, B, F8)[b] = sc;
+        for (int i4 = tid; 4 * i4 < Kp; i4 += blockDim.x) {
+            const int k0 = 4 * i4;
+            float xe[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (k0 < K)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    xe[e] = ld_dev_f(row + k0 + e);
+            store_digit_words<F8>(xe, sc, dig, B, Kp, b, k0);
+        }
+    };
+    if (dig_fp8)
+        put(std::true_type());
+    else
+        put(std::false_type());
 }
 
 // 16 waves when the grid is small (more loads in flight per workgroup), 8
@@ -1219,6 +1276,12 @@ static size_t lsh_attn_lds(const RouteSmem &L)
 struct LshAttnOpt {
     const int *lim = nullptr;
     bool wide16 = false;
+    // optional: the output rows as GEMV digit planes (xdig_prepare's layout
+    // for k = H * head_dim), written by split launches; dig_done tells
+    // whether this launch wrote them
+    void *dig = nullptr;
+    bool dig_fp8 = false;
+    bool *dig_done = nullptr;
 };
 
 // BE42_ATTN_SPLIT=0 keeps every launch at one workgroup per (query, KV head)
@@ -1257,8 +1320,12 @@ static int launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *s
             if (lds > 65536)
                 BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_attn_split<HD, G, STAGE>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            const int Kp = o.dig ? (int)xdig_kp(H * HD, o.dig_fp8) : 0;
             hipLaunchKernelGGL((k_lsh_attn_split<HD, G, STAGE>), dim3(B, P.n_kv, ns), dim3(kSplitWaves * 64), lds, s,
-                               P, q, slots, o.lim, H, k_sel, cap, scale, out, sel, nsel, sel_stride, split_spin_max());
+                               P, q, slots, o.lim, H, k_sel, cap, scale, out, sel, nsel, sel_stride, split_spin_max(),
+                               (uint8_t *)o.dig, Kp, (int)o.dig_fp8);
+            if (o.dig_done)
+                *o.dig_done = o.dig != nullptr;
             BE42_LAUNCH_CHECK();
             return BE42_OK;
         }
@@ -1449,6 +1516,30 @@ namespace be42 {
 
 // Prefill attention: query b of slot slots[b] sees the first lim[b]
 // positions, computed exactly as a one-query decode launch computes it.
+// be42_lsh_attention for the decoder's unfused steps: when the launch is a
+// split one, it also writes the output rows as the o projection's digit
+// planes (xdig, xdig_prepare's layout) and sets *done.
+int lsh_attention_digits(const be42_kv_pool &P, const float *q, const int *slots, int n_queries, int n_heads,
+                         int k_sel, int cand_cap, float scale, float *out, int *sel, int *n_sel, int sel_stride,
+                         void *xdig, bool fp8, bool *done, hipStream_t s)
+{
+    *done = false;
+    if ((long)n_queries * P.n_kv > 1024)
+        return be42_lsh_attention(&P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, sel, n_sel,
+                                  sel_stride, s);
+    BE42_CHECK(k_sel > 0 && k_sel <= kFusedMaxPages && cand_cap > 0 && cand_cap <= kMaxCand &&
+                   n_heads % P.n_kv == 0 && n_heads / P.n_kv <= 4 && (P.head_dim == 64 || P.head_dim == 128),
+               "lsh_attention_digits: unsupported shape");
+    if (n_queries <= 0)
+        return BE42_OK;
+    LshAttnOpt o;
+    o.dig = xdig;
+    o.dig_fp8 = fp8;
+    o.dig_done = done;
+    return launch_lsh_attn(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, sel, n_sel, sel_stride, o,
+                           s);
+}
+
 int lsh_attention_prefix(const be42_kv_pool &P, const float *q, const int *slots, const int *lim, int n_queries,
                          int n_heads, int k_sel, int cand_cap, float scale, float *out, hipStream_t s)
 {

@@ -1419,14 +1419,21 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
             BE42_HIP(hipMemcpyAsync(d->capture_v + (size_t)l * c.max_batch * kd, d->v, (size_t)B * kd * 4,
                                     hipMemcpyDeviceToDevice, st));
         const int *lslots = d->slots + (size_t)l * c.max_batch;
+        bool att_digits = false;   // the attention wrote d->att's digit planes into d->xdig
         if (!sparse) {
             DEC_TRY(be42_paged_attention(d->pool, d->q, B, H, P.page_table + (size_t)l * c.max_batch * P.max_logical,
                                          P.n_logical + (size_t)l * c.max_batch, P.max_logical, dense_max, scale,
                                          d->att, dense_max <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
         } else if (fused_route) {
-            // route + attention in one launch
-            DEC_TRY(be42_lsh_attention(d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, scale, d->att, d->sel,
-                                       d->nsel, std::max(c.sparse_k, 64), st));
+            // route + attention in one launch; without the fused layer a split
+            // launch also writes the o projection's digit planes
+            if (fz)
+                DEC_TRY(be42_lsh_attention(d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, scale, d->att,
+                                           d->sel, d->nsel, std::max(c.sparse_k, 64), st));
+            else
+                DEC_TRY(lsh_attention_digits(*d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, scale, d->att,
+                                             d->sel, d->nsel, std::max(c.sparse_k, 64), d->xdig, fp8 != 0,
+                                             &att_digits, st));
         } else {
             const int stride = std::max(c.sparse_k, 64);
             DEC_TRY(be42_lsh_route(d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, d->sel, d->nsel, stride,
@@ -1448,7 +1455,8 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
             DEC_TRY(launch_fused_layer(d, l, app, &head->pos, rope_len, st));
             continue;
         }
-        DEC_TRY(be42_gemv_prepare(d->xdig, d->att, qd, B, fp8, st));
+        if (!att_digits)
+            DEC_TRY(be42_gemv_prepare(d->xdig, d->att, qd, B, fp8, st));
         DEC_TRY(gemv(d, d->xb, L.wo, L.so, dim, qd, B, st));
         BE42_HIP(norm(L.ffn_norm, d->xb));                 // x += attention output
         DEC_TRY(gemv_multi(d, {{L.w1, L.s1, d->hb, c.hidden_dim}, {L.w3, L.s3, d->hb2, c.hidden_dim}}, dim, B, st));

@@ -69,4 +69,11 @@ int launch_append_run(const be42_kv_pool &P, const AppendRun &r, const int *d_li
 int lsh_attention_prefix(const be42_kv_pool &P, const float *q, const int *slots, const int *lim, int n_queries,
                          int n_heads, int k_sel, int cand_cap, float scale, float *out, hipStream_t s);
 
+// be42_lsh_attention that, when the launch splits each (query, KV head) pair
+// over several workgroups, also writes the output rows as GEMV digit planes
+// (xdig_prepare's layout, k = n_heads * head_dim) and sets *done
+int lsh_attention_digits(const be42_kv_pool &P, const float *q, const int *slots, int n_queries, int n_heads,
+                         int k_sel, int cand_cap, float scale, float *out, int *sel, int *n_sel, int sel_stride,
+                         void *xdig, bool fp8, bool *done, hipStream_t s);
+
 }  // namespace be42
