@@ -1020,10 +1020,16 @@ static bool fused_layer_fits(const be42_decoder_config &c, be42_decoder *d)
         (size_t)(nd + 8) * c.dim + 16 > (size_t)kFDigBytes ||
         (size_t)(c.n_heads / c.n_kv_heads + 2) * c.head_dim * 4 + 1024 > (size_t)kFDigBytes || c.n_kv_heads > cus)
         return false;
+    // one block per CU, but no more blocks than the largest phase has row
+    // tiles (or gate/up tile pairs): a small model's barriers then gather
+    // fewer blocks
+    const int units_max = std::max(std::max((c.dim + 15) / 16, (c.hidden_dim + 15) / 16),
+                                   (qd + 2 * kd + 15) / 16 + 2);
+    const int nb = std::max(std::min(cus, units_max), c.n_kv_heads);
     // every block's tiles (rounded up to a power of two) share its 8 waves,
     // and a wave's K steps must fit its registers
     auto ok = [&](int units, bool pairs, int K) {
-        const int cnt = (units + cus - 1) / cus * (pairs ? 2 : 1);
+        const int cnt = (units + nb - 1) / nb * (pairs ? 2 : 1);
         if (cnt > kFMaxTiles)
             return false;
         const int np = cnt <= 1 ? 1 : (cnt <= 2 ? 2 : (cnt <= 4 ? 4 : 8));
@@ -1033,7 +1039,7 @@ static bool fused_layer_fits(const be42_decoder_config &c, be42_decoder *d)
     if (!ok((c.dim + 15) / 16, false, qd) || !ok((c.hidden_dim + 15) / 16, true, c.dim) ||
         !ok((c.dim + 15) / 16, false, c.hidden_dim) || !ok((qd + 2 * kd + 15) / 16 + 2, false, c.dim))
         return false;
-    d->fnb = cus;
+    d->fnb = nb;
     return true;
 }
 
