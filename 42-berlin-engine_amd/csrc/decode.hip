@@ -237,6 +237,58 @@ __global__ __launch_bounds__(kRowT) void k_silu_mul(float *__restrict__ out, uin
     row_chunk_digits<FP8, NV>(h, n, dig, out, B, b, c, red);
 }
 
+// k_silu_mul of a whole row by one 1024-thread block (the decoder's batched
+// steps, without an fp32 copy): the same elements, maximum and digits as the
+// 256-thread chunked kernel -- a maximum does not depend on its order -- in
+// a quarter of the per-thread work.  NV * 4096 >= the digit planes' row.
+constexpr int kWideT = 1024;
+template <bool FP8, int NV>
+__global__ __launch_bounds__(kWideT) void k_silu_mul_wide(uint8_t *__restrict__ dig, const float *__restrict__ g,
+                                                         const float *__restrict__ u, int n, int B)
+{
+    __shared__ float red[kWideT / kWave];
+    const int b = blockIdx.x, tid = threadIdx.x, n4 = n >> 2, nvec = n & ~7;
+    const float4 *g4 = (const float4 *)(g + (size_t)b * n), *u4 = (const float4 *)(u + (size_t)b * n);
+    float4 gv[NV], uv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = min(tid + kWideT * j, n4 - 1);
+        gv[j] = g4[i];
+        uv[j] = u4[i];
+    }
+    float4 h[NV];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = tid + kWideT * j, e0 = 4 * i;
+        h[j] = make_float4(silu_mul1(gv[j].x, uv[j].x, e0 < nvec), silu_mul1(gv[j].y, uv[j].y, e0 + 1 < nvec),
+                           silu_mul1(gv[j].z, uv[j].z, e0 + 2 < nvec), silu_mul1(gv[j].w, uv[j].w, e0 + 3 < nvec));
+        if (i >= n4)
+            h[j] = f4_zero();
+        m = fmaxf(m, f4_absmax(h[j]));
+    }
+    m = wave_max(m);
+    if ((tid & (kWave - 1)) == 0)
+        red[tid / kWave] = m;
+    __syncthreads();
+    float amax = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWideT / kWave; w++)
+        amax = fmaxf(amax, red[w]);
+    const float sc = digit_scale<FP8>(amax);
+    const int Kp = (int)xdig_kp(n, FP8);
+    if (tid == 0)
+        xdig_scales(dig, n, B, FP8)[b] = sc;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int k0 = 4 * (tid + kWideT * j);
+        if (k0 < Kp) {
+            const float xe[4] = {h[j].x, h[j].y, h[j].z, h[j].w};
+            store_digit_words<FP8>(xe, sc, dig, B, Kp, b, k0);
+        }
+    }
+}
+
 // argmax_simd_f32: the maximum value wins; among equal maxima in the
 // 8-lane part (indices below 8*floor(n/8), n >= 8) the lowest lane (i % 8),
 // then the first index; tail entries win only with a strictly larger value.
@@ -1466,11 +1518,25 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         DEC_TRY(gemv(d, d->xb, L.wo, L.so, dim, qd, B, st));
         BE42_HIP(norm(L.ffn_norm, d->xb));                 // x += attention output
         DEC_TRY(gemv_multi(d, {{L.w1, L.s1, d->hb, c.hidden_dim}, {L.w3, L.s3, d->hb2, c.hidden_dim}}, dim, B, st));
-        launch_rows(fp8, c.hidden_dim, [&](auto f8, auto nv) {
-            hipLaunchKernelGGL((k_silu_mul<decltype(f8)::value, decltype(nv)::value>),
-                               dim3((c.hidden_dim + kChunk - 1) / kChunk, B), dim3(kRowT), 0, st, nullptr, dig, d->hb,
-                               d->hb2, c.hidden_dim, B, false);
-        });
+        const int nvw = (int)((xdig_kp(c.hidden_dim, fp8) + 4 * kWideT - 1) / (4 * kWideT));
+        if (nvw <= 2) {
+            auto wide = [&](auto f8, auto nv) {
+                hipLaunchKernelGGL((k_silu_mul_wide<decltype(f8)::value, decltype(nv)::value>), dim3(B),
+                                   dim3(kWideT), 0, st, dig, d->hb, d->hb2, c.hidden_dim, B);
+            };
+            if (fp8)
+                nvw <= 1 ? wide(std::true_type(), std::integral_constant<int, 1>())
+                         : wide(std::true_type(), std::integral_constant<int, 2>());
+            else
+                nvw <= 1 ? wide(std::false_type(), std::integral_constant<int, 1>())
+                         : wide(std::false_type(), std::integral_constant<int, 2>());
+        } else {
+            launch_rows(fp8, c.hidden_dim, [&](auto f8, auto nv) {
+                hipLaunchKernelGGL((k_silu_mul<decltype(f8)::value, decltype(nv)::value>),
+                                   dim3((c.hidden_dim + kChunk - 1) / kChunk, B), dim3(kRowT), 0, st, nullptr, dig,
+                                   d->hb, d->hb2, c.hidden_dim, B, false);
+            });
+        }
         BE42_LAUNCH_CHECK();
         DEC_TRY(gemv(d, d->xb, L.w2, L.s2, dim, c.hidden_dim, B, st));
         pending = d->xb;
