@@ -400,6 +400,63 @@ def digit_gemm_bench(lib, steps, warmup):
             "by_shape": rows}
 
 
+# ---- the drop-in boundary with host arrays (PCIe-inclusive) -----------------------
+def dropin_bench(lib, calls=50):
+    """op_matmul (ops_matmul.c:366) called the way the reference's forward
+    pass calls it: t_tensor operands in host memory, b = x as [k][1].  The
+    library mirrors a host weight once (the first call, timed apart as
+    `first_call_ms`: the weight's PCIe upload); every later call stages x in
+    and y out over PCIe and waits for the result, so `us_per_call` is the
+    caller's wall time per GEMV and `GBps` counts the algorithmic weight bytes
+    over it.  Reported beside the device-resident sweep; never `value`."""
+    import ctypes as C
+    import numpy as np
+
+    class TTensor(C.Structure):           # be42_engine.h t_tensor (tensor.h:19-39)
+        _fields_ = [("data", C.c_void_p), ("shape", C.c_int * 4), ("stride", C.c_int * 4), ("ndim", C.c_int),
+                    ("size", C.c_size_t), ("dtype", C.c_int), ("row_scale", C.c_void_p)]
+
+    def tt(a, dtype, rows, cols, scale=None):
+        t = TTensor()
+        t.data, t.ndim, t.size, t.dtype = a.ctypes.data, 2, rows * cols, dtype
+        t.shape[0], t.shape[1], t.stride[0], t.stride[1] = rows, cols, cols, 1
+        t.row_scale = scale.ctypes.data if scale is not None else None
+        return t
+
+    fn = lib.lib.op_matmul
+    fn.restype = C.c_int
+    fn.argtypes = [C.POINTER(TTensor)] * 3
+    rng = np.random.default_rng(17)
+    rows = []
+    for kind, dt in (("int8", 2), ("fp8", 3)):
+        for n, k in ((4096, 4096), (14336, 4096)):
+            if kind == "int8":
+                w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+            else:   # E4M3 codes without the NaN patterns (0x7F / 0xFF)
+                w = rng.integers(0, 0x7F, (n, k), dtype=np.uint8) | (rng.integers(0, 2, (n, k), dtype=np.uint8) << 7)
+            s = (rng.random(n, dtype=np.float32) * 0.015 + 0.005).astype(np.float32)
+            x = rng.standard_normal((k, 1)).astype(np.float32)
+            y = np.zeros((n, 1), np.float32)
+            ta, tb, to = tt(w, dt, n, k, s), tt(x, 0, k, 1), tt(y, 0, n, 1)
+            t0 = time.perf_counter()
+            if fn(C.byref(to), C.byref(ta), C.byref(tb)) != 0:
+                raise RuntimeError(f"op_matmul {kind} {n}x{k} failed")
+            first = time.perf_counter() - t0
+            for _ in range(3):
+                fn(C.byref(to), C.byref(ta), C.byref(tb))
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                fn(C.byref(to), C.byref(ta), C.byref(tb))
+            per = (time.perf_counter() - t0) / calls
+            nb = gemv_bytes(n, k, 1)
+            rows.append({"dtype": kind, "n": n, "k": k, "batch": 1, "first_call_ms": round(first * 1e3, 2),
+                         "us_per_call": round(per * 1e6, 2), "GBps": round(nb / per / 1e9, 1)})
+            del w, s, x, y
+    return {"workload": "op_matmul with host t_tensor operands (weights mirrored once, x / y staged over PCIe "
+                        "each call), configs[1] shapes 4096x4096 and 14336x4096, batch 1",
+            "calls": calls, "by_shape": rows}
+
+
 # ---- decode step (BASELINE.json configs[0] and configs[4]) -----------------------
 TINY = dict(n_layers=4, dim=512, n_heads=8, n_kv_heads=8, head_dim=64, hidden_dim=1408, vocab=4096)
 B3 = dict(n_layers=28, dim=3072, n_heads=24, n_kv_heads=8, head_dim=128, hidden_dim=8192, vocab=128256)
@@ -903,6 +960,7 @@ def main():
     ap.add_argument("--no-lsh", action="store_true", help="skip the LSH attention leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step leg")
+    ap.add_argument("--no-dropin", action="store_true", help="skip the host-array op_matmul (PCIe) leg")
     ap.add_argument("--no-3b", action="store_true", help="skip the 3B-model decode (its setup takes ~1 minute)")
     ap.add_argument("--pmc-probe", action="store_true", help="only run the kernels profiled for HBM traffic")
     ap.add_argument("--lsh-probe", action="store_true", help="only run the LSH launches profiled for HBM traffic")
@@ -1049,6 +1107,8 @@ def main():
                "config": {"workload": "GEMV sweep skipped (--no-gemv)", "parallelism": "single GPU"}}
     else:
         out, configs = gemv_sweep()
+    if not args.no_dropin:
+        out["dropin_pcie"] = dropin_bench(lib)
     if not args.no_decode:
         configs.clear()
         torch.cuda.empty_cache()
