@@ -64,6 +64,8 @@ SIGNATURES = {
     "be42_decoder_step": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "be42_decoder_prefill": (i32, [vp, i32, vp, i32, i32, vp, vp, vp]),
     "be42_decoder_next_tokens": (i32, [vp, vp]),
+    "be42_decoder_status": (i32, [vp]),
+    "be42_lsh_attention_status": (i32, [vp]),
     "be42_decoder_capture": (i32, [vp, vp, vp]),
     "be42_decoder_capture_kv": (i32, [vp, vp, vp]),
     "be42_decoder_capture_sel": (i32, [vp, vp]),
@@ -540,6 +542,10 @@ class Decoder:
         self.lib._call("be42_decoder_prefill", self.handle, int(seq), t.ctypes.data, len(t), int(pos0),
                        nxt.ctypes.data, self.lib.p(logits), self.lib.stream())
         return int(nxt[0])
+
+    def status(self):
+        """Waits for the queued steps; raises if a grid barrier timed out."""
+        self.lib._call("be42_decoder_status", self.handle)
 
     def capture(self, q=None, nsel=None):
         self.lib._call("be42_decoder_capture", self.handle, self.lib.p(q), self.lib.p(nsel))

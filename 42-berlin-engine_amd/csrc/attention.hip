@@ -939,6 +939,7 @@ __global__ __launch_bounds__(WAVES * 64, 4) void k_lsh_attn(const be42_kv_pool P
 constexpr int kSplitMaxPairs = 128;           // (query, KV head) pairs of a split launch
 constexpr int kSplitWaves = 16;                // the value layout a split launch reproduces
 constexpr unsigned kSplitSpinMax = 1u << 14;
+constexpr unsigned kSplitSpinCap = 1u << 20;   // largest poll limit a caller may set
 struct SplitSync {
     unsigned arrive, flag, done, pad[13];      // one 64-byte line per pair
 };
@@ -946,6 +947,10 @@ __device__ SplitSync g_split_sync[kSplitMaxPairs];
 __device__ float g_split_sc[kSplitMaxPairs][4][kSetMax * 17];          // scores, AttnShared::sc layout
 __device__ float g_split_o[kSplitMaxPairs][kSplitWaves][4 * 128];       // wave partials [g][dim]
 __device__ unsigned g_split_seq[kSplitMaxPairs];                         // pairs of a query done (digit output)
+// error word of split launches whose caller gave none (be42_lsh_attention):
+// 4 = a wait among a workgroup's own waves gave up (its output is invalid);
+// read and cleared by be42_lsh_attention_status
+__device__ int g_attn_err;
 
 __device__ __forceinline__ unsigned ld_dev_u(const unsigned *p)
 {
@@ -971,7 +976,8 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
                                                                     int cap, float scale, float *__restrict__ out,
                                                                     int *__restrict__ sel, int *__restrict__ nsel,
                                                                     int sel_stride, unsigned spin_max,
-                                                                    uint8_t *__restrict__ dig, int Kp, int dig_fp8)
+                                                                    uint8_t *__restrict__ dig, int Kp, int dig_fp8,
+                                                                    int *__restrict__ err)
 {
     constexpr int WAVES = kSplitWaves;
     static_assert(G <= 4 && HD <= 128, "exchange buffers");
@@ -1107,11 +1113,18 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (lane == 0)
                 __hip_atomic_fetch_add(&xcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            // every wave of the group gets here within its own bounded work
+            // (wave 1's cross-workgroup wait polls at most kSplitSpinCap
+            // times), so this bound is only a guard: reaching it means the
+            // scores may be incomplete, which the error word reports
             unsigned spins = 0;
             while (__hip_atomic_load(&xcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
                 __builtin_amdgcn_s_sleep(1);
-                if (++spins > (1u << 22))
+                if (++spins > (kSplitSpinCap << 2)) {
+                    if (lane == 0)
+                        __hip_atomic_store(err, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
+                }
             }
             asm volatile("" ::: "memory");
         };
@@ -1282,6 +1295,7 @@ struct LshAttnOpt {
     void *dig = nullptr;
     bool dig_fp8 = false;
     bool *dig_done = nullptr;
+    int *err = nullptr;   // device error word of split launches (else g_attn_err)
 };
 
 // BE42_ATTN_SPLIT=0 keeps every launch at one workgroup per (query, KV head)
@@ -1300,7 +1314,20 @@ static bool split_enabled()
 static unsigned split_spin_max()
 {
     const char *e = getenv("BE42_ATTN_SPLIT_SPIN");
-    return e ? (unsigned)strtoul(e, nullptr, 10) : kSplitSpinMax;
+    const unsigned long v = e ? strtoul(e, nullptr, 10) : kSplitSpinMax;
+    return v < kSplitSpinCap ? (unsigned)v : kSplitSpinCap;
+}
+
+// device address of g_attn_err (the current device's copy)
+static int *attn_err_default()
+{
+    static int *p[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return nullptr;
+    if (!p[dev] && hipGetSymbolAddress((void **)&p[dev], HIP_SYMBOL(g_attn_err)) != hipSuccess)
+        p[dev] = nullptr;
+    return p[dev];
 }
 
 template <bool BF16, int HD, int G, bool STAGE>
@@ -1321,9 +1348,11 @@ static int launch_lsh_attn_s(const be42_kv_pool &P, const float *q, const int *s
                 BE42_HIP(hipFuncSetAttribute((const void *)k_lsh_attn_split<HD, G, STAGE>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
             const int Kp = o.dig ? (int)xdig_kp(H * HD, o.dig_fp8) : 0;
+            int *err = o.err ? o.err : attn_err_default();
+            BE42_CHECK(err, "lsh attention: no address for the error word");
             hipLaunchKernelGGL((k_lsh_attn_split<HD, G, STAGE>), dim3(B, P.n_kv, ns), dim3(kSplitWaves * 64), lds, s,
                                P, q, slots, o.lim, H, k_sel, cap, scale, out, sel, nsel, sel_stride, split_spin_max(),
-                               (uint8_t *)o.dig, Kp, (int)o.dig_fp8);
+                               (uint8_t *)o.dig, Kp, (int)o.dig_fp8, err);
             if (o.dig_done)
                 *o.dig_done = o.dig != nullptr;
             BE42_LAUNCH_CHECK();
@@ -1469,6 +1498,22 @@ extern "C" int be42_paged_attention(const be42_kv_pool *pool, const float *q, in
     return BE42_OK;
 }
 
+extern "C" int be42_lsh_attention_status(void *stream)
+{
+    BE42_HIP(hipStreamSynchronize(as_stream(stream)));
+    int *p = attn_err_default();
+    BE42_CHECK(p, "be42_lsh_attention_status: no address for the error word");
+    int v = 0;
+    BE42_HIP(hipMemcpy(&v, p, sizeof v, hipMemcpyDeviceToHost));
+    if (v) {
+        const int zero = 0;
+        BE42_HIP(hipMemcpy(p, &zero, sizeof zero, hipMemcpyHostToDevice));
+    }
+    BE42_CHECK(v == 0, "be42_lsh_attention: a wait inside a split launch gave up (code %d); the output of a launch "
+                       "since the last check is invalid", v);
+    return BE42_OK;
+}
+
 extern "C" int be42_lsh_attention(const be42_kv_pool *pool, const float *q, const int *slots, int n_queries,
                                   int n_heads, int k_sel, int cand_cap, float scale, float *out, int *sel,
                                   int *n_sel, int sel_stride, void *stream)
@@ -1521,7 +1566,7 @@ namespace be42 {
 // planes (xdig, xdig_prepare's layout) and sets *done.
 int lsh_attention_digits(const be42_kv_pool &P, const float *q, const int *slots, int n_queries, int n_heads,
                          int k_sel, int cand_cap, float scale, float *out, int *sel, int *n_sel, int sel_stride,
-                         void *xdig, bool fp8, bool *done, hipStream_t s)
+                         void *xdig, bool fp8, bool *done, int *err, hipStream_t s)
 {
     *done = false;
     if ((long)n_queries * P.n_kv > 1024)
@@ -1536,6 +1581,7 @@ int lsh_attention_digits(const be42_kv_pool &P, const float *q, const int *slots
     o.dig = xdig;
     o.dig_fp8 = fp8;
     o.dig_done = done;
+    o.err = err;
     return launch_lsh_attn(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, sel, n_sel, sel_stride, o,
                            s);
 }

@@ -504,6 +504,8 @@ struct FusedArgs {
     float eps;
     unsigned *flags, *gen;
     int *err;
+    unsigned spin_max;   // polls before a grid-barrier wait gives up
+    unsigned bias;       // added to the numbers waited for (0; a test sets it so no wait completes)
 };
 
 struct GridBar {
@@ -511,6 +513,7 @@ struct GridBar {
     unsigned base;
     int nb;
     int *err;
+    unsigned spin_max, bias;
 };
 
 __device__ __forceinline__ bool flag_before(unsigned v, unsigned target) { return (int)(v - target) < 0; }
@@ -522,7 +525,7 @@ template <class F>
 __device__ __forceinline__ void grid_barrier(const GridBar &gb, unsigned idx, F &&during)
 {
     __shared__ int failed;
-    const unsigned target = gb.base + idx;
+    const unsigned target = gb.base + idx, awaited = target + gb.bias;
     wait_vmcnt<0>();              // this thread's stores have completed
     if (threadIdx.x == 0)
         failed = __hip_atomic_load(gb.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
@@ -536,8 +539,8 @@ __device__ __forceinline__ void grid_barrier(const GridBar &gb, unsigned idx, F 
         for (int i = threadIdx.x; i < gb.nb; i += blockDim.x) {
             unsigned spins = 0;
             while (flag_before(__hip_atomic_load(gb.flags + i * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                               target))
-                if (++spins > kFSpinMax) {
+                               awaited))
+                if (++spins > gb.spin_max) {
                     atomicExch(gb.err, 1);
                     break;
                 }
@@ -549,8 +552,8 @@ __device__ __forceinline__ void grid_barrier(const GridBar &gb, unsigned idx, F 
     if (threadIdx.x == 0 && !skip) {
         unsigned spins = 0;
         while (flag_before(__hip_atomic_load(gb.flags + gb.nb * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                           target))
-            if (++spins > kFSpinMax) {
+                           awaited))
+            if (++spins > gb.spin_max) {
                 atomicExch(gb.err, 2);
                 break;
             }
@@ -921,7 +924,8 @@ __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
         qcnt = 0;
     __syncthreads();
     QuadSync quad{&qcnt, 0, A.err};
-    GridBar gb{A.flags, __hip_atomic_load(A.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kFBars, nb, A.err};
+    GridBar gb{A.flags, __hip_atomic_load(A.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kFBars, nb, A.err,
+               A.spin_max, A.bias};
     v8i fr[kFMaxU];
 #pragma unroll
     for (int u = 0; u < kFMaxU; u++)
@@ -1027,7 +1031,7 @@ struct be42_decoder {
     void *params_host[2] = {nullptr, nullptr}, *params_dev[2] = {nullptr, nullptr};
     hipEvent_t params_free[2] = {nullptr, nullptr};
     int parity = 0;
-    int *next_host = nullptr;     // pinned copy of the argmax [kMaxBatch], then the fused layer's error flag
+    int *next_host = nullptr;     // pinned copy of d->next: the argmax [kMaxBatch], then the error word
     hipStream_t gstream = nullptr;
     hipEvent_t ev_in = nullptr, ev_out = nullptr;
     struct Key {
@@ -1046,8 +1050,12 @@ struct be42_decoder {
     // the fused layer of one-sequence steps: grid = the CU count; barrier
     // flags [(nb + 1) * 32], launch counter, error flag (device, zeroed at create)
     bool fused = false;
+    bool fail_barriers = false;   // test: every grid-barrier wait gives up
     int fnb = 0;
     unsigned *fflags = nullptr;
+    // a fused launch's error flag seen set: the decoder's state is invalid and
+    // every later step or prefill is refused (the device flag stays set)
+    int fault = 0;
     // prefill activations [kPrefillChunk][...], digit planes, and the chunk's
     // metadata (tokens [T], visible lengths [T], slots [n_layers][T]) with
     // its pinned host copy; allocated by the first prefill
@@ -1158,7 +1166,7 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
     alloc((void **)&d->sel, (size_t)B * std::max(c.sparse_k, 64) * 4);
     alloc((void **)&d->nsel, (size_t)B * 4);
     alloc((void **)&d->slots, (size_t)c.n_layers * B * 4);
-    alloc((void **)&d->next, (size_t)B * 4);
+    alloc((void **)&d->next, (size_t)(kMaxBatch + 1) * 4);   // tokens, then the step's error word
     alloc((void **)&d->arg_parts, (size_t)B * kArgChunks * sizeof(ArgPart));
     alloc((void **)&d->arg_cnt, (size_t)B * 4);
     alloc((void **)&d->cand, (size_t)B * std::max(c.cand_cap, 1) * 4);
@@ -1197,7 +1205,7 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
     if (e == hipSuccess)
         e = hipEventCreateWithFlags(&d->ev_out, hipEventDisableTiming);
     if (e == hipSuccess)
-        e = hipMemset(d->next, 0, (size_t)B * 4);
+        e = hipMemset(d->next, 0, (size_t)(kMaxBatch + 1) * 4);
     if (e == hipSuccess)
         e = hipMemset(d->arg_cnt, 0, (size_t)B * 4);
     {
@@ -1212,6 +1220,8 @@ extern "C" int be42_decoder_create(be42_decoder **out, const be42_decoder_config
             if (e == hipSuccess)
                 e = hipMemset(d->fflags, 0, fbytes);
             d->fused = e == hipSuccess;
+            const char *fb = getenv("BE42_DECODE_FAIL_BARRIERS");
+            d->fail_barriers = fb && fb[0] == '1';
         }
     }
     if (e == hipSuccess)
@@ -1384,7 +1394,9 @@ static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app,
     A.eps = c.norm_eps;
     A.flags = d->fflags;
     A.gen = d->fflags + ((size_t)d->fnb + 1) * 32;
-    A.err = (int *)(A.gen + 1);
+    A.err = d->next + kMaxBatch;
+    A.spin_max = d->fail_barriers ? 64u : kFSpinMax;
+    A.bias = d->fail_barriers ? 1u << 24 : 0u;
     const int nv = (dim + kChunk - 1) / kChunk;
     const bool fp8 = c.wkind != 0, bf16 = c.kv_kind == BE42_KV_BF16;
     auto go = [&](auto f8, auto kb, auto nvc) {
@@ -1485,13 +1497,9 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         } else if (fused_route) {
             // route + attention in one launch; without the fused layer a split
             // launch also writes the o projection's digit planes
-            if (fz)
-                DEC_TRY(be42_lsh_attention(d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, scale, d->att,
-                                           d->sel, d->nsel, std::max(c.sparse_k, 64), st));
-            else
-                DEC_TRY(lsh_attention_digits(*d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, scale, d->att,
-                                             d->sel, d->nsel, std::max(c.sparse_k, 64), d->xdig, fp8 != 0,
-                                             &att_digits, st));
+            DEC_TRY(lsh_attention_digits(*d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, scale, d->att,
+                                         d->sel, d->nsel, std::max(c.sparse_k, 64), fz ? nullptr : d->xdig,
+                                         fp8 != 0, &att_digits, d->next + kMaxBatch, st));
         } else {
             const int stride = std::max(c.sparse_k, 64);
             DEC_TRY(be42_lsh_route(d->pool, d->q, lslots, B, H, c.sparse_k, c.cand_cap, d->sel, d->nsel, stride,
@@ -1554,15 +1562,44 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     hipLaunchKernelGGL(k_argmax, dim3(kArgChunks, B), dim3(256), 0, st, d->next, lg, c.vocab, d->arg_parts,
                        d->arg_cnt);
     BE42_LAUNCH_CHECK();
-    BE42_HIP(hipMemcpyAsync(d->next_host, d->next, (size_t)B * 4, hipMemcpyDeviceToHost, st));
-    if (fz)
-        BE42_HIP(hipMemcpyAsync(d->next_host + kMaxBatch, d->fflags + ((size_t)d->fnb + 1) * 32 + 1, 4,
-                                hipMemcpyDeviceToHost, st));
+    BE42_HIP(hipMemcpyAsync(d->next_host, d->next, (size_t)(kMaxBatch + 1) * 4, hipMemcpyDeviceToHost, st));
     return BE42_OK;
 }
 
 static int launch_step(be42_decoder *d, int B, int pos, bool host_tokens, float *logits_out, hipStream_t caller,
                        bool *queued);
+
+// The fused launches' error flag as the last finished step copied it to the
+// host (wait: for the decoder's queued work first).  Once it is seen set the
+// decoder's results and cache are invalid, and every later call is refused.
+static int fault_check(be42_decoder *d, bool wait, const char *what)
+{
+    if (!d->fault) {
+        if (wait) {
+            BE42_HIP(hipEventSynchronize(d->ev_out));
+            d->fault = d->next_host[kMaxBatch];
+        } else {
+            const hipError_t q = hipEventQuery(d->ev_out);
+            if (q == hipSuccess)
+                d->fault = d->next_host[kMaxBatch];
+            else if (q == hipErrorNotReady)
+                (void)hipGetLastError();
+            else
+                BE42_HIP(q);
+        }
+    }
+    BE42_CHECK(d->fault == 0,
+               "%s: a bounded wait gave up in an earlier step (code %d: 1-2 a grid barrier of the fused layer, 3 its "
+               "wave sync, 4 the split attention's); the decoder's results and cache are invalid (destroy it)",
+               what, d->fault);
+    return BE42_OK;
+}
+
+extern "C" int be42_decoder_status(be42_decoder *d)
+{
+    BE42_CHECK(d, "be42_decoder_status: null decoder");
+    return fault_check(d, true, "be42_decoder_status");
+}
 
 extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
                                  float *logits_out, void *stream)
@@ -1575,6 +1612,7 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
     const int B = batch;
     for (int b = 0; tokens && b < B; b++)
         BE42_CHECK(tokens[b] >= 0 && tokens[b] < c.vocab, "be42_decoder_step: token %d out of range", tokens[b]);
+    DEC_TRY(fault_check(d, false, "be42_decoder_step"));
     // host parameters of this step into the pinned buffer of this parity,
     // once the step that used it last has copied it
     const int par = d->parity;
@@ -1606,10 +1644,7 @@ extern "C" int be42_decoder_step(be42_decoder *d, const int *tokens, int batch, 
         return rc;
     }
     if (next_tokens) {
-        BE42_HIP(hipEventSynchronize(d->ev_out));
-        BE42_CHECK(d->next_host[kMaxBatch] == 0,
-                   "be42_decoder_step: a grid barrier of the fused layer timed out (code %d); the step's results "
-                   "are invalid", d->next_host[kMaxBatch]);
+        DEC_TRY(fault_check(d, true, "be42_decoder_step"));
         memcpy(next_tokens, d->next_host, (size_t)B * sizeof(int));
     }
     return BE42_OK;
@@ -1866,6 +1901,7 @@ extern "C" int be42_decoder_prefill(be42_decoder *d, int seq, const int *tokens,
                "64 or 128 (the decode step serves the others token by token)");
     for (int i = 0; i < n; i++)
         BE42_CHECK(tokens[i] >= 0 && tokens[i] < c.vocab, "be42_decoder_prefill: token %d out of range", tokens[i]);
+    DEC_TRY(fault_check(d, false, "be42_decoder_prefill"));
     DEC_TRY(prefill_alloc(d));
     hipStream_t caller = as_stream(stream), st = d->gstream;
     BE42_HIP(hipEventRecord(d->ev_in, caller));

@@ -560,17 +560,35 @@ struct Runtime {
         uint64_t sample[kSampleWords];
     };
     std::unordered_map<const void *, Mirror> mirrors;   // host weight -> device copy
-    std::unordered_map<const t_block_manager *, be42_kv_pool *> pools;
-    std::unordered_map<const t_lsh_ctx *, float *> ctx_hpT;
+    // Every map below is keyed by the address of a caller's struct, which the
+    // caller may free and reuse for another struct: an entry is used only
+    // while the struct still holds what the entry recorded, and is dropped
+    // (its device memory freed) as soon as it does not.
+    struct Pool {
+        be42_kv_pool *pool = nullptr;
+        const t_kv_block *blocks = nullptr;   // block_manager_init's host arrays and shape
+        const int *page_table = nullptr;
+        int capacity = 0, n_layers = 0, n_kv_heads = 0, head_dim = 0, max_logical = 0;
+    };
+    std::unordered_map<const t_block_manager *, Pool> pools;
+    struct Ctx {
+        float *dev = nullptr;               // hp_transposed on the device
+        std::vector<float> host;            // what was uploaded (dim x 16)
+    };
+    std::unordered_map<const t_lsh_ctx *, Ctx> ctx_hpT;
     struct Index {
         uint16_t *hash = nullptr;   // [LSH_MAX_BLOCKS]
         float *sum = nullptr;       // [LSH_MAX_DIM]
-        int uploaded = 0;           // block hashes already on the device
+        int uploaded = 0;           // block hashes already on the device ...
+        std::vector<uint16_t> sent; // ... and their values
+        int count = 0;              // keys summed in `sum` since the last commit
     };
     std::unordered_map<const t_lsh_index *, Index> indexes;
     struct Linear {
         uint16_t *k = nullptr, *v = nullptr;   // device mirror [max_seq][heads][dim]
         size_t rows = 0, row = 0;
+        const void *hk = nullptr, *hv = nullptr;   // the arena rows kv_cache_init gave the struct
+        int max_seq = 0, heads = 0, dim = 0;
     };
     std::unordered_map<const t_kv_cache *, Linear> linear;
 };
@@ -666,13 +684,29 @@ const void *weight_dev(const void *host, size_t bytes)
     return m.dev;
 }
 
+bool pool_matches(const Runtime::Pool &p, const t_block_manager *bm)
+{
+    return p.blocks == bm->blocks && p.page_table == bm->page_table && p.capacity == bm->capacity &&
+           p.n_layers == bm->n_layers && p.n_kv_heads == bm->n_kv_heads && p.head_dim == bm->head_dim &&
+           p.max_logical == bm->max_logical;
+}
+
+void pool_drop(Runtime &r, std::unordered_map<const t_block_manager *, Runtime::Pool>::iterator it)
+{
+    hip_ok(hipDeviceSynchronize(), "block manager release");
+    be42_kv_destroy(it->second.pool);
+    r.pools.erase(it);
+}
+
 be42_kv_pool *pool_of(const t_block_manager *bm, const char *what)
 {
     Runtime &r = rt();
     auto it = r.pools.find(bm);
+    if (it != r.pools.end() && !pool_matches(it->second, bm))
+        pool_drop(r, it), it = r.pools.end();
     if (it == r.pools.end())
         die(what, "block manager was not created by block_manager_init of this library");
-    return it->second;
+    return it->second.pool;
 }
 
 // host mirror of the pool's allocator state
@@ -681,17 +715,22 @@ void sync_manager(t_block_manager *bm, be42_kv_pool *pool)
     ok(be42_kv_export(pool, bm->page_table, bm->free_stack, &bm->free_top, bm->logical_len), "be42_kv_export");
 }
 
+// The device copy of a context's transposed projection, uploaded again
+// whenever the struct's values differ from the ones last uploaded (a context
+// re-initialised, or another context at a reused address).
 const float *ctx_hpT(const t_lsh_ctx *ctx)
 {
     Runtime &r = rt();
-    auto it = r.ctx_hpT.find(ctx);
-    if (it != r.ctx_hpT.end())
-        return it->second;
-    float *d = nullptr;
-    hip_ok(hipMalloc((void **)&d, sizeof(ctx->hp_transposed)), "lsh ctx");
-    hip_ok(hipMemcpy(d, ctx->hp_transposed, sizeof(ctx->hp_transposed), hipMemcpyHostToDevice), "lsh ctx upload");
-    r.ctx_hpT[ctx] = d;
-    return d;
+    const size_t n = (size_t)LSH_MAX_DIM * 16;
+    const float *h = &ctx->hp_transposed[0][0];
+    Runtime::Ctx &c = r.ctx_hpT[ctx];
+    if (!c.dev)
+        hip_ok(hipMalloc((void **)&c.dev, n * sizeof(float)), "lsh ctx");
+    else if (c.host.size() == n && !memcmp(c.host.data(), h, n * sizeof(float)))
+        return c.dev;
+    c.host.assign(h, h + n);
+    hip_ok(hipMemcpy(c.dev, h, n * sizeof(float), hipMemcpyHostToDevice), "lsh ctx upload");
+    return c.dev;
 }
 
 Runtime::Index &index_of(const t_lsh_index *idx)
@@ -703,8 +742,29 @@ Runtime::Index &index_of(const t_lsh_index *idx)
         hip_ok(hipMalloc((void **)&x.sum, LSH_MAX_DIM * sizeof(float)), "lsh index");
         hip_ok(hipMemset(x.sum, 0, LSH_MAX_DIM * sizeof(float)), "lsh index");
         x.uploaded = 0;
+        x.count = 0;
+        x.sent.assign(LSH_MAX_BLOCKS, 0);
     }
     return x;
+}
+
+// Bring the device copy of the index's block hashes to [0, nb): hashes
+// uploaded before are trusted only while the struct still holds them (an
+// index rebuilt in place, or another index at a reused address, differs).
+void index_sync_hashes(Runtime::Index &x, const t_lsh_index *idx, int nb)
+{
+    int from = x.uploaded < nb ? x.uploaded : nb;
+    for (int i = 0; i < from; i++)
+        if (x.sent[i] != idx->block_hashes[i]) {
+            from = i;
+            break;
+        }
+    if (from < nb) {
+        hip_ok(hipMemcpy(x.hash + from, idx->block_hashes + from, (size_t)(nb - from) * 2, hipMemcpyHostToDevice),
+               "lsh index upload");
+        memcpy(x.sent.data() + from, idx->block_hashes + from, (size_t)(nb - from) * 2);
+    }
+    x.uploaded = nb;
 }
 
 // column chunks of the quantized GEMV
@@ -1113,12 +1173,8 @@ extern "C" void lsh_init(t_lsh_ctx *ctx, int dim, unsigned int seed)
         for (int h = 0; h < 16; h++)
             ctx->hp_transposed[d][h] = hpT[(size_t)d * 16 + h];
     ctx->initialized = 1;
-    std::lock_guard<std::mutex> g(rt().mu);
-    Runtime &r = rt();
-    auto it = r.ctx_hpT.find(ctx);
-    if (it != r.ctx_hpT.end())
-        hip_ok(hipMemcpy(it->second, ctx->hp_transposed, sizeof(ctx->hp_transposed), hipMemcpyHostToDevice),
-               "lsh_init");
+    // the device copy (if any) is refreshed by its next use, which compares it
+    // with these values
 }
 
 extern "C" void lsh_ctx_release(const t_lsh_ctx *ctx)
@@ -1128,7 +1184,7 @@ extern "C" void lsh_ctx_release(const t_lsh_ctx *ctx)
     auto it = r.ctx_hpT.find(ctx);
     if (it != r.ctx_hpT.end()) {
         hip_ok(hipDeviceSynchronize(), "lsh_ctx_release");
-        hip_ok(hipFree(it->second), "lsh_ctx_release");
+        hip_ok(hipFree(it->second.dev), "lsh_ctx_release");
         r.ctx_hpT.erase(it);
     }
 }
@@ -1145,6 +1201,7 @@ extern "C" void lsh_index_init(t_lsh_index *idx)
     std::lock_guard<std::mutex> g(rt().mu);
     Runtime::Index &x = index_of(idx);
     x.uploaded = 0;
+    x.count = 0;
     hip_ok(hipMemset(x.sum, 0, LSH_MAX_DIM * sizeof(float)), "lsh_index_init");
 }
 
@@ -1205,12 +1262,22 @@ extern "C" void lsh_update(t_lsh_index *idx, const t_lsh_ctx *ctx, const float *
         dim = LSH_MAX_DIM;
     Runtime::Index &x = index_of(idx);
     t_block_acc *acc = &idx->active;
+    // the running key sum lives on the device: it must hold the struct's
+    // `count` keys (an index at a reused address, or one the caller changed,
+    // starts again from zero when its block is empty and is refused otherwise)
+    if (acc->count != x.count) {
+        if (acc->count != 0)
+            die("lsh_update", "the index's active block was not accumulated by this library's lsh_update");
+        hip_ok(hipMemset(x.sum, 0, LSH_MAX_DIM * sizeof(float)), "lsh_update");
+        x.count = 0;
+    }
     if (acc->count == 0)
         acc->start_pos = pos;
     const float *dk = (const float *)in_dev(key, (size_t)dim * 4, kS0);
     hipLaunchKernelGGL(k_lsh_accumulate, dim3((dim + 255) / 256), dim3(256), 0, nullptr, x.sum, dk, dim);
     hip_ok(hipGetLastError(), "lsh_update");
     acc->count++;
+    x.count = acc->count;
     if (acc->count >= LSH_BLOCK_SIZE) {
         uint16_t *dh = (uint16_t *)scratch(kS1, 2);
         hipLaunchKernelGGL(k_lsh_commit, dim3(1), dim3(256), 0, nullptr, dh, x.sum, ctx_hpT(ctx), dim, ctx->dim,
@@ -1220,6 +1287,7 @@ extern "C" void lsh_update(t_lsh_index *idx, const t_lsh_ctx *ctx, const float *
         hip_ok(hipMemcpy(&h, dh, 2, hipMemcpyDeviceToHost), "lsh_update");
         lsh_insert_block(idx, h, acc->start_pos, acc->count);
         acc->count = 0;
+        x.count = 0;
     }
 }
 
@@ -1232,13 +1300,7 @@ extern "C" int lsh_find_candidates(const t_lsh_index *idx, uint16_t query_hash, 
     std::lock_guard<std::mutex> g(rt().mu);
     Runtime::Index &x = index_of(idx);
     const int nb = idx->n_blocks < LSH_MAX_BLOCKS ? idx->n_blocks : LSH_MAX_BLOCKS;
-    if (x.uploaded > nb)
-        x.uploaded = 0;
-    if (x.uploaded < nb)
-        hip_ok(hipMemcpy(x.hash + x.uploaded, idx->block_hashes + x.uploaded, (size_t)(nb - x.uploaded) * 2,
-                         hipMemcpyHostToDevice),
-               "lsh_find_candidates");
-    x.uploaded = nb;
+    index_sync_hashes(x, idx, nb);
     int cap = max_blocks < nb ? max_blocks : nb;
     if (cap > kCandCapMax) {
         char msg[96];
@@ -1272,6 +1334,13 @@ extern "C" int block_manager_init(t_block_manager *bm, int n_layers, int n_kv_he
                                   int max_blocks_per_layer)
 {
     std::lock_guard<std::mutex> g(rt().mu);
+    {
+        // a manager initialised again in place abandons its previous pool
+        Runtime &r = rt();
+        auto it = r.pools.find(bm);
+        if (it != r.pools.end())
+            pool_drop(r, it);
+    }
     memset(bm, 0, sizeof *bm);
     be42_kv_pool *pool = nullptr;
     if (be42_kv_create(&pool, BE42_KV_INT8, n_layers, n_kv_heads, head_dim, max_blocks_per_layer, nullptr)) {
@@ -1314,7 +1383,15 @@ extern "C" int block_manager_init(t_block_manager *bm, int n_layers, int n_kv_he
         b.lsh_hash = 0;
     }
     sync_manager(bm, pool);
-    rt().pools[bm] = pool;
+    Runtime::Pool &e = rt().pools[bm];
+    e.pool = pool;
+    e.blocks = bm->blocks;
+    e.page_table = bm->page_table;
+    e.capacity = bm->capacity;
+    e.n_layers = bm->n_layers;
+    e.n_kv_heads = bm->n_kv_heads;
+    e.head_dim = bm->head_dim;
+    e.max_logical = bm->max_logical;
     return 0;
 }
 
@@ -1323,11 +1400,8 @@ extern "C" void block_manager_free(t_block_manager *bm)
     std::lock_guard<std::mutex> g(rt().mu);
     Runtime &r = rt();
     auto it = r.pools.find(bm);
-    if (it != r.pools.end()) {
-        hip_ok(hipDeviceSynchronize(), "block_manager_free");
-        be42_kv_destroy(it->second);
-        r.pools.erase(it);
-    }
+    if (it != r.pools.end())
+        pool_drop(r, it);
     free(bm->blocks);
     free(bm->page_table);
     free(bm->free_stack);
@@ -1615,6 +1689,14 @@ static t_tensor view3(void *data, int d0, int d1, int d2)
     return t;
 }
 
+static void linear_drop(Runtime &r, std::unordered_map<const t_kv_cache *, Runtime::Linear>::iterator it)
+{
+    hip_ok(hipDeviceSynchronize(), "kv cache release");
+    hip_ok(hipFree(it->second.k), "kv cache release");
+    hip_ok(hipFree(it->second.v), "kv cache release");
+    r.linear.erase(it);
+}
+
 extern "C" void kv_cache_init(t_kv_cache *c, t_arena *a, t_kv_init_params *p)
 {
     c->max_seq_len = p->max_seq;
@@ -1625,30 +1707,63 @@ extern "C" void kv_cache_init(t_kv_cache *c, t_arena *a, t_kv_init_params *p)
     c->k = view3(arena_take(a, bytes), p->max_seq, p->num_heads, p->head_dim);
     c->v = view3(arena_take(a, bytes), p->max_seq, p->num_heads, p->head_dim);
     std::lock_guard<std::mutex> g(rt().mu);
-    Runtime::Linear &m = rt().linear[c];
-    if (m.k) {
-        hip_ok(hipDeviceSynchronize(), "kv_cache_init");
-        hip_ok(hipFree(m.k), "kv_cache_init");
-        hip_ok(hipFree(m.v), "kv_cache_init");
-    }
+    Runtime &r = rt();
+    auto it = r.linear.find(c);
+    if (it != r.linear.end())
+        linear_drop(r, it);
+    Runtime::Linear &m = r.linear[c];
     m.rows = (size_t)p->max_seq;
     m.row = (size_t)p->num_heads * p->head_dim;
+    m.hk = c->k.data;
+    m.hv = c->v.data;
+    m.max_seq = c->max_seq_len;
+    m.heads = c->num_heads;
+    m.dim = c->head_dim;
     hip_ok(hipMalloc((void **)&m.k, bytes ? bytes : 2), "kv_cache_init");
     hip_ok(hipMalloc((void **)&m.v, bytes ? bytes : 2), "kv_cache_init");
+    // zero like the arena rows, so rows past the current length read the same
+    hip_ok(hipMemset(m.k, 0, bytes ? bytes : 2), "kv_cache_init");
+    hip_ok(hipMemset(m.v, 0, bytes ? bytes : 2), "kv_cache_init");
 }
 
-// the device mirror of a cache: the one kv_cache_init made, or a staged copy
-// of the host rows [0, n) (a cache this library did not create)
+// The mirror kv_cache_init made for the struct at c, or null: an entry is
+// used only while the struct still names the arena rows and the shape it was
+// made for (a struct freed and its address reused by another cache, or a
+// cache the caller re-pointed, does not), and a stale entry is released.
+static Runtime::Linear *linear_entry(const t_kv_cache *c)
+{
+    Runtime &r = rt();
+    auto it = r.linear.find(c);
+    if (it == r.linear.end())
+        return nullptr;
+    const Runtime::Linear &m = it->second;
+    if (m.hk == c->k.data && m.hv == c->v.data && m.max_seq == c->max_seq_len && m.heads == c->num_heads &&
+        m.dim == c->head_dim)
+        return &it->second;
+    linear_drop(r, it);
+    return nullptr;
+}
+
+// the device rows of a cache: its mirror, or a staged copy of the host rows
+// [0, n) (a cache this library did not create)
 static const Runtime::Linear &linear_dev(const t_kv_cache *c, int n, Runtime::Linear &tmp)
 {
-    auto it = rt().linear.find(c);
-    if (it != rt().linear.end())
-        return it->second;
+    if (const Runtime::Linear *m = linear_entry(c))
+        return *m;
     tmp.row = (size_t)c->num_heads * c->head_dim;
     const size_t bytes = (size_t)n * tmp.row * 2;
     tmp.k = (uint16_t *)in_dev(c->k.data, bytes, kS6);
     tmp.v = (uint16_t *)in_dev(c->v.data, bytes, kS7);
     return tmp;
+}
+
+extern "C" void kv_cache_release(const t_kv_cache *c)
+{
+    std::lock_guard<std::mutex> g(rt().mu);
+    Runtime &r = rt();
+    auto it = r.linear.find(c);
+    if (it != r.linear.end())
+        linear_drop(r, it);
 }
 
 extern "C" void kv_cache_append(t_kv_cache *c, const t_tensor *k_in, const t_tensor *v_in)
@@ -1658,25 +1773,28 @@ extern "C" void kv_cache_append(t_kv_cache *c, const t_tensor *k_in, const t_ten
         return;
     }
     std::lock_guard<std::mutex> g(rt().mu);
-    auto it = rt().linear.find(c);
-    if (it == rt().linear.end())
-        die("kv_cache_append", "cache was not created by kv_cache_init of this library");
-    Runtime::Linear &m = it->second;
+    Runtime::Linear *m = linear_entry(c);
     const int idx = c->current_seq_len;
     const int row = c->num_heads * c->head_dim;
     uint16_t *hk = (uint16_t *)c->k.data + (size_t)idx * row, *hv = (uint16_t *)c->v.data + (size_t)idx * row;
-    uint16_t *dk = m.k + (size_t)idx * row, *dv = m.v + (size_t)idx * row;
     if (k_in->dtype == DTYPE_F32) {
+        // rounded to bf16 on the device: into the mirror's row, or (a cache
+        // without a mirror) into a staging row; then copied to the host row
         const float *fk = (const float *)in_dev(k_in->data, (size_t)row * 4, kS0);
         const float *fv = (const float *)in_dev(v_in->data, (size_t)row * 4, kS2);
-        ok(be42_kv_linear_append(m.k, m.v, idx, fk, fv, row, nullptr), "kv_cache_append");
-        hip_ok(hipMemcpy(hk, dk, (size_t)row * 2, hipMemcpyDeviceToHost), "kv_cache_append");
-        hip_ok(hipMemcpy(hv, dv, (size_t)row * 2, hipMemcpyDeviceToHost), "kv_cache_append");
+        uint16_t *mk = m ? m->k : (uint16_t *)scratch(kS6, (size_t)row * 2);
+        uint16_t *mv = m ? m->v : (uint16_t *)scratch(kS7, (size_t)row * 2);
+        const int at = m ? idx : 0;
+        ok(be42_kv_linear_append(mk, mv, at, fk, fv, row, nullptr), "kv_cache_append");
+        hip_ok(hipMemcpy(hk, mk + (size_t)at * row, (size_t)row * 2, hipMemcpyDeviceToHost), "kv_cache_append");
+        hip_ok(hipMemcpy(hv, mv + (size_t)at * row, (size_t)row * 2, hipMemcpyDeviceToHost), "kv_cache_append");
     } else {
         memcpy(hk, k_in->data, (size_t)row * 2);
         memcpy(hv, v_in->data, (size_t)row * 2);
-        hip_ok(hipMemcpy(dk, hk, (size_t)row * 2, hipMemcpyHostToDevice), "kv_cache_append");
-        hip_ok(hipMemcpy(dv, hv, (size_t)row * 2, hipMemcpyHostToDevice), "kv_cache_append");
+        if (m) {
+            hip_ok(hipMemcpy(m->k + (size_t)idx * row, hk, (size_t)row * 2, hipMemcpyHostToDevice), "kv_cache_append");
+            hip_ok(hipMemcpy(m->v + (size_t)idx * row, hv, (size_t)row * 2, hipMemcpyHostToDevice), "kv_cache_append");
+        }
     }
     c->current_seq_len++;
 }

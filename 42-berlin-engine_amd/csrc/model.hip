@@ -215,15 +215,26 @@ struct Json {
             ok = false;
         return s;
     }
+    // an optionally signed decimal integer read within [p, e) (the header is
+    // not NUL-terminated); values past 2^62 are an error
     long long num()
     {
         ws();
-        char *q = nullptr;
-        const long long v = strtoll(p, &q, 10);
-        if (q == p)
+        bool neg = false;
+        if (p < e && (*p == '-' || *p == '+'))
+            neg = *p++ == '-';
+        const char *d0 = p;
+        long long v = 0;
+        while (p < e && *p >= '0' && *p <= '9') {
+            if (v > ((1LL << 62) - 9) / 10) {
+                ok = false;
+                return 0;
+            }
+            v = v * 10 + (*p++ - '0');
+        }
+        if (p == d0)
             ok = false;
-        p = q;
-        return v;
+        return neg ? -v : v;
     }
     void skip_value()
     {
@@ -350,11 +361,13 @@ bool open_st(const char *path, StFile &F, std::string &err)
         }
         if (!J.ok)
             break;
-        size_t elems = 1;
+        size_t elems = 1, bytes = 0;
+        bool wrap = false;
         for (long long d : t.shape)
-            elems *= (size_t)(d > 0 ? d : 0);
-        if (!have_off || t.end < t.begin || t.end > F.data_size ||
-            (t.dt != DT_BAD && t.end - t.begin != elems * dt_size(t.dt))) {
+            wrap |= __builtin_mul_overflow(elems, (size_t)(d > 0 ? d : 0), &elems);
+        wrap |= t.dt != DT_BAD && __builtin_mul_overflow(elems, dt_size(t.dt), &bytes);
+        if (!have_off || wrap || t.end < t.begin || t.end > F.data_size ||
+            (t.dt != DT_BAD && t.end - t.begin != bytes)) {
             err = "tensor '" + t.name + "': data offsets do not match its shape and dtype";
             return false;
         }

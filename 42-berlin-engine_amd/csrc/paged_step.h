@@ -71,9 +71,10 @@ int lsh_attention_prefix(const be42_kv_pool &P, const float *q, const int *slots
 
 // be42_lsh_attention that, when the launch splits each (query, KV head) pair
 // over several workgroups, also writes the output rows as GEMV digit planes
-// (xdig_prepare's layout, k = n_heads * head_dim) and sets *done
+// (xdig_prepare's layout, k = n_heads * head_dim; none when xdig is null) and
+// sets *done; a split launch's bounded waits report to the device word *err
 int lsh_attention_digits(const be42_kv_pool &P, const float *q, const int *slots, int n_queries, int n_heads,
                          int k_sel, int cand_cap, float scale, float *out, int *sel, int *n_sel, int sel_stride,
-                         void *xdig, bool fp8, bool *done, hipStream_t s);
+                         void *xdig, bool fp8, bool *done, int *err, hipStream_t s);
 
 }  // namespace be42

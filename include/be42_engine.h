@@ -260,7 +260,8 @@ int select_top_k_blocks(int *selected, t_block_score *scores,     /* paged.h:211
  * directly -- and in a device mirror this library keeps per t_kv_cache
  * (created by kv_cache_init, updated by kv_cache_append / kv_cache_evict,
  * read by the attention functions below).  A cache that did not come from
- * kv_cache_init is uploaded on each attention call. */
+ * kv_cache_init is uploaded on each attention call, and kv_cache_append
+ * writes only its host rows. */
 typedef struct s_arena {                                           /* arena.h:18-23 */
     char *base;
     size_t size;
@@ -315,6 +316,13 @@ void kv_cache_append(t_kv_cache *c, const t_tensor *k,            /* kv_cache.h:
  * relu(bf16(q[h]) . k[h]) (q->data and w->data read as bf16; ties: lower
  * position first), compacted to the front in position order */
 void kv_cache_evict(t_kv_cache *c, t_evict_params *p);            /* kv_cache.h:46 */
+/* Release the device mirror kv_cache_init made for the struct at c (no
+ * counterpart in the reference, whose caches own only arena memory).  A
+ * mirror is also released by the next call that finds the struct at its
+ * address naming other arena rows or another shape than kv_cache_init gave
+ * it: a struct freed and reused for another cache is never read through the
+ * old mirror. */
+void kv_cache_release(const t_kv_cache *c);
 
 /* ---- linear-cache attention (src/compute/ops_attention.h:29-68) ------------ */
 typedef struct s_attention_params {                                /* ops_attention.h:29-40 */

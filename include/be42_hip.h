@@ -245,6 +245,10 @@ int  be42_paged_attention(const be42_kv_pool *pool, const float *q, int n_querie
 int  be42_lsh_attention(const be42_kv_pool *pool, const float *q, const int *slots, int n_queries,
                         int n_heads, int k_sel, int cand_cap, float scale, float *out, int *sel, int *n_sel,
                         int sel_stride, void *stream);
+/* Waits for `stream`; an error if a bounded wait inside a be42_lsh_attention
+ * launch gave up since the last call (that launch's output is invalid).  The
+ * word it reads is the device's, shared by every stream, and is cleared. */
+int  be42_lsh_attention_status(void *stream);
 
 /* ---- linear (non-paged) bf16 KV cache -----------------------------------------------
  * The cache layout of kv_cache.h:19-27: rows [T][n_kv][head_dim] bf16.
@@ -335,10 +339,19 @@ be42_kv_pool *be42_decoder_pool(be42_decoder *d);
  * (batch, dense or routed attention, token source, output buffers) and replayed
  * as a HIP graph (environment BE42_DECODE_NO_GRAPH=1 launches them one by one).
  * The call returns once the host side of the step is queued; it blocks only
- * for next_tokens, or when the step before the last still runs. */
+ * for next_tokens, or when the step before the last still runs.
+ * One-sequence steps run each layer as one launch whose blocks meet at grid
+ * barriers; a barrier wait that does not complete within its bound sets a
+ * device flag.  The step that sets it is reported by itself when next_tokens
+ * is given, else by the next be42_decoder_step / be42_decoder_prefill that
+ * finds it finished, or by be42_decoder_status; from then on the decoder
+ * refuses every step (its cache and results are invalid: destroy it). */
 int  be42_decoder_step(be42_decoder *d, const int *tokens, int batch, int pos, int *next_tokens,
                        float *logits_out, void *stream);
 int  be42_decoder_next_tokens(be42_decoder *d, const int **dev_ptr);
+/* Waits for the decoder's queued work; BE42_OK, or an error when a grid
+ * barrier of any step so far timed out. */
+int  be42_decoder_status(be42_decoder *d);
 /* Batched prefill (forward_prefill_batch, src/inference/inference.c:718-1112,
  * with its token-major / feature-major layout fixed): the n prompt tokens of
  * sequence seq at positions pos0 .. pos0+n-1, in passes of up to 256 tokens

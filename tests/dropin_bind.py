@@ -135,6 +135,7 @@ def bind(lib):
         "kv_cache_init": (None, [P(KvCache), P(Arena), P(KvInitParams)]),
         "kv_cache_append": (None, [P(KvCache), P(Tensor), P(Tensor)]),
         "kv_cache_evict": (None, [P(KvCache), P(EvictParams)]),
+        "kv_cache_release": (None, [P(KvCache)]),
         "flash_attention_head": (None, [vp, vp, vp, vp, i32, i32, f32]),
         "op_multihead_attention": (None, [P(AttentionParams)]),
         "op_attention_dense": (None, [P(AttentionParams), i32]),

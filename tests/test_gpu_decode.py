@@ -289,3 +289,35 @@ def test_fused_layer_matches_separate_launches(be, orc, monkeypatch, kind, kv_ki
         errs = np.abs(l0 - l1).max(axis=1) / np.abs(l0).max(axis=1)
         assert errs[0] <= 1e-5 and np.median(errs) <= 1e-4 and errs.max() <= 2e-2, (errs[0], np.median(errs),
                                                                                     errs.max())
+
+
+def test_barrier_timeout_is_reported(be, orc, monkeypatch):
+    """A fused-layer grid barrier whose wait gives up must be reported even
+    when no step asks for its tokens.  BE42_DECODE_FAIL_BARRIERS=1 makes every
+    wait of the fused launches look for a barrier number no block writes,
+    with a 64-poll bound: each wait ends, the launch runs to its end, and the
+    flag is set.  Steps without next_tokens are queued; the next step call
+    (or be42_decoder_status) must refuse, and keep refusing."""
+    rng = np.random.default_rng(5)
+    w = make_model(rng, 2, 512, 8, 8, 64, 1408, 4096, "int8")
+    _, gc = configs(2, 512, 8, 8, 64, 1408, 4096, 256, 1, "int8", OR_KV_INT8, 8, 64)
+    _, hpT = orc.lsh_init(64, 42)
+    wd = to_device(w)
+    monkeypatch.setenv("BE42_DECODE_FAIL_BARRIERS", "1")
+    dec = be42.Decoder(be, gc, wd, hpT)
+    monkeypatch.delenv("BE42_DECODE_FAIL_BARRIERS")
+    dec.step([1], 0, sync=False)
+    torch.cuda.synchronize()
+    with pytest.raises(be42.Be42Error, match="grid barrier"):
+        dec.step([2], 1, sync=False)
+    with pytest.raises(be42.Be42Error, match="grid barrier"):
+        dec.status()
+    with pytest.raises(be42.Be42Error, match="grid barrier"):
+        dec.step([2], 1)
+    dec.close()
+    # a decoder made without the knob is unaffected
+    ok = be42.Decoder(be, gc, wd, hpT)
+    ok.step([1], 0, sync=False)
+    ok.status()
+    assert ok.step([2], 1).shape == (1,)
+    ok.close()

@@ -1,8 +1,11 @@
 """configs[4] at full size: one decode step of the 3B-class model (28 layers,
 d 3072, 24 query / 8 KV heads of 128, FFN 8192, vocab 128256, FP8 E4M3
-per-row weights) for two sequences at position 32768 over a 32k-token bf16
-paged prefix, LSH-routed to 64 pages (candidate cap 64), against the oracle's
-transformer_forward on the same weights and prefix.
+per-row weights) for 1, 2 and 8 sequences at position 32768 over a 32k-token
+bf16 paged prefix, LSH-routed to 64 pages (candidate cap 64), against the
+oracle's transformer_forward on the same weights and prefix.  Batch 1 runs
+each layer as the one-launch fused layer after a split route + attention;
+batch 2 and 8 run the separate launches (attention split over 16 and 4
+workgroups per (sequence, KV head) pair).
 
 The prefix is N(0,1) K/V with the configs[3] planting (5% of the pages of
 each layer hold keys along that layer's q_mean at the step, found by probe
@@ -28,7 +31,6 @@ pytestmark = pytest.mark.gpu
 
 A = dict(n_layers=28, dim=3072, n_heads=24, n_kv=8, hd=128, hidden=8192, vocab=128256)
 T = 32768
-B = 2
 PAGE = 16
 
 
@@ -74,18 +76,19 @@ def plant(K, q, gen):
     K.view(K.shape[0], KV, hd)[rows] = u + torch.randn(rows.numel(), KV, hd, generator=gen, device="cuda") * 0.05
 
 
-def test_3b_decode_step_at_32k(be, orc):
+@pytest.mark.parametrize("B", [1, 2, 8])
+def test_3b_decode_step_at_32k(be, orc, B):
     gen = torch.Generator(device="cuda")
-    gen.manual_seed(4242)
+    gen.manual_seed(4242 + B)
     L, H, KV, hd = A["n_layers"], A["n_heads"], A["n_kv"], A["hd"]
     kd = KV * hd
-    print("3b: weights", flush=True)
+    print(f"3b: batch {B} weights", flush=True)
     wd = device_weights(be, gen)
     wh = host_copy(wd)
     _, hpT = orc.lsh_init(hd, 42)
     oc, gc = configs(L, A["dim"], H, KV, hd, A["hidden"], A["vocab"], T + 16, B, "fp8", OR_KV_BF16, 64, 64)
     dec = be42.Decoder(be, gc, wd, hpT)
-    toks = [17, 90001]
+    toks = [17, 90001, 3, 128255, 4096, 77777, 12, 65000][:B]
     # random prefix, then per layer: probe step -> that layer's queries ->
     # the layer's prefix rebuilt with planted pages (later layers see it)
     print("3b: prefix", flush=True)
@@ -122,7 +125,11 @@ def test_3b_decode_step_at_32k(be, orc):
     nxt = dec.step(toks, T, logits=logits)
     lg, hk, hv = logits.cpu().numpy(), ck.cpu().numpy(), cv.cpu().numpy()
     nsel, sel = cn.cpu().numpy(), cs.cpu().numpy()
-    assert (nsel == 64).all(), nsel
+    # planted pages hash like the layer's q_mean unless q_mean lies close to
+    # a hyperplane, where the noise flips that bit for some of them: a few
+    # (layer, sequence) routes then find fewer candidates and attend fewer
+    # pages (each route is still compared with the oracle's below)
+    assert (nsel == 64).mean() >= 0.9 and nsel.min() >= 32, nsel
     print("3b: oracle steps", flush=True)
     for b in range(B):
         oracles[b].log_selection()

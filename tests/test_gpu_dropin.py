@@ -166,6 +166,96 @@ def test_lsh_drop_in(dl, orc):
     dl.lsh_ctx_release(C.byref(ctx))
 
 
+def test_lsh_structs_at_reused_addresses(dl, orc):
+    """A t_lsh_ctx / t_lsh_index address that later holds another context or
+    index (a struct freed and reused, or overwritten by the caller): hashes,
+    candidates and block sums follow the struct's current contents
+    (ops_lsh.c:138-242, :256-430), not the device copies made for the earlier
+    struct."""
+    rng = np.random.default_rng(31)
+    ctx, other = D.LshCtx(), D.LshCtx()
+    dl.lsh_init(C.byref(ctx), 128, 42)
+    dl.lsh_init(C.byref(other), 128, 7)
+    hp42 = np.ctypeslib.as_array(ctx.hp_transposed)[:128].copy()
+    hp7 = np.ctypeslib.as_array(other.hp_transposed)[:128].copy()
+    v = rng.standard_normal(128).astype(np.float32)
+    assert dl.lsh_hash(C.byref(ctx), D.ptr(v)) == orc.lsh_hash(hp42, v)
+    C.memmove(C.addressof(ctx), C.addressof(other), C.sizeof(D.LshCtx))
+    for _ in range(4):
+        w = rng.standard_normal(128).astype(np.float32)
+        assert dl.lsh_hash(C.byref(ctx), D.ptr(w)) == orc.lsh_hash(hp7, w)
+    # lsh_init again in place: back to seed 42
+    dl.lsh_init(C.byref(ctx), 128, 42)
+    assert dl.lsh_hash(C.byref(ctx), D.ptr(v)) == orc.lsh_hash(hp42, v)
+
+    # an index searched once (its hashes uploaded), then replaced in place by
+    # another index with as many blocks but other hashes
+    idx, repl = D.LshIndex(), D.LshIndex()
+    dl.lsh_index_init(C.byref(idx))
+    dl.lsh_index_init(C.byref(repl))
+    want = OracleIndex(orc, 4096)
+    for i in range(300):
+        dl.lsh_insert_block(C.byref(idx), int(rng.choice([0x1234, 0x1235, 0x9234])), i, 1)
+        h = int(rng.choice([0x1234, 0x0F0F, 0x1236, 0x5234]))
+        dl.lsh_insert_block(C.byref(repl), h, i, 1)
+        want.insert(h, i, 1)
+    ids = np.zeros(64, np.int32)
+    dl.lsh_find_candidates(C.byref(idx), 0x1234, D.ptr(ids), 64)
+    C.memmove(C.addressof(idx), C.addressof(repl), C.sizeof(D.LshIndex))
+    for qh in (0x1234, 0x0F0F, 0x5234):
+        n = dl.lsh_find_candidates(C.byref(idx), qh, D.ptr(ids), 64)
+        np.testing.assert_array_equal(ids[:n], want.candidates(qh, 64))
+
+    # an index with a half-summed active block, replaced in place by a fresh
+    # index: the next block's hash is that of its own 64 keys only
+    acc = D.LshIndex()
+    dl.lsh_index_init(C.byref(acc))
+    for t in range(10):
+        dl.lsh_update(C.byref(acc), C.byref(ctx), D.ptr(rng.standard_normal(128).astype(np.float32)), 128, t)
+    fresh = D.LshIndex()
+    dl.lsh_index_init(C.byref(fresh))
+    C.memmove(C.addressof(acc), C.addressof(fresh), C.sizeof(D.LshIndex))
+    keys = rng.standard_normal((64, 128)).astype(np.float32)
+    for t in range(64):
+        dl.lsh_update(C.byref(acc), C.byref(ctx), D.ptr(keys[t]), 128, 100 + t)
+    s_ = np.zeros(128, np.float32)
+    for t in range(64):
+        s_ = (s_ + keys[t]).astype(np.float32)
+    assert acc.n_blocks == 1 and acc.block_starts[0] == 100
+    assert acc.block_hashes[0] == orc.lsh_hash(hp42, (s_ * np.float32(1.0 / 64)).astype(np.float32))
+    for x in (idx, repl, acc, fresh):
+        dl.lsh_index_release(C.byref(x))
+    dl.lsh_ctx_release(C.byref(ctx))
+    dl.lsh_ctx_release(C.byref(other))
+
+
+def test_block_manager_reinitialised_in_place(be, dl, orc):
+    """block_manager_init twice on one struct (other shapes the second time):
+    the second pool serves every call (paged.c:29-110, :195-272)."""
+    bm = D.BlockManager()
+    assert dl.block_manager_init(C.byref(bm), 2, 2, 64, 8) == 0
+    assert dl.block_manager_init(C.byref(bm), 1, 4, 128, 4) == 0
+    assert (bm.n_layers, bm.n_kv_heads, bm.head_dim, bm.max_logical) == (1, 4, 128, 4)
+    pkv = D.PagedKv(C.pointer(bm), 0, 0, 0)
+    rng = np.random.default_rng(3)
+    op = OraclePaged(orc, 1, 4, 128, 4, OR_KV_INT8)
+    for t in range(20):
+        k = rng.standard_normal(4 * 128).astype(np.float32)
+        v = rng.standard_normal(4 * 128).astype(np.float32)
+        dl.paged_kv_append(C.byref(pkv), D.ptr(k), D.ptr(v), t)
+        op.append(0, k, v, t)
+    assert pkv.n_blocks == 2 and bm.logical_len[0] == 2
+    for pos in (0, 7, 16, 19):
+        kp, vp_, ks, vs = C.c_void_p(), C.c_void_p(), C.c_float(), C.c_float()
+        dl.paged_kv_get_int8(C.byref(pkv), pos, 3, C.byref(kp), C.byref(vp_), C.byref(ks), C.byref(vs))
+        got = np.zeros(128, np.int8)
+        be.lib.be42_memcpy_d2h(got.ctypes.data, kp, 128, None)
+        arr = op.page_arrays(op.phys(0, pos // PAGE))
+        kq, kscale = arr[0].reshape(4, PAGE, 128), arr[2].reshape(4, PAGE)
+        assert np.array_equal(got, kq[3, pos % PAGE]) and np.float32(ks.value) == kscale[3, pos % PAGE]
+    dl.block_manager_free(C.byref(bm))
+
+
 def _manager(dl, n_layers, n_kv, hd, max_pages):
     bm = D.BlockManager()
     assert dl.block_manager_init(C.byref(bm), n_layers, n_kv, hd, max_pages) == 0

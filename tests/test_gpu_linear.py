@@ -287,3 +287,121 @@ def test_dropin_attention_on_foreign_cache(dl, orc):
     p = D.AttentionParams(q.ctypes.data, C.pointer(c), out.ctypes.data, H, n_kv, hd, scale, idx.ctypes.data, 40)
     dl.op_attention_sparse(C.byref(p))
     assert rel_err(out, orc.attention_linear(q, K, V, idx, H, scale)) <= ATTN_TOL
+
+
+def test_dropin_cache_struct_address_reused(dl, orc):
+    """One t_kv_cache address (a reused ctypes buffer) holds first a cache
+    made by kv_cache_init, then caller-filled caches of other shapes, then
+    library caches again: every call must read the rows of the cache the
+    struct holds at that moment (kv_cache.c:18-80, kv_cache_evict.c:34-70,
+    ops_attention.c:175-245), never a device mirror made for an earlier
+    struct at the same address."""
+    rng = np.random.default_rng(21)
+    raw = (C.c_uint8 * C.sizeof(D.KvCache))()
+    c = D.KvCache.from_buffer(raw)
+    scale_of = lambda hd: np.float32(1.0) / np.sqrt(np.float32(hd))  # noqa: E731
+    keep = []
+
+    def library_cache(max_seq, n_kv, hd, n_rows):
+        C.memset(raw, 0, C.sizeof(raw))
+        buf = np.zeros(2 * max_seq * n_kv * hd * 2 + 256, np.uint8)
+        arena = D.Arena(buf.ctypes.data, buf.nbytes, 0)
+        params = D.KvInitParams(max_seq, n_kv, hd)
+        dl.kv_cache_init(C.byref(c), C.byref(arena), C.byref(params))
+        keep.append(buf)
+        K = _bf16(orc, rng.standard_normal((n_rows, n_kv, hd)))
+        V = _bf16(orc, rng.standard_normal((n_rows, n_kv, hd)))
+        for t in range(n_rows):
+            dl.kv_cache_append(C.byref(c), C.byref(_vec(K[t], D.DTYPE_BF16)), C.byref(_vec(V[t], D.DTYPE_BF16)))
+        return K, V
+
+    def foreign_cache(T, n_kv, hd):
+        C.memset(raw, 0, C.sizeof(raw))
+        K = _bf16(orc, rng.standard_normal((T, n_kv, hd)))
+        V = _bf16(orc, rng.standard_normal((T, n_kv, hd)))
+        keep.extend([K, V])
+        c.k.data, c.v.data = K.ctypes.data, V.ctypes.data
+        c.max_seq_len, c.num_heads, c.head_dim, c.current_seq_len = T, n_kv, hd, T
+        return K, V
+
+    def check_attention(K, V, n_kv, hd, H):
+        T = K.shape[0]
+        q = rng.standard_normal(H * hd).astype(np.float32)
+        out = np.zeros(H * hd, np.float32)
+        sc = scale_of(hd)
+        idx = rng.permutation(T)[:min(40, T - 1)].astype(np.int32)
+        p = D.AttentionParams(q.ctypes.data, C.pointer(c), out.ctypes.data, H, n_kv, hd, sc, idx.ctypes.data,
+                              len(idx))
+        dl.op_attention_sparse(C.byref(p))
+        assert rel_err(out, orc.attention_linear(q, K, V, idx, H, sc)) <= ATTN_TOL
+        dl.op_multihead_attention(C.byref(p))
+        assert rel_err(out, orc.attention_linear(q, K, V, idx, H, sc)) <= ATTN_TOL
+        dl.op_attention_dense(C.byref(p), T)
+        assert rel_err(out, orc.attention_linear(q, K, V, None, H, sc)) <= ATTN_TOL
+        p.topk_idx, p.attend_k = None, 0
+        dl.op_multihead_attention(C.byref(p))
+        assert rel_err(out, orc.attention_linear(q, K, V, None, H, sc)) <= ATTN_TOL
+
+    def check_evict(K, V, n_kv, hd, keep_k, host):
+        K, V = K.copy(), V.copy()      # a foreign cache's rows are compacted in place
+        qe = _bf16(orc, rng.standard_normal((n_kv, hd)))
+        we = _bf16(orc, rng.uniform(0.5, 1.5, n_kv))
+        scratch = np.zeros(1 << 16, np.uint8)
+        sa = D.Arena(scratch.ctypes.data, scratch.nbytes, 0)
+        ep = D.EvictParams(C.pointer(_vec(qe, D.DTYPE_BF16)), C.pointer(_vec(we, D.DTYPE_BF16)), keep_k,
+                           C.pointer(sa))
+        dl.kv_cache_evict(C.byref(c), C.byref(ep))
+        gk, gv, m = orc.kv_evict(K, V, qe, we, keep_k)
+        assert c.current_seq_len == m == keep_k
+        np.testing.assert_array_equal(host("k")[:m], gk[:m])
+        np.testing.assert_array_equal(host("v")[:m], gv[:m])
+        return gk[:m], gv[:m]
+
+    def host_rows(which, n_kv, hd):
+        t = c.k if which == "k" else c.v
+        n = c.current_seq_len * n_kv * hd
+        return np.ctypeslib.as_array(C.cast(t.data, C.POINTER(C.c_uint16)), (n,)).reshape(-1, n_kv, hd).copy()
+
+    # a 3-row library cache, then a 150-row foreign cache of 4 x 128 at the
+    # same address (the sequence that once made op_attention_sparse refuse
+    # positions >= 3)
+    K, V = library_cache(3, 1, 64, 3)
+    check_attention(K, V, 1, 64, 2)
+    K, V = foreign_cache(150, 4, 128)
+    check_attention(K, V, 4, 128, 16)
+    K2, V2 = check_evict(K, V, 4, 128, 60, lambda w: host_rows(w, 4, 128))
+    check_attention(K2, V2, 4, 128, 16)
+    # a 400-row library cache of 1 x 64 (400 x 64 rows of mirror), then a
+    # foreign cache of fewer but 8x wider rows: read through the old mirror
+    # this would run past it
+    K, V = library_cache(400, 1, 64, 300)
+    check_attention(K, V, 1, 64, 4)
+    K, V = foreign_cache(100, 4, 128)
+    check_attention(K, V, 4, 128, 8)
+    # appending to a foreign cache writes its host rows (F32 rounded to bf16)
+    T = 100
+    big_k = np.zeros((T + 5, 4, 128), np.uint16)
+    big_v = np.zeros_like(big_k)
+    big_k[:T], big_v[:T] = K, V
+    keep.extend([big_k, big_v])
+    c.k.data, c.v.data, c.max_seq_len = big_k.ctypes.data, big_v.ctypes.data, T + 5
+    for t in range(5):
+        if t % 2:
+            nk = rng.standard_normal(4 * 128).astype(np.float32)
+            nv = rng.standard_normal(4 * 128).astype(np.float32)
+            dl.kv_cache_append(C.byref(c), C.byref(_vec(nk, D.DTYPE_F32)), C.byref(_vec(nv, D.DTYPE_F32)))
+            want_k, want_v = orc.f32_to_bf16(nk), orc.f32_to_bf16(nv)
+        else:
+            want_k = _bf16(orc, rng.standard_normal(4 * 128))
+            want_v = _bf16(orc, rng.standard_normal(4 * 128))
+            dl.kv_cache_append(C.byref(c), C.byref(_vec(want_k, D.DTYPE_BF16)), C.byref(_vec(want_v, D.DTYPE_BF16)))
+        np.testing.assert_array_equal(big_k[T + t].ravel(), want_k)
+        np.testing.assert_array_equal(big_v[T + t].ravel(), want_v)
+    assert c.current_seq_len == T + 5
+    check_attention(big_k, big_v, 4, 128, 8)
+    # a library cache again, released explicitly; the struct then reads as
+    # a foreign cache of its own arena rows
+    K, V = library_cache(64, 2, 64, 50)
+    check_attention(K, V, 2, 64, 4)
+    dl.kv_cache_release(C.byref(c))
+    check_attention(K, V, 2, 64, 4)

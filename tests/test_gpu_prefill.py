@@ -187,3 +187,66 @@ def test_prefill_rejects_bad_arguments(be, orc):
     with pytest.raises(be42.Be42Error, match="out of range"):
         dec.prefill(np.array([gc["vocab"]], np.int32))
     dec.close()
+
+
+@pytest.mark.parametrize("splits", [None, [100]])
+def test_prefill_fp8_forced_kv_against_oracle(be, orc, splits):
+    """FP8 weights and bf16 pages, against the oracle's transformer_forward
+    (not the GPU's own decode step): the prompt through be42_decoder_prefill
+    (one call, or two at pos0 = 0 and 100), then 8 greedy decode steps.  The
+    oracle runs the same tokens one at a time, fed the K/V rows the GPU wrote
+    (for the prompt: read back from the bf16 pages, values the oracle's own
+    bf16 rounding keeps; for the decode steps: captured per layer), so both
+    caches hold the same values.  The last prompt token's logits and every
+    decode step's must agree within the north star's 1e-3 (max|dl| / max|l|),
+    and the tokens must be identical outside near ties."""
+    from oracle_bind import OracleDecoder
+    rng = np.random.default_rng(808)
+    dims = (4, 512, 8, 8, 64, 1408, 4096)
+    L, dim, H, KV, hd, hidden, vocab = dims
+    w = make_model(rng, *dims, "fp8")
+    oc, gc = configs(*dims, 512, 1, "fp8", OR_KV_BF16, 8, 64)
+    _, hpT = orc.lsh_init(hd, 42)
+    dec = be42.Decoder(be, gc, to_device(w), hpT)
+    prompt = rng.integers(0, vocab, 270)
+    lg = torch.empty(vocab, device="cuda")
+    cuts = [0] + list(splits or []) + [len(prompt)]
+    nxt = None
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        nxt = dec.prefill(prompt[a:b], pos0=a, logits=lg)
+    gl = lg.cpu().numpy().copy()
+    snap = snapshot(dec, gc)
+    f32 = lambda u: (np.asarray(u, np.uint16).astype(np.uint32) << 16).view(np.float32)  # noqa: E731
+    n = len(prompt)
+    fk = np.zeros((n, L, KV * hd), np.float32)
+    fv = np.zeros_like(fk)
+    for layer in range(L):
+        k, v = snap[layer]["k"], snap[layer]["v"]        # [page][kv][16][hd], [page][kv][hd][16]
+        for t in range(n):
+            fk[t, layer] = f32(k[t // 16][:, t % 16, :]).ravel()
+            fv[t, layer] = f32(v[t // 16][:, :, t % 16]).ravel()
+    od = OracleDecoder(orc, oc, w, hpT)
+    ol = None
+    for t in range(n):
+        on, ol = od.step(int(prompt[t]), t, force_k=fk[t], force_v=fv[t])
+    err = np.max(np.abs(gl - ol)) / np.max(np.abs(ol))
+    assert err <= 1e-3, err
+    assert nxt == on or near_tie(ol), (nxt, on)
+    if nxt != on:
+        dec.close()
+        return
+    ck = torch.zeros((L, 1, KV * hd), device="cuda")
+    cv = torch.zeros_like(ck)
+    dec.capture_kv(ck, cv)
+    lg2 = torch.empty((1, vocab), device="cuda")
+    cur = nxt
+    for i in range(8):
+        g = int(dec.step([cur], n + i, logits=lg2)[0])
+        on, ol = od.step(cur, n + i, force_k=ck[:, 0].cpu().numpy(), force_v=cv[:, 0].cpu().numpy())
+        err = np.max(np.abs(lg2[0].cpu().numpy() - ol)) / np.max(np.abs(ol))
+        assert err <= 1e-3, (i, err)
+        if g != on:
+            assert near_tie(ol), (i, g, on)
+            break
+        cur = g
+    dec.close()

@@ -140,3 +140,31 @@ def test_check_header_offsets_validated(lib, tmp_path):
     open(m, "wb").write(bytes(raw))
     with pytest.raises(be42.Be42Error, match="data offsets do not match"):
         be42.model_check(lib, m, c)
+
+
+def test_check_header_numbers_stop_at_header_end(lib, tmp_path):
+    """The header is parsed within its own bytes: a number at its end does not
+    run on into the tensor data (here '2' + data '99]}}' would read as 299
+    and close the header)."""
+    m, c = paths(tmp_path)
+    write_config(c, **ARCH)
+    head = b'{"x":{"dtype":"I8","shape":[299],"data_offsets":[0,2'
+    with open(m, "wb") as f:
+        f.write(len(head).to_bytes(8, "little") + head + b"99]}}" + bytes(400))
+    with pytest.raises(be42.Be42Error, match="malformed safetensors header"):
+        be42.model_check(lib, m, c)
+
+
+@pytest.mark.parametrize("shape,offsets,pattern", [
+    # 2^32 x 2^32 x 16 elements wrap to 0 bytes in 64 bits
+    ("[4294967296,4294967296,16]", "[0,0]", "data offsets do not match"),
+    ("[1,99999999999999999999]", "[0,0]", "malformed safetensors header"),
+])
+def test_check_header_shape_overflow(lib, tmp_path, shape, offsets, pattern):
+    m, c = paths(tmp_path)
+    write_config(c, **ARCH)
+    head = ('{"x":{"dtype":"I8","shape":%s,"data_offsets":%s}}' % (shape, offsets)).encode()
+    with open(m, "wb") as f:
+        f.write(len(head).to_bytes(8, "little") + head + bytes(16))
+    with pytest.raises(be42.Be42Error, match=pattern):
+        be42.model_check(lib, m, c)
