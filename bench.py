@@ -147,12 +147,13 @@ def plant_keys_gpu(K, q, gen, cfg=LSH):
     return pages
 
 
-def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
+def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES, ctx=None):
     """Route + sparse attention over the first B sequences of one pool, for
-    each B in `batches`; every sequence is a 32k-token bf16 context."""
+    each B in `batches`; every sequence is a ctx-token bf16 context (32k
+    unless given)."""
     import numpy as np
     import torch
-    cfg = LSH
+    cfg = dict(LSH, ctx=ctx or LSH["ctx"])
     H, KVH, hd, T = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["ctx"]
     BM = max(batches)
     _, hpT = lib.lsh_projection(hd, 42)
@@ -166,7 +167,7 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
     exact_top, planted, page_mass = [], [], []
     for b in range(BM):
         K = torch.randn(T, KVH * hd, generator=gen, device="cuda")
-        planted.append(set(plant_keys_gpu(K, q[b], gen).tolist()))
+        planted.append(set(plant_keys_gpu(K, q[b], gen, cfg).tolist()))
         V = torch.randn(T, KVH * hd, generator=gen, device="cuda")
         pool.append(b, K, V, 0)
         # the selection over every page: the anchors (first, last) and the
@@ -240,8 +241,9 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
         route_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
         attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
         split_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / steps
-        assert torch.equal(fsel, sel) and torch.equal(fnsel, nsel), "fused and two-launch selections differ"
         ns = fnsel.cpu().numpy()
+        assert torch.equal(fnsel, nsel) and all(
+            torch.equal(fsel[b, :ns[b]], sel[b, :ns[b]]) for b in range(B)), "fused and two-launch selections differ"
         nc = ncand.cpu().numpy()
         # recall of the LSH route against the same selection over every
         # page (lsh_validate_recall's hits / k, ops_lsh.c:587, with the
@@ -254,7 +256,7 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
             rec.append(len(got & exact_top[b]) / cfg["k_sel"])
             found.append(len(got & planted[b]) / min(cfg["k_sel"] - 2, len(planted[b])))
             held.append(float(page_mass[b][sorted(got)].sum()))
-        nbytes = sum(lsh_bytes(int(a), int(c)) for a, c in zip(ns, nc))
+        nbytes = sum(lsh_bytes(int(a), int(c), cfg) for a, c in zip(ns, nc))
         kv_bytes = sum(int(a) * cfg["page"] * KVH * hd * 2 * 2 for a in ns)
         rows.append({"batch": B, "us_per_token": round(tot_ms * 1e3 / B, 3), "step_us": round(tot_ms * 1e3, 2),
                      "two_launch_us": round(split_ms * 1e3, 2), "route_us": round(route_ms * 1e3, 2),
@@ -272,7 +274,8 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES):
     roof = {"bound": "hbm", "kernel": "be42::k_attn_fused (route + attention, one launch)",
             "workload": f"batch {head['batch']}, {T}-token bf16 context",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": lsh_traffic(head["batch"]),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": lsh_traffic(head["batch"]) if T == LSH["ctx"] else None,
             "bytes_per_launch": launch_bytes, "launch_us": head["step_us"]}
     return {"roofline": roof,
             "recall_definition": "recall_at_k: share of the k pages the same ranking selects over every page "
@@ -1125,6 +1128,14 @@ def main():
         configs.clear()
         torch.cuda.empty_cache()
         out["lsh_attention"] = lsh_bench(lib, max(args.steps, 10), max(args.warmup, 2))
+        torch.cuda.empty_cache()
+        # configs[3]'s other contexts: 8k (512 pages per sequence) and 128k
+        # (8192 pages: twice the reference index's LSH_MAX_BLOCKS)
+        out["lsh_attention_8k"] = lsh_bench(lib, max(args.steps, 10), max(args.warmup, 2), ctx=8192)
+        torch.cuda.empty_cache()
+        out["lsh_attention_128k"] = lsh_bench(lib, max(args.steps, 10), max(args.warmup, 2), batches=[1, 16, 64],
+                                              ctx=131072)
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
         out["cpu_baseline"]["host"] = host_info()
