@@ -450,9 +450,12 @@ static void launch_gemm(float *Y, const uint8_t *X, const float *sx, const uint8
 
 // Kernel and tile choice.  K a multiple of 128 (and operands under 4 GiB):
 // the direct-to-LDS kernel, at 256 x 256 when that grid alone fills the 256
-// CUs, else at 128 x 128.  Otherwise the register-staged 16x16 kernel at
-// 128 x 128 when its grid holds two workgroups per CU, else 64 x 128.
-// BE42_GEMM_TILE = 1..4 forces one of the four (1 and 2 only where K allows).
+// CUs, at 64 x 128 (4 waves of 32 x 64, a 4-stage ring) when 128 x 128 tiles
+// would leave CUs idle (fewer than 256 tiles: M = 512 at N = 4096), else at
+// 128 x 128.  Otherwise the register-staged 16x16 kernel at 128 x 128 when
+// its grid holds two workgroups per CU, else 64 x 128.
+// BE42_GEMM_TILE = 1..5 forces one of the five (1, 2 and 5 only where K
+// allows; 5 is the 64 x 128 direct-to-LDS tile).
 template <bool FP8>
 static void gemm_dispatch(float *Y, const uint8_t *X, const float *sx, const uint8_t *W, const float *sw, int M,
                           int N, int K, hipStream_t s)
@@ -464,6 +467,8 @@ static void gemm_dispatch(float *Y, const uint8_t *X, const float *sx, const uin
     const int force = e ? atoi(e) : 0;
     if (dma && (force == 1 || (!force && tiles256 >= 256)))
         launch_gemm_dma<FP8, 256, 256, 2, 4, 2>(Y, X, sx, W, sw, M, N, K, s);
+    else if (dma && (force == 5 || (!force && tiles128 < 256)))
+        launch_gemm_dma<FP8, 64, 128, 2, 2, 4>(Y, X, sx, W, sw, M, N, K, s);
     else if (dma && (force == 2 || !force))
         launch_gemm_dma<FP8, 128, 128, 2, 2, 2>(Y, X, sx, W, sw, M, N, K, s);
     else if (force == 3 || (!force && tiles128 >= 512))

@@ -889,14 +889,15 @@ def lsh_probe():
 
 def gemm_probe():
     """For rocprofv3 runs: 5 launches each of the prefill GEMM at FP8
-    8192x4096x14336 (the best shape) and INT8 512x4096x4096."""
+    8192x4096x14336 (the best shape), INT8 2048x4096x14336 and INT8
+    512x4096x4096."""
     import torch
     import be42
     lib = be42.load()
     lib.init(0)
     g = torch.Generator(device="cuda")
     g.manual_seed(11)
-    for kind, m, n, k in (("fp8", 8192, 4096, 14336), ("int8", 512, 4096, 4096)):
+    for kind, m, n, k in (("fp8", 8192, 4096, 14336), ("int8", 2048, 4096, 14336), ("int8", 512, 4096, 4096)):
         qf = lib.quant_rows_int8 if kind == "int8" else lib.quant_rows_fp8
         wq, sw = qf(torch.randn(n, k, generator=g, device="cuda") * 0.02)
         xq, sx = qf(torch.randn(m, k, generator=g, device="cuda"))

@@ -131,16 +131,16 @@ def test_gemm_rejects_bad_shapes(be):
 
 
 @pytest.mark.parametrize("kind", ["int8", "fp8"])
-@pytest.mark.parametrize("tile", ["1", "2", "3", "4"])
+@pytest.mark.parametrize("tile", ["1", "2", "3", "4", "5"])
 def test_gemm_every_tile(be, orc, kind, tile, monkeypatch):
-    """Each kernel and workgroup tiling (BE42_GEMM_TILE: 1 = 256x256 and
-    2 = 128x128 on the direct-to-LDS 32x32 kernel, which needs k a multiple
-    of 128; 3 = 128x128 and 4 = 64x128 on the 16x16 kernel, here with k not
-    a multiple of the 128-byte stage) on a ragged shape whose edges cut
-    every tile."""
+    """Each kernel and workgroup tiling (BE42_GEMM_TILE: 1 = 256x256,
+    2 = 128x128 and 5 = 64x128 on the direct-to-LDS 32x32 kernel, which needs
+    k a multiple of 128; 3 = 128x128 and 4 = 64x128 on the 16x16 kernel, here
+    with k not a multiple of the 128-byte stage) on a ragged shape whose
+    edges cut every tile."""
     monkeypatch.setenv("BE42_GEMM_TILE", tile)
     rng = np.random.default_rng(77 + int(tile))
-    m, n, k = (300, 520, 1152) if tile in ("1", "2") else (300, 520, 1040)
+    m, n, k = (300, 520, 1152) if tile in ("1", "2", "5") else (300, 520, 1040)
     x, w = _inputs(rng, m, n, k)
     xq, sx = orc.quantize_rows(x, kind)
     wq, sw = orc.quantize_rows(w, kind)
