@@ -101,6 +101,44 @@ def cpu_baseline(seconds=10.0):
                       f"median of {len(times)} runs over {seconds:.0f} s"}
 
 
+def cpu_baseline_reference(seconds=10.0):
+    """The reference's own decode GEMV: op_matmul (ops_matmul.c:366) with BF16
+    weights and an fp32 column, i.e. matvec_bf16_f32_blocked (:57-153, AVX2
+    + OpenMP), compiled from the reference sources by oracle/Makefile into
+    oracle/_ref/libref42.so; 14336x4096 at batch 1 on a bounded sample.  The
+    reference has no INT8/FP8 GEMV, so its bytes are 2 per weight."""
+    import ctypes as C
+    import numpy as np
+    from oracle_bind import REF_SO, RefLib
+
+    if not os.path.exists(REF_SO):
+        return None
+    ref = RefLib()
+    cores = cpu_threads()
+    rng = np.random.default_rng(2)
+    n, k = 14336, 4096
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wb = (w.view(np.uint32) >> 16).astype(np.uint16)          # bf16 codes (truncated)
+    x = rng.standard_normal((k, 1)).astype(np.float32)
+    y = np.zeros((n, 1), np.float32)
+    call = lambda: ref.lib.ref_matmul(y.ctypes.data, 0, wb.ctypes.data, 1, n, k, x.ctypes.data, 0, 1)  # noqa: E731
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    if call() != 0:
+        return None
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end and len(times) < 500:
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    nbytes = 2 * n * k + 4 * k + 4 * n
+    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "reference",
+            "sample": f"reference op_matmul BF16 {n}x{k} x fp32 column (matvec_bf16_f32_blocked, AVX2 + OpenMP, "
+                      f"{cores} threads, built -O3 -march=x86-64-v3), median of {len(times)} runs over "
+                      f"{seconds:.0f} s; GB/s of bf16 weight bytes"}
+
+
 # ---- LSH sparse attention (BASELINE.json configs[3]) ------------------------
 LSH = dict(heads=32, kv_heads=8, head_dim=128, page=16, ctx=32768, k_sel=64, cap=64, planted=0.05)
 LSH_BATCHES = [1, 16, 64, 128]
@@ -1138,8 +1176,17 @@ def main():
                                               ctx=131072)
         torch.cuda.empty_cache()
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline()
-        out["cpu_baseline"]["host"] = host_info()
+        # the reference's own GEMV (BF16 weights) when its compiled sources
+        # are here; the oracle's INT8 port of its structure beside it
+        port = cpu_baseline()
+        port["host"] = host_info()
+        ref_gemv = cpu_baseline_reference()
+        if ref_gemv is not None:
+            ref_gemv["host"] = port["host"]
+            out["cpu_baseline"] = ref_gemv
+            out["cpu_baseline_port"] = port
+        else:
+            out["cpu_baseline"] = port
         if not args.no_lsh:
             out["lsh_attention"]["cpu_baseline"] = lsh_cpu_baseline()
         if not args.no_gemm:
