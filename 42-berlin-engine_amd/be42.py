@@ -597,6 +597,9 @@ class Model:
                        nxt.ctypes.data if sync else None, self.lib.p(logits), self.lib.stream())
         return nxt
 
+    def capture_kv(self, k=None, v=None):
+        self.lib._call("be42_decoder_capture_kv", self.dec, self.lib.p(k), self.lib.p(v))
+
     def close(self):
         if self.handle:
             self.lib.torch.cuda.synchronize()

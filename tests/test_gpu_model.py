@@ -78,3 +78,45 @@ def test_loaded_model_matches_direct_decoder(be, orc, tmp_path, kind, names, fmt
     model.close()
     direct.close()
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind,kv", [("int8", OR_KV_INT8), ("fp8", OR_KV_BF16)])
+def test_loaded_model_against_oracle(be, orc, tmp_path, kind, kv):
+    """A checkpoint of stored codes (I8 / F8_E4M3 + F32 row scales), loaded by
+    be42_model_load, against the oracle's transformer_forward on the same
+    numpy weights (not against another GPU decoder): 24 prompt tokens, then
+    greedy steps, the oracle fed the K/V rows the loaded decoder appended
+    (captured per layer), so both caches hold the same codes.  Every step's
+    logits within the north star's 1e-3 (max|dl| / max|l|), tokens
+    identical outside near ties."""
+    from oracle_bind import OracleDecoder
+    from test_gpu_decode import near_tie
+    rng = np.random.default_rng(91)
+    dims = tuple(TINY[k] for k in ("n_layers", "dim", "n_heads", "n_kv", "hd", "hidden", "vocab"))
+    w = make_model(rng, *dims, kind)
+    m, c = str(tmp_path / "m.safetensors"), str(tmp_path / "config.json")
+    write_checkpoint(m, w, kind, names="hf", fmt="codes")
+    write_config(c, **TINY, theta=10000.0)
+    model = be42.Model(be, m, c, max_seq=256, max_batch=1, kv_kind=be42.KV_INT8 if kv == OR_KV_INT8 else be42.KV_BF16,
+                       quant_kind=0 if kind == "int8" else 1)
+    oc, _ = configs(*dims, 256, 1, kind, kv, 64, 64)
+    _, hpT = orc.lsh_init(TINY["hd"], 42)                 # the loader's default projection seed
+    od = OracleDecoder(orc, oc, w, hpT)
+    L, kd, V = TINY["n_layers"], TINY["n_kv"] * TINY["hd"], TINY["vocab"]
+    ck = torch.zeros((L, 1, kd), device="cuda")
+    cv = torch.zeros_like(ck)
+    model.capture_kv(ck, cv)
+    logits = torch.empty((1, V), device="cuda")
+    tokens = rng.integers(0, V, 24)
+    cur = int(tokens[0])
+    for pos in range(24 + 8 - 1):
+        nxt = int(model.step([cur], pos, logits=logits)[0])
+        on, ol = od.step(cur, pos, force_k=ck[:, 0].cpu().numpy(), force_v=cv[:, 0].cpu().numpy())
+        gl = logits[0].cpu().numpy()
+        err = np.max(np.abs(gl - ol)) / np.max(np.abs(ol))
+        assert err <= 1e-3, (pos, err)
+        if pos >= 23 and nxt != on:
+            assert near_tie(ol), (pos, nxt, on)
+            break
+        cur = int(tokens[pos + 1]) if pos + 1 < 24 else nxt
+    model.close()
