@@ -80,6 +80,53 @@ __global__ __launch_bounds__(256) void k_gemv_prep(const float *__restrict__ x, 
     store_digit_words<FP8>(xe, s, dig, B, Kp, b, k0);
 }
 
+// The same digit planes for rows of at most 1024 * NV elements in one round
+// trip to memory: thread t loads float4 t of every 256-float4 chunk of the
+// row at once (zero past K), so the absmax needs no second pass.  Register j
+// holds chunk (blockIdx.x + j) mod chunks, so register 0 is already this
+// block's element (a register picked by blockIdx.x would be an indexed access,
+// which the compiler places in scratch memory).  Same grid and layout as
+// k_gemv_prep; the maximum is order-free, so the digits are the same bytes.
+template <bool FP8, int NV>
+__global__ __launch_bounds__(256) void k_gemv_prep_row(const float *__restrict__ x, int K, int Kp, int B,
+                                                       uint8_t *__restrict__ dig, float *__restrict__ sx)
+{
+    __shared__ float red[4];
+    const int b = blockIdx.y, t = threadIdx.x, nch = gridDim.x;
+    const float4 *x4 = (const float4 *)(x + (size_t)b * K);
+    const int n4 = K >> 2;
+    // unconditional loads at a clamped index, zeroed after: straight-line
+    // code keeps every load in flight at once and the array in registers
+    float4 v[NV];
+    bool in[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        int c = (int)blockIdx.x + j;
+        c = c >= nch ? c - nch : c;
+        const int i = 256 * c + t;
+        in[j] = j < nch && i < n4;
+        v[j] = x4[min(i, n4 - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+        if (!in[j])
+            v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    m = wave_max(m);
+    if ((t & 63) == 0)
+        red[t >> 6] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = digit_scale<FP8>(amax);
+    if (blockIdx.x == 0 && t == 0)
+        sx[b] = s;
+    const float xe[4] = {v[0].x, v[0].y, v[0].z, v[0].w};
+    store_digit_words<FP8>(xe, s, dig, B, Kp, b, blockIdx.x * kPrepChunk + t * 4);
+}
+
 __constant__ double kF8Weight[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 27000, 1.0 / 810000};
 
 // Up to three weight matrices that share one input (the q/k/v or gate/up
@@ -1083,11 +1130,29 @@ int xdig_prepare(void *buf, const float *x, int k, int batch, bool fp8, hipStrea
     uint8_t *dig = (uint8_t *)buf;
     const size_t dbytes = (size_t)xdig_layout(fp8).nd * batch * Kp;
     float *sx = (float *)(dig + ((dbytes + 255) & ~(size_t)255));
-    const dim3 grid((Kp + kPrepChunk - 1) / kPrepChunk, batch);
+    const int chunks = (Kp + kPrepChunk - 1) / kPrepChunk;
+    const dim3 grid(chunks, batch);
+    // one load per thread and register slot: rows up to 16 chunks (16384 k)
+    // in one round trip; longer rows by the two-pass kernel
+    auto row = [&](auto f8) {
+        constexpr bool F = decltype(f8)::value;
+        if (chunks <= 1)
+            hipLaunchKernelGGL((k_gemv_prep_row<F, 1>), grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+        else if (chunks <= 2)
+            hipLaunchKernelGGL((k_gemv_prep_row<F, 2>), grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+        else if (chunks <= 4)
+            hipLaunchKernelGGL((k_gemv_prep_row<F, 4>), grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+        else if (chunks <= 8)
+            hipLaunchKernelGGL((k_gemv_prep_row<F, 8>), grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+        else if (chunks <= 16)
+            hipLaunchKernelGGL((k_gemv_prep_row<F, 16>), grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+        else
+            hipLaunchKernelGGL(k_gemv_prep<F>, grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+    };
     if (fp8)
-        hipLaunchKernelGGL(k_gemv_prep<true>, grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+        row(std::true_type{});
     else
-        hipLaunchKernelGGL(k_gemv_prep<false>, grid, dim3(256), 0, s, x, k, Kp, batch, dig, sx);
+        row(std::false_type{});
     BE42_LAUNCH_CHECK();
     return BE42_OK;
 }
