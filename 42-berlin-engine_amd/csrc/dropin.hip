@@ -356,6 +356,44 @@ __global__ __launch_bounds__(256) void k_rope_heads(float *__restrict__ data, in
     x[i + half] = __fmaf_rn(x0, s, x1 * c);
 }
 
+// op_rope (ops_rope.c:278-353) on nvec [hd] vectors of F32 or BF16 data:
+// cs holds cos then sin of the hd / 2 angles (computed on the host with the
+// C library, as the reference does); inputs scaled by mscale when it is not
+// 1, then x0' = fma(x0, c, -(x1 * s)), x1' = fma(x0, s, x1 * c), the
+// compiled loop's contraction.
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_rope_ctx(void *__restrict__ data, int nvec, int hd,
+                                                  const float *__restrict__ cs, float mscale)
+{
+    const int half = hd / 2;
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (long long)nvec * half)
+        return;
+    const int v = (int)(t / half), j = (int)(t % half);
+    const size_t i0 = (size_t)v * hd + j, i1 = i0 + half;
+    float x0, x1;
+    if constexpr (BF16) {
+        x0 = bf16_to_f32(((const uint16_t *)data)[i0]);
+        x1 = bf16_to_f32(((const uint16_t *)data)[i1]);
+    } else {
+        x0 = ((const float *)data)[i0];
+        x1 = ((const float *)data)[i1];
+    }
+    if (mscale != 1.0f) {
+        x0 = x0 * mscale;
+        x1 = x1 * mscale;
+    }
+    const float c = cs[j], s = cs[half + j];
+    const float y0 = __fmaf_rn(x0, c, -(x1 * s)), y1 = __fmaf_rn(x0, s, x1 * c);
+    if constexpr (BF16) {
+        ((uint16_t *)data)[i0] = f32_to_bf16(y0);
+        ((uint16_t *)data)[i1] = f32_to_bf16(y1);
+    } else {
+        ((float *)data)[i0] = y0;
+        ((float *)data)[i1] = y1;
+    }
+}
+
 // sample_argmax (sampler.c:42-148) in one block.  F32: argmax_simd_f32 --
 // the maximum wins; equal maxima in the 8-lane part (indices below
 // 8 * floor(n / 8), n >= 8) go to the lowest lane (i % 8), then the first
@@ -998,6 +1036,68 @@ extern "C" void rope_apply_multihead_cached(float *data, int n_heads, int pos, c
                        ct + (size_t)pos * half, sn + (size_t)pos * half);
     hip_ok(hipGetLastError(), "rope_apply_multihead_cached");
     out_done(data, d, bytes, st);
+}
+
+// theta of pair index j2 = 2j without a thetas cache (get_yarn_theta and
+// compute_yarn_ramp, ops_rope.c:243-276): frequency index j2 / hd in float,
+// powers in double, the YaRN ramp between beta_slow / hd and beta_fast / hd
+// when factor > 1, its (1 - a) * t + a * ts fused on the first product as
+// the compiled reference evaluates it.
+static float yarn_theta(int j2, const t_rope_ctx *c)
+{
+    const float f = (float)j2 / (float)c->head_dim;
+    const double td = 1.0 / ::pow((double)c->theta_base, (double)f);
+    if (c->factor <= 1.0f)
+        return (float)td;
+    const float lo = c->beta_slow / (float)c->head_dim, hi = c->beta_fast / (float)c->head_dim;
+    if (f < lo)
+        return (float)td;
+    const double ts = 1.0 / ::pow((double)(c->theta_base * c->factor), (double)f);
+    if (f > hi)
+        return (float)ts;
+    const float a = (f - lo) / (hi - lo);
+    return (float)::fma(1.0 - (double)a, td, (double)a * ts);
+}
+
+extern "C" void op_rope(t_tensor *x, int pos, const t_rope_ctx *ctx)
+{
+    if (!x || !x->data || !ctx)
+        return;
+    const bool bf = x->dtype == DTYPE_BF16;
+    if (!bf && x->dtype != DTYPE_F32)
+        return;
+    const int hd = ctx->head_dim, half = hd / 2;
+    if (hd <= 0 || half == 0)
+        return;
+    const size_t nvec = x->size / (size_t)hd;
+    if (nvec == 0)
+        return;
+    const size_t n = nvec * (size_t)half;
+    if (nvec > (size_t)INT32_MAX || (n + 255) / 256 > (size_t)INT32_MAX)
+        die("op_rope", "tensor too large");
+    // angles and their cosine / sine on the host: cosf and sinf of the C
+    // library, the reference's own
+    std::vector<float> cs(2 * (size_t)half);
+    for (int j = 0; j < half; j++) {
+        const float th = ctx->thetas_cache ? ctx->thetas_cache[j] : yarn_theta(2 * j, ctx);
+        const float ang = (float)pos * th;
+        cs[j] = ::cosf(ang);
+        cs[half + j] = ::sinf(ang);
+    }
+    std::lock_guard<std::mutex> g(rt().mu);
+    const size_t bytes = x->size * (bf ? 2 : 4);
+    const float *dcs = (const float *)in_dev(cs.data(), cs.size() * 4, kS0);
+    bool st;
+    void *d = out_dev(x->data, bytes, kS1, &st);
+    if (st)
+        hip_ok(hipMemcpy(d, x->data, bytes, hipMemcpyHostToDevice), "op_rope");
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (bf)
+        hipLaunchKernelGGL(k_rope_ctx<true>, grid, dim3(256), 0, nullptr, d, (int)nvec, hd, dcs, ctx->mscale);
+    else
+        hipLaunchKernelGGL(k_rope_ctx<false>, grid, dim3(256), 0, nullptr, d, (int)nvec, hd, dcs, ctx->mscale);
+    hip_ok(hipGetLastError(), "op_rope");
+    out_done(x->data, d, bytes, st);
 }
 
 extern "C" int sample_argmax(const t_tensor *logits)

@@ -87,8 +87,25 @@ int op_matmul(t_tensor *out, const t_tensor *a, const t_tensor *b);
  * rope_apply_multihead_cached: rotates n_heads contiguous [head_dim] vectors
  * in place with the cache's tables (host tables, mirrored to HBM once);
  * positions at or past max_seq_len are left unchanged.
+ * op_rope: the same rotation for transformer_forward's path without a RoPE
+ * cache: x->size / head_dim vectors of F32 or BF16 x (other dtypes, a null x
+ * or data: nothing), thetas from ctx->thetas_cache (host, head_dim / 2
+ * floats) or the YaRN formula, angle pos * theta (ctx->pos is ignored),
+ * inputs scaled by mscale when it is not 1.
  * sample_argmax: index of the largest logit (F32: argmax_simd_f32's lane tie
  * rule; BF16: first maximum above -1e9). */
+typedef struct s_rope_ctx {                                        /* ops.h:19-31 */
+    int head_dim;
+    int pos;
+    float theta_base;
+    float beta_fast;    /* YaRN */
+    float beta_slow;
+    float factor;
+    float mscale;
+    int orig_ctx;
+    float *thetas_cache;  /* [head_dim / 2] or NULL */
+} t_rope_ctx;
+
 typedef struct s_rope_cache {                                      /* ops_rope.h:33-38 */
     float *cos_table;   /* [max_seq_len][head_dim / 2] */
     float *sin_table;
@@ -102,6 +119,7 @@ void op_silu_mul(t_tensor *out, const t_tensor *gate,                /* ops.h:41
                  const t_tensor *val);
 void rope_apply_multihead_cached(float *data, int n_heads, int pos,   /* ops_rope.h:80 */
                                  const t_rope_cache *cache);
+void op_rope(t_tensor *x, int pos, const t_rope_ctx *ctx);          /* ops.h:36 */
 int sample_argmax(const t_tensor *logits);                         /* sampler.h:19 */
 
 /* ---- quant codecs (src/compute/ops_quant.h:22-117) ------------------------- */

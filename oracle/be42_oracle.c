@@ -1076,6 +1076,71 @@ void or_rope_apply(float *data, int n_heads, int hd, int pos, int n_pos, const f
     }
 }
 
+/* theta of pair index j2 = 2j for op_rope without a thetas cache
+ * (get_yarn_theta / compute_yarn_ramp, ops_rope.c:243-276): frequency index
+ * j2 / hd in float, powers in double, YaRN ramp between beta_slow / hd and
+ * beta_fast / hd when factor > 1.  The ramp's (1 - a) * t + a * ts is fused
+ * by gcc (GNU C, -mfma) on its first product. */
+static float or_yarn_theta(int j2, int hd, float theta_base, float beta_fast, float beta_slow, float factor)
+{
+    const float f = (float)j2 / (float)hd;
+    const double td = 1.0 / pow(theta_base, f);
+    if (factor <= 1.0f)
+        return (float)td;
+    const float lo = beta_slow / (float)hd, hi = beta_fast / (float)hd;
+    if (f < lo)
+        return (float)td;
+    const double ts = 1.0 / pow(theta_base * factor, f);
+    if (f > hi)
+        return (float)ts;
+    const float a = (f - lo) / (hi - lo);
+    return (float)fma(1.0 - a, td, a * ts);
+}
+
+/* op_rope with t_rope_ctx, ops_rope.c:278-353: angle = (float)pos * theta[j],
+ * optional mscale on both inputs, x0' = fma(x0, cos, -(x1 * sin)),
+ * x1' = fma(x0, sin, x1 * cos) (gcc fuses each expression's first product);
+ * BF16 in (bits << 16) and out (round to nearest even).  Trailing elements
+ * beyond the last whole vector are left alone. */
+void or_op_rope(void *data, int bf16, int n, int pos, int hd, float theta_base, float beta_fast,
+                float beta_slow, float factor, float mscale, const float *thetas_cache)
+{
+    const int half = hd / 2;
+    if (hd <= 0 || half == 0)
+        return;
+    float *th = malloc(sizeof(float) * (size_t)half);
+    for (int j = 0; j < half; j++)
+        th[j] = thetas_cache ? thetas_cache[j] : or_yarn_theta(2 * j, hd, theta_base, beta_fast, beta_slow, factor);
+    const int nv = n / hd;
+    for (int v = 0; v < nv; v++)
+        for (int j = 0; j < half; j++) {
+            const float ang = (float)pos * th[j];
+            const float c = cosf(ang), s = sinf(ang);
+            const size_t i0 = (size_t)v * hd + j, i1 = i0 + half;
+            float x0, x1;
+            if (bf16) {
+                x0 = or_bf16_to_f32(((uint16_t *)data)[i0]);
+                x1 = or_bf16_to_f32(((uint16_t *)data)[i1]);
+            } else {
+                x0 = ((float *)data)[i0];
+                x1 = ((float *)data)[i1];
+            }
+            if (mscale != 1.0f) {
+                x0 = x0 * mscale;
+                x1 = x1 * mscale;
+            }
+            const float y0 = fmaf(x0, c, -(x1 * s)), y1 = fmaf(x0, s, x1 * c);
+            if (bf16) {
+                ((uint16_t *)data)[i0] = or_f32_to_bf16(y0);
+                ((uint16_t *)data)[i1] = or_f32_to_bf16(y1);
+            } else {
+                ((float *)data)[i0] = y0;
+                ((float *)data)[i1] = y1;
+            }
+        }
+    free(th);
+}
+
 /* fast_expf_avx2, ops_math_fast.h:105-126: clamp to [-87, 87], fused
  * 12102203 * x + 1065353216, convert with round-to-nearest-even. */
 static float fast_expf_vec(float x)

@@ -186,6 +186,10 @@ void or_rmsnorm(float *out, const float *x, const uint16_t *w, int dim, float ep
 void or_rope_table(float *cos_t, float *sin_t, int hd, int n_pos, float theta);          /* ops_rope.c:30-95 */
 void or_rope_apply(float *data, int n_heads, int hd, int pos, int n_pos,
                    const float *cos_t, const float *sin_t);                              /* ops_rope.c:192-228 */
+/* op_rope (legacy t_rope_ctx path): n elements of F32 (bf16 = 0) or BF16 data
+ * rotated in place as n / hd vectors; thetas_cache NULL = YaRN thetas. */
+void or_op_rope(void *data, int bf16, int n, int pos, int hd, float theta_base, float beta_fast,
+                float beta_slow, float factor, float mscale, const float *thetas_cache);  /* ops_rope.c:243-353 */
 void or_silu_mul(float *dst, const float *gate, const float *up, int n);                 /* ops_activation.c:48-105 */
 int  or_argmax(const float *x, int n);                                                   /* sampler.c:42-117 */
 int  or_sample_temperature(const float *x, int n, float temp, float r);                         /* sampler_temp.c:96-114 */

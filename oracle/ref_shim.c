@@ -273,6 +273,25 @@ void ref_silu_mul_bf16(uint16_t *dst, const uint16_t *gate, const uint16_t *up, 
     op_silu_mul_fused_bf16(dst, gate, up, (size_t)n);
 }
 
+/* op_rope through a t_rope_ctx: n elements (F32, or BF16 when bf16) */
+void ref_op_rope(void *data, int bf16, int n, int pos, int hd, float theta_base, float beta_fast,
+                 float beta_slow, float factor, float mscale, float *thetas)
+{
+    int s[1] = {n};
+    t_tensor t = tensor_view(data, s, 1);
+    t.dtype = bf16 ? DTYPE_BF16 : DTYPE_F32;
+    t_rope_ctx c;
+    memset(&c, 0, sizeof c);
+    c.head_dim = hd;
+    c.theta_base = theta_base;
+    c.beta_fast = beta_fast;
+    c.beta_slow = beta_slow;
+    c.factor = factor;
+    c.mscale = mscale;
+    c.thetas_cache = thetas;
+    op_rope(&t, pos, &c);
+}
+
 int ref_argmax_bf16(uint16_t *x, int n)
 {
     int s[1] = {n};

@@ -53,6 +53,12 @@ class RopeCache(C.Structure):
                 ("max_seq_len", C.c_int)]
 
 
+class RopeCtx(C.Structure):
+    _fields_ = [("head_dim", C.c_int), ("pos", C.c_int), ("theta_base", C.c_float), ("beta_fast", C.c_float),
+                ("beta_slow", C.c_float), ("factor", C.c_float), ("mscale", C.c_float), ("orig_ctx", C.c_int),
+                ("thetas_cache", C.c_void_p)]
+
+
 class LshStats(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in ("total_queries", "validated_queries", "topk_hits", "topk_total",
                                           "recall_scaled", "validation_count", "total_used_k", "k_samples")]
@@ -125,6 +131,7 @@ def bind(lib):
         "op_rmsnorm": (None, [P(Tensor), P(Tensor), P(Tensor), f32]),
         "op_silu_mul": (None, [P(Tensor), P(Tensor), P(Tensor)]),
         "rope_apply_multihead_cached": (None, [vp, i32, i32, P(RopeCache)]),
+        "op_rope": (None, [P(Tensor), i32, P(RopeCtx)]),
         "sample_argmax": (i32, [P(Tensor)]),
         "sample_temperature": (i32, [P(Tensor), f32, P(Arena)]),
         "sample_top_p": (i32, [P(Tensor), f32, f32, P(Arena)]),

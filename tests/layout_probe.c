@@ -10,6 +10,8 @@
 #include "compute/ops_quant.h"
 #include "memory/kv_cache.h"
 #include "compute/ops_attention.h"
+#include "compute/ops.h"
+#include "compute/ops_rope.h"
 #else
 #include "be42_engine.h"
 #endif
@@ -32,6 +34,9 @@ int main(void) {
   S(t_kv_init_params); S(t_evict_params); O(t_evict_params, w); O(t_evict_params, keep_k); O(t_evict_params, scratch);
   S(t_attention_params); O(t_attention_params, kv_cache); O(t_attention_params, output); O(t_attention_params, n_heads);
   O(t_attention_params, scale); O(t_attention_params, topk_idx); O(t_attention_params, attend_k);
+  S(t_rope_ctx); O(t_rope_ctx, pos); O(t_rope_ctx, theta_base); O(t_rope_ctx, mscale); O(t_rope_ctx, orig_ctx);
+  O(t_rope_ctx, thetas_cache);
+  S(t_rope_cache); O(t_rope_cache, sin_table); O(t_rope_cache, head_dim); O(t_rope_cache, max_seq_len);
   O(t_tensor, shape); O(t_tensor, stride); O(t_tensor, ndim); O(t_tensor, size); O(t_tensor, dtype);
   printf("DTYPE_F32 %d DTYPE_BF16 %d\n", (int)DTYPE_F32, (int)DTYPE_BF16);
   return 0;

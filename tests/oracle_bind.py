@@ -198,6 +198,8 @@ class Oracle:
         _sig(L, "or_rmsnorm", None, f32p, f32p, u16p, C.c_int, C.c_float)
         _sig(L, "or_rope_table", None, f32p, f32p, C.c_int, C.c_int, C.c_float)
         _sig(L, "or_rope_apply", None, f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p, f32p)
+        _sig(L, "or_op_rope", None, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
+             C.c_float, C.c_float, C.c_float, C.c_void_p)
         _sig(L, "or_silu_mul", None, f32p, f32p, f32p, C.c_int)
         _sig(L, "or_argmax", C.c_int, f32p, C.c_int)
         _sig(L, "or_sample_temperature", C.c_int, f32p, C.c_int, C.c_float, C.c_float)
@@ -242,6 +244,15 @@ class Oracle:
     def rope_apply(self, data, n_heads, hd, pos, cos_t, sin_t):
         d = np.ascontiguousarray(data, np.float32).copy()
         self.lib.or_rope_apply(d, n_heads, hd, pos, len(cos_t) // (hd // 2), cos_t, sin_t)
+        return d
+
+    def op_rope(self, data, pos, hd, theta_base=1e4, beta_fast=32.0, beta_slow=1.0, factor=1.0, mscale=1.0,
+                thetas=None):
+        """op_rope with a t_rope_ctx on a copy of data (float32, or uint16 as BF16)."""
+        d = np.ascontiguousarray(data).copy()
+        th = None if thetas is None else np.ascontiguousarray(thetas, np.float32)
+        self.lib.or_op_rope(d.ctypes.data, int(d.dtype == np.uint16), d.size, pos, hd, theta_base, beta_fast,
+                            beta_slow, factor, mscale, None if th is None else th.ctypes.data)
         return d
 
     def silu_mul(self, g, u):
@@ -565,6 +576,8 @@ class RefLib:
         _sig(L, "ref_sample_temperature", C.c_int, f32p, C.c_int, C.c_float)
         _sig(L, "ref_silu_mul_bf16", None, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int)
         _sig(L, "ref_argmax_bf16", C.c_int, C.c_void_p, C.c_int)
+        _sig(L, "ref_op_rope", None, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
+             C.c_float, C.c_float, C.c_float, C.c_void_p)
         _sig(L, "ref_validate_recall", C.c_float, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
              C.c_int)
         _sig(L, "ref_adaptive_k", C.c_int, C.c_void_p, C.c_int, C.c_float)

@@ -27,7 +27,8 @@ def test_layouts_match_ctypes_mirror(tmp_path):
     mirror = {"t_lsh_ctx": D.LshCtx, "t_block_acc": D.BlockAcc, "t_lsh_index": D.LshIndex, "t_kv_block": D.KvBlock,
               "t_block_manager": D.BlockManager, "t_paged_kv_cache": D.PagedKv, "t_block_score": D.BlockScore,
               "t_tensor": D.Tensor, "t_arena": D.Arena, "t_kv_cache": D.KvCache, "t_kv_init_params": D.KvInitParams,
-              "t_evict_params": D.EvictParams, "t_attention_params": D.AttentionParams}
+              "t_evict_params": D.EvictParams, "t_attention_params": D.AttentionParams, "t_rope_ctx": D.RopeCtx,
+              "t_rope_cache": D.RopeCache}
     for key, val in lay.items():
         if "." in key:
             t, f = key.split(".")

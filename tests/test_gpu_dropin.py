@@ -426,6 +426,37 @@ def test_adjacent_ops(dl, orc):
     assert dl.sample_argmax(C.byref(D.tensor(xb, D.DTYPE_BF16, 1, 1000))) == orc.argmax_bf16(xb)
 
 
+@pytest.mark.parametrize("hd,theta,factor,mscale,bf16,cache", [
+    (64, 1e4, 1.0, 1.0, False, False),
+    (128, 5e5, 8.0, 1.2079, False, False),      # YaRN ramp and mscale
+    (128, 1e4, 4.0, 1.0, True, False),
+    (96, 1e4, 1.0, 1.0, True, True),            # thetas cache, BF16
+])
+def test_op_rope_ctx(dl, orc, hd, theta, factor, mscale, bf16, cache):
+    """op_rope with a t_rope_ctx (transformer_forward without a RoPE cache)
+    through the drop-in, host and device data, bit-exact against the oracle
+    (pinned to the compiled reference); ctx->pos is ignored, the tail past the
+    last whole vector is untouched."""
+    rng = np.random.default_rng(hd + int(factor))
+    mscale = float(np.float32(mscale))
+    thetas = (1.0 / (theta ** (np.arange(0, hd, 2) / hd))).astype(np.float32) if cache else None
+    ctx = D.RopeCtx(hd, 999, theta, 32.0, 1.0, factor, mscale, 4096, None if thetas is None else thetas.ctypes.data)
+    dt = D.DTYPE_BF16 if bf16 else D.DTYPE_F32
+    for pos in (0, 1, 77, 5000, 131071):
+        x = rng.standard_normal(7 * hd + 5).astype(np.float32)
+        if bf16:
+            x = orc.f32_to_bf16(x)
+        want = orc.op_rope(x, pos, hd, theta_base=theta, factor=factor, mscale=mscale, thetas=thetas)
+        got = x.copy()
+        dl.op_rope(C.byref(D.tensor(got, dt, 1, got.size)), pos, C.byref(ctx))
+        np.testing.assert_array_equal(got, want)
+        xd = torch.from_numpy(x.view(np.int16) if bf16 else x).cuda()
+        dl.op_rope(C.byref(D.tensor(xd.data_ptr(), dt, 1, x.size)), pos, C.byref(ctx))
+        torch.cuda.synchronize()
+        gd = xd.cpu().numpy()
+        np.testing.assert_array_equal(gd.view(np.uint16) if bf16 else gd, want)
+
+
 def test_lsh_diagnostics(dl, orc, capfd):
     """lsh_validate_recall and adaptive_k_cutoff (ops_lsh.c:513-668) against
     the oracle (pinned to the compiled reference); the stats counters reset

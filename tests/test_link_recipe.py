@@ -113,6 +113,6 @@ def test_reference_links_against_library(tmp_path):
     assert not (defined & entry), sorted(defined & entry)
     imported = syms("-D", "--undefined-only")
     for name in ("op_matmul", "paged_kv_append", "op_paged_attention_sparse", "score_blocks",
-                 "select_top_k_blocks", "lsh_update", "op_rmsnorm", "op_silu_mul", "rope_apply_multihead_cached",
+                 "select_top_k_blocks", "lsh_update", "op_rmsnorm", "op_silu_mul", "rope_apply_multihead_cached", "op_rope",
                  "sample_argmax", "kv_cache_append", "op_multihead_attention"):
         assert name in imported, name

@@ -55,6 +55,65 @@ def test_rope(orc, ref, hd, theta):
                 np.testing.assert_allclose(ga ** 2 + gb ** 2, a ** 2 + b ** 2, rtol=2e-5, atol=1e-6)
 
 
+# op_rope's t_rope_ctx path (ops_rope.c:243-353): plain thetas, a YaRN ramp
+# with mscale, a thetas cache, BF16 data and a ragged tail
+ROPE_CASES = [
+    dict(hd=64, theta_base=1e4, factor=1.0, mscale=1.0, bf16=False, cache=False),
+    dict(hd=128, theta_base=5e5, factor=8.0, mscale=float(np.float32(np.sqrt(0.1 * np.log(8.0) + 1.0))),
+         bf16=False, cache=False),
+    dict(hd=128, theta_base=1e4, factor=4.0, mscale=1.0, bf16=True, cache=False),
+    dict(hd=96, theta_base=1e4, factor=1.0, mscale=1.0, bf16=True, cache=True),
+]
+
+
+def rope_case_data(orc, c, rng, nvec=5, tail=3):
+    x = rng.standard_normal(nvec * c["hd"] + tail).astype(np.float32)
+    return _bf16(orc, x) if c["bf16"] else x
+
+
+@pytest.mark.parametrize("case", range(len(ROPE_CASES)))
+def test_op_rope_ctx(orc, ref, case):
+    """Bit-exact against the compiled reference's op_rope; position 0 is the
+    identity, pairs keep their norm, the tail past the last whole vector is
+    untouched, and the reference's own unit cases (test_ops.c:110-170) hold."""
+    c = ROPE_CASES[case]
+    rng = np.random.default_rng(100 + case)
+    hd = c["hd"]
+    thetas = (1.0 / (c["theta_base"] ** (np.arange(0, hd, 2) / hd))).astype(np.float32) if c["cache"] else None
+    kw = dict(theta_base=c["theta_base"], beta_fast=32.0, beta_slow=1.0, factor=c["factor"], mscale=c["mscale"],
+              thetas=thetas)
+    for pos in (0, 1, 77, 5000, 131071):
+        x = rope_case_data(orc, c, rng)
+        got = orc.op_rope(x, pos, hd, **kw)
+        want = x.copy()
+        th = None if thetas is None else thetas.ctypes.data
+        ref.lib.ref_op_rope(want.ctypes.data, int(c["bf16"]), want.size, pos, hd, kw["theta_base"], 32.0, 1.0,
+                            kw["factor"], kw["mscale"], th)
+        assert np.array_equal(got, want), pos
+        nv = (x.size // hd) * hd
+        assert np.array_equal(got[nv:], x[nv:])
+        if c["bf16"]:
+            continue
+        xf, gf = x[:nv].reshape(-1, hd).astype(np.float64), got[:nv].reshape(-1, hd).astype(np.float64)
+        h = hd // 2
+        m2 = np.float64(c["mscale"]) ** 2
+        np.testing.assert_allclose(gf[:, :h] ** 2 + gf[:, h:] ** 2, m2 * (xf[:, :h] ** 2 + xf[:, h:] ** 2),
+                                   rtol=2e-5, atol=1e-6)
+        if pos == 0 and c["mscale"] == 1.0:
+            assert np.array_equal(got, x)
+    # the reference's unit inputs (head_dim 4, theta 1e4, BF16 data): position
+    # 0 is the identity; at position 1 pair (0, 2) turns by 1 radian and pair
+    # (1, 3) by 0.01.  (test_rope_pos_one expects cos 1 and sin 1 at indices 0
+    # and 1, an interleaved pairing; op_rope pairs j with j + head_dim / 2,
+    # which the compiled reference confirms above.)
+    t = _bf16(orc, [1.0, 2.0, 3.0, 4.0])
+    assert np.array_equal(orc.op_rope(t, 0, 4), t)
+    r = orc.op_rope(_bf16(orc, [1.0, 0.0, 1.0, 0.0]), 1, 4)
+    f = (r.astype(np.uint32) << 16).view(np.float32)
+    want = [np.cos(1.0) - np.sin(1.0), 0.0, np.sin(1.0) + np.cos(1.0), 0.0]
+    np.testing.assert_allclose(f, want, atol=1e-2)
+
+
 @pytest.mark.parametrize("n", [1408, 8192, 13])
 def test_silu_mul(orc, ref, n):
     rng = np.random.default_rng(n)
