@@ -1048,24 +1048,29 @@ def main():
                     configs.append(dict(kind=kind, n=n, k=k, b=b, pool=pool, s=s0, x=x, xdig=xdig, y=y, i=0))
         torch.cuda.synchronize()
 
-        def run_step(ev=None):
+        # one step: the 24 GEMVs y = W x through the library's x -> y entry
+        # point (be42_gemv_q8 / be42_gemv_fp8: a prepare launch forming the
+        # digit planes of x, then the GEMV launch).  With prepared=True
+        # (breakdown only) the GEMV launch alone, on digits prepared
+        # beforehand.
+        def run_step(ev=None, prepared=False):
             for ci, c in enumerate(configs):
                 w = c["pool"][c["i"] % len(c["pool"])]
                 c["i"] += 1
                 if ev is not None:
                     ev[ci][0].record()
-                lib.gemv_prepare(c["x"], c["kind"], buf=c["xdig"])
+                if prepared:
+                    lib.gemv_prepared(w, c["s"], c["xdig"], c["b"], c["kind"], c["y"])
+                else:
+                    lib.gemv(w, c["s"], c["x"], c["kind"], out=c["y"])
                 if ev is not None:
                     ev[ci][1].record()
-                lib.gemv_prepared(w, c["s"], c["xdig"], c["b"], c["kind"], c["y"])
-                if ev is not None:
-                    ev[ci][2].record()
 
         for _ in range(args.warmup):
             run_step()
         torch.cuda.synchronize()
 
-        # the timed steps: nothing but the 24 (prepare + GEMV) pairs
+        # the timed steps: nothing but the 24 x -> y GEMVs
         t0 = time.perf_counter()
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
@@ -1081,16 +1086,21 @@ def main():
         ms_per_step = total_ms / args.steps
         value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-        # breakdown, in further steps: an event pair around each launch
-        evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in configs]
+        # breakdown, in further steps: an event pair around each x -> y call
+        # (op_us), and around each GEMV launch on prepared digits (kernel_us)
+        evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in configs]
+               for _ in range(args.steps)]
+        evk = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in configs]
                for _ in range(args.steps)]
         for s in range(args.steps):
             run_step(evs[s])
+        for s in range(args.steps):
+            run_step(evk[s], prepared=True)
         torch.cuda.synchronize()
         sweep = []
         for ci, c in enumerate(configs):
-            op_ms = sum(evs[s][ci][0].elapsed_time(evs[s][ci][2]) for s in range(args.steps)) / args.steps
-            main_ms = sum(evs[s][ci][1].elapsed_time(evs[s][ci][2]) for s in range(args.steps)) / args.steps
+            op_ms = sum(evs[s][ci][0].elapsed_time(evs[s][ci][1]) for s in range(args.steps)) / args.steps
+            main_ms = sum(evk[s][ci][0].elapsed_time(evk[s][ci][1]) for s in range(args.steps)) / args.steps
             nb = gemv_bytes(c["n"], c["k"], c["b"])
             row = {"dtype": c["kind"], "n": c["n"], "k": c["k"], "batch": c["b"],
                    "op_us": round(op_ms * 1e3, 2), "kernel_us": round(main_ms * 1e3, 2),
