@@ -8,10 +8,11 @@
 // per-element dequantisation: the fp32 activations are split once per call
 // into fixed-point digits of the MFMA input type, so that
 //     x[b][j] = s_b * sum_d digit_d[b][j] * R^-d   (R = 254 for INT8, 30 for FP8)
-// to ~2^-24 relative to max|x[b]|, and each digit plane is one MFMA operand.
+// (INT8 to ~2^-24 relative to max|x[b]|, FP8 to ~1.2e-6), and each digit
+// plane is one MFMA operand.
 //   INT8: 3 int8 digits in [-127, 127], v_mfma_i32_16x16x64_i8, exact int32
 //         accumulators, recombined in fp64 in the epilogue.
-//   FP8:  5 integer digits in [-15, 15] stored as E4M3 codes (exact),
+//   FP8:  4 integer digits in [-15, 15] stored as E4M3 codes (exact),
 //         v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales, fp32 accumulators.
 // The per-row scale is applied once per output, in the epilogue.
 //
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(256) void k_gemv_prep_row(const float *__restrict__
     store_digit_words<FP8>(xe, s, dig, B, Kp, b, blockIdx.x * kPrepChunk + t * 4);
 }
 
-__constant__ double kF8Weight[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 27000, 1.0 / 810000};
+__constant__ double kF8Weight[kF8Digits] = {1.0, 1.0 / 30, 1.0 / 900, 1.0 / 27000};
 
 // Up to three weight matrices that share one input (the q/k/v or gate/up
 // projections of a decode step) stream in one launch: their rows are
@@ -254,7 +255,7 @@ __device__ __forceinline__ void epi_store(const EpiOps<RT> &E, int t, int g, int
 // Operands of one MFMA: A = 16 weight rows x STEP k (row r = lane % 16, k
 // slice lane / 16), B = STEP k x 16 columns, where column c of column group nc
 // is digit plane d = (16*nc + c) % ND of batch row b = (16*nc + c) / ND.
-// A batch of <= 5 (INT8) or <= 3 (FP8) rows therefore needs one MFMA per
+// A batch of <= 5 (INT8) or <= 4 (FP8) rows therefore needs one MFMA per
 // weight tile: NC = ceil(batch * ND / 16) MFMAs in general.
 //   INT8: STEP 64, 16 bytes per lane, v_mfma_i32_16x16x64_i8, exact int32.
 //   FP8:  STEP 128, 32 bytes per lane, unit-scale v_mfma_scale_f32_16x16x128_f8f6f4.
@@ -1202,7 +1203,7 @@ static TileCfg split_slab_tile(int n, int k, int batch, bool fp8)
 
 static TileCfg pick_tile(bool fp8, int nc, int n, int k, int batch)
 {
-    // 3+ column groups (FP8 batch >= 7, INT8 batch >= 11) otherwise: the
+    // 3+ column groups (FP8 batch >= 9, INT8 batch >= 11) otherwise: the
     // LDS-resident digit slab kernel; many rows (k > 4096): one block of 8
     // waves x 4 row tiles per row range, each ring stage 16 rows x 512
     // contiguous bytes; long rows, or FP8 at 4096 .. 14336 rows: split K,
@@ -1211,11 +1212,12 @@ static TileCfg pick_tile(bool fp8, int nc, int n, int k, int batch)
     // most 4 steps (k <= 4096): many rows (the lm_head) at any batch,
     // 8193 .. 32768 rows at one column group (measured: 14336 x 4096 FP8
     // batch 1 -6%, INT8 batch 4 -16%), and past 4096 rows at 2-4 column
-    // groups (measured against the other kernels at batch 4-16: the 3B
-    // model's q/k/v (5120 x 3072) FP8 batch 4 15.7 -> 9.4 us, INT8 batch 16
-    // 19.2 -> 10.6 us; gate/up (16384 x 3072) FP8 batch 8 17.8 -> 15.7 us;
-    // 14336 x 4096 INT8 batch 16 19.6 -> 17.5 us).  At 5 groups (FP8 batch
-    // >= 13) the split slab kernel is as fast or faster.
+    // groups (measured against the other kernels at batch 4-16, with five
+    // FP8 digit planes then: the 3B model's q/k/v (5120 x 3072) FP8 batch 4
+    // 15.7 -> 9.4 us, INT8 batch 16 19.2 -> 10.6 us; gate/up (16384 x 3072)
+    // FP8 batch 8 17.8 -> 15.7 us; 14336 x 4096 INT8 batch 16 19.6 ->
+    // 17.5 us; with four planes FP8 batch 16 is 4 groups, and 14336 x 4096
+    // runs 29.1 -> 26.7 us here instead of on the split slab kernel).
     if (n > 32768 || (n > 8192 && nc < 3) || (n > 4096 && nc >= 2 && nc <= 4)) {
         const int steps = (int)(xdig_kp(k, fp8) / 128);
         if (steps % kCoopWaves == 0 && steps / kCoopWaves <= 4)

@@ -392,7 +392,7 @@ def digit_gemm_bench(lib, steps, warmup):
     """The prefill's projections: fp32 activations (N(0,1)) as digit planes
     against per-row INT8 / FP8 weights, at the 3B model's layer shapes for a
     1024-token pass (q/k/v and gate/up as one multi-segment launch).  The
-    matrix cores run nd = 3 (INT8) or 5 (FP8) digit products per logical
+    matrix cores run nd = 3 (INT8) or 4 (FP8) digit products per logical
     multiply-add: 'TOPS' counts 2 M N K nd, 'logical_TOPS' 2 M N K."""
     import torch
     g = torch.Generator(device="cuda")
@@ -402,7 +402,7 @@ def digit_gemm_bench(lib, steps, warmup):
     shapes = [("qkv", [d, kvd, kvd], d), ("o", [d], d), ("gate_up", [F, F], d), ("down", [d], F)]
     rows = []
     for kind in KINDS:
-        nd = 3 if kind == "int8" else 5
+        nd = 3 if kind == "int8" else 4
         qf = lib.quant_rows_int8 if kind == "int8" else lib.quant_rows_fp8
         for name, ns, k in shapes:
             segs = [qf(torch.randn(n, k, generator=g, device="cuda") * 0.02) for n in ns]
@@ -437,7 +437,7 @@ def digit_gemm_bench(lib, steps, warmup):
             del segs, x, buf, outs
             torch.cuda.empty_cache()
     return {"workload": "prefill projections of configs[4] for a 1024-token pass: fp32 activations as digit planes "
-                        "(INT8 3, FP8 5) x per-row INT8/FP8 weights, be42_gemm_prepared_multi",
+                        "(INT8 3, FP8 4) x per-row INT8/FP8 weights, be42_gemm_prepared_multi",
             "by_shape": rows}
 
 

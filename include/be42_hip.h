@@ -87,7 +87,7 @@ int be42_gemv_fp8_prepared(float *y, const uint8_t *w, const float *w_scale, con
  * memory (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc).  The digit planes live in a fixed 8 MiB device array per GPU,
  * held until the process ends, so k * batch is limited to what fits:
- * be42_gemv_xdig_bytes(k, batch, fp8) <= 8 MiB (k <= 104,448 at batch 16
+ * be42_gemv_xdig_bytes(k, batch, fp8) <= 8 MiB (k <= 130,048 at batch 16
  * for FP8, 174,080 for INT8), else BE42_EINVAL.  Same kernels and results as
  * the allocating entry points.  Every call on one GPU shares that array:
  * calls that overlap on one GPU (two streams, two threads) race. */

@@ -128,9 +128,10 @@ def test_gemv_multi_segments(be, orc, kind, b):
     for y, want, one in zip(outs, wants, singles):
         y = y.cpu().numpy()
         _check(y, want)
-        # the digit-split path is far inside the north-star tolerance
+        # the digit-split path is far inside the north-star tolerance (FP8:
+        # four digit planes, each element to ~1.2e-6 of max|x|)
         assert rel_err(y, one.cpu().numpy()) <= 1e-6
-        assert rel_err(y, want) <= 1e-5
+        assert rel_err(y, want) <= (1e-5 if kind == "int8" else 4e-5)
 
 
 @pytest.mark.parametrize("kind", ["int8", "fp8"])

@@ -45,7 +45,7 @@ def test_gemv_noalloc_matches_gemv(be, orc, kind):
 
 
 def test_gemv_noalloc_refuses_oversize(be):
-    k, b = 131072, 16                     # 10 MiB of FP8 digit planes
+    k, b = 131072, 16                     # 8 MiB of FP8 digit planes and the scales
     y = torch.zeros((b, 16), device="cuda")
     w = torch.zeros((16, k), dtype=torch.uint8, device="cuda")
     s = torch.ones(16, device="cuda")
