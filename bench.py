@@ -309,7 +309,7 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES, ctx=None):
     head = max(rows, key=lambda r: r["frac_of_hbm_peak"])
     launch_bytes = head["bytes_per_step"]
     achieved = launch_bytes / (head["step_us"] * 1e-6) / 1e9
-    roof = {"bound": "hbm", "kernel": "be42::k_attn_fused (route + attention, one launch)",
+    roof = {"bound": "hbm", "kernel": "be42::k_lsh_attn (route + sparse attention, one launch)",
             "workload": f"batch {head['batch']}, {T}-token bf16 context",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
