@@ -23,16 +23,22 @@ constexpr int kCntHash = kScanWaves * kProbes, kCntTotal = kCntHash + 1, kCntMid
 
 struct RouteSmem {
     int off_qm, off_q0, off_hp, off_cnt, off_offs, off_cand, off_mid, off_sc, off_rk, off_mpt, off_ph,
-        off_pt, stage, bytes;
+        off_pt, stage, stage_pt, bytes;
 };
 
 // LDS the router's own layout may take (dynamic shared memory), leaving room
 // for the static LDS of the kernels that embed it.
 constexpr int kRouteLdsBudget = 96 * 1024;
+// The page table is staged too only while the layout stays within this, so
+// that two route + attention workgroups (~25 KB of static LDS each) still
+// share a CU: at 128k context (8192 pages) staging it would take 32 KB more
+// and leave one workgroup per CU.  Unstaged, the router reads the ~66
+// entries it needs (the anchors and the middle entries) from HBM.
+constexpr int kRouteLdsStagePt = 40 * 1024;
 
 // LDS layout of the router.  When they fit in the budget, the layer's page
-// hashes and page table are staged there (stage = max_logical), else read
-// from HBM (stage = 0).
+// hashes (stage = max_logical) and page table (stage_pt) are staged there,
+// else read from HBM.
 __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical)
 {
     RouteSmem r;
@@ -47,8 +53,9 @@ __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical
     r.off_sc = o;   o += cap * 4;
     r.off_rk = o;   o += 4 * cap * 4;             // partial ranks, [4][cap]
     r.off_mpt = o;  o += cap * 4 + 4 * 4;
-    r.stage = o + max_logical * 6 + 32 <= kRouteLdsBudget ? max_logical : 0;
-    r.off_pt = o;   o += (r.stage * 4 + 15) & ~15;
+    r.stage = o + max_logical * 2 + 16 <= kRouteLdsBudget ? max_logical : 0;
+    r.stage_pt = r.stage && o + max_logical * 6 + 32 <= kRouteLdsStagePt ? 1 : 0;
+    r.off_pt = o;   o += r.stage_pt ? (r.stage * 4 + 15) & ~15 : 0;
     r.off_ph = o;   o += (r.stage * 2 + 15) & ~15;
     r.bytes = o;
     return r;
@@ -78,7 +85,7 @@ __device__ __forceinline__ RouteView route_view(unsigned char *smem, const Route
     V.sc = (float *)(smem + L.off_sc);
     V.mpt = (int *)(smem + L.off_mpt);   // [cap] physical page of mid[e]; [cap], [cap+1]: first, last page
     V.ph_s = (uint16_t *)(smem + L.off_ph);
-    V.pt_s = (int *)(smem + L.off_pt);
+    V.pt_s = L.stage_pt ? (int *)(smem + L.off_pt) : nullptr;   // page table staged
     V.rk = (int *)(smem + L.off_rk);
     return V;
 }
@@ -111,7 +118,9 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
     //    heads for q_mean; then q_mean (inference.c:291-295: sum in head
     //    order, then / n_heads)
     const uint16_t *ph = STAGE ? ph_s : P.page_hash + base;
-    const int *ptab = STAGE ? V.pt_s : P.page_table + base;
+    const bool spt = STAGE && V.pt_s;
+    // entry i of the layer's page table, from LDS when staged
+    auto ptab = [&](int i) -> int { return spt ? V.pt_s[i] : P.page_table[base + i]; };
     if (tid < kRouteThreads) {
         // unconditional loads at clamped indices (a conditional load is a
         // branch, and the compiler then waits for each load on its own);
@@ -124,10 +133,10 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int i = j * kRouteThreads + tid;
-            if (STAGE) {
+            if (STAGE)
                 hv[j] = P.page_hash[base + min(i, ih)];
+            if (spt)
                 pv[j] = P.page_table[base + min(i, ip)];
-            }
             wv[j] = P.hpT[min(i, iw)];
         }
 #pragma unroll
@@ -138,7 +147,7 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
             const int i = j * kRouteThreads + tid;
             if (STAGE && i < nidx)
                 ph_s[i] = hv[j];
-            if (STAGE && i < n)
+            if (spt && i < n)
                 V.pt_s[i] = pv[j];
             if (i < hd * 16)
                 hp[(i & 15) * (hd + 4) + (i >> 4)] = wv[j];   // hpT[d][bit] -> hp[bit][d]
@@ -147,7 +156,7 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
         for (int i = 8 * kRouteThreads + tid; STAGE && i < max(nidx, n); i += kRouteThreads) {
             if (i < nidx)
                 ph_s[i] = P.page_hash[base + i];
-            if (i < n)
+            if (spt && i < n)
                 V.pt_s[i] = P.page_table[base + i];
         }
         for (int i = 8 * kRouteThreads + tid; i < hd * 16; i += kRouteThreads)
@@ -165,8 +174,8 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
     }
     __syncthreads();
     if (tid == 0) {
-        mpt[cap] = ptab[0];
-        mpt[cap + 1] = ptab[n - 1];
+        mpt[cap] = ptab(0);
+        mpt[cap + 1] = ptab(n - 1);
     }
     if (wave == 0) {
         float s = 0.0f;
@@ -306,7 +315,7 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
     for (int e0 = 0; tid < kRouteThreads && e0 < nm; e0 += 128) {
         const int e = e0 + (tid >> 1), half = tid & 1;
         const int ee = e < nm ? e : nm - 1;
-        const int phys = ptab[mid[ee]];
+        const int phys = ptab(mid[ee]);
         const float s = dot_ref8x2(q0, P.centroid + (size_t)phys * hd, hd, half);
         if (half == 0 && e < nm) {
             sc[e] = s;
