@@ -38,8 +38,6 @@
 
 namespace be42 {
 
-constexpr int kPg = 16;
-
 __device__ __forceinline__ void load_row_f32(float *dst, const void *base, size_t elem_off, int n, bool bf16,
                                              float scale)
 {
@@ -789,11 +787,19 @@ __device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD
     attn_values_finish<HD, G, WAVES>(S, b, kvh, H, out);
 }
 
+// Attention of routed queries: query b's selection is sel[b * sel_stride ..]
+// (nsel[b] pages, in the router's output order).  With lim (and slots), query
+// b sees the first lim[b] positions of slot slots[b]: its last visible page
+// holds lim[b] - 16 (pages - 1) tokens.  The phases and the order of every
+// sum are those of k_lsh_attn's selection-order path, so at the same WAVES
+// an output equals k_lsh_attn's.
 template <bool BF16, int HD, int G, int WAVES, int UNR>
 __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P, const float *__restrict__ q,
                                                            const int *__restrict__ sel,
-                                                           const int *__restrict__ nsel, int sel_stride, int H,
-                                                           float scale, float *__restrict__ out)
+                                                           const int *__restrict__ nsel, int sel_stride,
+                                                           const int *__restrict__ slots,
+                                                           const int *__restrict__ lim, int H, float scale,
+                                                           float *__restrict__ out)
 {
     __shared__ AttnShared<HD, G, WAVES> S;
     __shared__ float red[WAVES * G * HD];
@@ -801,13 +807,24 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
     const int b = blockIdx.x, kvh = blockIdx.y;
     const int ns = min(nsel[b], kFusedMaxPages);
     const int *selb = sel + (size_t)b * sel_stride;
+    int last_ph = -1, last_nt = 0;
+    if (lim) {
+        const int lim_b = lim[b], n = (lim_b + kPg - 1) / kPg;
+        last_ph = n > 0 ? P.page_table[(size_t)slots[b] * P.max_logical + n - 1] : -1;
+        last_nt = lim_b - kPg * (n - 1);
+    }
     attn_load_q(S, q, b, kvh, H);
     for (int i = threadIdx.x; i < ns; i += blockDim.x) {
         const int ph = selb[i];
         S.pphys[i] = ph;
-        S.pnt[i] = P.ntok[ph];
+        S.pnt[i] = ph == last_ph ? last_nt : P.ntok[ph];
     }
     __syncthreads();
+    if (ns <= 0) {
+        for (int i = threadIdx.x; i < G * HD; i += blockDim.x)
+            out[((size_t)b * H + kvh * G) * HD + i] = 0.0f;
+        return;
+    }
     attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns, scale, 0, WAVES);
     __syncthreads();
     attn_weights(S, ns, nullptr);
@@ -1236,42 +1253,49 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
 
 // 16 waves when the grid is small (more loads in flight per workgroup), 8
 // waves once there are enough workgroups to fill the chip.
+// slots / lim: as k_attn_fused (lim null: every slot's whole cache).
+// wide16 keeps 16 waves for any grid (k_lsh_attn's wide16).
+struct FusedOpt {
+    const int *slots = nullptr, *lim = nullptr;
+    bool wide16 = false;
+};
+
 template <bool BF16, int HD, int G>
 static void launch_fused_g(const be42_kv_pool &P, const float *q, const int *sel, const int *nsel, int sel_stride,
-                           int B, int H, float scale, float *out, hipStream_t s)
+                           int B, int H, float scale, float *out, const FusedOpt &o, hipStream_t s)
 {
     const dim3 grid(B, P.n_kv);
-    if ((long)B * P.n_kv < 512)
+    if ((long)B * P.n_kv < 512 || o.wide16)
         hipLaunchKernelGGL((k_attn_fused<BF16, HD, G, 16, 8>), grid, dim3(1024), 0, s, P, q, sel, nsel, sel_stride,
-                           H, scale, out);
+                           o.slots, o.lim, H, scale, out);
     else
-        hipLaunchKernelGGL((k_attn_fused<BF16, HD, G, 8, 8>), grid, dim3(512), 0, s, P, q, sel, nsel, sel_stride, H,
-                           scale, out);
+        hipLaunchKernelGGL((k_attn_fused<BF16, HD, G, 8, 8>), grid, dim3(512), 0, s, P, q, sel, nsel, sel_stride,
+                           o.slots, o.lim, H, scale, out);
 }
 
 template <bool BF16, int HD>
 static bool launch_fused_hd(const be42_kv_pool &P, const float *q, const int *sel, const int *nsel, int sel_stride,
-                            int B, int H, float scale, float *out, hipStream_t s)
+                            int B, int H, float scale, float *out, const FusedOpt &o, hipStream_t s)
 {
     switch (H / P.n_kv) {
-    case 1: launch_fused_g<BF16, HD, 1>(P, q, sel, nsel, sel_stride, B, H, scale, out, s); return true;
-    case 2: launch_fused_g<BF16, HD, 2>(P, q, sel, nsel, sel_stride, B, H, scale, out, s); return true;
-    case 3: launch_fused_g<BF16, HD, 3>(P, q, sel, nsel, sel_stride, B, H, scale, out, s); return true;
-    case 4: launch_fused_g<BF16, HD, 4>(P, q, sel, nsel, sel_stride, B, H, scale, out, s); return true;
+    case 1: launch_fused_g<BF16, HD, 1>(P, q, sel, nsel, sel_stride, B, H, scale, out, o, s); return true;
+    case 2: launch_fused_g<BF16, HD, 2>(P, q, sel, nsel, sel_stride, B, H, scale, out, o, s); return true;
+    case 3: launch_fused_g<BF16, HD, 3>(P, q, sel, nsel, sel_stride, B, H, scale, out, o, s); return true;
+    case 4: launch_fused_g<BF16, HD, 4>(P, q, sel, nsel, sel_stride, B, H, scale, out, o, s); return true;
     default: return false;
     }
 }
 
 static bool launch_fused(const be42_kv_pool &P, const float *q, const int *sel, const int *nsel, int sel_stride, int B,
-                         int H, float scale, float *out, hipStream_t s)
+                         int H, float scale, float *out, hipStream_t s, const FusedOpt &o = FusedOpt())
 {
     const bool bf16 = P.kind == BE42_KV_BF16;
     if (P.head_dim == 128)
-        return bf16 ? launch_fused_hd<true, 128>(P, q, sel, nsel, sel_stride, B, H, scale, out, s)
-                    : launch_fused_hd<false, 128>(P, q, sel, nsel, sel_stride, B, H, scale, out, s);
+        return bf16 ? launch_fused_hd<true, 128>(P, q, sel, nsel, sel_stride, B, H, scale, out, o, s)
+                    : launch_fused_hd<false, 128>(P, q, sel, nsel, sel_stride, B, H, scale, out, o, s);
     if (P.head_dim == 64)
-        return bf16 ? launch_fused_hd<true, 64>(P, q, sel, nsel, sel_stride, B, H, scale, out, s)
-                    : launch_fused_hd<false, 64>(P, q, sel, nsel, sel_stride, B, H, scale, out, s);
+        return bf16 ? launch_fused_hd<true, 64>(P, q, sel, nsel, sel_stride, B, H, scale, out, o, s)
+                    : launch_fused_hd<false, 64>(P, q, sel, nsel, sel_stride, B, H, scale, out, o, s);
     return false;
 }
 
@@ -1586,17 +1610,35 @@ int lsh_attention_digits(const be42_kv_pool &P, const float *q, const int *slots
                            s);
 }
 
+// The router runs once per query (k_route), then the attention of every
+// (query, KV head) pair over that selection (k_attn_fused at 16 waves, the
+// layout a one-query decode launch sums in); k_lsh_attn would repeat the
+// router in each KV head's workgroup.
 int lsh_attention_prefix(const be42_kv_pool &P, const float *q, const int *slots, const int *lim, int n_queries,
-                         int n_heads, int k_sel, int cand_cap, float scale, float *out, hipStream_t s)
+                         int n_heads, int k_sel, int cand_cap, float scale, float *out, int *sel, int *nsel,
+                         int sel_stride, hipStream_t s)
 {
     BE42_CHECK(k_sel > 0 && k_sel <= kFusedMaxPages && cand_cap > 0 && cand_cap <= kMaxCand &&
                    n_heads % P.n_kv == 0 && n_heads / P.n_kv <= 4 && (P.head_dim == 64 || P.head_dim == 128),
                "prefill attention: unsupported shape (k %d, cap %d, %d heads / %d kv, head_dim %d)", k_sel, cand_cap,
                n_heads, P.n_kv, P.head_dim);
-    LshAttnOpt o;
+    BE42_CHECK(slots && lim && sel && nsel && sel_stride >= prefix_sel_stride(k_sel),
+               "prefill attention: needs slots, lim and a selection workspace of stride >= %d (got %d)",
+               prefix_sel_stride(k_sel), sel_stride);
+    if (n_queries <= 0)
+        return BE42_OK;
+    const int rc = launch_route(P, q, slots, lim, n_queries, n_heads, k_sel, cand_cap, sel, nsel, sel_stride, nullptr,
+                                nullptr, nullptr, s);
+    if (rc != BE42_OK)
+        return rc;
+    FusedOpt o;
+    o.slots = slots;
     o.lim = lim;
     o.wide16 = true;
-    return launch_lsh_attn(P, q, slots, n_queries, n_heads, k_sel, cand_cap, scale, out, nullptr, nullptr, 0, o, s);
+    BE42_CHECK(launch_fused(P, q, sel, nsel, sel_stride, n_queries, n_heads, scale, out, s, o),
+               "prefill attention: unsupported head grouping");
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
 }
 
 }  // namespace be42

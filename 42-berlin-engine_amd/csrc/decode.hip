@@ -1064,6 +1064,9 @@ struct be42_decoder {
     void *pdig = nullptr;
     int *pmeta = nullptr, *pmeta_host = nullptr;
     size_t pmeta_bytes = 0;
+    // the chunk's page selections [kPrefillChunk][psel_stride] and counts
+    int *psel = nullptr, *pnsel = nullptr;
+    int psel_stride = 0;
 };
 
 // Whether the fused layer kernel serves this shape at batch 1 (sets d->fnb).
@@ -1264,7 +1267,8 @@ extern "C" void be42_decoder_destroy(be42_decoder *d)
         (void)hipHostFree(d->pmeta_host);
     void *ptrs[] = {d->cos_t, d->sin_t, d->x, d->xb, d->xn, d->q, d->k, d->v, d->att, d->hb, d->hb2, d->logits, d->sel,
                     d->nsel, d->slots, d->next, d->cand, d->ncand, d->xdig, d->attn_ws, d->arg_parts, d->arg_cnt, d->fflags,
-                    d->px, d->pxn, d->pq, d->pk, d->pv, d->patt, d->pxb, d->phb, d->phb2, d->pdig, d->pmeta};
+                    d->px, d->pxn, d->pq, d->pk, d->pv, d->patt, d->pxb, d->phb, d->phb2, d->pdig, d->pmeta,
+                    d->psel, d->pnsel};
     for (void *p : ptrs)
         if (p)
             (void)hipFree(p);
@@ -1789,12 +1793,15 @@ static int prefill_alloc(be42_decoder *d)
     alloc(&d->pdig, be42_gemm_xdig_bytes(wide, (int)T, c.wkind));
     d->pmeta_bytes = ((2 + (size_t)c.n_layers) * T + (size_t)c.n_layers * append_run_list_cap((int)T)) * sizeof(int);
     alloc((void **)&d->pmeta, d->pmeta_bytes);
+    d->psel_stride = prefix_sel_stride(c.sparse_k);
+    alloc((void **)&d->psel, T * d->psel_stride * sizeof(int));
+    alloc((void **)&d->pnsel, T * sizeof(int));
     if (e == hipSuccess)
         e = hipHostMalloc((void **)&d->pmeta_host, d->pmeta_bytes, hipHostMallocDefault);
     if (e != hipSuccess) {
         void **ptrs[] = {(void **)&d->px, (void **)&d->pxn, (void **)&d->pq, (void **)&d->pk, (void **)&d->pv,
                          (void **)&d->patt, (void **)&d->pxb, (void **)&d->phb, (void **)&d->phb2, &d->pdig,
-                         (void **)&d->pmeta};
+                         (void **)&d->pmeta, (void **)&d->psel, (void **)&d->pnsel};
         for (void **p : ptrs)
             if (*p) {
                 (void)hipFree(*p);
@@ -1866,7 +1873,7 @@ static int prefill_pass(be42_decoder *d, int seq, int T, int p0, const AppendRun
         // the pass's K/V rows and the pages they fill: one launch each
         DEC_TRY(launch_append_run(*d->pool, runs[l], d->pmeta + list_off[l], d->pk, d->pv, st));
         DEC_TRY(lsh_attention_prefix(*d->pool, d->pq, d->pmeta + (size_t)(2 + l) * T, lim, T, H, c.sparse_k,
-                                     c.cand_cap, scale, d->patt, st));
+                                     c.cand_cap, scale, d->patt, d->psel, d->pnsel, d->psel_stride, st));
         DEC_TRY(xdig_prepare(d->pdig, d->patt, qd, T, fp8 != 0, st));
         DEC_TRY(pgemm(d, d->pxb, L.wo, L.so, dim, qd, T, st));
         BE42_HIP(norm(L.ffn_norm, d->pxb));                 // x += attention output

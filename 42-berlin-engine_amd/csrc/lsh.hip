@@ -31,13 +31,18 @@
 #include <cmath>
 
 #include "be42_common.h"
+#include "paged_step.h"
 #include "route.h"
 
 namespace be42 {
 
+// With lim, query b sees only the first lim[b] positions of its slot (the
+// pages and LSH index it saw when position lim[b] - 1 was the newest), as in
+// k_lsh_attn.
 template <bool STAGE>
 __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float *__restrict__ q,
-                                               const int *__restrict__ slots, int H, int k_sel, int cap,
+                                               const int *__restrict__ slots, const int *__restrict__ lim, int H,
+                                               int k_sel, int cap,
                                                int *__restrict__ sel, int *__restrict__ nsel, int sel_stride,
                                                int *__restrict__ cand_out, int *__restrict__ ncand_out,
                                                uint16_t *__restrict__ qhash_out)
@@ -47,7 +52,8 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
     const int b = blockIdx.x, tid = threadIdx.x;
     const int layer = slots ? slots[b] : b;
     const int base = layer * P.max_logical;
-    const int n = P.n_logical[layer];
+    const int lim_b = lim ? lim[b] : 0;
+    const int n = lim ? (lim_b + kPg - 1) / kPg : P.n_logical[layer];
     int *selb = sel + (size_t)b * sel_stride;
 
     if (n <= 0 || n <= k_sel) {
@@ -61,7 +67,7 @@ __global__ __launch_bounds__(256) void k_route(const be42_kv_pool P, const float
         }
         return;
     }
-    const int nidx = min(P.n_indexed[layer], P.max_logical);
+    const int nidx = min(lim ? min(P.n_indexed[layer], lim_b / kPg) : P.n_indexed[layer], P.max_logical);
     route_prepare<STAGE>(P, q + (size_t)b * H * P.head_dim, base, n, nidx, H, cap, V,
                          qhash_out ? qhash_out + b : nullptr, cand_out ? cand_out + (size_t)b * cap : nullptr,
                          ncand_out ? ncand_out + b : nullptr);
@@ -147,6 +153,24 @@ __global__ __launch_bounds__(256) void k_lsh_candidates(const uint16_t *__restri
         n_out[b] = total;
 }
 
+int launch_route(const be42_kv_pool &P, const float *q, const int *slots, const int *lim, int n_queries, int H,
+                 int k_sel, int cap, int *sel, int *nsel, int sel_stride, int *cand, int *ncand, uint16_t *qhash,
+                 hipStream_t s)
+{
+    const RouteSmem L = route_smem(P.head_dim, cap, P.max_logical);
+    const void *fn = L.stage ? (const void *)k_route<true> : (const void *)k_route<false>;
+    if (L.bytes > 65536)
+        BE42_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes));
+    if (L.stage)
+        hipLaunchKernelGGL(k_route<true>, dim3(n_queries), dim3(256), (size_t)L.bytes, s, P, q, slots, lim, H, k_sel,
+                           cap, sel, nsel, sel_stride, cand, ncand, qhash);
+    else
+        hipLaunchKernelGGL(k_route<false>, dim3(n_queries), dim3(256), (size_t)L.bytes, s, P, q, slots, lim, H,
+                           k_sel, cap, sel, nsel, sel_stride, cand, ncand, qhash);
+    BE42_LAUNCH_CHECK();
+    return BE42_OK;
+}
+
 }  // namespace be42
 
 using namespace be42;
@@ -225,16 +249,6 @@ extern "C" int be42_lsh_route(const be42_kv_pool *pool, const float *q, const in
                "be42_lsh_route: sel_stride %d must be >= max(k, 64)", sel_stride);
     if (n_queries == 0)
         return BE42_OK;
-    const RouteSmem L = route_smem(pool->head_dim, cand_cap, pool->max_logical);
-    const void *fn = L.stage ? (const void *)k_route<true> : (const void *)k_route<false>;
-    if (L.bytes > 65536)
-        BE42_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes));
-    if (L.stage)
-        hipLaunchKernelGGL(k_route<true>, dim3(n_queries), dim3(256), (size_t)L.bytes, as_stream(stream), *pool, q,
-                           slots, n_heads, k_sel, cand_cap, sel, n_sel, sel_stride, cand, n_cand, qhash);
-    else
-        hipLaunchKernelGGL(k_route<false>, dim3(n_queries), dim3(256), (size_t)L.bytes, as_stream(stream), *pool, q,
-                           slots, n_heads, k_sel, cand_cap, sel, n_sel, sel_stride, cand, n_cand, qhash);
-    BE42_LAUNCH_CHECK();
-    return BE42_OK;
+    return be42::launch_route(*pool, q, slots, nullptr, n_queries, n_heads, k_sel, cand_cap, sel, n_sel, sel_stride,
+                              cand, n_cand, qhash, as_stream(stream));
 }

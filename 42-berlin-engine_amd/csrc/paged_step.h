@@ -61,13 +61,23 @@ int plan_append_run(be42_kv_pool *pool, int layer, int pos0, int n, int *L, Appe
 int launch_append_run(const be42_kv_pool &P, const AppendRun &r, const int *d_lists, const float *k, const float *v,
                       hipStream_t s);
 
+// device: the router (k_route, lsh.hip) of n_queries queries; lim (device,
+// optional) as in lsh_attention_prefix; cand / ncand / qhash optional
+int launch_route(const be42_kv_pool &P, const float *q, const int *slots, const int *lim, int n_queries, int H,
+                 int k_sel, int cap, int *sel, int *nsel, int sel_stride, int *cand, int *ncand, uint16_t *qhash,
+                 hipStream_t s);
+
 // device: paged attention of n_queries queries of the slots slots[b] (device
 // array), query b seeing only the first lim[b] positions of its slot (its
 // pages, LSH index and last page as they were when position lim[b] - 1 was
 // the newest), each computed exactly as a one-query decode launch computes it
-// (attention.hip); needs k_sel <= 64, groups of <= 4 heads, head_dim 64/128
+// (attention.hip); needs k_sel <= 64, groups of <= 4 heads, head_dim 64/128.
+// sel / nsel: device workspace of n_queries selections (sel_stride >=
+// prefix_sel_stride(k_sel) ints each) and counts.
+inline int prefix_sel_stride(int k_sel) { return k_sel > 64 ? k_sel : 64; }
 int lsh_attention_prefix(const be42_kv_pool &P, const float *q, const int *slots, const int *lim, int n_queries,
-                         int n_heads, int k_sel, int cand_cap, float scale, float *out, hipStream_t s);
+                         int n_heads, int k_sel, int cand_cap, float scale, float *out, int *sel, int *nsel,
+                         int sel_stride, hipStream_t s);
 
 // be42_lsh_attention that, when the launch splits each (query, KV head) pair
 // over several workgroups, also writes the output rows as GEMV digit planes

@@ -11,6 +11,7 @@
 
 namespace be42 {
 
+constexpr int kPg = 16;             // tokens per KV page
 constexpr int kProbes = 17;
 constexpr int kMaxCand = 256;       // router candidate cap
 constexpr int kMaxCandList = 512;   // be42_lsh_candidates cap
