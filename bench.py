@@ -981,6 +981,40 @@ def gemm_probe():
         del wq, sw, xq, sx, y
 
 
+def decode_probe():
+    """For rocprofv3 runs (--pmc counters or --kernel-trace): the configs[4]
+    3B model (FP8 weights, bf16 pages) at batch 1 after a 64-token prompt,
+    10 decode steps (each a fused-layer launch per layer over 100.8 MB of
+    weights: 2.8 GB per step, so the 256 MB Infinity Cache serves no weight
+    of the next step), then 10 copies of 1 GiB as the byte reference of the
+    FETCH_SIZE / WRITE_SIZE counters.  The context is short (dense
+    attention): the fused layer's traffic does not depend on it."""
+    import numpy as np
+    import torch
+    import be42
+    lib = be42.load()
+    lib.init(0)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(41)
+    A = B3
+    w = decoder_weights(lib, A, "fp8", gen)
+    _, hpT = lib.lsh_projection(A["head_dim"], 42)
+    dec = be42.Decoder(lib, decoder_cfg(A, 256, 1, 1, be42.KV_BF16), w, hpT)
+    prompt = np.random.default_rng(6).integers(0, A["vocab"], 64)
+    tok = dec.prefill(prompt)
+    for i in range(10):
+        tok = dec.step([int(tok)] if i == 0 else None, 64 + i, sync=False, batch=1)
+    torch.cuda.synchronize()
+    dec.status()
+    dec.close()
+    src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("decode probe done", flush=True)
+
+
 PMC_CONFIG = ("fp8", 128256, 4096, 16)
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_fp8_128256x4096_b16_pmc.txt")
 
@@ -1041,6 +1075,8 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true", help="only run the kernels profiled for HBM traffic")
     ap.add_argument("--lsh-probe", action="store_true", help="only run the LSH launches profiled for HBM traffic")
     ap.add_argument("--gemm-probe", action="store_true", help="only run the GEMM launches profiled for counters")
+    ap.add_argument("--decode-probe", action="store_true",
+                    help="only run 3B batch-1 decode steps (fused layers) profiled for HBM traffic")
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe()
@@ -1050,6 +1086,9 @@ def main():
         return
     if args.gemm_probe:
         gemm_probe()
+        return
+    if args.decode_probe:
+        decode_probe()
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
