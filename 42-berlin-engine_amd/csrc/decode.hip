@@ -427,7 +427,9 @@ __global__ __launch_bounds__(256) void k_rope_rows(float *__restrict__ q, float 
 // from the fp32 vector itself), and streams its row tiles of the phase's
 // weights straight from HBM into MFMA operand registers.  A phase's input
 // vector is loaded first; half of the block's weight loads leave while the
-// other half of its waves compute the digit planes.  (Weight loads issued
+// other half of its waves compute the digit planes; the phase's row scales
+// and output addresses load with the vector, so that only the cross-wave sum
+// and the stores follow the last matrix instruction.  (Weight loads issued
 // before a barrier were measured to slow the barrier itself more than they
 // gained, and so was a barrier in which every block reads a packed array of
 // all the arrival flags.)
@@ -460,6 +462,10 @@ __device__ __forceinline__ float ld_dev(const float *p)
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_dev(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(__attribute__((address_space(1))) float *p, float v)
 {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -527,13 +533,14 @@ __device__ __forceinline__ void grid_barrier(const GridBar &gb, unsigned idx, F 
     __shared__ int failed;
     const unsigned target = gb.base + idx, awaited = target + gb.bias;
     wait_vmcnt<0>();              // this thread's stores have completed
-    if (threadIdx.x == 0)
-        failed = __hip_atomic_load(gb.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
     __syncthreads();
-    if (threadIdx.x == 0)
+    // arrive, then read the error word (its round trip overlaps the wait)
+    if (threadIdx.x == 0) {
         __hip_atomic_store(gb.flags + blockIdx.x * 32, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        failed = __hip_atomic_load(gb.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    }
     during();
-    asm volatile("" ::: "memory");
+    __syncthreads();
     const bool skip = failed;
     if (blockIdx.x == 0 && !skip) {
         for (int i = threadIdx.x; i < gb.nb; i += blockDim.x) {
@@ -587,6 +594,32 @@ __device__ __forceinline__ T seg_sel(const T (&a)[3], int seg)
     return seg == 0 ? a[0] : (seg == 1 ? a[1] : a[2]);
 }
 
+// seg_sel for a per-lane seg: the three entries are first made scalars, so
+// that the choice is a per-lane select and not an indexed (vector) load
+// from the kernel arguments, which the next dependent load would wait for.
+// Pointers come back as global-memory pointers (a generic one would make
+// its loads and stores flat accesses, which LDS waits also count).
+template <class T>
+using gptr = __attribute__((address_space(1))) T *;
+__device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
+template <class T>
+__device__ __forceinline__ gptr<T> sgpr(T *p)
+{
+    const uint64_t u = (uint64_t)(uintptr_t)p;
+    return (gptr<T>)(((uint64_t)(uint32_t)sgpr((int)(uint32_t)(u >> 32)) << 32) | (uint32_t)sgpr((int)(uint32_t)u));
+}
+__device__ __forceinline__ int seg_sel_lane(const int (&a)[3], int seg)
+{
+    const int a0 = sgpr(a[0]), a1 = sgpr(a[1]), a2 = sgpr(a[2]);
+    return seg == 0 ? a0 : (seg == 1 ? a1 : a2);
+}
+template <class T>
+__device__ __forceinline__ gptr<T> seg_sel_lane(T *const (&a)[3], int seg)
+{
+    const gptr<T> a0 = sgpr(a[0]), a1 = sgpr(a[1]), a2 = sgpr(a[2]);
+    return seg == 0 ? a0 : (seg == 1 ? a1 : a2);
+}
+
 // wave -> (tile slot, step range): the tiles rounded up to a power of two
 // share the 8 waves, each tile's waves splitting its K steps
 struct FWave {
@@ -613,7 +646,8 @@ __device__ __forceinline__ FWave ph_wave(int nt, int steps, int wave)
 // same k positions)
 __device__ __forceinline__ void ph_prefetch(const FPhase &ph, int b, int nb, v8i (&fr)[kFMaxU], int lo, int hi)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
     if (wave < lo || wave >= hi)
         return;
     const FWave fw = ph_wave(ph_count(ph, b, nb), ph.steps, wave);
@@ -633,12 +667,53 @@ __device__ __forceinline__ void ph_prefetch(const FPhase &ph, int b, int nb, v8i
     }
 }
 
+// What thread i (< 16 x the block's tiles) of a phase needs after the
+// matrix instructions: its row's weight scale and where its output goes
+// (for gate/up: the scale of its gate or up row, and the output of pair
+// i / 16).  Loaded when the phase starts, so that these dependent loads
+// overlap the input vector's instead of following the last MFMA.
+struct FOut {
+    gptr<float> y;   // output element, nullptr if none
+    float sw;     // row scale (0 past the rows)
+    int ok;       // the row exists
+    int tail;     // gate/up: the pair's row is past the last multiple of 8
+};
+__device__ __forceinline__ FOut ph_out(const FPhase &ph, int b, int nb)
+{
+    FOut o{nullptr, 0.0f, 0, 0};
+    const int nt = ph_count(ph, b, nb), i = threadIdx.x;
+    if (i < nt * 16) {
+        const int j = i >> 4, r = i & 15;
+        int seg, lt;
+        ph_slot(ph, b, nb, j, seg, lt);
+        const int row = lt * 16 + r;
+        if (row < seg_sel_lane(ph.n, seg)) {
+            o.ok = 1;
+            o.sw = seg_sel_lane(ph.sw, seg)[row];
+            if (!ph.silu)
+                o.y = seg_sel_lane(ph.y, seg) + row;
+        }
+    }
+    if (ph.silu && i < (nt / 2) * 16) {
+        int seg, lt;
+        ph_slot(ph, b, nb, 2 * (i >> 4), seg, lt);
+        const int row = lt * 16 + (i & 15);
+        const int n0 = sgpr(ph.n[0]);
+        if (row < n0) {
+            o.y = sgpr(ph.y[0]) + row;
+            o.tail = row >= (n0 & ~7);
+        }
+    }
+    return o;
+}
+
 // The phase's MFMAs against the digit planes in LDS (dig[d][Kp]), the
 // cross-wave sum of each tile's partials, and the outputs (device-scope
-// stores).  sx: the digit scale of the input.
+// stores).  sx: the digit scale of the input; oo: ph_out of this thread.
 template <bool FP8>
 __device__ __forceinline__ void ph_compute(const FPhase &ph, int b, int nb, const v8i (&fr)[kFMaxU],
-                                           const uint8_t *dig, int Kp, float sx, long long (*part)[16], float *ybuf)
+                                           const uint8_t *dig, int Kp, float sx, long long (*part)[16], float *ybuf,
+                                           const FOut &oo)
 {
     constexpr int ND = FP8 ? kF8Digits : kI8Digits;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c = lane & 15, g = lane >> 4;
@@ -706,25 +781,17 @@ __device__ __forceinline__ void ph_compute(const FPhase &ph, int b, int nb, cons
                 it += part[w0 + w][r];
             tot = (double)it;
         }
-        int seg, lt;
-        ph_slot(ph, b, nb, j, seg, lt);
-        const int row = lt * 16 + r, n = seg_sel(ph.n, seg);
-        const float y = row < n ? (float)(tot * ((double)sx * sxw * (double)seg_sel(ph.sw, seg)[row])) : 0.0f;
+        const float y = oo.ok ? (float)(tot * ((double)sx * sxw * (double)oo.sw)) : 0.0f;
         if (ph.silu)
             ybuf[i] = y;
-        else if (row < n)
-            st_dev(seg_sel(ph.y, seg) + row, y);
+        else if (oo.y)
+            st_dev(oo.y, y);
     }
     if (ph.silu) {
         __syncthreads();
-        if (i < (nt / 2) * 16) {
+        if (oo.y) {
             const int p = i >> 4, r = i & 15;
-            int seg, lt;
-            ph_slot(ph, b, nb, 2 * p, seg, lt);
-            const int row = lt * 16 + r;
-            if (row < ph.n[0])
-                st_dev(ph.y[0] + row, silu_mul1(ybuf[2 * p * 16 + r], ybuf[(2 * p + 1) * 16 + r],
-                                                row < (ph.n[0] & ~7)));
+            st_dev(oo.y, silu_mul1(ybuf[2 * p * 16 + r], ybuf[(2 * p + 1) * 16 + r], !oo.tail));
         }
     }
 }
@@ -939,16 +1006,19 @@ __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
         return [pp, b, nb, &fr] { ph_prefetch(*pp, b, nb, fr, 0, kFW); };
     };
     // o projection of the attention output
+    FOut oo = ph_out(A.o, b, nb);
     float sx = vec_digits<FP8>(A.att, A.qd, dig, red, quad, wload(A.o));
-    ph_compute<FP8>(A.o, b, nb, fr, dig, A.qd, sx, part, ybuf);
+    ph_compute<FP8>(A.o, b, nb, fr, dig, A.qd, sx, part, ybuf, oo);
     grid_barrier(gb, 1, [] {});
     // h = x + o, RMSNorm, gate/up, SiLU * up
+    oo = ph_out(A.gu, b, nb);
     sx = norm_digits<FP8, NV>(A.X, A.XB, A.ffn_norm, A.Hb, A.dim, A.eps, dig, red, b, nb, quad, wload(A.gu));
-    ph_compute<FP8>(A.gu, b, nb, fr, dig, A.dim, sx, part, ybuf);
+    ph_compute<FP8>(A.gu, b, nb, fr, dig, A.dim, sx, part, ybuf, oo);
     grid_barrier(gb, 2, [] {});
     // down projection
+    oo = ph_out(A.down, b, nb);
     sx = vec_digits<FP8>(A.H2, A.hidden, dig, red, quad, wload(A.down));
-    ph_compute<FP8>(A.down, b, nb, fr, dig, A.hidden, sx, part, ybuf);
+    ph_compute<FP8>(A.down, b, nb, fr, dig, A.hidden, sx, part, ybuf, oo);
     if (A.qkv.nseg == 0) {
         // last layer: h and the down output stay for the final norm
         if (b == 0 && threadIdx.x == 0)
@@ -957,8 +1027,9 @@ __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
     }
     grid_barrier(gb, 3, [] {});
     // next layer: x = h + down, RMSNorm, q/k/v
+    oo = ph_out(A.qkv, b, nb);
     sx = norm_digits<FP8, NV>(A.Hb, A.XB, A.attn_norm, A.X, A.dim, A.eps, dig, red, b, nb, quad, wload(A.qkv));
-    ph_compute<FP8>(A.qkv, b, nb, fr, dig, A.dim, sx, part, ybuf);
+    ph_compute<FP8>(A.qkv, b, nb, fr, dig, A.dim, sx, part, ybuf, oo);
     grid_barrier(gb, 4, [] {});
     if (b == 0 && threadIdx.x == 0)
         __hip_atomic_store(A.gen, gb.base / kFBars + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
