@@ -239,8 +239,8 @@ int  be42_paged_attention(const be42_kv_pool *pool, const float *q, int n_querie
  * bit for bit, and the same attention up to the order of the V sum.
  * k_sel <= 64, cand_cap <= 256, n_heads / n_kv <= 4, head_dim 64 or 128.
  * sel / n_sel (both or neither) receive the selection as be42_lsh_route
- * writes it (sel_stride >= 64).  Above 512 (query, KV head) pairs it runs as
- * the two launches (the library workspace holds the selection when sel is
+ * writes it (sel_stride >= 64).  From 1024 (query, KV head) pairs on it runs
+ * as the two launches (the library workspace holds the selection when sel is
  * NULL). */
 int  be42_lsh_attention(const be42_kv_pool *pool, const float *q, const int *slots, int n_queries,
                         int n_heads, int k_sel, int cand_cap, float scale, float *out, int *sel, int *n_sel,
