@@ -942,10 +942,14 @@ static int gemm_dig_run(bool fp8, const be42_gemv_seg *segs, int nseg, const voi
     const int force = e ? atoi(e) : 0;
     if (dma && force != 1) {
         if (fp8) {
+            // 64 tokens x 256 features: each wave's 4 digit fragments and 2
+            // weight fragments feed 8 matrix instructions (with 128 features,
+            // 5 fragments fed 4, and the LDS reads bounded the loop: the 3B
+            // shapes 15-20% slower)
             if (force == 3)
                 launch_gemm_dig_dma<true, 2, 2, 2, 2>(S, dig, sx, m, k, s);
             else
-                launch_gemm_dig_dma<true, 2, 4, 1, 2>(S, dig, sx, m, k, s);
+                launch_gemm_dig_dma<true, 2, 4, 2, 2>(S, dig, sx, m, k, s);
         } else {
             if (force == 3)
                 launch_gemm_dig_dma<false, 2, 2, 2, 3>(S, dig, sx, m, k, s);
