@@ -363,6 +363,9 @@ __device__ __forceinline__ float group_sum(float a)
 template <int HD, int G, int WAVES>
 struct AttnShared {
     float qs[G][HD];
+    // the q split of the matrix-core scores, per lane and 32-dim block
+    // (attn_q_store), for kernels that form it once for all their waves
+    uint4 qp[kWave][HD / 32];
     float sc[G][kSetMax * 17];
     float lsh[G];
     int pphys[kSetMax], pnt[kSetMax], order[kFusedMaxPages];
@@ -396,46 +399,72 @@ struct QParts {
     bf16x8_t a[HD / 32];
 };
 
+// lane `lane`'s A operand of 32-dim block j: its part of the 8 dims it holds
+template <int HD, int G, int WAVES>
+__device__ __forceinline__ uint4 attn_q_word(const AttnShared<HD, G, WAVES> &S, int lane, int j)
+{
+    const int r = lane & 15, gi = lane >> 4;
+    const int g = r >> 2, part = r & 3;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        uint16_t h[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float q = g < G ? S.qs[g < G ? g : 0][32 * j + 8 * gi + i + e] : 0.0f;
+            const uint16_t hi = f32_to_bf16(q);
+            const float r1 = q - bf16_to_f32(hi);
+            const uint16_t mid = f32_to_bf16(r1);
+            const float r2 = r1 - bf16_to_f32(mid);
+            const uint16_t lo = f32_to_bf16(r2);
+            h[e] = part == 0 ? hi : (part == 1 ? mid : (part == 2 ? lo : (uint16_t)0));
+        }
+        w[i / 2] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 template <int HD, int G, int WAVES>
 __device__ __forceinline__ QParts<HD> attn_q_parts(const AttnShared<HD, G, WAVES> &S)
 {
-    constexpr int NJ = HD / 32;
-    const int lane = threadIdx.x & 63, r = lane & 15, gi = lane >> 4;
-    const int g = r >> 2, part = r & 3;
     QParts<HD> Q;
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            uint16_t h[2];
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const float q = g < G ? S.qs[g < G ? g : 0][32 * j + 8 * gi + i + e] : 0.0f;
-                const uint16_t hi = f32_to_bf16(q);
-                const float r1 = q - bf16_to_f32(hi);
-                const uint16_t mid = f32_to_bf16(r1);
-                const float r2 = r1 - bf16_to_f32(mid);
-                const uint16_t lo = f32_to_bf16(r2);
-                h[e] = part == 0 ? hi : (part == 1 ? mid : (part == 2 ? lo : (uint16_t)0));
-            }
-            w[i / 2] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-        }
-        Q.a[j] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
-    }
+    for (int j = 0; j < HD / 32; j++)
+        Q.a[j] = __builtin_bit_cast(bf16x8_t, attn_q_word(S, threadIdx.x & 63, j));
     return Q;
+}
+
+// S.qp from S.qs by threads t0, t0 + nt, ... (one (lane, block) word each)
+template <int HD, int G, int WAVES>
+__device__ __forceinline__ void attn_q_store(AttnShared<HD, G, WAVES> &S, int t, int nt)
+{
+    for (int i = t; i < kWave * (HD / 32); i += nt)
+        S.qp[i / (HD / 32)][i % (HD / 32)] = attn_q_word(S, i / (HD / 32), i % (HD / 32));
 }
 
 // scores of the pages at slots [lo, ns) of S.pphys, UNR pages per wave step,
 // by waves w0 .. w0+nw-1
-template <int HD, int G, int WAVES, int UNR>
+template <int HD, int G, int WAVES, int UNR, bool QLDS = false>
 __device__ __forceinline__ void attn_scores_mfma(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
                                                  float scale, int w0, int nw, int lo = 0)
 {
     constexpr int NJ = HD / 32;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = lane & 15, gi = lane >> 4;
-    const QParts<HD> Q = attn_q_parts<HD, G, WAVES>(S);
+    // a wave with no page to score skips the q split too (with few pages
+    // most waves have none, and their vector work would only slow the ones
+    // that do, and the heap replay, on the same SIMDs)
+    if (lo + (wave - w0) * UNR >= ns)
+        return;
+    QParts<HD> Q;
+    if constexpr (QLDS) {
+        // formed once for the workgroup (attn_q_store)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            Q.a[j] = __builtin_bit_cast(bf16x8_t, S.qp[lane][j]);
+    } else {
+        Q = attn_q_parts<HD, G, WAVES>(S);
+    }
     const int n_kv = P.n_kv;
     for (int s0 = lo + (wave - w0) * UNR; s0 < ns; s0 += nw * UNR) {
         uint4 kb[UNR][NJ];
@@ -462,12 +491,12 @@ __device__ __forceinline__ void attn_scores_mfma(const be42_kv_pool &P, AttnShar
 
 // A. scores of the ns pages of S.pphys (slot order) for the G heads, by
 // waves w0 .. w0+nw-1.
-template <bool BF16, int HD, int G, int WAVES, int UNR>
+template <bool BF16, int HD, int G, int WAVES, int UNR, bool QLDS = false>
 __device__ __forceinline__ void attn_scores(const be42_kv_pool &P, AttnShared<HD, G, WAVES> &S, int kvh, int ns,
                                             float scale, int w0, int nw)
 {
     if constexpr (BF16 && (HD == 64 || HD == 128)) {
-        attn_scores_mfma<HD, G, WAVES, 4>(P, S, kvh, ns, scale, w0, nw);
+        attn_scores_mfma<HD, G, WAVES, 4, QLDS>(P, S, kvh, ns, scale, w0, nw);
         return;
     }
     constexpr int RL = HD / 8;                 // lanes per row
@@ -898,7 +927,9 @@ __global__ __launch_bounds__(WAVES * 64, 4) void k_lsh_attn(const be42_kv_pool P
         return;
     }
     const int nidx = min(lim ? min(P.n_indexed[layer], lim_b / kPg) : P.n_indexed[layer], P.max_logical);
-    route_prepare<STAGE>(P, q + (size_t)b * H * HD, base, n, nidx, H, cap, V, nullptr, nullptr, nullptr);
+    // the waves the router leaves idle form the q split meanwhile
+    route_prepare<STAGE>(P, q + (size_t)b * H * HD, base, n, nidx, H, cap, V, nullptr, nullptr, nullptr,
+                         [&] { attn_q_store(S, tid - kRouteThreads, blockDim.x - kRouteThreads); });
     const int nm = route_middles(V);
     const int ns0 = V.mpt[cap + 1] != V.mpt[cap] ? 2 : 1;
     const int nset = ns0 + nm;
@@ -919,7 +950,7 @@ __global__ __launch_bounds__(WAVES * 64, 4) void k_lsh_attn(const be42_kv_pool P
                 nsel[b] = ns;
         }
     } else if (early) {
-        attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, nset, scale, 1, WAVES - 1);
+        attn_scores<BF16, HD, G, WAVES, UNR, true>(P, S, kvh, nset, scale, 1, WAVES - 1);
     }
     __syncthreads();
     const int ns = set_n;
@@ -932,7 +963,7 @@ __global__ __launch_bounds__(WAVES * 64, 4) void k_lsh_attn(const be42_kv_pool P
             S.pnt[i] = page_nt(ph);
         }
         __syncthreads();
-        attn_scores<BF16, HD, G, WAVES, UNR>(P, S, kvh, ns, scale, 0, WAVES);
+        attn_scores<BF16, HD, G, WAVES, UNR, true>(P, S, kvh, ns, scale, 0, WAVES);
         __syncthreads();
     }
     attn_weights(S, ns, early ? S.order : nullptr);
@@ -1052,7 +1083,9 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
     }
     attn_load_q(S, q, b, kvh, H);
     const int nidx = min(lim ? min(P.n_indexed[layer], lim_b / kPg) : P.n_indexed[layer], P.max_logical);
-    route_prepare<STAGE>(P, q + (size_t)b * H * HD, base, n, nidx, H, cap, V, nullptr, nullptr, nullptr);
+    // the waves the router leaves idle form the q split meanwhile
+    route_prepare<STAGE>(P, q + (size_t)b * H * HD, base, n, nidx, H, cap, V, nullptr, nullptr, nullptr,
+                         [&] { attn_q_store(S, tid - kRouteThreads, blockDim.x - kRouteThreads); });
     const int nm = route_middles(V);
     const int ns0 = V.mpt[cap + 1] != V.mpt[cap] ? 2 : 1;
     const int nset = ns0 + nm;
@@ -1103,7 +1136,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
         }
         sync();
         if (alone) {
-            attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, E, scale, w0, WAVES - w0, 0);
+            attn_scores_mfma<HD, G, WAVES, 1, true>(P, S, kvh, E, scale, w0, WAVES - w0, 0);
         } else {
             for (int i = t; i < G * E * kPg; i += nt) {
                 const int g = i / (E * kPg), r = i % (E * kPg), sl = r / kPg;
@@ -1145,7 +1178,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
             }
             asm volatile("" ::: "memory");
         };
-        attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, hi, scale, 1, WAVES - 1, lo);
+        attn_scores_mfma<HD, G, WAVES, 1, true>(P, S, kvh, hi, scale, 1, WAVES - 1, lo);
         sync15();      // every wave's scores are in LDS before any is published
         exchange(1, nset, sync15);
     }
@@ -1161,7 +1194,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
         __syncthreads();
         lo = z * ns / NS;
         hi = (z + 1) * ns / NS;
-        attn_scores_mfma<HD, G, WAVES, 1>(P, S, kvh, hi, scale, 0, WAVES, lo);
+        attn_scores_mfma<HD, G, WAVES, 1, true>(P, S, kvh, hi, scale, 0, WAVES, lo);
         __syncthreads();
         exchange(0, ns, [] { __syncthreads(); });
         __syncthreads();

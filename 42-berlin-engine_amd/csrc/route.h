@@ -51,7 +51,8 @@ __host__ __device__ inline RouteSmem route_smem(int hd, int cap, int max_logical
     r.off_offs = o; o += kScanWaves * kProbes * 4 + 4 * 4;
     r.off_cand = o; o += cap * 4;
     r.off_mid = o;  o += cap * 4;
-    r.off_sc = o;   o += cap * 4;
+    o = (o + 15) & ~15;                          // route_select reads sc four at a time
+    r.off_sc = o;   o += (cap * 4 + 15) & ~15;
     r.off_rk = o;   o += 4 * cap * 4;             // partial ranks, [4][cap]
     r.off_mpt = o;  o += cap * 4 + 4 * 4;
     r.stage = o + max_logical * 2 + 16 <= kRouteLdsBudget ? max_logical : 0;
@@ -92,10 +93,6 @@ __device__ __forceinline__ RouteView route_view(unsigned char *smem, const Route
 }
 
 __device__ __forceinline__ int rl(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
-__device__ __forceinline__ float rlf(float v, int lane)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
 
 // Phases 0-4 for one query over n > k pages of a layer (page table row
 // `base`): staging, q_mean and its hash, the candidate scan, concatenation
@@ -104,10 +101,10 @@ __device__ __forceinline__ float rlf(float v, int lane)
 // page), mpt[e] (physical page), sc[e] for e < cnt[kCntMid], and the
 // first and last physical page in mpt[cap], mpt[cap + 1]; qhash_b, cand_b
 // and ncand_b (optional) receive the query hash and the candidate list.
-template <bool STAGE>
+template <bool STAGE, class Idle>
 __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float *__restrict__ qb, int base, int n,
                                               int nidx, int H, int cap, const RouteView &V, uint16_t *qhash_b,
-                                              int *cand_b, int *ncand_b)
+                                              int *cand_b, int *ncand_b, Idle &&idle)
 {
     const int hd = P.head_dim;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -174,6 +171,8 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
         }
     }
     __syncthreads();
+    if (tid >= kRouteThreads)
+        idle();
     if (tid == 0) {
         mpt[cap] = ptab(0);
         mpt[cap + 1] = ptab(n - 1);
@@ -359,6 +358,14 @@ __device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float
 
 }
 
+template <bool STAGE>
+__device__ __forceinline__ void route_prepare(const be42_kv_pool &P, const float *__restrict__ qb, int base, int n,
+                                              int nidx, int H, int cap, const RouteView &V, uint16_t *qhash_b,
+                                              int *cand_b, int *ncand_b)
+{
+    route_prepare<STAGE>(P, qb, base, n, nidx, H, cap, V, qhash_b, cand_b, ncand_b, [] {});
+}
+
 __device__ __forceinline__ int route_middles(const RouteView &V) { return V.cnt[kCntMid]; }
 
 // Phase 5 on wave 0: selection = [first page, last page] + the reference
@@ -392,11 +399,28 @@ __device__ __forceinline__ int route_select(int k_sel, int cap, const RouteView 
     // (rank, entry) keys, which order exactly as the scores
     int rk[4];
     if (nm <= kWave) {
-        // entry lane's rank: a broadcast of every entry's score in turn
+        // entry lane's rank: the scores four at a time as LDS broadcasts
+        // (every lane reads one address; sc is 16-byte aligned, its entries
+        // rounded up to four).  Reading lanes' scores across the wave one
+        // at a time (a readlane per entry) took twice as long next to the
+        // waves that score the pages meanwhile.
         const float own = V.sc[min(lane, max(nm - 1, 0))];
+        const float4 *sc4 = (const float4 *)V.sc;
         int r = 0;
-        for (int j = 0; j < nm; j++)
-            r += rlf(own, j) < own ? 1 : 0;
+        for (int j0 = 0; j0 < nm; j0 += 16) {
+            float4 x[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                x[u] = sc4[min(j0 / 4 + u, (nm - 1) / 4)];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int j = j0 + 4 * u;
+                r += j < nm && x[u].x < own ? 1 : 0;
+                r += j + 1 < nm && x[u].y < own ? 1 : 0;
+                r += j + 2 < nm && x[u].z < own ? 1 : 0;
+                r += j + 3 < nm && x[u].w < own ? 1 : 0;
+            }
+        }
         rk[0] = r;
         rk[1] = rk[2] = rk[3] = 0;
     } else {
