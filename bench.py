@@ -309,7 +309,14 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES, ctx=None):
     head = max(rows, key=lambda r: r["frac_of_hbm_peak"])
     launch_bytes = head["bytes_per_step"]
     achieved = launch_bytes / (head["step_us"] * 1e-6) / 1e9
-    roof = {"bound": "hbm", "kernel": "be42::k_lsh_attn (route + sparse attention, one launch)",
+    # be42_lsh_attention's dispatch: up to 64 (query, KV head) pairs the split
+    # launch, below 1024 the fused route + attention, from 1024 the router's
+    # own launch and then the fused attention
+    pairs = head["batch"] * KVH
+    kname = ("be42::k_lsh_attn_split (route + sparse attention, one launch)" if pairs <= 64 else
+             "be42::k_lsh_attn (route + sparse attention, one launch)" if pairs < 1024 else
+             "be42::k_route + be42::k_attn_fused (route, then sparse attention: two launches)")
+    roof = {"bound": "hbm", "kernel": kname,
             "workload": f"batch {head['batch']}, {T}-token bf16 context",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -323,8 +330,9 @@ def lsh_bench(lib, steps, warmup, batches=LSH_BATCHES, ctx=None):
             "workload": f"configs[3]: B sequences x {T}-token bf16 paged KV (page 16), {H} heads / {KVH} KV heads, "
                         f"head_dim {hd}, top-K {cfg['k_sel']} pages, candidate cap {cfg['cap']}, 5% planted pages; "
                         f"one step = route + sparse attention of one decode token per sequence "
-                        f"(be42_lsh_attention: one launch up to 512 query x KV-head pairs, two above; "
-                        f"route_us / attention_us time the work as two launches)",
+                        f"(be42_lsh_attention: one launch below 1024 query x KV-head pairs, from 1024 the "
+                        f"router's own launch then the attention; route_us / attention_us time the work as "
+                        f"be42_lsh_route + be42_paged_attention)",
             "us_per_token": head["us_per_token"], "batch": head["batch"], "recall_at_k": head["recall_at_k"],
             "frac_of_hbm_peak": head["frac_of_hbm_peak"], "by_batch": rows}
 
@@ -897,12 +905,13 @@ def gemm_cpu_baseline(seconds=10.0):
             "sample": f"oracle or_gemm_fp8 M={m} N={n} K={k}, OpenMP {cores} threads, median of {len(ts)} runs"}
 
 
-LSH_PMC_SUMMARY = os.path.join(ROOT, "profiles", "lsh_attn_fused_32k_pmc.txt")
+LSH_PMC_SUMMARY = os.path.join(ROOT, "profiles", "lsh_attn_32k_pmc.txt")
 
 
 def lsh_traffic(batch):
-    """HBM bytes per launch of the fused route + attention at this batch, from
-    the committed rocprofv3 --pmc summary (scaled like the GEMV's)."""
+    """HBM bytes per step of the route + attention at this batch (its one or
+    two launches), from the committed rocprofv3 --pmc summary (scaled like
+    the GEMV's)."""
     if not os.path.exists(LSH_PMC_SUMMARY):
         return None
     for line in open(LSH_PMC_SUMMARY):
