@@ -8,26 +8,98 @@
 // one index with a uniform number the caller supplies:
 //   temperature: the first index whose running sum of p exceeds r
 //                (sampler_random_float's draw);
-//   top-p:       p sorted descending (a stable radix sort: equal
-//                probabilities keep ascending index order, where the
-//                reference's qsort leaves them unspecified), the shortest
-//                prefix whose running sum exceeds top_p, r = u * that sum
-//                (u = rand() / RAND_MAX), the first sorted entry whose
-//                running sum exceeds r.
-// The sums run as block-wide scans: equal to the reference's sequential sums
-// to fp32 rounding, so the drawn index is the reference's unless r lies within
-// that rounding of a boundary.  Where no running sum exceeds r (possible only
-// through rounding) the reference returns n, an index past the vocabulary;
-// here the last index is returned.
+//   top-p:       in the order of p descending (equal probabilities in
+//                ascending index order, where the reference's qsort leaves
+//                them unspecified), the shortest prefix whose running sum
+//                exceeds top_p, r = u * that sum (u = rand() / RAND_MAX),
+//                the first entry of the prefix whose running sum exceeds r.
+// The temperature sampler's running sums are formed 64 entries at a time
+// (lane prefix sums plus a carried sum), equal to the reference's
+// sequential fp32 sums to rounding.  Where no running sum exceeds
+// r (possible only through rounding) the reference returns n, an index past
+// the vocabulary; here the last index is returned.
+//
+// Top-p never sorts: both cuts are weighted selections.  The entry at which
+// the descending-order running sum first exceeds a threshold is found by a
+// most-significant-byte-first radix select over the bit patterns of the
+// (non-negative) probabilities, where each pass sums the probabilities of the
+// remaining candidates per byte value and keeps the byte whose bucket holds
+// the crossing; after four passes the crossing entry's value is known, and
+// among the entries of that value (ascending index) the crossing is the
+// (T - sum above) / value-th.  The sums are exact: probabilities as 62-bit
+// fixed point (p * 2^62, truncated) in 64-bit integer additions, so they do
+// not depend on the order of the atomic additions, and they are the float64
+// running sums to ~n * 2^-62 -- closer than the reference's fp32 sums.
 #include <cstring>
-
-#include <rocprim/device/device_radix_sort.hpp>
 
 #include "be42_common.h"
 
 namespace be42 {
 
 constexpr int kSampT = 1024;
+
+// The loops below read a row with their loads issued U at a time (the
+// values into registers first, then used in the same order as one at a
+// time): a loop that uses each value as it arrives waits a full memory
+// round trip per element, and one block walks a whole 128k-entry row.
+//   strided: i = t, t + kSampT, ... (thread t), f(i, v)
+template <int U, class Ld, class F>
+__device__ __forceinline__ void strided_batches(int n, Ld &&ld, F &&f)
+{
+    for (int i0 = threadIdx.x; i0 < n; i0 += U * kSampT) {
+        decltype(ld(0)) v[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const int i = i0 + j * kSampT;
+            v[j] = ld(i < n ? i : i0);
+        }
+#pragma unroll
+        for (int j = 0; j < U; j++)
+            if (i0 + j * kSampT < n)
+                f(i0 + j * kSampT, v[j]);
+    }
+}
+//   wave:    entries c0 .. c1 - 1 of one wave, 64 a step (lane l: entry
+//            a + l, T(0) past c1), f(a, v) returns true (wave-uniform) to stop
+template <int U, class T, class F>
+__device__ __forceinline__ void wave_steps(const T *__restrict__ q, int c0, int c1, F &&f)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    for (int a0 = c0; a0 < c1; a0 += kWave * U) {
+        T v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = a0 + kWave * u + lane;
+            v[u] = i < c1 ? q[i] : T(0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (a0 + kWave * u < c1 && f(a0 + kWave * u, v[u]))
+                return;
+    }
+}
+
+// the block's row split into one contiguous range per wave, whole steps of 64
+__device__ __forceinline__ void wave_range(int n, int &c0, int &c1)
+{
+    constexpr int NW = kSampT / kWave;
+    const int cw = (((n + NW - 1) / NW) + kWave - 1) & ~(kWave - 1);
+    c0 = min(n, (int)(threadIdx.x / kWave) * cw);
+    c1 = min(n, c0 + cw);
+}
+
+// inclusive prefix sum over the lanes (DPP row shifts, then row broadcasts)
+__device__ __forceinline__ float wave_prefix_sum(float v)
+{
+    v = v + dpp_mov<0x111>(0.0f, v);         // row_shr:1
+    v = v + dpp_mov<0x112>(0.0f, v);         // row_shr:2
+    v = v + dpp_mov<0x114>(0.0f, v);         // row_shr:4
+    v = v + dpp_mov<0x118>(0.0f, v);         // row_shr:8
+    v = v + dpp_mov<0x142, 0xA>(0.0f, v);    // row_bcast:15 into rows 1, 3
+    v = v + dpp_mov<0x143, 0xC>(0.0f, v);    // row_bcast:31 into rows 2, 3
+    return v;
+}
+__device__ __forceinline__ float lane63(float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)); }
 
 __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max)
 {
@@ -55,62 +127,61 @@ __global__ __launch_bounds__(kSampT) void k_probs(float *__restrict__ p, const v
                     : ((const float *)logits)[(size_t)b * n + i];
     };
     float m = max_from_first ? x(0) : -1e9f;
-    for (int i = threadIdx.x; i < n; i += kSampT)
-        m = fmaxf(m, x(i));
+    strided_batches<16>(n, x, [&](int, float v) { m = fmaxf(m, v); });
     m = block_reduce(m, red, true);
     float *pb = p + (size_t)b * n;
     float s = 0.0f;
-    for (int i = threadIdx.x; i < n; i += kSampT) {
-        const float e = expf(__fdiv_rn(x(i) - m, temp));
+    strided_batches<16>(n, x, [&](int i, float v) {
+        const float e = expf(__fdiv_rn(v - m, temp));
         pb[i] = e;
         s += e;
-    }
+    });
     s = block_reduce(s, red, false);
-    for (int i = threadIdx.x; i < n; i += kSampT)
-        pb[i] = __fdiv_rn(pb[i], s);
+    strided_batches<16>(n, [&](int i) { return pb[i]; }, [&](int i, float v) { pb[i] = __fdiv_rn(v, s); });
 }
 
-// Exclusive block scan of one float per thread (thread order).
-__device__ __forceinline__ float block_excl_scan(float v, float *sh)
+// The first position i < lim whose running sum of q exceeds thr, or -1.
+// Each wave walks its own contiguous range 64 entries a step; a step's
+// running sums are the lanes' prefix sums plus the sum carried from the
+// steps before (the range's first step carries the sum of the ranges before).
+// sh: 2 * (kSampT / 64) floats.
+__device__ int block_first_exceeding(const float *__restrict__ q, int lim, float thr, float *sh, int *found)
 {
-    sh[threadIdx.x] = v;
-    __syncthreads();
-    for (int o = 1; o < kSampT; o <<= 1) {
-        const float a = threadIdx.x >= (unsigned)o ? sh[threadIdx.x - o] : 0.0f;
-        __syncthreads();
-        sh[threadIdx.x] += a;
-        __syncthreads();
-    }
-    const float incl = sh[threadIdx.x];
-    return incl - v;
-}
-
-// The first position i < lim (thread t walks the contiguous chunk
-// [t C, (t + 1) C)) whose running sum of q exceeds thr, or -1; with thr_rel the
-// threshold is thr times the running sum at position lim - 1.
-__device__ int block_first_exceeding(const float *__restrict__ q, int lim, float thr, bool thr_rel, float *sh,
-                                     int *found, float *total)
-{
-    const int C = (lim + kSampT - 1) / kSampT;
-    const int i0 = min(lim, (int)threadIdx.x * C), i1 = min(lim, i0 + C);
-    float cs = 0.0f;
-    for (int i = i0; i < i1; i++)
-        cs += q[i];
-    const float pre = block_excl_scan(cs, sh);
-    if (threadIdx.x == kSampT - 1)
-        *total = pre + cs;
+    constexpr int NW = kSampT / kWave;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+    int c0, c1;
+    wave_range(lim, c0, c1);
+    float carry = 0.0f;
+    wave_steps<8>(q, c0, c1, [&](int, float v) {
+        carry += lane63(wave_prefix_sum(v));
+        return false;
+    });
+    if (lane == 0)
+        sh[wave] = carry;
     if (threadIdx.x == 0)
         *found = INT32_MAX;
     __syncthreads();
-    const float r = thr_rel ? thr * *total : thr;
-    float cum = pre;
-    for (int i = i0; i < i1; i++) {
-        cum += q[i];
-        if (cum > r) {
-            atomicMin(found, i);
-            break;
+    if (threadIdx.x == 0) {
+        float o = 0.0f;
+        for (int w = 0; w < NW; w++) {
+            const float t = sh[w];
+            sh[NW + w] = o;
+            o += t;
         }
     }
+    __syncthreads();
+    carry = sh[NW + wave];
+    wave_steps<8>(q, c0, c1, [&](int a, float v) {
+        const float ps = wave_prefix_sum(v);
+        const unsigned long long m = __ballot(carry + ps > thr);
+        if (m) {
+            if (lane == 0)
+                atomicMin(found, a + __ffsll((unsigned long long)m) - 1);
+            return true;
+        }
+        carry += lane63(ps);
+        return false;
+    });
     __syncthreads();
     const int f = *found;
     __syncthreads();
@@ -120,40 +191,222 @@ __device__ int block_first_exceeding(const float *__restrict__ q, int lim, float
 __global__ __launch_bounds__(kSampT) void k_pick_temperature(int *__restrict__ out, const float *__restrict__ p, int n,
                                                              const float *__restrict__ r)
 {
-    __shared__ float sh[kSampT];
+    __shared__ float sh[2 * (kSampT / kWave)];
     __shared__ int found;
-    __shared__ float total;
     const int b = blockIdx.x;
-    const int i = block_first_exceeding(p + (size_t)b * n, n, r[b], false, sh, &found, &total);
+    const int i = block_first_exceeding(p + (size_t)b * n, n, r[b], sh, &found);
     if (threadIdx.x == 0)
         out[b] = i < 0 ? n - 1 : i;
 }
 
-// sorted probabilities ps and their indices: cut at top_p, then draw
-__global__ __launch_bounds__(kSampT) void k_pick_top_p(int *__restrict__ out, const float *__restrict__ ps,
-                                                       const int *__restrict__ idx, int n, float top_p,
-                                                       const float *__restrict__ u)
+// the bit fields of a probability's pattern the three passes resolve
+// (12, 12 and 8 bits: the first pass spreads over exponent and 4 mantissa
+// bits, so the atomic additions of one wave rarely meet in one bucket)
+constexpr int kSelPasses = 3;
+constexpr int kSelShift[kSelPasses] = {20, 8, 0};
+constexpr int kSelBits[kSelPasses] = {12, 12, 8};
+constexpr int kSelBins = 1 << 12;
+
+// p as 62-bit fixed point, floor(p * 2^62), from the bits of p in [0, 1]:
+// mantissa (with its leading 1) shifted by exponent - 88 (0 for zero,
+// subnormal, negative or NaN patterns; those above 1 do not occur)
+__device__ __forceinline__ unsigned long long fixp_bits(unsigned k)
 {
-    __shared__ float sh[kSampT];
-    __shared__ int found;
-    __shared__ float total;
-    const int b = blockIdx.x;
-    const float *pb = ps + (size_t)b * n;
-    const int *ib = idx + (size_t)b * n;
-    // the set: the prefix through the first running sum above top_p
-    const int c = block_first_exceeding(pb, n, top_p, false, sh, &found, &total);
-    const int count = c < 0 ? n : c + 1;
-    // r = u * (the set's running sum); the first entry whose running sum exceeds it
-    const int j = block_first_exceeding(pb, count, u[b], true, sh, &found, &total);
-    if (threadIdx.x == 0)
-        out[b] = ib[j < 0 ? count - 1 : j];
+    const int e = (int)(k >> 23);   // the sign bit makes negative patterns > 255
+    if (e == 0 || e > 127)
+        return 0ull;
+    const unsigned long long m = (unsigned long long)((k & 0x7FFFFFu) | 0x800000u);
+    const int sh = e - 88;
+    return sh >= 0 ? m << sh : (sh > -64 ? m >> -sh : 0ull);
+}
+__device__ __forceinline__ unsigned long long fixp(float p) { return fixp_bits(__float_as_uint(p)); }
+
+struct TopPShared {
+    unsigned long long hist[kSelBins];   // bucket sums of a pass
+    unsigned long long scan[kSampT];
+    int isum[kSampT / kWave];
+    unsigned long long total, above;
+    int pos, bin, idx;
+};
+
+// Exclusive block scan of one value per thread (thread order).
+template <class T>
+__device__ __forceinline__ T block_excl_scan_t(T v, T *sh)
+{
+    sh[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = 1; o < kSampT; o <<= 1) {
+        const T a = threadIdx.x >= (unsigned)o ? sh[threadIdx.x - o] : T(0);
+        __syncthreads();
+        sh[threadIdx.x] += a;
+        __syncthreads();
+    }
+    const T incl = sh[threadIdx.x];
+    __syncthreads();
+    return incl - v;
 }
 
-__global__ void k_iota_rows(int *__restrict__ v, int n, int batch)
+// The entry of p[0 .. n) at which the running sum of fixp(p), taken in
+// descending order of p with equal values in ascending index order, first
+// exceeds T; -1 if none does.  *above: the running sum before that entry;
+// *all: the sum of every entry.  Called by the whole block.
+__device__ int weighted_select(const float *__restrict__ p, int n, unsigned long long T, TopPShared &S,
+                               unsigned long long *above, unsigned long long *all)
 {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < (size_t)n * batch)
-        v[i] = (int)(i % n);
+    const int tid = threadIdx.x;
+    unsigned prefix = 0, pmask = 0;
+    unsigned long long base = 0;   // the sum of the entries above the current bucket
+    for (int pass = 0; pass < kSelPasses; pass++) {
+        const int shift = kSelShift[pass], nb = 1 << kSelBits[pass];
+        for (int i = tid; i < nb; i += kSampT)
+            S.hist[i] = 0ull;
+        if (tid == 0)
+            S.pos = INT32_MAX;
+        __syncthreads();
+        strided_batches<16>(n, [&](int i) { return __float_as_uint(p[i]); }, [&](int, unsigned k) {
+            if ((k & pmask) == prefix) {
+                const unsigned long long f = fixp_bits(k);
+                if (f)
+                    atomicAdd(&S.hist[(k >> shift) & (nb - 1)], f);
+            }
+        });
+        __syncthreads();
+        // thread t takes the buckets at descending positions 4t .. 4t + 3
+        unsigned long long h[4], ts = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int d = 4 * tid + j;
+            h[j] = d < nb ? S.hist[nb - 1 - d] : 0ull;
+            ts += h[j];
+        }
+        const unsigned long long ex = block_excl_scan_t<unsigned long long>(ts, S.scan);
+        if (pass == 0 && tid == kSampT - 1)
+            S.total = ex + ts;
+        unsigned long long acc = base + ex;
+        int hit = -1;
+        unsigned long long hit_above = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (hit < 0 && h[j] && acc + h[j] > T) {
+                hit = 4 * tid + j;
+                hit_above = acc;
+            }
+            acc += h[j];
+        }
+        if (hit >= 0)
+            atomicMin(&S.pos, hit);
+        __syncthreads();
+        const int pos = S.pos;
+        if (hit >= 0 && hit == pos) {
+            S.bin = nb - 1 - pos;
+            S.above = hit_above;
+        }
+        __syncthreads();
+        if (pass == 0)
+            *all = S.total;
+        const int bin = S.bin;
+        base = S.above;
+        __syncthreads();   // S is rewritten by the next pass
+        if (pos == INT32_MAX)
+            return -1;
+        prefix |= (unsigned)bin << shift;
+        pmask |= (unsigned)(nb - 1) << shift;
+    }
+    // the crossing entry has the value whose bits are `prefix`; among the
+    // entries of that value (ascending index) it is the k-th
+    const unsigned long long fv = fixp(__uint_as_float(prefix));   // > 0: its bucket's sum is positive
+    const unsigned long long k = (T - base) / fv;
+    const int wave = tid / kWave, lane = tid & (kWave - 1);
+    int c0, c1;
+    wave_range(n, c0, c1);
+    auto match = [&](int a, float v) { return __ballot(a + lane < c1 && __float_as_uint(v) == prefix); };
+    int cnt = 0;   // entries of that value in this wave's range
+    wave_steps<8>(p, c0, c1, [&](int a, float v) {
+        cnt += __popcll(match(a, v));
+        return false;
+    });
+    if (lane == 0)
+        S.isum[wave] = cnt;
+    if (tid == 0)
+        S.idx = -1;
+    __syncthreads();
+    int off = 0;
+    for (int w = 0; w < wave; w++)
+        off += S.isum[w];
+    if ((unsigned long long)off <= k && k < (unsigned long long)(off + cnt)) {
+        int rem = (int)(k - (unsigned long long)off);
+        wave_steps<8>(p, c0, c1, [&](int a, float v) {
+            unsigned long long m = match(a, v);
+            const int c = __popcll(m);
+            if (rem < c) {
+                for (int j = 0; j < rem; j++)
+                    m &= m - 1;
+                if (lane == 0)
+                    S.idx = a + __ffsll(m) - 1;
+                return true;
+            }
+            rem -= c;
+            return false;
+        });
+    }
+    __syncthreads();
+    *above = base + k * fv;
+    const int idx = S.idx;
+    __syncthreads();
+    return idx;
+}
+
+// The last entry in descending order: the smallest value, the largest index
+// among equal ones.
+__device__ int last_entry(const float *__restrict__ p, int n, TopPShared &S)
+{
+    const int tid = threadIdx.x;
+    unsigned long long best = 0;   // (~key << 32 | index): the largest is the last entry
+    strided_batches<16>(n, [&](int i) { return __float_as_uint(p[i]); }, [&](int i, unsigned k) {
+        const unsigned long long c = ((unsigned long long)~k << 32) | (unsigned)i;
+        best = c > best ? c : best;
+    });
+    unsigned long long *words = S.scan;
+    words[tid] = best;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long t = 0;
+        for (int i = 0; i < kSampT; i++)
+            t = words[i] > t ? words[i] : t;
+        S.idx = (int)(unsigned)t;
+    }
+    __syncthreads();
+    const int idx = S.idx;
+    __syncthreads();
+    return idx;
+}
+
+// probabilities p (one row per block): cut at top_p, then draw with u
+__global__ __launch_bounds__(kSampT) void k_top_p(int *__restrict__ out, const float *__restrict__ p, int n,
+                                                  float top_p, const float *__restrict__ u)
+{
+    __shared__ TopPShared S;
+    const float *pb = p + (size_t)blockIdx.x * n;
+    // the set: through the first entry whose running sum exceeds top_p
+    // (the sums stay near 2^62: a threshold of 2 or more is never exceeded)
+    const unsigned long long T1 =
+        top_p >= 2.0f ? ~0ull : (top_p > 0.0f ? (unsigned long long)((double)top_p * 0x1p62) : 0ull);
+    unsigned long long above, all;
+    const int c = weighted_select(pb, n, T1, S, &above, &all);
+    const unsigned long long total = c >= 0 ? above + fixp(pb[c]) : all;
+    // r = u * (the set's sum); the first entry whose running sum exceeds it,
+    // or the set's last entry when none does
+    const float uu = u[blockIdx.x];
+    const unsigned long long R = uu > 0.0f ? (unsigned long long)fmin((double)uu * (double)total, 1.8e19) : 0ull;
+    int pick = -1;
+    if (R < total) {
+        unsigned long long a2, all2;
+        pick = weighted_select(pb, n, R, S, &a2, &all2);
+    }
+    if (pick < 0)
+        pick = c >= 0 ? c : last_entry(pb, n, S);
+    if (threadIdx.x == 0)
+        out[blockIdx.x] = pick;
 }
 
 int probs_launch(float *p, const void *logits, bool bf16, int n, int batch, float temp, bool max_first,
@@ -170,8 +423,6 @@ int probs_launch(float *p, const void *logits, bool bf16, int n, int batch, floa
 }  // namespace be42
 
 using namespace be42;
-
-static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // logits_bf16: logits are bf16 (the reference's DTYPE_BF16 tensors)
 extern "C" int be42_sample_temperature_dt(int *out, const void *logits, int logits_bf16, int n, int batch, float temp,
@@ -203,28 +454,13 @@ extern "C" int be42_sample_top_p_dt(int *out, const void *logits, int logits_bf1
     BE42_CHECK(out && logits && u, "be42_sample_top_p: null pointer");
     BE42_CHECK(n > 0 && batch > 0, "be42_sample_top_p: n %d, batch %d", n, batch);
     hipStream_t s = as_stream(stream);
-    const size_t rowsz = (size_t)n * batch;
-    size_t sort_bytes = 0;
-    BE42_HIP(rocprim::radix_sort_pairs_desc(nullptr, sort_bytes, (const float *)nullptr, (float *)nullptr,
-                                            (const int *)nullptr, (int *)nullptr, (unsigned)n, 0, 32, s));
-    const size_t fb = align256(rowsz * 4);
-    uint8_t *ws = (uint8_t *)workspace(4 * fb + align256(sort_bytes), s);
-    if (!ws)
+    float *p = (float *)workspace((size_t)n * batch * 4, s);
+    if (!p)
         return BE42_ENOMEM;
-    float *p = (float *)ws, *ps = (float *)(ws + fb);
-    int *iv = (int *)(ws + 2 * fb), *is = (int *)(ws + 3 * fb);
-    void *tmp = ws + 4 * fb;
-    int rc = probs_launch(p, logits, logits_bf16 != 0, n, batch, temp, true, s);
+    const int rc = probs_launch(p, logits, logits_bf16 != 0, n, batch, temp, true, s);
     if (rc)
         return rc;
-    hipLaunchKernelGGL(k_iota_rows, dim3((unsigned)((rowsz + 255) / 256)), dim3(256), 0, s, iv, n, batch);
-    BE42_LAUNCH_CHECK();
-    for (int b = 0; b < batch; b++) {
-        size_t bytes = sort_bytes;
-        BE42_HIP(rocprim::radix_sort_pairs_desc(tmp, bytes, p + (size_t)b * n, ps + (size_t)b * n, iv + (size_t)b * n,
-                                                is + (size_t)b * n, (unsigned)n, 0, 32, s));
-    }
-    hipLaunchKernelGGL(k_pick_top_p, dim3(batch), dim3(kSampT), 0, s, out, ps, is, n, top_p, u);
+    hipLaunchKernelGGL(k_top_p, dim3(batch), dim3(kSampT), 0, s, out, p, n, top_p, u);
     BE42_LAUNCH_CHECK();
     return BE42_OK;
 }

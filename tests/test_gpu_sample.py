@@ -1,8 +1,9 @@
 """Temperature and top-p sampling on the GPU (be42_sample_temperature /
 be42_sample_top_p, and the drop-in sample_temperature / sample_top_p) against
 the oracle (tests/test_oracle_sample.py pins it to the compiled reference).
-The GPU sums probabilities as block scans, the oracle (and the reference)
-sequentially in fp32, which over 128k terms drifts from the exact running
+The GPU sums probabilities 64 at a time with a carried sum (temperature)
+or exactly in 62-bit fixed point (top-p), the oracle (and the reference) sequentially in
+fp32, which over 128k terms drifts from the exact running
 sum by up to ~1e-4 -- more than the mean probability of a 128k vocabulary, so
 near most draws the reference's own pick is set by its rounding.  Every GPU
 pick is checked to be the exact (float64) pick to within that drift (the
@@ -132,6 +133,24 @@ def test_top_p_ties_keep_index_order(be, orc):
         got = be.sample_top_p(torch.from_numpy(x).cuda(), 1.0, 0.8,
                               torch.tensor([u], dtype=torch.float32, device="cuda")).item()
         assert got == orc.sample_top_p(x[0], 1.0, 0.8, u), u
+
+
+def test_top_p_edges(be, orc):
+    """A draw of u = 1 exceeds no running sum of the set: the set's last
+    entry.  top_p >= 1 cuts nothing: the set is every entry, and its last one
+    is the smallest probability.  top_p = 0: the set is the largest entry."""
+    rng = np.random.default_rng(17)
+    x = logits_batch(rng, 1, 3000, 2.0)
+    xt = torch.from_numpy(x).cuda()
+    for top_p, u in ((0.9, 1.0), (1.5, 1.0), (1.5, 0.5), (0.0, 0.3), (0.0, 1.0)):
+        got = be.sample_top_p(xt, 1.0, top_p, torch.tensor([u], dtype=torch.float32, device="cuda")).item()
+        ok, near = top_p_case(x[0], 1.0, top_p, u)
+        assert ok(got), (top_p, u, got)
+        if top_p != 0.9 or not near:
+            assert got == orc.sample_top_p(x[0], 1.0, top_p, u), (top_p, u, got)
+    p = probs64(x[0], 1.0, True)
+    assert be.sample_top_p(xt, 1.0, 1.5, torch.tensor([1.0], device="cuda")).item() == int(np.argmin(p))
+    assert be.sample_top_p(xt, 1.0, 0.0, torch.tensor([0.7], device="cuda")).item() == int(np.argmax(p))
 
 
 def test_dropin_samplers(be, orc):
