@@ -648,8 +648,8 @@ __device__ __forceinline__ void attn_values_load(const be42_kv_pool &P, AttnShar
 }
 
 // out = (sum over the waves' partial o) * (1 / l)
-template <int HD, int G, int WAVES>
-__device__ __forceinline__ void attn_values_finish(const AttnShared<HD, G, WAVES> &S, int b, int kvh, int H,
+template <int HD, int G, int WAVES, int SW>
+__device__ __forceinline__ void attn_values_finish(const AttnShared<HD, G, SW> &S, int b, int kvh, int H,
                                                    float *__restrict__ out)
 {
     const int tid = threadIdx.x;
@@ -679,8 +679,8 @@ typedef int v2i_t __attribute__((ext_vector_type(2)));
 // The pages of wave `wave` of a WAVES-wave layout (positions wave * UNR +
 // WAVES * UNR * i + u) into put(index, value), index = g * HD + dim: the
 // partial o of that wave.
-template <int HD, int G, int WAVES, int UNR, class Put>
-__device__ __forceinline__ void attn_values_mfma_wave(const be42_kv_pool &P, const AttnShared<HD, G, WAVES> &S,
+template <int HD, int G, int WAVES, int UNR, int SW, class Put>
+__device__ __forceinline__ void attn_values_mfma_wave(const be42_kv_pool &P, const AttnShared<HD, G, SW> &S,
                                                       int kvh, int ns, const int *order, int wave, Put &&put)
 {
     constexpr int NT = HD / 16;
@@ -821,8 +821,11 @@ __device__ __forceinline__ void attn_values(const be42_kv_pool &P, AttnShared<HD
 // b sees the first lim[b] positions of slot slots[b]: its last visible page
 // holds lim[b] - 16 (pages - 1) tokens.  The phases and the order of every
 // sum are those of k_lsh_attn's selection-order path, so at the same WAVES
-// an output equals k_lsh_attn's.
-template <bool BF16, int HD, int G, int WAVES, int UNR>
+// an output equals k_lsh_attn's.  VW > WAVES (bf16 pages): the values are
+// summed in the layout of VW waves, each wave forming the partials of waves
+// wave, wave + WAVES, ..., so that the output equals that of a VW-wave launch
+// (and of the split decode kernel) with fewer waves per workgroup.
+template <bool BF16, int HD, int G, int WAVES, int UNR, int VW = WAVES>
 __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P, const float *__restrict__ q,
                                                            const int *__restrict__ sel,
                                                            const int *__restrict__ nsel, int sel_stride,
@@ -830,8 +833,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
                                                            const int *__restrict__ lim, int H, float scale,
                                                            float *__restrict__ out)
 {
+    static_assert(VW == WAVES || (BF16 && (HD == 64 || HD == 128) && VW % WAVES == 0), "value layout");
     __shared__ AttnShared<HD, G, WAVES> S;
-    __shared__ float red[WAVES * G * HD];
+    __shared__ float red[VW * G * HD];
     S.red = red;
     const int b = blockIdx.x, kvh = blockIdx.y;
     const int ns = min(nsel[b], kFusedMaxPages);
@@ -858,7 +862,16 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_fused(const be42_kv_pool P,
     __syncthreads();
     attn_weights(S, ns, nullptr);
     __syncthreads();
-    attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out, nullptr);
+    if constexpr (VW == WAVES) {
+        attn_values<BF16, HD, G, WAVES, UNR>(P, S, b, kvh, ns, H, out, nullptr);
+    } else {
+        for (int vw = threadIdx.x >> 6; vw < VW; vw += WAVES) {
+            float *dst = red + vw * G * HD;
+            attn_values_mfma_wave<HD, G, VW, 4>(P, S, kvh, ns, nullptr, vw, [dst](int i, float v) { dst[i] = v; });
+        }
+        __syncthreads();
+        attn_values_finish<HD, G, VW>(S, b, kvh, H, out);
+    }
 }
 
 // LSH route + sparse attention of one query in one kernel: workgroup
@@ -1287,7 +1300,9 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_lsh_attn_split(const be42_
 // 16 waves when the grid is small (more loads in flight per workgroup), 8
 // waves once there are enough workgroups to fill the chip.
 // slots / lim: as k_attn_fused (lim null: every slot's whole cache).
-// wide16 keeps 16 waves for any grid (k_lsh_attn's wide16).
+// wide16 keeps the 16-wave layout for any grid (k_lsh_attn's wide16): bf16
+// pages from 8-wave workgroups that sum the values in that layout, others
+// at 16 waves.
 struct FusedOpt {
     const int *slots = nullptr, *lim = nullptr;
     bool wide16 = false;
@@ -1298,6 +1313,14 @@ static void launch_fused_g(const be42_kv_pool &P, const float *q, const int *sel
                            int B, int H, float scale, float *out, const FusedOpt &o, hipStream_t s)
 {
     const dim3 grid(B, P.n_kv);
+    if constexpr (BF16 && (HD == 64 || HD == 128)) {
+        // the 16-wave value layout from 8-wave workgroups (two per CU)
+        if (o.wide16) {
+            hipLaunchKernelGGL((k_attn_fused<BF16, HD, G, 8, 8, 16>), grid, dim3(512), 0, s, P, q, sel, nsel,
+                               sel_stride, o.slots, o.lim, H, scale, out);
+            return;
+        }
+    }
     if ((long)B * P.n_kv < 512 || o.wide16)
         hipLaunchKernelGGL((k_attn_fused<BF16, HD, G, 16, 8>), grid, dim3(1024), 0, s, P, q, sel, nsel, sel_stride,
                            o.slots, o.lim, H, scale, out);
