@@ -24,6 +24,7 @@
 #include <initializer_list>
 #include <vector>
 
+#include "attn_dev.h"
 #include "be42_common.h"
 #include "paged_dev.h"
 #include "paged_step.h"
@@ -512,6 +513,8 @@ struct FusedArgs {
     int *err;
     unsigned spin_max;   // polls before a grid-barrier wait gives up
     unsigned bias;       // added to the numbers waited for (0; a test sets it so no wait completes)
+    float *att_out;      // the next layer's dense attention output (null: a launch of its own)
+    float att_scale;
 };
 
 struct GridBar {
@@ -978,6 +981,46 @@ __device__ __forceinline__ float norm_digits(const float *x, const float *delta,
     return red[12];
 }
 
+// The next layer's dense attention for KV head kvh, after this block's K/V
+// append (blocks 0 .. KV-1 of the tail): what a one-query k_attn_fused launch
+// at 16 waves computes over the sequence's pages, from this block's 8 waves
+// (the scores and weights of every token as there, the values summed in the
+// 16-wave layout: attn_values_layout), so the step's output is the same bit
+// for bit.  The page list is the one the append leaves -- the slot's table
+// before it, the appended token's page at its logical position, holding
+// position + 1 tokens -- formed here from the append's arguments, since block
+// 0 publishes the table and token count and other blocks do not wait for it.
+// qs: the G rotated query rows of the group (LDS); lds: free LDS for the
+// phases' shared state and the 16 partial outputs.
+constexpr int kTailAttnOff = 4096;   // bytes of the tail's scratch before the attention state
+template <bool BF16KV, int HD, int G>
+__device__ __forceinline__ void tail_attention(const FusedArgs &A, int kvh, const float *qs, uint8_t *lds)
+{
+    using SH = AttnShared<HD, G, kFW>;
+    constexpr size_t kRedOff = (sizeof(SH) + 15) & ~(size_t)15;
+    static_assert(kTailAttnOff + kRedOff + 16 * G * HD * 4 <= kFDigBytes, "tail attention LDS");
+    static_assert((G + 3) * HD * 4 <= kTailAttnOff, "tail scratch");
+    SH &S = *reinterpret_cast<SH *>(lds);
+    S.red = reinterpret_cast<float *>(lds + kRedOff);
+    const be42_kv_pool &P = A.P;
+    const AppendStepArgs &a = *A.app;
+    const int off = a.pos[0] % kPg, blk = a.pos[0] / kPg, phys = a.phys[0], slot = a.slot[0];
+    const int ns = min(blk + 1, kFusedMaxPages);
+    for (int i = threadIdx.x; i < G * HD; i += blockDim.x)
+        S.qs[i / HD][i % HD] = qs[i];
+    for (int i = threadIdx.x; i < ns; i += blockDim.x) {
+        const int ph = i == blk ? phys : P.page_table[(size_t)slot * a.max_logical + i];
+        S.pphys[i] = ph;
+        S.pnt[i] = ph == phys ? off + 1 : P.ntok[ph];
+    }
+    __syncthreads();
+    attn_scores<BF16KV, HD, G, kFW, 8>(P, S, kvh, ns, A.att_scale, 0, kFW);
+    __syncthreads();
+    attn_weights(S, ns, nullptr);
+    __syncthreads();
+    attn_values_layout<BF16KV, HD, G, kFW, 16, 8>(P, S, 0, kvh, ns, A.H, A.att_out, nullptr);
+}
+
 template <bool FP8, bool BF16KV, int NV>
 __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
 {
@@ -1065,6 +1108,14 @@ __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
         krow[i] = ks[i];
     if (A.app->n > 0)
         append_seal_tail<BF16KV>(A.P, *A.app, 0, b, ks, vs, cs);
+    if (A.att_out) {
+        wait_vmcnt<0>();   // this block's K/V row is in memory
+        __syncthreads();
+        if (hd == 128 && G == 3)
+            tail_attention<BF16KV, 128, 3>(A, b, qs, dig + kTailAttnOff);
+        else
+            tail_attention<BF16KV, 64, 1>(A, b, qs, dig + kTailAttnOff);
+    }
 }
 
 // Tokens of one prefill pass (positions p0 .. p0 + T - 1 of one sequence).
@@ -1410,8 +1461,10 @@ static FPhase one_phase(const void *w, const float *sw, float *y, int n, int K)
     return p;
 }
 
+// att_out: the fused launch also computes the next layer's dense attention
+// into it (enqueue_step's tail_att), else null.
 static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app, const int *pos_p, int rope_len,
-                              hipStream_t st)
+                              hipStream_t st, float *att_out, float att_scale)
 {
     const be42_decoder_config &c = d->c;
     const be42_decoder_layer &L = d->w.layers[l];
@@ -1472,6 +1525,8 @@ static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app,
     A.err = d->next + kMaxBatch;
     A.spin_max = d->fail_barriers ? 64u : kFSpinMax;
     A.bias = d->fail_barriers ? 1u << 24 : 0u;
+    A.att_out = l + 1 < c.n_layers ? att_out : nullptr;
+    A.att_scale = att_scale;
     const int nv = (dim + kChunk - 1) / kChunk;
     const bool fp8 = c.wkind != 0, bf16 = c.kv_kind == BE42_KV_BF16;
     auto go = [&](auto f8, auto kb, auto nvc) {
@@ -1544,6 +1599,11 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     // one sequence: everything of a layer after its attention (and the next
     // layer's q/k/v and append) in one fused launch
     const bool fz = d->fused && B == 1;
+    // dense steps of one sequence: each fused launch also runs the next
+    // layer's attention (its tail has the rotated q and the appended K/V), for
+    // the group shapes it is built for and selections of <= 64 pages
+    const bool tail_att = fz && !sparse && dense_max <= kFusedMaxPages &&
+                          ((hd == 128 && H / KV == 3) || (hd == 64 && H / KV == 1));
     for (int l = 0; l < c.n_layers; l++) {
         const be42_decoder_layer &L = d->w.layers[l];
         if (!fz || l == 0) {
@@ -1566,9 +1626,11 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         const int *lslots = d->slots + (size_t)l * c.max_batch;
         bool att_digits = false;   // the attention wrote d->att's digit planes into d->xdig
         if (!sparse) {
-            DEC_TRY(be42_paged_attention(d->pool, d->q, B, H, P.page_table + (size_t)l * c.max_batch * P.max_logical,
-                                         P.n_logical + (size_t)l * c.max_batch, P.max_logical, dense_max, scale,
-                                         d->att, dense_max <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
+            if (!(tail_att && l > 0))
+                DEC_TRY(be42_paged_attention(d->pool, d->q, B, H,
+                                             P.page_table + (size_t)l * c.max_batch * P.max_logical,
+                                             P.n_logical + (size_t)l * c.max_batch, P.max_logical, dense_max, scale,
+                                             d->att, dense_max <= 64 ? 1 : 4, d->attn_ws, d->attn_ws_bytes, st));
         } else if (fused_route) {
             // route + attention in one launch; without the fused layer a split
             // launch also writes the o projection's digit planes
@@ -1593,7 +1655,7 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
                                     hipMemcpyDeviceToDevice, st));
         }
         if (fz) {
-            DEC_TRY(launch_fused_layer(d, l, app, &head->pos, rope_len, st));
+            DEC_TRY(launch_fused_layer(d, l, app, &head->pos, rope_len, st, tail_att ? d->att : nullptr, scale));
             continue;
         }
         if (!att_digits)

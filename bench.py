@@ -992,12 +992,12 @@ def gemm_probe():
 
 def decode_probe():
     """For rocprofv3 runs (--pmc counters or --kernel-trace): the configs[4]
-    3B model (FP8 weights, bf16 pages) at batch 1 after a 64-token prompt,
-    10 decode steps (each a fused-layer launch per layer over 100.8 MB of
-    weights: 2.8 GB per step, so the 256 MB Infinity Cache serves no weight
-    of the next step), then 10 copies of 1 GiB as the byte reference of the
-    FETCH_SIZE / WRITE_SIZE counters.  The context is short (dense
-    attention): the fused layer's traffic does not depend on it."""
+    3B model (FP8 weights, bf16 pages) at batch 1 after a 1088-token prompt
+    (68 pages: the steps route, as at 32k), 10 decode steps (each a
+    fused-layer launch per layer over 100.8 MB of weights: 2.8 GB per step,
+    so the 256 MB Infinity Cache serves no weight of the next step), then 10
+    copies of 1 GiB as the byte reference of the FETCH_SIZE / WRITE_SIZE
+    counters."""
     import numpy as np
     import torch
     import be42
@@ -1008,11 +1008,12 @@ def decode_probe():
     A = B3
     w = decoder_weights(lib, A, "fp8", gen)
     _, hpT = lib.lsh_projection(A["head_dim"], 42)
-    dec = be42.Decoder(lib, decoder_cfg(A, 256, 1, 1, be42.KV_BF16), w, hpT)
-    prompt = np.random.default_rng(6).integers(0, A["vocab"], 64)
+    dec = be42.Decoder(lib, decoder_cfg(A, 2048, 1, 1, be42.KV_BF16), w, hpT)
+    n_prompt = 1088
+    prompt = np.random.default_rng(6).integers(0, A["vocab"], n_prompt)
     tok = dec.prefill(prompt)
     for i in range(10):
-        tok = dec.step([int(tok)] if i == 0 else None, 64 + i, sync=False, batch=1)
+        tok = dec.step([int(tok)] if i == 0 else None, n_prompt + i, sync=False, batch=1)
     torch.cuda.synchronize()
     dec.status()
     dec.close()
