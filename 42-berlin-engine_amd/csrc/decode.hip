@@ -498,6 +498,14 @@ struct FPhase {
     int nseg, K, steps, units, silu;
 };
 
+// The embedding row of a step's token: codes [vocab][dim] (INT8 or FP8) and
+// one scale per row, as k_embed dequantizes them.
+struct EmbRow {
+    const uint8_t *emb;
+    const float *scale;
+    const int *tok;   // the token (device memory)
+};
+
 struct FusedArgs {
     FPhase o, gu, down, qkv;      // qkv.nseg == 0: the last layer
     const float *att;
@@ -515,6 +523,7 @@ struct FusedArgs {
     unsigned bias;       // added to the numbers waited for (0; a test sets it so no wait completes)
     float *att_out;      // the next layer's dense attention output (null: a launch of its own)
     float att_scale;
+    EmbRow er;           // k_fused_layer<..., START>: the step's token, whose embedding is layer 0's input
 };
 
 struct GridBar {
@@ -896,17 +905,21 @@ __device__ __forceinline__ float vec_digits(const float *x, int K, uint8_t *dig,
 // x + delta (both written by other blocks), RMSNorm with w, into digit
 // planes, with the work split as in vec_digits; block b writes its share of
 // x + delta to x_out.  Threads < kRowT (waves 0-3) hold the row exactly as
-// k_rmsnorm's threads do (same sum of squares, same reduction tree).
-template <bool FP8, int NV, class Mid>
+// k_rmsnorm's threads do (same sum of squares, same reduction tree).  EMB:
+// the row is instead the embedding of er's token, formed as k_embed forms it
+// (x and delta unused).
+template <bool FP8, int NV, bool EMB = false, class Mid>
 __device__ __forceinline__ float norm_digits(const float *x, const float *delta, const uint16_t *w, float *x_out,
                                              int dim, float eps, uint8_t *dig, float *red, int b, int nb,
-                                             QuadSync &q, Mid &&mid)
+                                             QuadSync &q, Mid &&mid, const EmbRow &er = EmbRow{})
 {
     constexpr int ND = FP8 ? kF8Digits : kI8Digits;
     const int tid = threadIdx.x, n4 = dim >> 2;
     float *sx_ = dig_stage(dig, ND, dim), *sd_ = sx_ + dim;
-    vec_to_lds(x, sx_, dim);
-    vec_to_lds(delta, sd_, dim);
+    if constexpr (!EMB) {
+        vec_to_lds(x, sx_, dim);
+        vec_to_lds(delta, sd_, dim);
+    }
     asm volatile("" ::: "memory");
     __syncthreads();              // the vectors' loads leave before any weight load of the block
     if (tid >= kRowT) {
@@ -914,14 +927,29 @@ __device__ __forceinline__ float norm_digits(const float *x, const float *delta,
     } else {
         float4 v[NV], h[NV];
         uint2 wv[NV];
-        wait_vmcnt<0>();
-        quad_sync(q);
+        if constexpr (EMB) {
+            const int tok = *er.tok;
+            const float es = er.scale[tok];
+            const uint8_t *row = er.emb + (size_t)tok * dim;
+            auto dq = [](uint32_t c) { return FP8 ? fp8_to_f32((uint8_t)c) : (float)(int8_t)(uint8_t)c; };
 #pragma unroll
-        for (int j = 0; j < NV; j++) {
-            const int i = min(tid + kRowT * j, n4 - 1);
-            const float4 xv = *(const float4 *)(sx_ + 4 * i), dv = *(const float4 *)(sd_ + 4 * i);
-            v[j] = make_float4(xv.x + dv.x, xv.y + dv.y, xv.z + dv.z, xv.w + dv.w);
-            wv[j] = ((const uint2 *)w)[i];
+            for (int j = 0; j < NV; j++) {
+                const int i = min(tid + kRowT * j, n4 - 1);
+                const uint32_t c4 = *(const uint32_t *)(row + 4 * i);
+                v[j] = make_float4(dq(c4 & 0xFFu) * es, dq((c4 >> 8) & 0xFFu) * es, dq((c4 >> 16) & 0xFFu) * es,
+                                   dq(c4 >> 24) * es);
+                wv[j] = ((const uint2 *)w)[i];
+            }
+        } else {
+            wait_vmcnt<0>();
+            quad_sync(q);
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const int i = min(tid + kRowT * j, n4 - 1);
+                const float4 xv = *(const float4 *)(sx_ + 4 * i), dv = *(const float4 *)(sd_ + 4 * i);
+                v[j] = make_float4(xv.x + dv.x, xv.y + dv.y, xv.z + dv.z, xv.w + dv.w);
+                wv[j] = ((const uint2 *)w)[i];
+            }
         }
         float ss = 0.0f;
 #pragma unroll
@@ -1021,7 +1049,7 @@ __device__ __forceinline__ void tail_attention(const FusedArgs &A, int kvh, cons
     attn_values_layout<BF16KV, HD, G, kFW, 16, 8>(P, S, 0, kvh, ns, A.H, A.att_out, nullptr);
 }
 
-template <bool FP8, bool BF16KV, int NV>
+template <bool FP8, bool BF16KV, int NV, bool START>
 __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
 {
     __shared__ __align__(16) uint8_t dig[kFDigBytes];
@@ -1048,30 +1076,39 @@ __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
         const FPhase *pp = &ph;
         return [pp, b, nb, &fr] { ph_prefetch(*pp, b, nb, fr, 0, kFW); };
     };
-    // o projection of the attention output
-    FOut oo = ph_out(A.o, b, nb);
-    float sx = vec_digits<FP8>(A.att, A.qd, dig, red, quad, wload(A.o));
-    ph_compute<FP8>(A.o, b, nb, fr, dig, A.qd, sx, part, ybuf, oo);
-    grid_barrier(gb, 1, [] {});
-    // h = x + o, RMSNorm, gate/up, SiLU * up
-    oo = ph_out(A.gu, b, nb);
-    sx = norm_digits<FP8, NV>(A.X, A.XB, A.ffn_norm, A.Hb, A.dim, A.eps, dig, red, b, nb, quad, wload(A.gu));
-    ph_compute<FP8>(A.gu, b, nb, fr, dig, A.dim, sx, part, ybuf, oo);
-    grid_barrier(gb, 2, [] {});
-    // down projection
-    oo = ph_out(A.down, b, nb);
-    sx = vec_digits<FP8>(A.H2, A.hidden, dig, red, quad, wload(A.down));
-    ph_compute<FP8>(A.down, b, nb, fr, dig, A.hidden, sx, part, ybuf, oo);
-    if (A.qkv.nseg == 0) {
-        // last layer: h and the down output stay for the final norm
-        if (b == 0 && threadIdx.x == 0)
-            __hip_atomic_store(A.gen, gb.base / kFBars + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
+    FOut oo;
+    float sx;
+    if constexpr (!START) {
+        // o projection of the attention output
+        oo = ph_out(A.o, b, nb);
+        sx = vec_digits<FP8>(A.att, A.qd, dig, red, quad, wload(A.o));
+        ph_compute<FP8>(A.o, b, nb, fr, dig, A.qd, sx, part, ybuf, oo);
+        grid_barrier(gb, 1, [] {});
+        // h = x + o, RMSNorm, gate/up, SiLU * up
+        oo = ph_out(A.gu, b, nb);
+        sx = norm_digits<FP8, NV>(A.X, A.XB, A.ffn_norm, A.Hb, A.dim, A.eps, dig, red, b, nb, quad, wload(A.gu));
+        ph_compute<FP8>(A.gu, b, nb, fr, dig, A.dim, sx, part, ybuf, oo);
+        grid_barrier(gb, 2, [] {});
+        // down projection
+        oo = ph_out(A.down, b, nb);
+        sx = vec_digits<FP8>(A.H2, A.hidden, dig, red, quad, wload(A.down));
+        ph_compute<FP8>(A.down, b, nb, fr, dig, A.hidden, sx, part, ybuf, oo);
+        if (A.qkv.nseg == 0) {
+            // last layer: h and the down output stay for the final norm
+            if (b == 0 && threadIdx.x == 0)
+                __hip_atomic_store(A.gen, gb.base / kFBars + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        grid_barrier(gb, 3, [] {});
     }
-    grid_barrier(gb, 3, [] {});
-    // next layer: x = h + down, RMSNorm, q/k/v
+    // next layer: x = h + down (the step's first launch: x = the token's
+    // embedding), RMSNorm, q/k/v
     oo = ph_out(A.qkv, b, nb);
-    sx = norm_digits<FP8, NV>(A.Hb, A.XB, A.attn_norm, A.X, A.dim, A.eps, dig, red, b, nb, quad, wload(A.qkv));
+    if constexpr (START)
+        sx = norm_digits<FP8, NV, true>(nullptr, nullptr, A.attn_norm, A.X, A.dim, A.eps, dig, red, b, nb, quad,
+                                        wload(A.qkv), A.er);
+    else
+        sx = norm_digits<FP8, NV>(A.Hb, A.XB, A.attn_norm, A.X, A.dim, A.eps, dig, red, b, nb, quad, wload(A.qkv));
     ph_compute<FP8>(A.qkv, b, nb, fr, dig, A.dim, sx, part, ybuf, oo);
     grid_barrier(gb, 4, [] {});
     if (b == 0 && threadIdx.x == 0)
@@ -1462,12 +1499,15 @@ static FPhase one_phase(const void *w, const float *sw, float *y, int n, int K)
 }
 
 // att_out: the fused launch also computes the next layer's dense attention
-// into it (enqueue_step's tail_att), else null.
+// into it (enqueue_step's tail_att), else null.  start_tok: the step's first
+// launch (l = -1): the embedding of that token, layer 0's RMSNorm, q/k/v,
+// RoPE and append (and, with att_out, its attention).
 static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app, const int *pos_p, int rope_len,
-                              hipStream_t st, float *att_out, float att_scale)
+                              hipStream_t st, float *att_out, float att_scale, const int *start_tok = nullptr)
 {
     const be42_decoder_config &c = d->c;
-    const be42_decoder_layer &L = d->w.layers[l];
+    const bool start = start_tok != nullptr;
+    const be42_decoder_layer &L = d->w.layers[start ? 0 : l];
     const int dim = c.dim, hidden = c.hidden_dim, qd = c.n_heads * c.head_dim, kd = c.n_kv_heads * c.head_dim;
     FusedArgs A{};
     A.o = one_phase(L.wo, L.so, d->xb, dim, qd);
@@ -1478,8 +1518,8 @@ static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app,
     A.gu.nseg = 2;
     A.gu.silu = 1;
     A.down = one_phase(L.w2, L.s2, d->xb, dim, hidden);
-    if (l + 1 < c.n_layers) {
-        const be42_decoder_layer &N = d->w.layers[l + 1];
+    if (start || l + 1 < c.n_layers) {
+        const be42_decoder_layer &N = d->w.layers[start ? 0 : l + 1];
         A.qkv = one_phase(N.wq, N.sq, d->q, qd, dim);
         A.qkv.w[1] = (const uint8_t *)N.wk;
         A.qkv.w[2] = (const uint8_t *)N.wv;
@@ -1494,7 +1534,7 @@ static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app,
         A.qkv.tend[2] = qd / 16 + 2 * (kd / 16);
         A.qkv.units = A.qkv.tend[2];
         A.attn_norm = N.attn_norm;
-        A.app = app + l + 1;
+        A.app = app + (start ? 0 : l + 1);
     } else {
         A.qkv.nseg = 0;
         A.app = app + l;
@@ -1525,13 +1565,18 @@ static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app,
     A.err = d->next + kMaxBatch;
     A.spin_max = d->fail_barriers ? 64u : kFSpinMax;
     A.bias = d->fail_barriers ? 1u << 24 : 0u;
-    A.att_out = l + 1 < c.n_layers ? att_out : nullptr;
+    A.att_out = start || l + 1 < c.n_layers ? att_out : nullptr;
     A.att_scale = att_scale;
+    A.er = EmbRow{(const uint8_t *)d->w.emb, d->w.emb_s, start_tok};
     const int nv = (dim + kChunk - 1) / kChunk;
     const bool fp8 = c.wkind != 0, bf16 = c.kv_kind == BE42_KV_BF16;
     auto go = [&](auto f8, auto kb, auto nvc) {
-        hipLaunchKernelGGL((k_fused_layer<decltype(f8)::value, decltype(kb)::value, decltype(nvc)::value>),
-                           dim3(d->fnb), dim3(kFT), 0, st, A);
+        if (start)
+            hipLaunchKernelGGL((k_fused_layer<decltype(f8)::value, decltype(kb)::value, decltype(nvc)::value, true>),
+                               dim3(d->fnb), dim3(kFT), 0, st, A);
+        else
+            hipLaunchKernelGGL((k_fused_layer<decltype(f8)::value, decltype(kb)::value, decltype(nvc)::value, false>),
+                               dim3(d->fnb), dim3(kFT), 0, st, A);
     };
     auto pick_nv = [&](auto f8, auto kb) {
         switch (nv) {
@@ -1564,14 +1609,20 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     const AppendStepArgs *app = (const AppendStepArgs *)(params + sizeof(StepHead));
     BE42_HIP(hipMemcpyAsync(params, d->params_host[parity], d->params_bytes, hipMemcpyHostToDevice, st));
     const int *tok = dev_tokens ? d->next : head->tokens;
+    // one sequence: the embedding, layer 0's norm, q/k/v, RoPE and append in
+    // one fused launch (below), and everything of a layer after its
+    // attention (and the next layer's q/k/v and append) in one fused launch
+    const bool fz = d->fused && B == 1;
     const dim3 eg((dim + 255) / 256, B);
-    if (fp8)
-        hipLaunchKernelGGL(k_embed<true>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, tok,
-                           dim);
-    else
-        hipLaunchKernelGGL(k_embed<false>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s, tok,
-                           dim);
-    BE42_LAUNCH_CHECK();
+    if (!fz) {
+        if (fp8)
+            hipLaunchKernelGGL(k_embed<true>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s,
+                               tok, dim);
+        else
+            hipLaunchKernelGGL(k_embed<false>, eg, dim3(256), 0, st, d->x, (const uint8_t *)d->w.emb, d->w.emb_s,
+                               tok, dim);
+        BE42_LAUNCH_CHECK();
+    }
     uint8_t *dig = (uint8_t *)d->xdig;
     // the residual stream alternates between x and xn: a norm with a pending
     // delta writes x + delta to the other buffer
@@ -1596,17 +1647,16 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     const int dense_max = std::min(c.sparse_k, P.max_logical);
     const float *pending = nullptr;   // residual delta not yet added to x
     const bool fused_route = c.sparse_k <= 64 && c.cand_cap <= 256 && H / KV <= 4 && (hd == 64 || hd == 128);
-    // one sequence: everything of a layer after its attention (and the next
-    // layer's q/k/v and append) in one fused launch
-    const bool fz = d->fused && B == 1;
     // dense steps of one sequence: each fused launch also runs the next
     // layer's attention (its tail has the rotated q and the appended K/V), for
     // the group shapes it is built for and selections of <= 64 pages
     const bool tail_att = fz && !sparse && dense_max <= kFusedMaxPages &&
                           ((hd == 128 && H / KV == 3) || (hd == 64 && H / KV == 1));
+    if (fz)
+        DEC_TRY(launch_fused_layer(d, -1, app, &head->pos, rope_len, st, tail_att ? d->att : nullptr, scale, tok));
     for (int l = 0; l < c.n_layers; l++) {
         const be42_decoder_layer &L = d->w.layers[l];
-        if (!fz || l == 0) {
+        if (!fz) {
             BE42_HIP(norm(L.attn_norm, pending));
             DEC_TRY(gemv_multi(d, {{L.wq, L.sq, d->q, qd}, {L.wk, L.sk, d->k, kd}, {L.wv, L.sv, d->v, kd}}, dim, B,
                                st));
@@ -1626,7 +1676,7 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
         const int *lslots = d->slots + (size_t)l * c.max_batch;
         bool att_digits = false;   // the attention wrote d->att's digit planes into d->xdig
         if (!sparse) {
-            if (!(tail_att && l > 0))
+            if (!tail_att)
                 DEC_TRY(be42_paged_attention(d->pool, d->q, B, H,
                                              P.page_table + (size_t)l * c.max_batch * P.max_logical,
                                              P.n_logical + (size_t)l * c.max_batch, P.max_logical, dense_max, scale,
