@@ -291,6 +291,37 @@ def test_fused_layer_matches_separate_launches(be, orc, monkeypatch, kind, kv_ki
                                                                                     errs.max())
 
 
+@pytest.mark.parametrize("kv_kind", [OR_KV_INT8, OR_KV_BF16])
+def test_fused_layer_group3_matches_separate_launches(be, orc, monkeypatch, kv_kind):
+    """As above for the 3B model's head group (3 query heads per KV head,
+    head_dim 128), whose dense steps run the next layer's attention in the
+    fused launch's tail from 8 waves in the 16-wave layout of the separate
+    attention launch: 2 layers, d 768, 6/2 heads, sparse_k 8 (positions past
+    128 route), INT8 weights, logits of every step bit-identical."""
+    rng = np.random.default_rng(78)
+    w = make_model(rng, 2, 768, 6, 2, 128, 1536, 1024, "int8")
+    oc, gc = configs(2, 768, 6, 2, 128, 1536, 1024, 512, 1, "int8", kv_kind, 8, 64)
+    _, hpT = orc.lsh_init(128, 42)
+    wd = to_device(w)
+    prompt = rng.integers(0, 1024, 140)
+
+    def run():
+        dec = be42.Decoder(be, gc, wd, hpT)
+        lg = torch.empty((1, 1024), device="cuda")
+        outs = []
+        for pos in range(140):
+            dec.step([int(prompt[pos])], pos, logits=lg)
+            outs.append(lg[0].cpu().numpy().copy())
+        dec.close()
+        return np.array(outs)
+
+    monkeypatch.setenv("BE42_DECODE_FUSED", "0")
+    l0 = run()
+    monkeypatch.delenv("BE42_DECODE_FUSED")
+    l1 = run()
+    np.testing.assert_array_equal(l0, l1)
+
+
 def test_barrier_timeout_is_reported(be, orc, monkeypatch):
     """A fused-layer grid barrier whose wait gives up must be reported even
     when no step asks for its tokens.  BE42_DECODE_FAIL_BARRIERS=1 makes every
