@@ -524,6 +524,7 @@ struct FusedArgs {
     float *att_out;      // the next layer's dense attention output (null: a launch of its own)
     float att_scale;
     EmbRow er;           // k_fused_layer<..., START>: the step's token, whose embedding is layer 0's input
+    int pf_route;        // the next layer's attention routes: warm the L2 with its routing tables
 };
 
 struct GridBar {
@@ -1113,8 +1114,26 @@ __global__ __launch_bounds__(kFT, 1) void k_fused_layer(const FusedArgs A)
     grid_barrier(gb, 4, [] {});
     if (b == 0 && threadIdx.x == 0)
         __hip_atomic_store(A.gen, gb.base / kFBars + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (b >= A.KV)
+    if (b >= A.KV) {
+        if (A.pf_route && b < A.KV + 8 && threadIdx.x < kWave) {
+            // Blocks KV .. KV + 7 (one per XCD; they have no tail): the next
+            // layer's routing tables (its page hashes and page-table row, the
+            // projection) into their XCD's L2, one word per 128-byte line into
+            // an LDS word nobody reads, so that the router's first loads hit L2.
+            const AppendStepArgs &ap = *A.app;
+            const size_t base = (size_t)ap.slot[0] * ap.max_logical;
+            const int hd = A.P.head_dim, n = ap.pos[0] / kPg + 1;
+            const int lh = (n + 63) / 64, lt = (n + 31) / 32, lp = (hd * 16 + 31) / 32;
+            for (int li = threadIdx.x; li < lh + lt + lp; li += kWave) {
+                const void *src = li < lh        ? (const void *)(A.P.page_hash + base + min(li * 64, n - 1))
+                                  : li < lh + lt ? (const void *)(A.P.page_table + base + min((li - lh) * 32, n - 1))
+                                                 : (const void *)(A.P.hpT + min((li - lh - lt) * 32, hd * 16 - 1));
+                __builtin_amdgcn_global_load_lds(src, (lds_void *)(dig + kFDigBytes - 256), 4, 0, 0);
+            }
+            wait_vmcnt<0>();   // the LDS writes land before the workgroup ends
+        }
         return;
+    }
     // RoPE of the q heads of KV head b and of k head b, K/V append and seal
     const int hd = A.P.head_dim, half = hd / 2, G = A.H / A.KV, tid = threadIdx.x;
     float *qs = (float *)dig, *ks = qs + G * hd, *vs = ks + hd, *cs = vs + hd;
@@ -1503,7 +1522,8 @@ static FPhase one_phase(const void *w, const float *sw, float *y, int n, int K)
 // launch (l = -1): the embedding of that token, layer 0's RMSNorm, q/k/v,
 // RoPE and append (and, with att_out, its attention).
 static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app, const int *pos_p, int rope_len,
-                              hipStream_t st, float *att_out, float att_scale, const int *start_tok = nullptr)
+                              hipStream_t st, float *att_out, float att_scale, const int *start_tok = nullptr,
+                              bool pf_route = false)
 {
     const be42_decoder_config &c = d->c;
     const bool start = start_tok != nullptr;
@@ -1568,6 +1588,7 @@ static int launch_fused_layer(be42_decoder *d, int l, const AppendStepArgs *app,
     A.att_out = start || l + 1 < c.n_layers ? att_out : nullptr;
     A.att_scale = att_scale;
     A.er = EmbRow{(const uint8_t *)d->w.emb, d->w.emb_s, start_tok};
+    A.pf_route = pf_route && (start || l + 1 < c.n_layers);
     const int nv = (dim + kChunk - 1) / kChunk;
     const bool fp8 = c.wkind != 0, bf16 = c.kv_kind == BE42_KV_BF16;
     auto go = [&](auto f8, auto kb, auto nvc) {
@@ -1653,7 +1674,8 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
     const bool tail_att = fz && !sparse && dense_max <= kFusedMaxPages &&
                           ((hd == 128 && H / KV == 3) || (hd == 64 && H / KV == 1));
     if (fz)
-        DEC_TRY(launch_fused_layer(d, -1, app, &head->pos, rope_len, st, tail_att ? d->att : nullptr, scale, tok));
+        DEC_TRY(launch_fused_layer(d, -1, app, &head->pos, rope_len, st, tail_att ? d->att : nullptr, scale, tok,
+                                   sparse && fused_route));
     for (int l = 0; l < c.n_layers; l++) {
         const be42_decoder_layer &L = d->w.layers[l];
         if (!fz) {
@@ -1705,7 +1727,8 @@ static int enqueue_step(be42_decoder *d, int B, bool sparse, bool dev_tokens, fl
                                     hipMemcpyDeviceToDevice, st));
         }
         if (fz) {
-            DEC_TRY(launch_fused_layer(d, l, app, &head->pos, rope_len, st, tail_att ? d->att : nullptr, scale));
+            DEC_TRY(launch_fused_layer(d, l, app, &head->pos, rope_len, st, tail_att ? d->att : nullptr, scale,
+                                       nullptr, sparse && fused_route));
             continue;
         }
         if (!att_digits)
