@@ -153,6 +153,34 @@ def test_top_p_edges(be, orc):
     assert be.sample_top_p(xt, 1.0, 0.0, torch.tensor([0.7], device="cuda")).item() == int(np.argmax(p))
 
 
+@pytest.mark.parametrize("n", [1, 2, 5, 63, 65])
+def test_samplers_short_rows(be, orc, n):
+    """Rows shorter than a wave or a block: the per-wave ranges of the
+    temperature walk and of the top-p tie pass are mostly empty, and one
+    entry is its own set; every pick equals the oracle's (short rows keep
+    the fp32 drift far below the gaps between their running sums)."""
+    rng = np.random.default_rng(500 + n)
+    B = 4
+    x = logits_batch(rng, B, n, 2.0)
+    xt = torch.from_numpy(x).cuda()
+    for rep in range(3):
+        u = rng.uniform(0, 1, B).astype(np.float32)
+        ut = torch.from_numpy(u).cuda()
+        gt = be.sample_temperature(xt, 1.0, ut).cpu().numpy()
+        gp = be.sample_top_p(xt, 1.0, 0.9, ut).cpu().numpy()
+        for b in range(B):
+            ok, near = temperature_case(x[b], 1.0, float(u[b]))
+            assert ok(int(gt[b])), (n, rep, b)
+            if not near:
+                assert gt[b] == orc.sample_temperature(x[b], 1.0, float(u[b])), (n, rep, b)
+            ok, near = top_p_case(x[b], 1.0, 0.9, float(u[b]))
+            assert ok(int(gp[b])), (n, rep, b)
+            if not near:
+                assert gp[b] == orc.sample_top_p(x[b], 1.0, 0.9, float(u[b])), (n, rep, b)
+            if n == 1:
+                assert gt[b] == 0 and gp[b] == 0
+
+
 def test_dropin_samplers(be, orc):
     dl = D.bind(be.lib)
     rng = np.random.default_rng(9)
